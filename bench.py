@@ -1,0 +1,226 @@
+"""Token2Wav hot-path benchmark on one MI355X: 10-step CFG Euler DiT solve + HiFT, B=32 CFG rows (16 streams x 400
+mel frames, chunk-causal attention with chunk 50), random-init weights, synthetic inputs resident in HBM.
+
+Prints one JSON line: mel frames/s of the 16 streams' output (value), audio-seconds/s, per-chunk p50 latency of a
+streaming chunk (300-frame cached prompt + 50 new frames, one stream, CFG pair, 10 steps, + HiFT), the roofline of
+the dominant kernel (the DiT's conv1 GEMM, timed with HIP events on its own stream) and the fp32 CPU oracle baseline
+timed on a bounded sample on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (AMD public spec)
+
+
+def dit_flops_per_solve(cfg, rows_T: list[int], chunk: int) -> tuple[float, float]:
+    """Algorithmic FLOPs of one 10-step CFG solve over real tokens: GEMMs 28 H^2 D + 2*320 H + 2 H mel per token per
+    step (both CFG rows counted) and attention 4 H per visible (query, key) pair per block."""
+    H, D, mel = cfg.hidden, cfg.depth, cfg.mel
+    per_tok = 28 * H * H * D + 2 * 4 * mel * H + 2 * H * mel
+    toks = 2 * sum(rows_T)
+    pairs = 0
+    for T in rows_T:
+        c = np.arange(T) // chunk if chunk > 0 else np.zeros(T, dtype=int)
+        lim = np.minimum(T, (c + 1) * chunk) if chunk > 0 else np.full(T, T)
+        pairs += 2 * int(lim.sum())
+    return float(per_tok * toks * cfg.steps), float(4 * H * pairs * D * cfg.steps)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--streams", type=int, default=16)
+    ap.add_argument("--frames", type=int, default=400)
+    ap.add_argument("--chunk", type=int, default=50)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-hift", action="store_true")
+    ap.add_argument("--latency-reps", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (no sharding or collectives); use --gpus 1", file=sys.stderr)
+        return 2
+
+    import t2w_amd  # noqa: F401
+    from t2w_amd import _lib
+    from t2w_amd.config import DiTConfig, HiFTConfig
+    from t2w_amd.dit import DiTModel, FastDiT
+    from t2w_amd.weights import init_dit, init_hift
+
+    dev = "cuda"
+    cfg = DiTConfig()
+    W = init_dit(cfg, seed=2)
+    model = DiTModel(W, cfg)
+    model.drop_table_weights()
+    n, T = args.streams, args.frames
+    fd = FastDiT(model, n_slots=max(8192, 2 * n * T + 4096), max_streams=n + 2, use_graphs=True)
+    g = torch.Generator().manual_seed(2)
+    mus = [torch.randn(cfg.mel, T, generator=g).to(dev) for _ in range(n)]
+    spks = torch.randn(n, cfg.mel, generator=g).to(dev)
+    caches = [fd.new_cache() for _ in range(n)]
+
+    hift = None
+    if not args.no_hift:
+        from t2w_amd.hift import HiFTModel
+
+        Wh = init_hift(HiFTConfig(), seed=3)
+        hift = HiFTModel(Wh, HiFTConfig())
+        hsrc = torch.zeros(n, 1, 0, device=dev)
+        hnoise = hift.noise([1000 + i for i in range(n)], T * hift.cfg.upsample_scale)
+
+    def step():
+        mels = fd.solve(caches, mus, spks, None, [False] * n, chunk=args.chunk)
+        if hift is not None:
+            mel = torch.stack(mels)
+            hift.forward_noise(mel, hsrc, *hnoise)
+        return mels
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    frames = n * T
+    gemm_f, attn_f = dit_flops_per_solve(cfg, [T] * n, args.chunk)
+
+    # DiT solve alone (for the MFMA fraction of the whole solve)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(max(1, args.steps // 2)):
+        fd.solve(caches, mus, spks, None, [False] * n, chunk=args.chunk)
+    torch.cuda.synchronize()
+    dit_dt = (time.perf_counter() - t1) / max(1, args.steps // 2)
+
+    # dominant kernel: the conv1 GEMM (taps mode, bf16 out) at this workload's shape, HIP events on its own stream
+    H, N = cfg.hidden, 2 * n * T
+    R = 2 * n
+    P = torch.randn(N + 2 * R, H, device=dev).bfloat16()
+    Wc = (torch.randn(H, 3 * H, device=dev) * 0.02).bfloat16()
+    bc = torch.zeros(H, device=dev)
+    tok_row = np.repeat(np.arange(R), T)
+    a_src = torch.from_numpy((np.arange(N) + 2 * tok_row).astype(np.int32)).to(dev)
+    out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
+    s = torch.cuda.Stream()
+    L = _lib.lib()
+    with torch.cuda.stream(s):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        for _ in range(3):
+            _lib.check(L.t2w_gemm_bf16(P.data_ptr(), H, a_src.data_ptr(), Wc.data_ptr(), bc.data_ptr(), None, out.data_ptr(), H, N, H, 3 * H, 0, s.cuda_stream))
+        e0.record(s)
+        for _ in range(reps):
+            _lib.check(L.t2w_gemm_bf16(P.data_ptr(), H, a_src.data_ptr(), Wc.data_ptr(), bc.data_ptr(), None, out.data_ptr(), H, N, H, 3 * H, 0, s.cuda_stream))
+        e1.record(s)
+    s.synchronize()
+    k_ms = e0.elapsed_time(e1) / reps
+    k_tflops = 2.0 * N * H * 3 * H / (k_ms * 1e-3) / 1e12
+
+    # per-chunk latency: one stream, 300-frame prompt cached, 50 new frames, CFG pair, 10 steps, + HiFT of the window
+    lat = None
+    if args.latency_reps > 0:
+        fl = FastDiT(model, n_slots=4096, max_streams=2, use_graphs=True)
+        c = fl.new_cache(keep=300)
+        pm = torch.randn(cfg.mel, 300, generator=g).to(dev)
+        fl.solve([c], [pm], spks[:1], [torch.randn(cfg.mel, 300, generator=g).to(dev)], [True])
+        wm = torch.randn(cfg.mel, 50, generator=g).to(dev)
+        hs = None
+        if hift is not None:
+            hs = (torch.zeros(1, 1, 0, device=dev), *hift.noise([7], 50 * hift.cfg.upsample_scale))
+        ts = []
+        for i in range(args.latency_reps + 3):
+            torch.cuda.synchronize()
+            a = time.perf_counter()
+            m = fl.solve([c], [wm], spks[:1], None, [False])
+            if hift is not None:
+                hift.forward_noise(m[0][None], *hs)
+            torch.cuda.synchronize()
+            if i >= 3:
+                ts.append(time.perf_counter() - a)
+        lat = float(np.median(ts) * 1e3)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(W, T, args.chunk, hift_weights=Wh if hift is not None else None)
+
+    res = {
+        "metric": "Token2Wav mel frames/s (10-step CFG DiT+HiFT, B=32) + per-chunk p50 latency",
+        "value": frames / dt,
+        "unit": "mel frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dt * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, seeded N(0,1) inputs)",
+        "config": {"workload": f"{n} streams x {T} mel frames, CFG B={2 * n}, chunk-causal {args.chunk}, 10-step Euler DiT"
+                               + ("" if hift is None else " + HiFT fp32"),
+                   "global_batch": 2 * n, "seq_len": T, "parallelism": "single GPU"},
+        "audio_seconds_per_s": frames / 50.0 / dt,
+        "p50_chunk_latency_ms": lat,
+        "dit_solve_ms": dit_dt * 1e3,
+        "dit_mfma_frac": (gemm_f + attn_f) / dit_dt / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<128,128,2,2,EPI_BF16,taps> (DiT conv1)", "achieved": k_tflops,
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": k_tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
+                     "launch_ms": k_ms, "flops_per_launch": 2.0 * N * H * 3 * H},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res))
+    return 0
+
+
+def cpu_baseline(W, T: int, chunk: int, hift_weights=None) -> dict:
+    """fp32 CPU oracle on this host's cores: one estimator forward of one stream's CFG pair (2 rows x T frames,
+    chunk-causal) x 10 steps, plus HiFT of the stream's T-frame mel; mel frames/s of that one stream."""
+    from oracle import dit as od
+    from oracle import hift as oh
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    d = od.dims_of(W)
+    g = torch.Generator().manual_seed(5)
+    x, mu = torch.randn(2, 80, T, generator=g), torch.randn(2, 80, T, generator=g)
+    spk = torch.randn(2, 80, generator=g)
+    cnn = torch.zeros(d.depth, 2, 2 * d.hidden, 2)
+    att = torch.zeros(d.depth, 2, d.heads, 0, 2 * d.head_dim)
+    mask = od.chunk_mask(T, chunk)[None].expand(2, T, T)
+    tr = torch.full((2,), T, dtype=torch.int64)
+    with torch.no_grad():
+        temb = od.t_embed(W, torch.full((2,), 0.5))
+        t0 = time.perf_counter()
+        od.estimator_chunk(W, d, x, mu, temb, spk, torch.zeros_like(mu), cnn, att, mask, tr)
+        fwd = time.perf_counter() - t0
+        hift_s = 0.0
+        if hift_weights is not None:
+            h = oh.HiFT(hift_weights)
+            mel = torch.randn(1, 80, T, generator=g) * 2 - 5
+            ri, nz = oh.hift_noise(9, [1], T * 480)
+            t0 = time.perf_counter()
+            oh.forward_noise(h, mel, torch.zeros(1, 1, 0), ri, nz)
+            hift_s = time.perf_counter() - t0
+    total = 10 * fwd + hift_s
+    return {"value": T / total, "unit": "mel frames/s", "cores": cores, "kind": "port",
+            "sample": f"fp32 oracle: 1 estimator forward of a CFG pair (2 x {T} frames, chunk {chunk}) timed and x10 steps, "
+                      f"+ HiFT of one {T}-frame mel ({'timed' if hift_weights is not None else 'not run'}); forward {fwd:.2f} s, HiFT {hift_s:.2f} s"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,145 @@
+/* C ABI of the MI355X Token2Wav hot path (libt2w_hip.so, gfx950).
+ *
+ * Plain pointers and sizes only.  Every tensor argument is a device pointer unless stated otherwise; weights are bf16
+ * [out, in] row-major, biases / norm affines / tables fp32.  Every launch goes on the caller's stream (a hipStream_t
+ * passed as void*); nothing here synchronises.  Functions return 0 on success, a nonzero status otherwise, with the
+ * message in t2w_last_error() (thread-local).
+ *
+ * Reference interfaces replaced (paths in the reference repository):
+ *   t2w_dit_solve        FastDiT.solve body (engine/runtime/dit_fast.py:269-344, graph replay :458-472) and
+ *                        BatchedToken2Wav._solve (engine/runtime/token2wav_batch.py:632-702)
+ *   t2w_dit_forward      BatchedToken2Wav._estimator_temb (engine/runtime/token2wav_batch.py:787-810)
+ *   t2w_dit_build_mods   FastDiT._modulations (engine/runtime/dit_fast.py:157-178)
+ *   t2w_gemm_bf16        F.linear of the block GEMMs (engine/runtime/dit_fast.py:283-301)
+ *   t2w_attention        FlashInfer BatchPrefillWithPagedKVCacheWrapper.run (engine/runtime/dit_fast.py:291)
+ *   t2w_qk_norm_scatter  dit_kernels.qk_norm_scatter (engine/runtime/dit_kernels.py:132-142)
+ *   t2w_ln_mod           dit_kernels.ln_mod (engine/runtime/dit_kernels.py:27-31)
+ *   t2w_hift_*           hift_forward_noise / _hift_decode / istft_overlap_add (engine/models/token2wav.py:128-236)
+ *   t2w_graph_*          torch.cuda.CUDAGraph capture / replay of the solve and HiFT (dit_fast.py:392-422,
+ *                        hift_graph.py:35-47)
+ */
+#ifndef T2W_H
+#define T2W_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int t2w_abi_version(void);
+const char* t2w_last_error(void);
+
+/* ---------------------------------------------------------------- DiT estimator and CFG Euler solve */
+
+typedef struct t2w_dit t2w_dit;
+
+typedef struct {
+  int mel, hidden, depth, heads, head_dim, ffn, freq, steps;
+  float eps_block, eps_qk, eps_conv, eps_final, cfg_rate;
+} t2w_dit_dims;
+
+typedef struct {
+  const void* qkv_w; const float* qkv_b;     /* [3H, H]: to_q | to_k | to_v */
+  const float* qn_w; const float* qn_b;       /* q_norm [64] */
+  const float* kn_w; const float* kn_b;       /* k_norm [64] */
+  const void* proj_w; const float* proj_b;    /* [H, H] */
+  const void* c1_w; const float* c1_b;        /* [H, 3H] frame-major: tap 0 multiplies frame t-2 */
+  const float* cln_w; const float* cln_b;     /* conv block LayerNorm [H] */
+  const void* c2_w; const float* c2_b;        /* [H, 3H] */
+  const void* fc1_w; const float* fc1_b;      /* [F, H] */
+  const void* fc2_w; const float* fc2_b;      /* [H, F] */
+} t2w_dit_block;
+
+typedef struct {
+  const void* in_w; const float* in_b;        /* [H, 4 mel]: x | mu | spk | cond */
+  const void* out_w; const float* out_b;      /* [mel, H] */
+  const float* mods;                          /* [steps, depth, 9, H]: shift, 1 + scale, gate of msa, mlp, conv */
+  const float* final_mods;                    /* [steps, 2, H]: shift, 1 + scale */
+  const float* dts;                           /* HOST pointer [steps]: Euler step sizes */
+} t2w_dit_globals;
+
+int t2w_dit_create(const t2w_dit_dims* dims, t2w_dit** out);
+int t2w_dit_set_block(t2w_dit* m, int block, const t2w_dit_block* w);
+int t2w_dit_set_globals(t2w_dit* m, const t2w_dit_globals* g);
+void t2w_dit_destroy(t2w_dit* m);
+
+/* Timestep conditioning tables for S <= 16 t values (fp32 weights):
+ * emb = [cos(1000 t f) | sin(1000 t f)]; temb = W2 silu(W0 emb + b0) + b2;
+ * mods_out[s] = Wada silu(temb) + bada (depth * 9H values, then 1 added to the scale columns);
+ * final_out[s] = Wfin silu(temb) + bfin (2H values, 1 added to the scale half). */
+typedef struct {
+  const float* freqs;                         /* [freq / 2] */
+  const float* te0_w; const float* te0_b;     /* [H, freq] */
+  const float* te2_w; const float* te2_b;     /* [H, H] */
+  const float* ada_w; const float* ada_b;     /* [depth * 9H, H] */
+  const float* fin_w; const float* fin_b;     /* [2H, H] */
+} t2w_mod_weights;
+
+size_t t2w_dit_mods_workspace_bytes(const t2w_dit* m, int S);
+int t2w_dit_build_mods(const t2w_dit* m, const t2w_mod_weights* w, const float* ts, int S, float* mods_out,
+                       float* final_out, void* workspace, void* stream);
+
+/* One packed ragged call.  Rows 0..R/2-1 are the conditional rows of the requests, R/2..R-1 the unconditional rows in
+ * the same order; a row's tokens are contiguous, the first half of the tokens belong to the conditional rows. */
+typedef struct {
+  int n_tok, n_rows, half, n_tiles, chunk;
+  const float* x0;          /* [half, mel] initial noise of the conditional tokens */
+  const float* stat;        /* [half, 3 mel]: mu | spk | cond of the conditional tokens (unconditional: zeros) */
+  const float* in_rows;     /* t2w_dit_forward only: [n_tok, 4 mel] full estimator input rows */
+  float* out;               /* solve: [half, mel] final x; forward: [n_tok, mel] dphi */
+  const int* tok_row;       /* [n_tok] row of each token */
+  const int* tok_pos;       /* [n_tok] position inside its row */
+  const int* a_src;         /* [n_tok] tok + 2 * row: first frame of its conv window in the padded frame buffer */
+  const int* new_slot;      /* [n_tok] key slot receiving the token's key / value */
+  const int* row_start;     /* [R] */
+  const int* row_len;       /* [R] */
+  const int* row_kv_off;    /* [R] offset of the row's key list in kv_idx */
+  const int* row_kv_len;    /* [R] length of the row's key list (its tokens first, then its cached keys) */
+  const int* conv_rd;       /* [R] conv cache row slot read */
+  const int* conv_wr;       /* [R] conv cache row slot written (never one that any row reads in this call) */
+  const int* kv_idx;
+  const int* tiles;         /* [n_tiles, 2] (row, first position) of each 64-query attention tile */
+  void* k_pool;             /* [steps * depth, n_slots, H] bf16 */
+  void* v_pool;
+  long long pool_layer_stride;  /* n_slots * H */
+  void* conv_pool;          /* [row slots, steps, depth, 2, 2, H] bf16 */
+  void* workspace;
+  size_t workspace_bytes;
+} t2w_solve_args;
+
+size_t t2w_dit_workspace_bytes(const t2w_dit* m, int n_tok, int n_rows);
+int t2w_dit_solve(const t2w_dit* m, const t2w_solve_args* a, void* stream);
+/* One estimator evaluation at Euler step `step`'s key/value and conv-cache layers with the given tables
+ * (mods [depth, 9, H], final_mods [2, H]) on in_rows; writes dphi [n_tok, mel] to a->out. */
+int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const float* mods, const float* final_mods,
+                    void* stream);
+
+/* ---------------------------------------------------------------- kernel-level entry points (tests, benchmarks) */
+
+/* C = A . W^T + bias; epi 0: bf16 out, 1: GELU-tanh bf16 out, 2: C(fp32) += gate * (.), 3: fp32 out.
+ * a_src non-null: conv taps mode, A row m = frames a_src[m] .. a_src[m] + K / lda - 1 of A (rows lda wide). */
+int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
+                  void* C, int ldc, int M, int N, int K, int epi, void* stream);
+int t2w_ln_mod(const float* h, const float* shift, const float* scale1, float eps, void* out, int N, int H,
+               void* stream);
+int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const float* kw, const float* kb, float eps,
+                        void* q_out, void* k_pool, void* v_pool, const int* slots, int N, int heads, void* stream);
+int t2w_attention(const void* q, const void* k_pool, const void* v_pool, void* out, const int* kv_idx,
+                  const int* row_start, const int* row_len, const int* row_kv_off, const int* row_kv_len,
+                  const int* tiles, int n_tiles, int heads, int chunk, float scale, void* stream);
+
+/* ---------------------------------------------------------------- graphs (hipGraph capture of a stream) */
+
+typedef struct t2w_graph t2w_graph;
+int t2w_graph_begin(void* stream);
+int t2w_graph_end(void* stream, t2w_graph** out);
+int t2w_graph_launch(t2w_graph* g, void* stream);
+void t2w_graph_destroy(t2w_graph* g);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* T2W_H */

@@ -1,0 +1,105 @@
+"""ctypes binding of ``libt2w_hip.so`` (the C ABI declared in ``include/t2w.h``).
+
+The library is loaded from the package directory; a missing library is an error (there is no CPU fallback).  Device
+pointers are passed as integers from ``torch.Tensor.data_ptr()`` and the stream as the raw ``hipStream_t`` of torch's
+current stream.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "libt2w_hip.so"
+
+P = C.c_void_p
+I = C.c_int
+F = C.c_float
+FP = C.POINTER(C.c_float)
+
+
+class DitDims(C.Structure):
+    _fields_ = [(n, I) for n in ("mel", "hidden", "depth", "heads", "head_dim", "ffn", "freq", "steps")] + \
+               [(n, F) for n in ("eps_block", "eps_qk", "eps_conv", "eps_final", "cfg_rate")]
+
+
+class DitBlock(C.Structure):
+    _fields_ = [(n, P) for n in ("qkv_w", "qkv_b", "qn_w", "qn_b", "kn_w", "kn_b", "proj_w", "proj_b", "c1_w", "c1_b",
+                                 "cln_w", "cln_b", "c2_w", "c2_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b")]
+
+
+class DitGlobals(C.Structure):
+    _fields_ = [(n, P) for n in ("in_w", "in_b", "out_w", "out_b", "mods", "final_mods")] + [("dts", FP)]
+
+
+class ModWeights(C.Structure):
+    _fields_ = [(n, P) for n in ("freqs", "te0_w", "te0_b", "te2_w", "te2_b", "ada_w", "ada_b", "fin_w", "fin_b")]
+
+
+class SolveArgs(C.Structure):
+    _fields_ = [(n, I) for n in ("n_tok", "n_rows", "half", "n_tiles", "chunk")] + \
+               [(n, P) for n in ("x0", "stat", "in_rows", "out", "tok_row", "tok_pos", "a_src", "new_slot", "row_start", "row_len",
+                                 "row_kv_off", "row_kv_len", "conv_rd", "conv_wr", "kv_idx", "tiles", "k_pool", "v_pool")] + \
+               [("pool_layer_stride", C.c_longlong), ("conv_pool", P), ("workspace", P), ("workspace_bytes", C.c_size_t)]
+
+
+_SIGS = {
+    "t2w_abi_version": (I, []),
+    "t2w_last_error": (C.c_char_p, []),
+    "t2w_dit_create": (I, [C.POINTER(DitDims), C.POINTER(P)]),
+    "t2w_dit_set_block": (I, [P, I, C.POINTER(DitBlock)]),
+    "t2w_dit_set_globals": (I, [P, C.POINTER(DitGlobals)]),
+    "t2w_dit_destroy": (None, [P]),
+    "t2w_dit_mods_workspace_bytes": (C.c_size_t, [P, I]),
+    "t2w_dit_build_mods": (I, [P, C.POINTER(ModWeights), P, I, P, P, P, P]),
+    "t2w_dit_workspace_bytes": (C.c_size_t, [P, I, I]),
+    "t2w_dit_solve": (I, [P, C.POINTER(SolveArgs), P]),
+    "t2w_dit_forward": (I, [P, C.POINTER(SolveArgs), I, P, P, P]),
+    "t2w_gemm_bf16": (I, [P, I, P, P, P, P, P, I, I, I, I, I, P]),
+    "t2w_ln_mod": (I, [P, P, P, F, P, I, I, P]),
+    "t2w_qk_norm_scatter": (I, [P, P, P, P, P, F, P, P, P, P, I, I, P]),
+    "t2w_attention": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, F, P]),
+    "t2w_graph_begin": (I, [P]),
+    "t2w_graph_end": (I, [P, C.POINTER(P)]),
+    "t2w_graph_launch": (I, [P, P]),
+    "t2w_graph_destroy": (None, [P]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (raises when it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH.name} is not built: run __graft_entry__.build() (hipcc, gfx950)")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        raise RuntimeError(f"t2w {what}: {lib().t2w_last_error().decode()}")
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGS)
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(stream=None) -> int:
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream

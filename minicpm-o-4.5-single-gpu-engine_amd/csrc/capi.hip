@@ -1,0 +1,323 @@
+// C-ABI layer: the DiT model object, the whole CFG Euler solve as one call, kernel-level entry points and hipGraph
+// capture.  No allocation happens in any compute call: the caller passes a workspace of t2w_dit_workspace_bytes().
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/t2w.h"
+#include "t2w_internal.h"
+
+using namespace t2w;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const char* what, hipError_t e = hipSuccess) {
+  char buf[512];
+  if (e != hipSuccess)
+    snprintf(buf, sizeof buf, "%s: %s", what, hipGetErrorString(e));
+  else
+    snprintf(buf, sizeof buf, "%s", what);
+  g_err = buf;
+  return 1;
+}
+
+#define T2W_CHECK(expr, what)                 \
+  do {                                        \
+    hipError_t e_ = (expr);                   \
+    if (e_ != hipSuccess) return fail(what, e_); \
+  } while (0)
+
+size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
+struct t2w_dit {
+  t2w_dit_dims d;
+  std::vector<t2w_dit_block> blocks;
+  std::vector<bool> block_set;
+  t2w_dit_globals g;
+  std::vector<float> dts;
+  bool globals_set = false;
+};
+
+namespace {
+
+struct Work {  // carve of the caller's workspace for n tokens, R rows
+  bf16_t* a_in; float* x; float* h; bf16_t* abuf; bf16_t* big; bf16_t* q; bf16_t* ao; bf16_t* P; float* dphi;
+};
+
+size_t carve(const t2w_dit_dims& d, int N, int R, char* base, Work* w) {
+  const int H = d.hidden, M = d.mel;
+  const size_t bigc = (size_t)N * (size_t)(3 * H > d.ffn ? 3 * H : d.ffn);
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return base ? (void*)(base + o) : nullptr; };
+  Work t;
+  t.a_in = (bf16_t*)take((size_t)N * 4 * M * 2);
+  t.x = (float*)take((size_t)N * M * 4);
+  t.h = (float*)take((size_t)N * H * 4);
+  t.abuf = (bf16_t*)take((size_t)N * H * 2);
+  t.big = (bf16_t*)take(bigc * 2);
+  t.q = (bf16_t*)take((size_t)N * H * 2);
+  t.ao = (bf16_t*)take((size_t)N * H * 2);
+  t.P = (bf16_t*)take((size_t)(N + 2 * R) * H * 2);
+  t.dphi = (float*)take((size_t)N * M * 4);
+  if (w) *w = t;
+  return off;
+}
+
+int check_model(const t2w_dit* m) {
+  if (!m) return fail("null model");
+  if (!m->globals_set) return fail("model globals not set");
+  for (size_t b = 0; b < m->block_set.size(); ++b)
+    if (!m->block_set[b]) return fail("model block weights not set");
+  return 0;
+}
+
+GemmArgs gemm_args(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate, void* C,
+                   int ldc, int M, int N, int K) {
+  GemmArgs g;
+  g.A = (const bf16_t*)A;
+  g.lda = lda;
+  g.a_src = a_src;
+  g.tapC = lda;
+  g.B = (const bf16_t*)W;
+  g.ldb = K;
+  g.bias = bias;
+  g.gate = gate;
+  g.C = C;
+  g.ldc = ldc;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  return g;
+}
+
+// One estimator evaluation from w.a_in (bf16 [N, 4 mel]) to w.dphi (fp32 [N, mel]) at Euler step `step`.
+int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int step, const float* mods,
+                  const float* fmods, float* dphi, hipStream_t st) {
+  const t2w_dit_dims& d = m->d;
+  const int N = a->n_tok, R = a->n_rows, H = d.hidden, F = d.ffn, M = d.mel, D = d.depth;
+  T2W_CHECK(gemm_bf16(gemm_args(w.a_in, 4 * M, nullptr, m->g.in_w, m->g.in_b, nullptr, w.h, H, N, H, 4 * M), EPI_F32, st), "in_proj");
+  const long long cstride = (long long)d.steps * D * 4 * H;
+  for (int b = 0; b < D; ++b) {
+    const t2w_dit_block& k = m->blocks[b];
+    const float* md = mods + (size_t)b * 9 * H;
+    const float *sh_a = md, *sc_a = md + H, *g_a = md + 2 * H, *sh_m = md + 3 * H, *sc_m = md + 4 * H, *g_m = md + 5 * H;
+    const float *sh_c = md + 6 * H, *sc_c = md + 7 * H, *g_c = md + 8 * H;
+    T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st), "ln_mod msa");
+    T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H), EPI_BF16, st), "qkv");
+    const size_t layer = (size_t)(step * D + b) * (size_t)a->pool_layer_stride;
+    bf16_t* kp = (bf16_t*)a->k_pool + layer;
+    bf16_t* vp = (bf16_t*)a->v_pool + layer;
+    T2W_CHECK(qk_norm_scatter(w.big, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, w.q, kp, vp, a->new_slot, N, d.heads, st), "qk_norm");
+    AttnArgs at;
+    at.q = w.q; at.k_pool = kp; at.v_pool = vp; at.out = w.ao; at.kv_idx = a->kv_idx; at.row_start = a->row_start;
+    at.row_len = a->row_len; at.row_kv_off = a->row_kv_off; at.row_kv_len = a->row_kv_len; at.tiles = a->tiles;
+    at.n_tiles = a->n_tiles; at.heads = d.heads; at.chunk = a->chunk; at.scale = 1.0f / sqrtf((float)d.head_dim);
+    T2W_CHECK(attention(at, st), "attention");
+    T2W_CHECK(gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H), EPI_RESID_F32, st), "proj");
+    ConvPlace cp;
+    cp.P = w.P; cp.tok_row = a->tok_row; cp.tok_pos = a->tok_pos; cp.row_start = a->row_start; cp.row_len = a->row_len;
+    cp.rd = a->conv_rd; cp.wr = a->conv_wr; cp.cache_stride = cstride; cp.N = N; cp.R = R;
+    bf16_t* cbase = (bf16_t*)a->conv_pool + ((size_t)(step * D + b) * 2) * 2 * H;
+    cp.cache_base = cbase;
+    cp.cache_out_base = cbase;
+    T2W_CHECK(ln_mod_conv(w.h, sh_c, sc_c, d.eps_block, cp, H, st), "ln_mod_conv");
+    T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H), EPI_BF16, st), "conv1");
+    cp.cache_base = cbase + 2 * H;
+    cp.cache_out_base = cbase + 2 * H;
+    T2W_CHECK(ln_mish_conv(w.ao, k.cln_w, k.cln_b, d.eps_conv, cp, H, st), "ln_mish_conv");
+    T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H), EPI_RESID_F32, st), "conv2");
+    T2W_CHECK(ln_mod(w.h, sh_m, sc_m, d.eps_block, w.abuf, N, H, st), "ln_mod mlp");
+    T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.fc1_w, k.fc1_b, nullptr, w.big, F, N, F, H), EPI_GELU_BF16, st), "fc1");
+    T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F), EPI_RESID_F32, st), "fc2");
+  }
+  T2W_CHECK(ln_mod(w.h, fmods, fmods + H, d.eps_final, w.abuf, N, H, st), "final norm");
+  T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, m->g.out_w, m->g.out_b, nullptr, dphi, M, N, M, H), EPI_F32, st), "final linear");
+  return 0;
+}
+
+int check_args(const t2w_dit* m, const t2w_solve_args* a) {
+  if (check_model(m)) return 1;
+  if (!a) return fail("null args");
+  if (a->n_tok <= 0 || a->n_rows <= 0) return fail("empty call");
+  if (a->workspace_bytes < carve(m->d, a->n_tok, a->n_rows, nullptr, nullptr)) return fail("workspace too small");
+  if (a->chunk < 0) return fail("negative chunk");
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int t2w_abi_version(void) { return 1; }
+
+const char* t2w_last_error(void) { return g_err.c_str(); }
+
+int t2w_dit_create(const t2w_dit_dims* dims, t2w_dit** out) {
+  if (!dims || !out) return fail("null argument");
+  const t2w_dit_dims& d = *dims;
+  if (d.head_dim != 64) return fail("head_dim must be 64");
+  if (d.hidden != d.heads * 64) return fail("hidden must be heads * 64");
+  if (d.hidden != 256 && d.hidden != 512 && d.hidden != 1024) return fail("hidden must be 256, 512 or 1024");
+  if ((4 * d.mel) % 64 || d.ffn % 64) return fail("4 * mel and ffn must be multiples of 64");
+  if (d.depth <= 0 || d.steps <= 0 || d.steps > 16) return fail("bad depth / steps");
+  t2w_dit* m = new t2w_dit();
+  m->d = d;
+  m->blocks.resize(d.depth);
+  m->block_set.assign(d.depth, false);
+  *out = m;
+  return 0;
+}
+
+int t2w_dit_set_block(t2w_dit* m, int block, const t2w_dit_block* w) {
+  if (!m || !w || block < 0 || block >= m->d.depth) return fail("bad block");
+  m->blocks[block] = *w;
+  m->block_set[block] = true;
+  return 0;
+}
+
+int t2w_dit_set_globals(t2w_dit* m, const t2w_dit_globals* g) {
+  if (!m || !g || !g->dts) return fail("bad globals");
+  m->g = *g;
+  m->dts.assign(g->dts, g->dts + m->d.steps);
+  m->g.dts = m->dts.data();
+  m->globals_set = true;
+  return 0;
+}
+
+void t2w_dit_destroy(t2w_dit* m) { delete m; }
+
+size_t t2w_dit_mods_workspace_bytes(const t2w_dit* m, int S) {
+  if (!m) return 0;
+  return align_up((size_t)S * m->d.freq * 4) + 2 * align_up((size_t)S * m->d.hidden * 4);
+}
+
+int t2w_dit_build_mods(const t2w_dit* m, const t2w_mod_weights* w, const float* ts, int S, float* mods_out, float* final_out,
+                       void* workspace, void* stream) {
+  if (!m || !w || S <= 0 || S > 16) return fail("bad build_mods arguments");
+  hipStream_t st = (hipStream_t)stream;
+  const int H = m->d.hidden, Fq = m->d.freq, D = m->d.depth;
+  char* base = (char*)workspace;
+  float* emb = (float*)base;
+  float* h1 = (float*)(base + align_up((size_t)S * Fq * 4));
+  float* temb = (float*)(base + align_up((size_t)S * Fq * 4) + align_up((size_t)S * H * 4));
+  T2W_CHECK(temb_sinusoid(ts, w->freqs, emb, S, Fq / 2, st), "sinusoid");
+  T2W_CHECK(gemv_rows_f32(emb, Fq, 0, w->te0_w, w->te0_b, h1, H, S, H, Fq, 1, st), "t_embedder.0");
+  T2W_CHECK(gemv_rows_f32(h1, H, 0, w->te2_w, w->te2_b, temb, H, S, H, H, 0, st), "t_embedder.2");
+  T2W_CHECK(gemv_rows_f32(temb, H, 1, w->ada_w, w->ada_b, mods_out, D * 9 * H, S, D * 9 * H, H, 0, st), "adaLN");
+  T2W_CHECK(gemv_rows_f32(temb, H, 1, w->fin_w, w->fin_b, final_out, 2 * H, S, 2 * H, H, 0, st), "final adaLN");
+  for (int j = 1; j < 9; j += 3) T2W_CHECK(add_one_cols(mods_out, S * D, 9 * H, j * H, H, st), "1 + scale");
+  T2W_CHECK(add_one_cols(final_out, S, 2 * H, H, H, st), "1 + scale");
+  return 0;
+}
+
+size_t t2w_dit_workspace_bytes(const t2w_dit* m, int n_tok, int n_rows) {
+  if (!m) return 0;
+  return carve(m->d, n_tok, n_rows, nullptr, nullptr);
+}
+
+int t2w_dit_solve(const t2w_dit* m, const t2w_solve_args* a, void* stream) {
+  if (check_args(m, a)) return 1;
+  if (2 * a->half != a->n_tok) return fail("n_tok must be 2 * half");
+  hipStream_t st = (hipStream_t)stream;
+  const t2w_dit_dims& d = m->d;
+  Work w;
+  carve(d, a->n_tok, a->n_rows, (char*)a->workspace, &w);
+  T2W_CHECK(pack_inputs(a->x0, a->stat, w.a_in, w.x, a->half, d.mel, st), "pack_inputs");
+  for (int s = 0; s < d.steps; ++s) {
+    if (run_estimator(m, a, w, s, m->g.mods + (size_t)s * d.depth * 9 * d.hidden, m->g.final_mods + (size_t)s * 2 * d.hidden, w.dphi, st))
+      return 1;
+    T2W_CHECK(euler_update(w.x, w.dphi, w.a_in, s + 1 == d.steps ? a->out : nullptr, a->half, d.mel, m->dts[s], d.cfg_rate, st),
+              "euler");
+  }
+  return 0;
+}
+
+int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const float* mods, const float* final_mods, void* stream) {
+  if (check_args(m, a)) return 1;
+  if (!a->in_rows) return fail("in_rows required");
+  if (step < 0 || step >= m->d.steps) return fail("bad step");
+  hipStream_t st = (hipStream_t)stream;
+  Work w;
+  carve(m->d, a->n_tok, a->n_rows, (char*)a->workspace, &w);
+  T2W_CHECK(convert_rows_bf16(a->in_rows, w.a_in, (long long)a->n_tok * 4 * m->d.mel, st), "convert");
+  if (run_estimator(m, a, w, step, mods, final_mods, a->out, st)) return 1;
+  return 0;
+}
+
+int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate, void* C, int ldc,
+                  int M, int N, int K, int epi, void* stream) {
+  if (K % 64) return fail("K must be a multiple of 64");
+  if (epi < 0 || epi > 3) return fail("bad epilogue");
+  if (a_src && (K % lda)) return fail("taps mode: K must be a multiple of lda");
+  T2W_CHECK(gemm_bf16(gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K), epi, (hipStream_t)stream), "gemm");
+  return 0;
+}
+
+int t2w_ln_mod(const float* h, const float* shift, const float* scale1, float eps, void* out, int N, int H, void* stream) {
+  T2W_CHECK(ln_mod(h, shift, scale1, eps, (bf16_t*)out, N, H, (hipStream_t)stream), "ln_mod");
+  return 0;
+}
+
+int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const float* kw, const float* kb, float eps, void* q_out,
+                        void* k_pool, void* v_pool, const int* slots, int N, int heads, void* stream) {
+  T2W_CHECK(qk_norm_scatter((const bf16_t*)qkv, qw, qb, kw, kb, eps, (bf16_t*)q_out, (bf16_t*)k_pool, (bf16_t*)v_pool, slots, N, heads,
+                            (hipStream_t)stream),
+            "qk_norm");
+  return 0;
+}
+
+int t2w_attention(const void* q, const void* k_pool, const void* v_pool, void* out, const int* kv_idx, const int* row_start,
+                  const int* row_len, const int* row_kv_off, const int* row_kv_len, const int* tiles, int n_tiles, int heads, int chunk,
+                  float scale, void* stream) {
+  AttnArgs at;
+  at.q = (const bf16_t*)q; at.k_pool = (const bf16_t*)k_pool; at.v_pool = (const bf16_t*)v_pool; at.out = (bf16_t*)out;
+  at.kv_idx = kv_idx; at.row_start = row_start; at.row_len = row_len; at.row_kv_off = row_kv_off; at.row_kv_len = row_kv_len;
+  at.tiles = tiles; at.n_tiles = n_tiles; at.heads = heads; at.chunk = chunk; at.scale = scale;
+  T2W_CHECK(attention(at, (hipStream_t)stream), "attention");
+  return 0;
+}
+
+struct t2w_graph {
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+};
+
+int t2w_graph_begin(void* stream) {
+  T2W_CHECK(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal), "begin capture");
+  return 0;
+}
+
+int t2w_graph_end(void* stream, t2w_graph** out) {
+  hipGraph_t g;
+  T2W_CHECK(hipStreamEndCapture((hipStream_t)stream, &g), "end capture");
+  hipGraphExec_t ex;
+  hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return fail("instantiate", e);
+  }
+  *out = new t2w_graph{g, ex};
+  return 0;
+}
+
+int t2w_graph_launch(t2w_graph* g, void* stream) {
+  if (!g) return fail("null graph");
+  T2W_CHECK(hipGraphLaunch(g->exec, (hipStream_t)stream), "graph launch");
+  return 0;
+}
+
+void t2w_graph_destroy(t2w_graph* g) {
+  if (!g) return;
+  (void)hipGraphExecDestroy(g->exec);
+  (void)hipGraphDestroy(g->graph);
+  delete g;
+}
+
+}  // extern "C"

@@ -1,0 +1,209 @@
+// bf16 MFMA GEMM for the DiT linears: C = epilogue(A[M,K] . W[N,K]^T + bias), fp32 accumulation.
+//
+// CDNA4 design: v_mfma_f32_32x32x16_bf16 tiles on wave64, LDS-staged A/W tiles of 64 K-values (128 B rows, 16-byte
+// chunks XOR-swizzled by row so the fragment reads of 32 consecutive rows spread over all banks), two LDS stages with
+// the next tile's global loads in flight during the MFMAs, XCD-aware block order.  The weight operand is passed to the
+// MFMA as its "A" side so each lane ends up holding four consecutive output columns (16-byte fp32 / 8-byte bf16
+// stores in the epilogue).
+//
+// A operand modes: dense rows, or "taps" rows for the kernel-3 causal convs: row m of A is the three frames starting
+// at frame a_src[m] of a frame buffer whose rows are lda wide (no im2col copy in HBM; the host lays the two cached
+// frames of every packed row in front of its frames).
+#include "common.h"
+#include "t2w_internal.h"
+
+namespace t2w {
+
+namespace {
+
+constexpr int BK = 64;  // K values per stage (128 bytes of bf16 per tile row)
+
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+
+template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA blocks per wave
+  constexpr int APASS = BM * 8 / NT, BPASS = BN * 8 / NT;
+  static_assert(APASS * NT == BM * 8 && BPASS * NT == BN * 8, "tile / thread mismatch");
+
+  __shared__ uint4 lds[2][(BM + BN) * 8];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
+  const int nblk = gm * gn;
+  int b = blockIdx.x;
+  const int full = (nblk / 8) * 8;  // blocks b, b+8, .. run on one XCD: give each XCD a contiguous band of tiles
+  if (b < full) b = (b % 8) * (nblk / 8) + b / 8;
+  const int mt = b / gn, nt = b % gn;
+  const int m0 = mt * BM, n0 = nt * BN;
+
+  // per-thread global load sources (rows fixed over the K loop)
+  const bf16_t* asrc[APASS];
+  bool aok[APASS];
+  int arow[APASS], achunk[APASS];
+#pragma unroll
+  for (int p = 0; p < APASS; ++p) {
+    int idx = tid + p * NT;
+    arow[p] = idx >> 3;
+    achunk[p] = idx & 7;
+    int m = m0 + arow[p];
+    aok[p] = m < g.M;
+    int mm = aok[p] ? m : 0;
+    if (TAPS)
+      asrc[p] = g.A + (size_t)g.a_src[mm] * g.lda + achunk[p] * 8;
+    else
+      asrc[p] = g.A + (size_t)mm * g.lda + achunk[p] * 8;
+  }
+  const bf16_t* bsrc[BPASS];
+  bool bok[BPASS];
+  int brow[BPASS], bchunk[BPASS];
+#pragma unroll
+  for (int p = 0; p < BPASS; ++p) {
+    int idx = tid + p * NT;
+    brow[p] = idx >> 3;
+    bchunk[p] = idx & 7;
+    int n = n0 + brow[p];
+    bok[p] = n < g.N;
+    bsrc[p] = g.B + (size_t)(bok[p] ? n : 0) * g.ldb + bchunk[p] * 8;
+  }
+
+  uint4 ra[APASS], rb[BPASS];
+  auto gload = [&](int k0) {
+    size_t aoff;
+    if (TAPS) {
+      int tap = k0 / g.tapC;
+      aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);
+    } else {
+      aoff = k0;
+    }
+#pragma unroll
+    for (int p = 0; p < APASS; ++p) ra[p] = aok[p] ? *(const uint4*)(asrc[p] + aoff) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int p = 0; p < BPASS; ++p) rb[p] = bok[p] ? *(const uint4*)(bsrc[p] + k0) : make_uint4(0, 0, 0, 0);
+  };
+  auto lstore = [&](int s) {
+#pragma unroll
+    for (int p = 0; p < APASS; ++p) lds[s][swz(arow[p], achunk[p])] = ra[p];
+#pragma unroll
+    for (int p = 0; p < BPASS; ++p) lds[s][BM * 8 + swz(brow[p], bchunk[p])] = rb[p];
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int KT = g.K / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int s = kt & 1;
+    if (kt + 1 < KT) gload((kt + 1) * BK);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int chunk = kk * 2 + (lane >> 5);
+      bf16x8 af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        int row = wm * WTM + i * 32 + (lane & 31);
+        af[i] = as_bf16x8(lds[s][swz(row, chunk)]);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        int row = wn * WTN + j * 32 + (lane & 31);
+        bfr[j] = as_bf16x8(lds[s][BM * 8 + swz(row, chunk)]);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < KT) lstore(s ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds row m = .. + lane%32 and columns n = .. + (r/4)*8 + (lane/32)*4 + r%4
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * WTM + i * 32 + (lane & 31);
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * WTN + j * 32 + q * 8 + (lane >> 5) * 4;
+        if (n >= g.N) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
+        if (n + 3 < g.N) {
+          const float4 bb = *(const float4*)(g.bias + n);
+          v[0] += bb.x; v[1] += bb.y; v[2] += bb.z; v[3] += bb.w;
+          if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) {
+            if (EPI == EPI_GELU_BF16) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+            }
+            uint2 o = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+            *(uint2*)((bf16_t*)g.C + (size_t)m * g.ldc + n) = o;
+          } else if (EPI == EPI_RESID_F32) {
+            float* hp = (float*)g.C + (size_t)m * g.ldc + n;
+            float4 h = *(float4*)hp;
+            const float4 gg = *(const float4*)(g.gate + n);
+            h.x += gg.x * v[0]; h.y += gg.y * v[1]; h.z += gg.z * v[2]; h.w += gg.w * v[3];
+            *(float4*)hp = h;
+          } else {
+            *(float4*)((float*)g.C + (size_t)m * g.ldc + n) = make_float4(v[0], v[1], v[2], v[3]);
+          }
+        } else {
+          for (int e = 0; e < 4 && n + e < g.N; ++e) {
+            float x = v[e] + g.bias[n + e];
+            if (EPI == EPI_BF16) ((bf16_t*)g.C)[(size_t)m * g.ldc + n + e] = f2bf(x);
+            else if (EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[(size_t)m * g.ldc + n + e] = f2bf(gelu_tanh(x));
+            else if (EPI == EPI_RESID_F32) ((float*)g.C)[(size_t)m * g.ldc + n + e] += g.gate[n + e] * x;
+            else ((float*)g.C)[(size_t)m * g.ldc + n + e] = x;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
+hipError_t launch_cfg(const GemmArgs& g, hipStream_t st) {
+  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, TAPS>), dim3(gm * gn), dim3(64 * WM * WN), 0, st, g);
+  return hipGetLastError();
+}
+
+template <int EPI, bool TAPS>
+hipError_t launch_epi(const GemmArgs& g, hipStream_t st) {
+  return launch_cfg<128, 128, 2, 2, EPI, TAPS>(g, st);
+}
+
+}  // namespace
+
+hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st) {
+  if (g.M <= 0 || g.N <= 0) return hipSuccess;
+  const bool taps = g.a_src != nullptr;
+  switch (epi * 2 + (taps ? 1 : 0)) {
+    case EPI_BF16 * 2: return launch_epi<EPI_BF16, false>(g, st);
+    case EPI_BF16 * 2 + 1: return launch_epi<EPI_BF16, true>(g, st);
+    case EPI_GELU_BF16 * 2: return launch_epi<EPI_GELU_BF16, false>(g, st);
+    case EPI_GELU_BF16 * 2 + 1: return launch_epi<EPI_GELU_BF16, true>(g, st);
+    case EPI_RESID_F32 * 2: return launch_epi<EPI_RESID_F32, false>(g, st);
+    case EPI_RESID_F32 * 2 + 1: return launch_epi<EPI_RESID_F32, true>(g, st);
+    case EPI_F32 * 2: return launch_epi<EPI_F32, false>(g, st);
+    case EPI_F32 * 2 + 1: return launch_epi<EPI_F32, true>(g, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace t2w

@@ -1,0 +1,85 @@
+// Internal launch interfaces shared by the kernel files and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace t2w {
+
+typedef uint16_t bf16_t;
+
+enum Epi { EPI_BF16 = 0, EPI_GELU_BF16 = 1, EPI_RESID_F32 = 2, EPI_F32 = 3 };
+
+struct GemmArgs {
+  const bf16_t* A;     // dense: A[m * lda + k]; taps: A[(a_src[m] + k / tapC) * lda + k % tapC]
+  int lda;
+  const int* a_src;    // taps mode when non-null
+  int tapC;
+  const bf16_t* B;     // weights [N, K] row-major
+  int ldb;
+  const float* bias;   // [N]
+  const float* gate;   // [N], EPI_RESID_F32: C += gate * (acc + bias)
+  void* C;
+  int ldc;
+  int M, N, K;         // K % 64 == 0
+};
+
+hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st);
+
+// Per-token row kernels of the DiT block (H = hidden, one wave per token).
+hipError_t ln_mod(const float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H,
+                  hipStream_t st);
+
+struct ConvPlace {   // where the normed frames of a causal conv go (the padded frame buffer and the conv caches)
+  bf16_t* P;          // [N + 2 R, H]: per row r its two cached frames, then its T_r frames
+  const int* tok_row; // [N]
+  const int* tok_pos; // [N]
+  const int* row_start;  // [R] first token of row r
+  const int* row_len;    // [R]
+  const bf16_t* cache_base;  // conv cache pool; row r reads frames at cache_base + rd[r] * cache_stride
+  bf16_t* cache_out_base;    // and writes its new frames at cache_out_base + wr[r] * cache_stride
+  const int* rd;
+  const int* wr;
+  long long cache_stride;    // elements between row slots
+  int N, R;
+};
+
+hipError_t ln_mod_conv(const float* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H,
+                       hipStream_t st);
+hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float eps, const ConvPlace& cp, int H,
+                        hipStream_t st);
+hipError_t qk_norm_scatter(const bf16_t* qkv, const float* qw, const float* qb, const float* kw, const float* kb,
+                           float eps, bf16_t* q_out, bf16_t* k_pool, bf16_t* v_pool, const int* slots, int N, int heads,
+                           hipStream_t st);
+
+struct AttnArgs {
+  const bf16_t* q;        // [N, heads, 64]
+  const bf16_t* k_pool;   // [slots, heads, 64]
+  const bf16_t* v_pool;
+  bf16_t* out;            // [N, heads * 64]
+  const int* kv_idx;      // concatenated per-row key slot lists: the row's new tokens first, then its cached keys
+  const int* row_start;   // [R] first token
+  const int* row_len;     // [R] new tokens T_r
+  const int* row_kv_off;  // [R] offset into kv_idx
+  const int* row_kv_len;  // [R] keys in the list (T_r + cached)
+  const int* tiles;       // [n_tiles, 2]: (row, first query position) of each 64-query tile
+  int n_tiles, heads, chunk;  // chunk > 0: a new frame sees new frames of its own and earlier chunks only
+  float scale;
+};
+hipError_t attention(const AttnArgs& a, hipStream_t st);
+
+hipError_t pack_inputs(const float* x0, const float* stat, bf16_t* a_in, float* x, int half, int mel, hipStream_t st);
+hipError_t euler_update(float* x, const float* dphi, bf16_t* a_in, float* out, int half, int mel, float dt, float cfg,
+                        hipStream_t st);
+
+// Timestep conditioning tables (run once per model): rows of fp32 vectors.
+hipError_t temb_sinusoid(const float* ts, const float* freqs, float* out, int S, int half, hipStream_t st);
+hipError_t gemv_rows_f32(const float* in, int ld_in, int in_act, const float* W, const float* b, float* out, int ld_out,
+                         int S, int O, int K, int out_act, hipStream_t st);
+hipError_t add_one_cols(float* tab, int rows, int stride, int offset, int n, hipStream_t st);
+
+hipError_t convert_rows_bf16(const float* src, bf16_t* dst, long long n, hipStream_t st);
+hipError_t copy_rows_bf16(const bf16_t* src, bf16_t* dst, const int* src_row, const int* dst_row, int n_rows,
+                          long long row_elems, hipStream_t st);
+
+}  // namespace t2w

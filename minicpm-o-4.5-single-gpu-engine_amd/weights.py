@@ -1,0 +1,100 @@
+"""Seeded random-init weights of the DiT estimator and HiFT (fp32 master copies on the host).
+
+No checkpoint is available offline, so every workload runs on random-init weights of the real architecture.  Names
+follow the stepaudio2 module attributes the reference reads (``engine/runtime/dit_fast.py:131-145``,
+``engine/models/token2wav.py:160-236``).  Linear and conv weights and biases are uniform in ``+-1/sqrt(fan_in)`` (torch's
+default init); LayerNorm affines are ``1 + 0.1 N`` / ``0.1 N``; Snake alphas uniform in [0.5, 1.5]; the f0 classifier is
+scaled so that a mel of the workloads' statistics gives both voiced (> 10 Hz) and unvoiced frames.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .config import DiTConfig, HiFTConfig
+
+
+class _Init:
+    def __init__(self, seed: int):
+        self.g = torch.Generator().manual_seed(int(seed))
+
+    def uniform(self, shape, bound):
+        return (torch.rand(*shape, generator=self.g) * 2 - 1) * bound
+
+    def linear(self, W, name, out_f, in_f, scale=1.0):
+        bd = 1.0 / math.sqrt(in_f)
+        W[name + ".weight"] = self.uniform((out_f, in_f), bd) * scale
+        W[name + ".bias"] = self.uniform((out_f,), bd) * scale
+
+    def conv(self, W, name, out_c, in_c, k):
+        bd = 1.0 / math.sqrt(in_c * k)
+        W[name + ".weight"] = self.uniform((out_c, in_c, k), bd)
+        W[name + ".bias"] = self.uniform((out_c,), bd)
+
+    def conv_t(self, W, name, in_c, out_c, k):
+        bd = 1.0 / math.sqrt(out_c * k)
+        W[name + ".weight"] = self.uniform((in_c, out_c, k), bd)
+        W[name + ".bias"] = self.uniform((out_c,), bd)
+
+    def norm(self, W, name, n):
+        W[name + ".weight"] = 1 + 0.1 * torch.randn(n, generator=self.g)
+        W[name + ".bias"] = 0.1 * torch.randn(n, generator=self.g)
+
+
+def init_dit(cfg: DiTConfig = DiTConfig(), seed: int = 0) -> dict[str, torch.Tensor]:
+    ini = _Init(seed)
+    H, W = cfg.hidden, {}
+    ini.linear(W, "t_embedder.mlp.0", H, cfg.freq)
+    ini.linear(W, "t_embedder.mlp.2", H, H)
+    ini.linear(W, "in_proj", H, cfg.in_dim)
+    for b in range(cfg.depth):
+        p = f"blocks.{b}."
+        ini.linear(W, p + "adaLN_modulation.1", 9 * H, H)
+        for n in ("to_q", "to_k", "to_v", "proj"):
+            ini.linear(W, p + "attn." + n, H, H)
+        ini.norm(W, p + "attn.q_norm", cfg.head_dim)
+        ini.norm(W, p + "attn.k_norm", cfg.head_dim)
+        ini.conv(W, p + "conv.block.1", H, H, 3)
+        ini.norm(W, p + "conv.block.3", H)
+        ini.conv(W, p + "conv.block.6", H, H, 3)
+        ini.linear(W, p + "mlp.fc1", cfg.ffn, H)
+        ini.linear(W, p + "mlp.fc2", H, cfg.ffn)
+    ini.linear(W, "final_layer.adaLN_modulation.1", 2 * H, H)
+    ini.linear(W, "final_layer.linear", cfg.mel, H)
+    W["rand_noise"] = torch.randn(1, cfg.mel, cfg.noise_frames, generator=ini.g)
+    return W
+
+
+def init_hift(cfg: HiFTConfig = HiFTConfig(), seed: int = 0) -> dict[str, torch.Tensor]:
+    ini = _Init(seed)
+    W = {}
+    c = cfg.f0_channels
+    for i in range(cfg.f0_layers):
+        ini.conv(W, f"f0_predictor.condnet.{2 * i}", c, cfg.mel if i == 0 else c, 3)
+    ini.linear(W, "f0_predictor.classifier", 1, c, scale=400.0)
+    W["f0_predictor.classifier.bias"] = W["f0_predictor.classifier.bias"].abs() + 20.0
+    ini.linear(W, "m_source.l_linear", 1, cfg.harmonics + 1)
+    ini.conv(W, "conv_pre", cfg.base, cfg.mel, 7)
+    chans = [cfg.base] + cfg.stage_channels
+    for i, (u, k) in enumerate(zip(cfg.up_rates, cfg.up_kernels)):
+        ini.conv_t(W, f"ups.{i}", chans[i], chans[i + 1], k)
+    nsrc = cfg.n_fft + 2
+    for i, (u, k) in enumerate(zip(cfg.down_rates, cfg.src_res_kernels)):
+        ch = cfg.stage_channels[i]
+        ini.conv(W, f"source_downs.{i}", ch, nsrc, 1 if u == 1 else 2 * u)
+        _resblock(ini, W, f"source_resblocks.{i}", ch, k, cfg.res_dilations)
+    for i, ch in enumerate(cfg.stage_channels):
+        for j, k in enumerate(cfg.res_kernels):
+            _resblock(ini, W, f"resblocks.{i * len(cfg.res_kernels) + j}", ch, k, cfg.res_dilations)
+    ini.conv(W, "conv_post", cfg.n_fft + 2, cfg.stage_channels[-1], 7)
+    return W
+
+
+def _resblock(ini: _Init, W, p, ch, k, dils):
+    for j, _ in enumerate(dils):
+        ini.conv(W, f"{p}.convs1.{j}", ch, ch, k)
+        ini.conv(W, f"{p}.convs2.{j}", ch, ch, k)
+        W[f"{p}.activations1.{j}.alpha"] = 0.5 + torch.rand(ch, generator=ini.g)
+        W[f"{p}.activations2.{j}.alpha"] = 0.5 + torch.rand(ch, generator=ini.g)

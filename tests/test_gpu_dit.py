@@ -1,0 +1,113 @@
+"""DiT estimator and CFG Euler solve on the GPU against the fp32 CPU oracle (same seeded random-init weights/inputs).
+
+Tolerance: bf16 GEMM operands with fp32 accumulation, fp32 residual stream and Euler state: mel rel-L2 <= 2e-2 against
+the fp32 oracle (the reference's own fast-vs-reference FP16 bounds are 2e-2 for setups and 3e-2 for windows,
+``tests/engine/test_dit_fast.py:86,103`` of the reference); measured values are printed.
+"""
+
+import pytest
+import torch
+
+import t2w_amd  # noqa: F401
+from t2w_amd.config import DiTConfig
+from t2w_amd.dit import DiTModel, FastDiT
+from t2w_amd.weights import init_dit
+from oracle import dit as od
+from conftest import rel
+
+pytestmark = pytest.mark.gpu
+
+TINY = DiTConfig(hidden=256, depth=2, heads=4, ffn=512)
+TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    W = init_dit(TINY, seed=11)
+    model = DiTModel(W, TINY)
+    return W, model
+
+
+@pytest.fixture(scope="module")
+def full():
+    W = init_dit(DiTConfig(), seed=0)
+    model = DiTModel(W, DiTConfig())
+    return W, model
+
+
+def test_estimator_forward_config1(dev, full):
+    """One estimator forward at the config-1 shape: B=2 rows, T=100, t=0.5, cond zeros, seed 0."""
+    W, model = full
+    fd = FastDiT(model, n_slots=1024, max_streams=2)
+    g = torch.Generator().manual_seed(0)
+    x, mu = torch.randn(2, 80, 100, generator=g), torch.randn(2, 80, 100, generator=g)
+    spk = torch.randn(2, 80, generator=g)
+    cond = torch.zeros(2, 80, 100)
+    ref = od.estimator_forward(W, od.dims_of(W), x, mu, torch.full((2,), 0.5), spk, cond)
+    got = fd.estimator_forward(x.cuda(), mu.cuda(), 0.5, spk.cuda(), cond.cuda()).cpu()
+    e = rel(got, ref)
+    print("config1 estimator rel-L2", e, "max-abs", float((got - ref).abs().max()))
+    assert e < TOL
+
+
+def _stream_case(W, model, graphs: bool):
+    d = od.dims_of(W, steps=TINY.steps)
+    fd = FastDiT(model, n_slots=4096, max_streams=4, use_graphs=graphs)
+    g = torch.Generator().manual_seed(1)
+    prompts = [70, 40]
+    caches = [fd.new_cache(keep=p) for p in prompts]
+    refc = [od.empty_cache(d, keep=p) for p in prompts]
+    spks = torch.randn(2, 80, generator=g)
+    mus = [torch.randn(80, p, generator=g) for p in prompts]
+    conds = [torch.randn(80, p, generator=g) for p in prompts]
+    errs = []
+    ref = od.solve(W, d, W["rand_noise"], refc, mus, spks, conds, [True, True])
+    got = fd.solve(caches, [m.cuda() for m in mus], spks.cuda(), [c.cuda() for c in conds], [True, True])
+    errs.append(max(rel(a.cpu(), b) for a, b in zip(got, ref)))
+    for w in range(5):
+        Ts = [50, 16 if w == 0 else 50]
+        keep = [w < 4, True]
+        if w == 4:
+            Ts[0] = 34
+        mus = [torch.randn(80, t, generator=g) for t in Ts]
+        ref = od.solve(W, d, W["rand_noise"], refc, mus, spks, None, keep)
+        got = fd.solve(caches, [m.cuda() for m in mus], spks.cuda(), None, keep)
+        errs.append(max(rel(a.cpu(), b) for a, b in zip(got, ref)))
+        assert [c.length for c in caches] == [c.length for c in refc], w
+    for c in caches:
+        fd.release(c)
+    assert fd.pool.in_use() == 0
+    return errs
+
+
+def test_solve_streaming_tiny(dev, tiny):
+    """Prompt setups (cond = prompt mel), then windows past the trim point, a 16-frame first window and a final flush
+    that keeps nothing, two requests per ragged call; caches and trims must follow the oracle's."""
+    W, model = tiny
+    errs = _stream_case(W, model, graphs=False)
+    print("stream rel-L2 per call", errs)
+    assert max(errs) < TOL
+
+
+def test_solve_streaming_graphs_equal_eager(dev, tiny):
+    W, model = tiny
+    a = _stream_case(W, model, graphs=False)
+    b = _stream_case(W, model, graphs=True)
+    assert a == b
+
+
+def test_chunk_causal_whole_sequence(dev, tiny):
+    """A whole 150-frame row per request under the chunk-causal mask (chunk 50) equals the oracle's."""
+    W, model = tiny
+    d = od.dims_of(W, steps=TINY.steps)
+    fd = FastDiT(model, n_slots=4096, max_streams=4)
+    g = torch.Generator().manual_seed(2)
+    Ts = [150, 120, 37]
+    mus = [torch.randn(80, t, generator=g) for t in Ts]
+    spks = torch.randn(3, 80, generator=g)
+    ref = od.solve(W, d, W["rand_noise"], [od.empty_cache(d) for _ in Ts], mus, spks, None, [False] * 3, chunk=50)
+    caches = [fd.new_cache() for _ in Ts]
+    got = fd.solve(caches, [m.cuda() for m in mus], spks.cuda(), None, [False] * 3, chunk=50)
+    errs = [rel(a.cpu(), b) for a, b in zip(got, ref)]
+    print("chunk-causal rel-L2", errs)
+    assert max(errs) < TOL

@@ -1,0 +1,155 @@
+"""Kernel-level parity on the GPU: each HIP kernel against a plain PyTorch fp32 computation of the same op."""
+
+import ctypes as C
+
+import pytest
+import torch
+
+import t2w_amd  # noqa: F401
+from t2w_amd import _lib
+from conftest import rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm(A, W, bias, C_, epi, gate=None, a_src=None, lda=None, K=None):
+    L = _lib.lib()
+    M = C_.shape[0] if a_src is None else a_src.numel()
+    N = W.shape[0]
+    K = K or A.shape[1]
+    _lib.check(L.t2w_gemm_bf16(A.data_ptr(), lda or A.shape[1], _lib.ptr(a_src), W.data_ptr(), bias.data_ptr(), _lib.ptr(gate),
+                               C_.data_ptr(), C_.shape[1], M, N, K, epi, _lib.stream_handle()), "gemm")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 64), (100, 80, 1024), (333, 1024, 320), (1000, 3072, 1024), (257, 2048, 2048)])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_gemm_dense(dev, M, N, K, epi):
+    g = torch.Generator(device=dev).manual_seed(M * 7 + N + K + epi)
+    A = torch.randn(M, K, device=dev, generator=g).bfloat16()
+    W = (torch.randn(N, K, device=dev, generator=g) / K ** 0.5).bfloat16()
+    bias = torch.randn(N, device=dev, generator=g)
+    ref = A.float() @ W.float().t() + bias
+    if epi in (0, 1):
+        out = torch.full((M, N), 7.0, device=dev).bfloat16()
+        _gemm(A, W, bias, out, epi)
+        if epi == 1:
+            ref = torch.nn.functional.gelu(ref, approximate="tanh")
+        assert rel(out.float(), ref) < 6e-3
+    elif epi == 2:
+        h = torch.randn(M, N, device=dev, generator=g)
+        gate = torch.randn(N, device=dev, generator=g)
+        expect = h + gate * ref
+        _gemm(A, W, bias, h, 2, gate=gate)
+        assert rel(h, expect) < 1e-5
+    else:
+        out = torch.zeros(M, N, device=dev)
+        _gemm(A, W, bias, out, 3)
+        assert rel(out, ref) < 1e-5
+
+
+@pytest.mark.parametrize("lens", [[5, 0, 1, 2, 3, 40, 0, 17, 1, 56], [400] * 3])
+def test_gemm_conv_taps(dev, lens):
+    """Taps mode: row m reads three consecutive frames starting at a_src[m] of the padded frame buffer; equals a
+    kernel-3 conv over [2 cached frames | row frames] (F.conv1d, fp32)."""
+    H = 256
+    g = torch.Generator(device=dev).manual_seed(11)
+    R, N = len(lens), sum(lens)
+    P = torch.randn(N + 2 * R, H, device=dev, generator=g).bfloat16()
+    w = (torch.randn(H, H, 3, device=dev, generator=g) / (3 * H) ** 0.5)
+    Wfm = w.permute(0, 2, 1).reshape(H, 3 * H).bfloat16().contiguous()
+    bias = torch.randn(H, device=dev, generator=g)
+    tok_row = [r for r, t in enumerate(lens) for _ in range(t)]
+    a_src = torch.tensor([i + 2 * r for i, r in enumerate(tok_row)], dtype=torch.int32, device=dev)
+    out = torch.zeros(N, H, device=dev)
+    _gemm(P, Wfm, bias, out, 3, a_src=a_src, lda=H, K=3 * H)
+    refs, o = [], 0
+    for r, t in enumerate(lens):
+        if t:
+            frames = P[o + 2 * r: o + 2 * r + 2 + t].float().t()[None]  # [1, H, 2 + t]
+            refs.append(torch.nn.functional.conv1d(frames, w.bfloat16().float(), bias)[0].t())
+        o += t
+    assert rel(out, torch.cat(refs)) < 1e-5
+
+
+def test_ln_mod(dev):
+    L = _lib.lib()
+    g = torch.Generator(device=dev).manual_seed(2)
+    for H in (256, 512, 1024):
+        N = 77
+        h = torch.randn(N, H, device=dev, generator=g) * 3 + 1
+        sh, sc = torch.randn(H, device=dev, generator=g), 1 + torch.randn(H, device=dev, generator=g)
+        out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
+        _lib.check(L.t2w_ln_mod(h.data_ptr(), sh.data_ptr(), sc.data_ptr(), 1e-6, out.data_ptr(), N, H, _lib.stream_handle()))
+        torch.cuda.synchronize()
+        ref = torch.nn.functional.layer_norm(h, (H,), eps=1e-6) * sc + sh
+        assert rel(out.float(), ref) < 4e-3
+
+
+def test_qk_norm_scatter(dev):
+    L = _lib.lib()
+    g = torch.Generator(device=dev).manual_seed(5)
+    for heads in (4, 16):
+        H, N = heads * 64, 333
+        qkv = (torch.randn(N, 3 * H, device=dev, generator=g) * 3 + torch.randn(3 * H, device=dev, generator=g)).bfloat16()
+        qw, qb, kw, kb = (torch.randn(64, device=dev, generator=g) for _ in range(4))
+        slots = torch.randperm(2048, device=dev, generator=g)[:N].int()
+        q = torch.zeros(N, H, dtype=torch.bfloat16, device=dev)
+        kp = torch.zeros(2048, H, dtype=torch.bfloat16, device=dev)
+        vp = torch.zeros_like(kp)
+        _lib.check(L.t2w_qk_norm_scatter(qkv.data_ptr(), qw.data_ptr(), qb.data_ptr(), kw.data_ptr(), kb.data_ptr(), 1e-6, q.data_ptr(),
+                                         kp.data_ptr(), vp.data_ptr(), slots.data_ptr(), N, heads, _lib.stream_handle()))
+        torch.cuda.synchronize()
+        x = qkv.float().view(N, 3, heads, 64)
+        ln = lambda t, w, b: torch.nn.functional.layer_norm(t, (64,), w, b, 1e-6)  # noqa: E731
+        assert rel(q.float().view(N, heads, 64), ln(x[:, 0], qw, qb)) < 4e-3
+        assert rel(kp[slots.long()].float().view(N, heads, 64), ln(x[:, 1], kw, kb)) < 4e-3
+        assert torch.equal(vp[slots.long()], qkv.view(N, 3, H)[:, 2])
+
+
+@pytest.mark.parametrize("chunk", [0, 50, 7])
+def test_attention_paged_block_causal(dev, chunk):
+    """Rows of new frames with cached keys in scattered slots; mask: cached keys always visible, new keys by chunk."""
+    L = _lib.lib()
+    g = torch.Generator(device=dev).manual_seed(9 + chunk)
+    heads, n_slots = 4, 4096
+    H = heads * 64
+    lens = [50, 1, 0, 130, 64, 65]
+    cached = [300, 0, 7, 0, 100, 33]
+    N = sum(lens)
+    q = torch.randn(N, H, device=dev, generator=g).bfloat16()
+    kp = torch.randn(n_slots, H, device=dev, generator=g).bfloat16()
+    vp = torch.randn(n_slots, H, device=dev, generator=g).bfloat16()
+    perm = torch.randperm(n_slots, generator=torch.Generator().manual_seed(chunk)).tolist()
+    kv, row_start, row_kv_off, row_kv_len, tiles, o = [], [], [], [], [], 0
+    lists = []
+    for r, (t, c) in enumerate(zip(lens, cached)):
+        lst = [perm.pop() for _ in range(t + c)]
+        lists.append(lst)
+        row_start.append(o)
+        row_kv_off.append(len(kv))
+        row_kv_len.append(t + c)
+        kv += lst
+        tiles += [v for q0 in range(0, t, 64) for v in (r, q0)]
+        o += t
+    it = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)  # noqa: E731
+    out = torch.zeros(N, H, dtype=torch.bfloat16, device=dev)
+    keep = [it(x) for x in (kv, row_start, lens, row_kv_off, row_kv_len, tiles)]  # alive until the kernel ran
+    _lib.check(L.t2w_attention(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), out.data_ptr(), *[t.data_ptr() for t in keep], len(tiles) // 2,
+                               heads, chunk, 0.125, _lib.stream_handle()))
+    torch.cuda.synchronize()
+    for r, (t, c) in enumerate(zip(lens, cached)):
+        if t == 0:
+            continue
+        idx = torch.tensor(lists[r], device=dev)
+        qq = q[row_start[r]:row_start[r] + t].float().view(t, heads, 64).transpose(0, 1)
+        kk = kp[idx].float().view(t + c, heads, 64).transpose(0, 1)
+        vv = vp[idx].float().view(t + c, heads, 64).transpose(0, 1)
+        s = qq @ kk.transpose(1, 2) * 0.125
+        vis = torch.ones(t, t + c, dtype=torch.bool, device=dev)
+        if chunk > 0:
+            cid = torch.arange(t, device=dev) // chunk
+            vis[:, :t] = cid[None, :] <= cid[:, None]
+        s = s.masked_fill(~vis[None], float("-inf"))
+        ref = (torch.softmax(s, -1) @ vv).transpose(0, 1).reshape(t, H)
+        assert rel(out[row_start[r]:row_start[r] + t].float(), ref) < 1e-2, r
