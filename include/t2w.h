@@ -14,7 +14,8 @@
  *   t2w_attention        FlashInfer BatchPrefillWithPagedKVCacheWrapper.run (engine/runtime/dit_fast.py:291)
  *   t2w_qk_norm_scatter  dit_kernels.qk_norm_scatter (engine/runtime/dit_kernels.py:132-142)
  *   t2w_ln_mod           dit_kernels.ln_mod (engine/runtime/dit_kernels.py:27-31)
- *   t2w_hift_*           hift_forward_noise / _hift_decode / istft_overlap_add (engine/models/token2wav.py:128-236)
+ *   t2w_hift_forward     hift_forward_noise + _hift_decode + istft_overlap_add (engine/models/token2wav.py:128-236),
+ *                        with the hift_lean Snake / folded weight norm (engine/runtime/hift_lean.py:27-30, 107-134)
  *   t2w_graph_*          torch.cuda.CUDAGraph capture / replay of the solve and HiFT (dit_fast.py:392-422,
  *                        hift_graph.py:35-47)
  */
@@ -129,6 +130,48 @@ int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const
 int t2w_attention(const void* q, const void* k_pool, const void* v_pool, void* out, const int* kv_idx,
                   const int* row_start, const int* row_len, const int* row_kv_off, const int* row_kv_len,
                   const int* tiles, int n_tiles, int heads, int chunk, float scale, void* stream);
+
+/* ---------------------------------------------------------------- HiFT vocoder (fp32) */
+
+typedef struct t2w_hift t2w_hift;
+
+typedef struct {
+  int mel, base, n_up, harmonics, f0_channels, f0_layers, sr, n_fft, hop;
+  int up_rates[3], up_kernels[3], res_kernels[3], res_dilations[3], src_kernels[3];
+  float sine_amp, noise_std, voiced_threshold, lrelu_slope, audio_limit;
+} t2w_hift_dims;
+
+typedef struct { const float* w; const float* b; } t2w_conv;  /* w [Cout, taps, Cin]; transposed convs:
+                                                                   [u, Cout, ceil(k / u), Cin] polyphase */
+typedef struct {
+  t2w_conv c1[3], c2[3];
+  const float* a1[3]; const float* inv1[3];  /* Snake alpha and 1 / (alpha + 1e-9) before convs1[j] */
+  const float* a2[3]; const float* inv2[3];
+} t2w_resblock;
+
+typedef struct {
+  t2w_conv f0[5]; const float* f0_head_w; const float* f0_head_b;  /* f0 predictor: 5 x (conv k3 + ELU), Linear(C -> 1) */
+  const float* src_w; const float* src_b;                           /* NSF merge Linear(harmonics + 1 -> 1) */
+  t2w_conv conv_pre, ups[3], src_down[3], conv_post;
+  t2w_resblock src_res[3], res[9];
+  const float* window;                                              /* [n_fft] periodic Hann */
+} t2w_hift_weights;
+
+int t2w_hift_create(const t2w_hift_dims* dims, const t2w_hift_weights* w, t2w_hift** out);
+void t2w_hift_destroy(t2w_hift* h);
+/* Plan of a call over n_items rows with frames[i] mel frames (host array): ints for t2w_hift_plan to fill, which the
+ * caller copies to device memory; workspace bytes. */
+int t2w_hift_plan_ints(int n_items);
+int t2w_hift_plan(const t2w_hift* h, int n_items, const int* frames, int* plan_host);
+size_t t2w_hift_workspace_bytes(const t2w_hift* h, int n_items, const int* frames);
+/* hift_forward_noise for rows of different lengths, time-major and packed: mel [sum T, mel]; noise [sum 480 T, harmonics
+ * + 1]; cache_source [n_items, S] replaces each row's first S source samples; speech / source out [sum 480 T].
+ * f0_override / source_override (optional, device): use these instead of the f0 predictor / the NSF source. f0_out
+ * (optional): the f0 used [sum T]. */
+int t2w_hift_forward(const t2w_hift* h, int n_items, const int* frames, const int* plan_dev, const float* mel,
+                     const float* noise, const float* cache_source, int S, const float* f0_override,
+                     const float* source_override, float* speech, float* source, float* f0_out, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- graphs (hipGraph capture of a stream) */
 

@@ -44,6 +44,25 @@ class SolveArgs(C.Structure):
                [("pool_layer_stride", C.c_longlong), ("conv_pool", P), ("workspace", P), ("workspace_bytes", C.c_size_t)]
 
 
+class HiftDims(C.Structure):
+    _fields_ = [(n, I) for n in ("mel", "base", "n_up", "harmonics", "f0_channels", "f0_layers", "sr", "n_fft", "hop")] + \
+               [(n, I * 3) for n in ("up_rates", "up_kernels", "res_kernels", "res_dilations", "src_kernels")] + \
+               [(n, F) for n in ("sine_amp", "noise_std", "voiced_threshold", "lrelu_slope", "audio_limit")]
+
+
+class Conv(C.Structure):
+    _fields_ = [("w", P), ("b", P)]
+
+
+class ResBlock(C.Structure):
+    _fields_ = [("c1", Conv * 3), ("c2", Conv * 3)] + [(n, P * 3) for n in ("a1", "inv1", "a2", "inv2")]
+
+
+class HiftWeights(C.Structure):
+    _fields_ = [("f0", Conv * 5), ("f0_head_w", P), ("f0_head_b", P), ("src_w", P), ("src_b", P), ("conv_pre", Conv), ("ups", Conv * 3),
+                ("src_down", Conv * 3), ("conv_post", Conv), ("src_res", ResBlock * 3), ("res", ResBlock * 9), ("window", P)]
+
+
 _SIGS = {
     "t2w_abi_version": (I, []),
     "t2w_last_error": (C.c_char_p, []),
@@ -60,6 +79,12 @@ _SIGS = {
     "t2w_ln_mod": (I, [P, P, P, F, P, I, I, P]),
     "t2w_qk_norm_scatter": (I, [P, P, P, P, P, F, P, P, P, P, I, I, P]),
     "t2w_attention": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, F, P]),
+    "t2w_hift_create": (I, [C.POINTER(HiftDims), C.POINTER(HiftWeights), C.POINTER(P)]),
+    "t2w_hift_destroy": (None, [P]),
+    "t2w_hift_plan_ints": (I, [I]),
+    "t2w_hift_plan": (I, [P, I, P, P]),
+    "t2w_hift_workspace_bytes": (C.c_size_t, [P, I, P]),
+    "t2w_hift_forward": (I, [P, I, P, P, P, P, P, I, P, P, P, P, P, P, C.c_size_t, P]),
     "t2w_graph_begin": (I, [P]),
     "t2w_graph_end": (I, [P, C.POINTER(P)]),
     "t2w_graph_launch": (I, [P, P]),

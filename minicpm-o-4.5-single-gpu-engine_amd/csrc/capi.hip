@@ -36,6 +36,10 @@ size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace
 
+namespace t2w {
+int set_error(const char* what, hipError_t e) { return fail(what, e); }
+}  // namespace t2w
+
 struct t2w_dit {
   t2w_dit_dims d;
   std::vector<t2w_dit_block> blocks;

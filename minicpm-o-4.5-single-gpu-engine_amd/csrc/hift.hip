@@ -1,0 +1,310 @@
+// HiFT vocoder kernels (fp32): implicit-GEMM 1-D convolutions on fp32 MFMA, the NSF harmonic source, STFT and ISTFT.
+//
+// Activations are time-major ([rows, channels], one item's frames contiguous), so for every tap a conv's K slice over
+// input channels is contiguous and the GEMM is rows x Cout x (taps * Cin).  Transposed convolutions run as `u`
+// polyphase convolutions (phase p of the output sees taps p, p + u, .. of the kernel over inputs q, q - 1, ..).  The
+// activation before a conv (leaky ReLU, Snake) is applied while its input tile is staged in LDS; the epilogue adds the
+// bias and, for ResBlocks, the residual and the running mean over the stage's three ResBlocks.
+#include "common.h"
+#include "hift_internal.h"
+
+namespace t2w {
+
+namespace {
+
+constexpr int CBM = 64, CBN = 64, CBK = 16, CLD = CBK + 1;  // LDS rows padded to 17 floats
+
+// exact twiddles of the 16-point DFT: cos / sin(2 pi m / 16)
+__constant__ float kCos16[16] = {1.0f, 0.923879533f, 0.707106781f, 0.382683432f, 0.0f, -0.382683432f, -0.707106781f, -0.923879533f,
+                                 -1.0f, -0.923879533f, -0.707106781f, -0.382683432f, 0.0f, 0.382683432f, 0.707106781f, 0.923879533f};
+__constant__ float kSin16[16] = {0.0f, 0.382683432f, 0.707106781f, 0.923879533f, 1.0f, 0.923879533f, 0.707106781f, 0.382683432f,
+                                 0.0f, -0.382683432f, -0.707106781f, -0.923879533f, -1.0f, -0.923879533f, -0.707106781f, -0.382683432f};
+
+__device__ __forceinline__ float pre_act(float v, int pre, float slope, float a, float inv) {
+  if (pre == PRE_LEAKY) return v > 0.f ? v : v * slope;
+  if (pre == PRE_SNAKE) {
+    const float s = sinf(__fmul_rn(v, a));
+    return __fadd_rn(v, __fmul_rn(inv, __fmul_rn(s, s)));
+  }
+  return v;
+}
+
+__global__ void __launch_bounds__(256) conv_f32_kernel(ConvDesc c) {
+  __shared__ float xs[CBM * CLD];
+  __shared__ float ws[CBN * CLD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
+  const int Tin = c.in_len[b], Tout = c.out_len[b];
+  const int oo = c.off_out[ph];
+  // output rows r with 0 <= r * s_out + oo < Tout
+  const int r_lo = oo >= 0 ? 0 : (-oo + c.s_out - 1) / c.s_out;
+  const int r_hi = Tout - 1 - oo < 0 ? -1 : (Tout - 1 - oo) / c.s_out;
+  const int r0 = r_lo + blockIdx.x * CBM;
+  if (r0 > r_hi) return;
+  const int co0 = blockIdx.y * CBN;
+  const float* xb = c.x + (size_t)c.in_off[b] * c.ldx;
+  const float* wph = c.w + (size_t)ph * c.Cout * c.taps * c.Cin;
+
+  f32x16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+
+  // staging assignment: 4 consecutive K values of one row per thread
+  const int lrow = tid >> 2, lk = (tid & 3) * 4;
+  for (int j = 0; j < c.taps; ++j) {
+    const int rr = r0 + lrow;
+    const int in_row = rr * c.s_in + j * c.d_in + c.off_in[ph];
+    const bool rok = rr <= r_hi && in_row >= 0 && in_row < Tin;
+    const int co = co0 + lrow;
+    for (int k0 = 0; k0 < c.Cin; k0 += CBK) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int ci = k0 + lk + e;
+        float v = 0.f;
+        if (rok && ci < c.Cin) {
+          v = xb[(size_t)in_row * c.ldx + ci];
+          if (c.pre) v = pre_act(v, c.pre, c.slope, c.alpha ? c.alpha[ci] : 0.f, c.inv ? c.inv[ci] : 0.f);
+        }
+        xs[lrow * CLD + lk + e] = v;
+        ws[lrow * CLD + lk + e] = (co < c.Cout && ci < c.Cin) ? wph[((size_t)co * c.taps + j) * c.Cin + ci] : 0.f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < CBK / 2; ++kk) {
+        const float a = ws[(wn * 32 + (lane & 31)) * CLD + 2 * kk + (lane >> 5)];
+        const float bb = xs[(wm * 32 + (lane & 31)) * CLD + 2 * kk + (lane >> 5)];
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, acc, 0, 0, 0);
+      }
+      __syncthreads();
+    }
+  }
+  // lane: output row r0 + wm*32 + lane%32, channels co0 + wn*32 + (q*8) + (lane/32)*4 + e
+  const int r = r0 + wm * 32 + (lane & 31);
+  if (r > r_hi) return;
+  const size_t row = (size_t)c.out_off[b] + (size_t)(r * c.s_out + oo);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int co = co0 + wn * 32 + q * 8 + (lane >> 5) * 4 + e;
+      if (co >= c.Cout) continue;
+      float v = __fadd_rn(acc[q * 4 + e], c.bias[co]);
+      float* yp = c.y + row * c.ldy + co;
+      switch (c.epi) {
+        case EPI_STORE: *yp = v; break;
+        case EPI_ELU: *yp = v > 0.f ? v : expm1f(v); break;
+        case EPI_RES: *yp = __fadd_rn(v, c.res[row * c.ldy + co]); break;
+        case EPI_ADD_RES: *yp = __fadd_rn(*yp, __fadd_rn(v, c.res[row * c.ldy + co])); break;
+        case EPI_RES_MEAN: {
+          v = __fadd_rn(v, c.res[row * c.ldy + co]);
+          float* sp = c.sum + row * c.ldy + co;
+          if (c.sum_mode == 0) *sp = v;
+          else if (c.sum_mode == 1) *sp = __fadd_rn(*sp, v);
+          else *sp = __fdiv_rn(__fadd_rn(*sp, v), (float)c.sum_div);
+        } break;
+      }
+    }
+  }
+}
+
+// f0 = |w . x + b| per frame (one wave per frame row, Linear(C -> 1) then abs)
+__global__ void __launch_bounds__(256) f0_head_kernel(const float* x, int C, const float* w, const float* b, float* f0, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  float s = 0.f;
+  for (int c = lane; c < C; c += 64) s += x[(size_t)r * C + c] * w[c];
+  s = wave_sum(s);
+  if (lane == 0) f0[r] = fabsf(s + b[0]);
+}
+
+// Frame-rate phase of harmonic h of item i: rad_f = (f0_f (h + 1) / sr) mod 1; phase_f = (sum_{g <= f} rad_g) 2 pi;
+// stored already multiplied by the upsampling scale (the reference's F.interpolate(phase * 480, scale 480) input).
+// One thread per (item, harmonic): the running sum is a sequential fp64 accumulation rounded to fp32 per frame, as
+// torch's CPU cumsum does for fp32.
+__global__ void phase_kernel(const float* f0, const int* fr_off, const int* fr_len, int n_items, int harm, float sr, float scale,
+                             float* phase) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_items * harm) return;
+  const int it = i / harm, h = i % harm;
+  const int o = fr_off[it], T = fr_len[it];
+  const float mult = (float)(h + 1);
+  double cum = 0.0;
+  for (int f = 0; f < T; ++f) {
+    const float fn = __fmul_rn(f0[o + f], mult);
+    const float rad = fmodf(__fdiv_rn(fn, sr), 1.0f);
+    cum += (double)rad;
+    const float ph = __fmul_rn(__fmul_rn((float)cum, 2.0f), 3.14159265358979323846f);
+    phase[(size_t)(o + f) * harm + h] = __fmul_rn(ph, scale);
+  }
+}
+
+// Per sample n of item i: phase_n by linear interpolation of the frame phases (align_corners=False, source index
+// (n + 0.5) / scale - 0.5 clamped at 0), sine = sin(phase) amp, voiced/unvoiced noise mix, tanh(Linear(9 -> 1)); the
+// first S samples come from the item's source cache.
+__global__ void source_kernel(const float* phase, const float* f0, const int* fr_off, const int* fr_len, const int* smp_off,
+                              int n_items, int harm, float inv_scale, int up, float amp, float noise_std, float unv, float thr,
+                              const float* noise, const float* lw, const float* lb, const float* cache, int S, float* out) {
+  const int it = blockIdx.y;
+  const int T = fr_len[it];
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int ns = T * up;
+  if (n >= ns) return;
+  const size_t so = (size_t)smp_off[it] + n;
+  if (n < S) {
+    out[so] = cache[(size_t)it * S + n];
+    return;
+  }
+  const int fo = fr_off[it];
+  float src = __fsub_rn(__fmul_rn(inv_scale, __fadd_rn((float)n, 0.5f)), 0.5f);
+  if (src < 0.f) src = 0.f;
+  int i0 = (int)src;
+  if (i0 > T - 1) i0 = T - 1;
+  const int i1 = i0 + (i0 < T - 1 ? 1 : 0);
+  const float l1 = __fsub_rn(src, (float)i0), l0 = __fsub_rn(1.0f, l1);
+  const float fv = f0[fo + n / up];
+  const float uv = fv > thr ? 1.0f : 0.0f;
+  const float namp = __fadd_rn(__fmul_rn(uv, noise_std), __fmul_rn(__fsub_rn(1.0f, uv), unv));
+  float acc = 0.f;
+  for (int h = 0; h < harm; ++h) {
+    // torch's CPU kernel rounds l1 * p1 and fuses l0 * p0 into the sum
+    const float p = fmaf(l0, phase[(size_t)(fo + i0) * harm + h], __fmul_rn(l1, phase[(size_t)(fo + i1) * harm + h]));
+    float sine = __fmul_rn(sinf(p), amp);
+    sine = __fadd_rn(__fmul_rn(sine, uv), __fmul_rn(namp, noise[so * harm + h]));
+    acc = fmaf(sine, lw[h], acc);
+  }
+  out[so] = tanhf(__fadd_rn(acc, lb[0]));
+}
+
+// STFT of the source (n_fft 16, hop 4, centred, reflect padding, periodic Hann window): frame f of item i ->
+// [re_0..re_8 | im_0..im_8]
+__global__ void stft_kernel(const float* s, const int* smp_off, const int* smp_len, const int* fr_off, const int* fr_len,
+                            const float* win, float* out) {
+  const int it = blockIdx.y;
+  const int f = blockIdx.x * blockDim.x + threadIdx.x;
+  const int F = fr_len[it];
+  if (f >= F) return;
+  const int n = smp_len[it];
+  const float* x = s + smp_off[it];
+  float v[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    int p = f * 4 + k - 8;
+    if (p < 0) p = -p;
+    if (p >= n) p = 2 * (n - 1) - p;
+    v[k] = __fmul_rn(x[p], win[k]);
+  }
+  float* o = out + (size_t)(fr_off[it] + f) * 18;
+#pragma unroll
+  for (int b = 0; b < 9; ++b) {
+    float re = 0.f, im = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      re = fmaf(v[k], kCos16[(b * k) & 15], re);
+      im = fmaf(-v[k], kSin16[(b * k) & 15], im);
+    }
+    o[b] = re;
+    o[9 + b] = im;
+  }
+}
+
+// ISTFT (``istft_overlap_add``): per output sample, the inverse real FFT values of the <= 4 overlapping frames (mag =
+// min(exp(x_re), 100), phase = sin(x_im), spectrum mag (cos phase, sin phase)), windowed, summed, divided by the summed
+// squared window; n_fft / 2 trimmed at both ends; clamped to +-limit.
+__global__ void istft_kernel(const float* x, const int* fr_off, const int* fr_len, const int* smp_off, const float* win, float limit,
+                             float* out) {
+  const int it = blockIdx.y;
+  const int F = fr_len[it];
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int ns = (F - 1) * 4;
+  if (n >= ns) return;
+  const int p = n + 8;
+  int fa = (p - 15 + 3) / 4;
+  if (p - 15 < 0) fa = 0;
+  int fb = p / 4;
+  if (fb > F - 1) fb = F - 1;
+  float y = 0.f, env = 0.f;
+  for (int f = fa; f <= fb; ++f) {
+    const int i = p - 4 * f;
+    const float* xf = x + (size_t)(fr_off[it] + f) * 18;
+    // irfft at index i: (1/16) [X0 + (-1)^i X8 + 2 sum_{k=1..7} (Re X_k cos(2 pi k i / 16) - Im X_k sin(2 pi k i / 16))]
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      const float mag = fminf(expf(xf[k]), 100.0f);
+      const float ph = sinf(xf[9 + k]);
+      const float re = __fmul_rn(mag, cosf(ph)), im = __fmul_rn(mag, sinf(ph));
+      const float c = kCos16[(k * i) & 15], s = kSin16[(k * i) & 15];
+      // the imaginary parts of DC and Nyquist are ignored
+      acc += (k == 0 || k == 8) ? re * c : 2.0f * (re * c - im * s);
+    }
+    const float w = win[i];
+    y = fmaf(acc * (1.0f / 16.0f), w, y);
+    env = fmaf(w, w, env);
+  }
+  float v = y / env;
+  v = fminf(fmaxf(v, -limit), limit);
+  out[smp_off[it] + n] = v;
+}
+
+// rows 1.. of each item's ups output were written one row down; row 0 = input row 1 (ReflectionPad1d((1, 0)))
+__global__ void reflect_kernel(float* x, int C, const int* off, int n_items) {
+  const int it = blockIdx.y;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C || it >= n_items) return;
+  float* b = x + (size_t)off[it] * C;
+  b[c] = b[2 * C + c];
+}
+
+inline unsigned cdiv(long long a, long long b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace
+
+hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
+  if (c.n_items <= 0 || max_rows <= 0) return hipSuccess;
+  if (c.n_phase < 1 || c.n_phase > 8) return hipErrorInvalidValue;
+  dim3 grid(cdiv(max_rows, CBM), cdiv(c.Cout, CBN), c.n_items * c.n_phase);
+  hipLaunchKernelGGL(conv_f32_kernel, grid, dim3(256), 0, st, c);
+  return hipGetLastError();
+}
+
+hipError_t f0_head(const float* x, int C, const float* w, const float* b, float* f0, int rows, hipStream_t st) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(f0_head_kernel, dim3(cdiv(rows, 4)), dim3(256), 0, st, x, C, w, b, f0, rows);
+  return hipGetLastError();
+}
+
+hipError_t nsf_phase(const float* f0, const int* fr_off, const int* fr_len, int n_items, int harm, float sr, float scale, float* phase,
+                     hipStream_t st) {
+  hipLaunchKernelGGL(phase_kernel, dim3(cdiv(n_items * harm, 64)), dim3(64), 0, st, f0, fr_off, fr_len, n_items, harm, sr, scale, phase);
+  return hipGetLastError();
+}
+
+hipError_t nsf_source(const float* phase, const float* f0, const int* fr_off, const int* fr_len, const int* smp_off, int n_items,
+                      int max_frames, int harm, float inv_scale, int up, float amp, float noise_std, float unv, float thr,
+                      const float* noise, const float* lw, const float* lb, const float* cache, int S, float* out, hipStream_t st) {
+  dim3 grid(cdiv((long long)max_frames * up, 256), n_items);
+  hipLaunchKernelGGL(source_kernel, grid, dim3(256), 0, st, phase, f0, fr_off, fr_len, smp_off, n_items, harm, inv_scale, up, amp, noise_std,
+                     unv, thr, noise, lw, lb, cache, S, out);
+  return hipGetLastError();
+}
+
+hipError_t stft16(const float* s, const int* smp_off, const int* smp_len, const int* fr_off, const int* fr_len, int n_items, int max_fr,
+                  const float* win, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(stft_kernel, dim3(cdiv(max_fr, 128), n_items), dim3(128), 0, st, s, smp_off, smp_len, fr_off, fr_len, win, out);
+  return hipGetLastError();
+}
+
+hipError_t istft16(const float* x, const int* fr_off, const int* fr_len, const int* smp_off, int n_items, int max_smp, const float* win,
+                   float limit, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(istft_kernel, dim3(cdiv(max_smp, 256), n_items), dim3(256), 0, st, x, fr_off, fr_len, smp_off, win, limit, out);
+  return hipGetLastError();
+}
+
+hipError_t reflect_rows(float* x, int C, const int* off, int n_items, hipStream_t st) {
+  hipLaunchKernelGGL(reflect_kernel, dim3(cdiv(C, 256), n_items), dim3(256), 0, st, x, C, off, n_items);
+  return hipGetLastError();
+}
+
+}  // namespace t2w

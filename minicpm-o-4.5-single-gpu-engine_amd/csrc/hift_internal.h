@@ -1,0 +1,43 @@
+// Internal launch interfaces of the HiFT kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace t2w {
+
+enum PreAct { PRE_NONE = 0, PRE_LEAKY = 1, PRE_SNAKE = 2 };
+enum ConvEpi { EPI_STORE = 0, EPI_ELU = 1, EPI_RES = 2, EPI_ADD_RES = 3, EPI_RES_MEAN = 4 };
+
+// y[out_off[b] + r * s_out + off_out[ph], co] = epi(bias[co] + sum_{j, ci} w[ph, co, j, ci] act(x[in_off[b] + r * s_in +
+// j * d_in + off_in[ph], ci])), inputs outside [0, in_len[b]) read as zero.
+struct ConvDesc {
+  const float* x; int ldx;
+  const int* in_off; const int* in_len;
+  float* y; int ldy;
+  const int* out_off; const int* out_len;
+  const float* w; const float* bias;  // w [n_phase, Cout, taps, Cin]
+  int Cin, Cout, taps;
+  int s_in, d_in, s_out;
+  int n_phase;
+  int off_in[8], off_out[8];
+  int pre; float slope; const float* alpha; const float* inv;
+  int epi; const float* res; float* sum; int sum_mode; int sum_div;
+  int n_items;
+};
+
+hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st);
+hipError_t f0_head(const float* x, int C, const float* w, const float* b, float* f0, int rows, hipStream_t st);
+hipError_t nsf_phase(const float* f0, const int* fr_off, const int* fr_len, int n_items, int harm, float sr, float scale, float* phase,
+                     hipStream_t st);
+hipError_t nsf_source(const float* phase, const float* f0, const int* fr_off, const int* fr_len, const int* smp_off, int n_items,
+                      int max_frames, int harm, float inv_scale, int up, float amp, float noise_std, float unvoiced_amp, float thr,
+                      const float* noise, const float* lw, const float* lb, const float* cache, int S, float* out, hipStream_t st);
+hipError_t stft16(const float* s, const int* smp_off, const int* smp_len, const int* fr_off, const int* fr_len, int n_items, int max_fr,
+                  const float* win, float* out, hipStream_t st);
+hipError_t istft16(const float* x, const int* fr_off, const int* fr_len, const int* smp_off, int n_items, int max_smp, const float* win,
+                   float limit, float* out, hipStream_t st);
+hipError_t reflect_rows(float* x, int C, const int* off, int n_items, hipStream_t st);
+
+int set_error(const char* what, hipError_t e);  // records the message for t2w_last_error(); returns 1
+
+}  // namespace t2w

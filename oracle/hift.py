@@ -207,10 +207,10 @@ def istft_overlap_add(spec: torch.Tensor, n_fft: int, hop: int, window: torch.Te
     return (y / env)[:, half:total - half]
 
 
-def source(h: HiFT, mel: torch.Tensor, cache_source: torch.Tensor, rand_ini: torch.Tensor, noise: torch.Tensor) -> torch.Tensor:
-    """The NSF source ``s`` [B, 1, 480 T] (``token2wav.py:218-235``)."""
+def source(h: HiFT, mel: torch.Tensor, cache_source: torch.Tensor, rand_ini: torch.Tensor, noise: torch.Tensor, f0=None) -> torch.Tensor:
+    """The NSF source ``s`` [B, 1, 480 T] (``token2wav.py:218-235``); ``f0`` [B, T] replaces the f0 predictor's."""
     gen = h.m_source.l_sin_gen
-    f0 = h.f0_predictor(mel)
+    f0 = h.f0_predictor(mel) if f0 is None else f0
     s = h.f0_upsamp(f0[:, None]).transpose(1, 2)  # [B, n, 1]
     fn = s * torch.arange(1, gen.harmonic_num + 2, dtype=torch.float32)[None, None, :]
     rad = (fn / gen.sampling_rate) % 1
