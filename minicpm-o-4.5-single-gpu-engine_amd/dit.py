@@ -163,6 +163,49 @@ class FastCache:
         return len(self.rows[0].order)
 
 
+def plan_call(rows: list[FastRow], Ts: list[int], new: list[list[int]], keep: list[bool], cnn_scratch: int) -> dict:
+    """Host plan of one call (``engine/runtime/dit_fast.py:223-266``): rows ``[cond 0..n-1 | uncond 0..n-1]`` each with
+    its window's ``Ts[i]`` tokens and freshly allocated key slots ``new[r]``.  Returns the device tables (in
+    ``t2w_solve_args`` order; kv_idx last because its length varies) and the bookkeeping the solve needs afterwards."""
+    n = len(Ts)
+    lens = Ts + Ts
+    tok_row, tok_pos, new_slot = [], [], []
+    row_start, row_kv_off, row_kv_len, rd, wr, kv, tiles = [], [], [], [], [], [], []
+    o = 0
+    for r, (row, t, nw) in enumerate(zip(rows, lens, new)):
+        row_start.append(o)
+        tok_row += [r] * t
+        tok_pos += list(range(t))
+        new_slot += nw
+        row_kv_off.append(len(kv))
+        kv += nw + row.order  # the row's new frames first (masking is by position), then its cache
+        row_kv_len.append(t + len(row.order))
+        rd.append(row.cnn[row.cur])
+        wr.append(row.cnn[1 - row.cur] if keep[r % n] else cnn_scratch)
+        tiles += [v for q0 in range(0, t, 64) for v in (r, q0)]
+        o += t
+    a_src = [i + 2 * r for i, r in enumerate(tok_row)]
+    parts = [tok_row, tok_pos, a_src, new_slot, row_start, lens, row_kv_off, row_kv_len, rd, wr, tiles, kv]
+    return {"n_tok": o, "n_rows": 2 * n, "half": o // 2, "n_tiles": len(tiles) // 2, "parts": parts, "new": new, "rows": rows}
+
+
+def advance_row(r: FastRow, new: list[int], keep: bool, keep_len: int) -> list[int]:
+    """After a solve: a kept window's slots join the row as ``[new, cache]`` (the reference's concatenation order), then
+    the order is trimmed to its first ``keep_len`` and last 100 entries (``engine/runtime/dit_fast.py:480-490``) and
+    the conv caches swap to the slot just written; a window that is not kept leaves the row as it was.  Returns the
+    slots to release."""
+    if not keep:
+        return list(new)
+    order = new + r.order
+    freed = []
+    if len(order) > keep_len + TRIM_SUFFIX:
+        freed = order[keep_len:len(order) - TRIM_SUFFIX]
+        order = order[:keep_len] + order[len(order) - TRIM_SUFFIX:]
+    r.order = order
+    r.cur = 1 - r.cur
+    return freed
+
+
 class FastDiT:
     """The packed ragged CFG Euler solve over per-request caches (``FastDiT`` of ``engine/runtime/dit_fast.py``)."""
 
@@ -217,29 +260,9 @@ class FastDiT:
 
     # --- planning ---------------------------------------------------------------------------------------------------
     def _plan(self, caches: list[FastCache], Ts: list[int], keep: list[bool]) -> dict:
-        n = len(caches)
         rows = [c.rows[0] for c in caches] + [c.rows[1] for c in caches]
-        lens = Ts + Ts
-        new = [self.pool.alloc(t) for t in lens]
-        tok_row, tok_pos, new_slot = [], [], []
-        row_start, row_kv_off, row_kv_len, rd, wr, kv, tiles = [], [], [], [], [], [], []
-        o = 0
-        for r, (row, t, nw) in enumerate(zip(rows, lens, new)):
-            row_start.append(o)
-            tok_row += [r] * t
-            tok_pos += list(range(t))
-            new_slot += nw
-            row_kv_off.append(len(kv))
-            kv += nw + row.order
-            row_kv_len.append(t + len(row.order))
-            rd.append(row.cnn[row.cur])
-            wr.append(row.cnn[1 - row.cur] if keep[r % n] else self.cnn_scratch)
-            tiles += [v for q0 in range(0, t, 64) for v in (r, q0)]
-            o += t
-        N = o
-        a_src = [i + 2 * r for i, r in enumerate(tok_row)]
-        parts = [tok_row, tok_pos, a_src, new_slot, row_start, lens, row_kv_off, row_kv_len, rd, wr, tiles, kv]  # kv last: its length varies
-        return {"n_tok": N, "n_rows": 2 * n, "half": N // 2, "n_tiles": len(tiles) // 2, "parts": parts, "new": new, "rows": rows}
+        new = [self.pool.alloc(t) for t in Ts + Ts]
+        return plan_call(rows, Ts, new, keep, self.cnn_scratch)
 
     def _workspace(self, N: int, R: int) -> torch.Tensor:
         need = _lib.lib().t2w_dit_workspace_bytes(self.model.handle, N, R)
@@ -288,15 +311,7 @@ class FastDiT:
         out = self._run(p, x0.contiguous(), stat, chunk)
         for i, c in enumerate(caches):
             for r, nw in ((p["rows"][i], p["new"][i]), (p["rows"][n + i], p["new"][n + i])):
-                if keep[i]:
-                    order = nw + r.order  # [new, cache], the reference's concatenation order
-                    if len(order) > c.keep + TRIM_SUFFIX:
-                        self.pool.release(order[c.keep:len(order) - TRIM_SUFFIX])
-                        order = order[:c.keep] + order[len(order) - TRIM_SUFFIX:]
-                    r.order = order
-                    r.cur = 1 - r.cur
-                else:
-                    self.pool.release(nw)
+                self.pool.release(advance_row(r, nw, keep[i], c.keep))
         res, o = [], 0
         for t in Ts:
             res.append(out[o:o + t].t())
