@@ -49,6 +49,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-hift", action="store_true")
     ap.add_argument("--latency-reps", type=int, default=20)
+    ap.add_argument("--hift-fp32", action="store_true", help="HiFT decoder in strict fp32 (default: bf16 MFMA decoder)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no sharding or collectives); use --gpus 1", file=sys.stderr)
@@ -77,7 +78,7 @@ def main() -> int:
         from t2w_amd.hift import HiFTModel
 
         Wh = init_hift(HiFTConfig(), seed=3)
-        hift = HiFTModel(Wh, HiFTConfig())
+        hift = HiFTModel(Wh, HiFTConfig(), decode_bf16=not args.hift_fp32)
         hsrc = torch.zeros(n, 1, 0, device=dev)
         hnoise = hift.noise([1000 + i for i in range(n)], T * hift.cfg.upsample_scale)
 
@@ -117,6 +118,7 @@ def main() -> int:
     a_src = torch.from_numpy((np.arange(N) + 2 * tok_row).astype(np.int32)).to(dev)
     out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
     s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())  # operands were written on the default stream
     L = _lib.lib()
     with torch.cuda.stream(s):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -172,13 +174,13 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (random-init weights, seeded N(0,1) inputs)",
         "config": {"workload": f"{n} streams x {T} mel frames, CFG B={2 * n}, chunk-causal {args.chunk}, 10-step Euler DiT"
-                               + ("" if hift is None else " + HiFT fp32"),
+                               + ("" if hift is None else (" + HiFT fp32" if args.hift_fp32 else " + HiFT (bf16-MFMA decoder, fp32 f0/source)")),
                    "global_batch": 2 * n, "seq_len": T, "parallelism": "single GPU"},
         "audio_seconds_per_s": frames / 50.0 / dt,
         "p50_chunk_latency_ms": lat,
         "dit_solve_ms": dit_dt * 1e3,
         "dit_mfma_frac": (gemm_f + attn_f) / dit_dt / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<128,128,2,2,EPI_BF16,taps> (DiT conv1)", "achieved": k_tflops,
+        "roofline": {"bound": "mfma", "kernel": "gemm_lds_kernel<256,256,4,2,EPI_BF16,taps> (DiT conv1)", "achieved": k_tflops,
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": k_tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
                      "launch_ms": k_ms, "flops_per_launch": 2.0 * N * H * 3 * H},
         "cpu_baseline": cpu,

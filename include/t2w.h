@@ -123,6 +123,10 @@ int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const f
  * a_src non-null: conv taps mode, A row m = frames a_src[m] .. a_src[m] + K / lda - 1 of A (rows lda wide). */
 int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                   void* C, int ldc, int M, int N, int K, int epi, void* stream);
+/* t2w_gemm_bf16 with an explicit tile configuration (-1: chosen by shape; 0: 128x128, 1: 256x128, 2: 128x256,
+ * 3: 256x256 of 4 waves, 4: 256x256 of 8 waves) for tile sweeps. */
+int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
+                       void* C, int ldc, int M, int N, int K, int epi, int tile, void* stream);
 int t2w_ln_mod(const float* h, const float* shift, const float* scale1, float eps, void* out, int N, int H,
                void* stream);
 int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const float* kw, const float* kb, float eps,
@@ -141,8 +145,11 @@ typedef struct {
   float sine_amp, noise_std, voiced_threshold, lrelu_slope, audio_limit;
 } t2w_hift_dims;
 
-typedef struct { const float* w; const float* b; } t2w_conv;  /* w [Cout, taps, Cin]; transposed convs:
-                                                                   [u, Cout, ceil(k / u), Cin] polyphase */
+typedef struct {
+  const float* w; const float* b;  /* w [Cout, taps, Cin]; transposed convs: [u, Cout, ceil(k / u), Cin] polyphase */
+  const void* wbf;                 /* optional bf16 copy [phases, Cout padded to 64, taps, Cin padded to 64] (zeros in
+                                      the padding) for the bf16-MFMA decoder; null: the conv always runs fp32 */
+} t2w_conv;
 typedef struct {
   t2w_conv c1[3], c2[3];
   const float* a1[3]; const float* inv1[3];  /* Snake alpha and 1 / (alpha + 1e-9) before convs1[j] */
@@ -171,7 +178,10 @@ size_t t2w_hift_workspace_bytes(const t2w_hift* h, int n_items, const int* frame
 int t2w_hift_forward(const t2w_hift* h, int n_items, const int* frames, const int* plan_dev, const float* mel,
                      const float* noise, const float* cache_source, int S, const float* f0_override,
                      const float* source_override, float* speech, float* source, float* f0_out, void* workspace,
-                     size_t workspace_bytes, void* stream);
+                     size_t workspace_bytes, int decode_bf16, void* stream);
+/* decode_bf16: the decoder's stride-1 and transposed convs (conv_pre, upsampling, ResBlocks, conv_post) on bf16 MFMA
+ * with fp32 activations and accumulation; the f0 predictor, the NSF source, the source downsampling convs, STFT and ISTFT
+ * stay fp32. */
 
 /* ---------------------------------------------------------------- graphs (hipGraph capture of a stream) */
 

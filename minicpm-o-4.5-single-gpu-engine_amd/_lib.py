@@ -51,7 +51,7 @@ class HiftDims(C.Structure):
 
 
 class Conv(C.Structure):
-    _fields_ = [("w", P), ("b", P)]
+    _fields_ = [("w", P), ("b", P), ("wbf", P)]
 
 
 class ResBlock(C.Structure):
@@ -76,6 +76,7 @@ _SIGS = {
     "t2w_dit_solve": (I, [P, C.POINTER(SolveArgs), P]),
     "t2w_dit_forward": (I, [P, C.POINTER(SolveArgs), I, P, P, P]),
     "t2w_gemm_bf16": (I, [P, I, P, P, P, P, P, I, I, I, I, I, P]),
+    "t2w_gemm_bf16_tile": (I, [P, I, P, P, P, P, P, I, I, I, I, I, I, P]),
     "t2w_ln_mod": (I, [P, P, P, F, P, I, I, P]),
     "t2w_qk_norm_scatter": (I, [P, P, P, P, P, F, P, P, P, P, I, I, P]),
     "t2w_attention": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, F, P]),
@@ -84,7 +85,7 @@ _SIGS = {
     "t2w_hift_plan_ints": (I, [I]),
     "t2w_hift_plan": (I, [P, I, P, P]),
     "t2w_hift_workspace_bytes": (C.c_size_t, [P, I, P]),
-    "t2w_hift_forward": (I, [P, I, P, P, P, P, P, I, P, P, P, P, P, P, C.c_size_t, P]),
+    "t2w_hift_forward": (I, [P, I, P, P, P, P, P, I, P, P, P, P, P, P, C.c_size_t, I, P]),
     "t2w_graph_begin": (I, [P]),
     "t2w_graph_end": (I, [P, C.POINTER(P)]),
     "t2w_graph_launch": (I, [P, P]),

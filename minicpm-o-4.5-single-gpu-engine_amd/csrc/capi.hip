@@ -257,10 +257,16 @@ int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const f
 
 int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate, void* C, int ldc,
                   int M, int N, int K, int epi, void* stream) {
+  return t2w_gemm_bf16_tile(A, lda, a_src, W, bias, gate, C, ldc, M, N, K, epi, -1, stream);
+}
+
+int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate, void* C, int ldc,
+                       int M, int N, int K, int epi, int tile, void* stream) {
   if (K % 64) return fail("K must be a multiple of 64");
   if (epi < 0 || epi > 3) return fail("bad epilogue");
   if (a_src && (K % lda)) return fail("taps mode: K must be a multiple of lda");
-  T2W_CHECK(gemm_bf16(gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K), epi, (hipStream_t)stream), "gemm");
+  if (tile > 9) return fail("bad tile configuration");
+  T2W_CHECK(gemm_bf16(gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K), epi, (hipStream_t)stream, tile), "gemm");
   return 0;
 }
 

@@ -40,16 +40,18 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 __device__ __forceinline__ float gelu_tanh(float x) {
-  // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+  // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3), written as x / (1 + exp(-2u)): one exp, one divide
   const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-  float u = k0 * (x + k1 * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(u));
+  const float u = k0 * (x + k1 * x * x * x);
+  return __fdividef(x, 1.0f + __expf(-2.0f * u));
 }
 
 __device__ __forceinline__ float mish(float y) {
-  // y * tanh(softplus(y)), softplus with torch's threshold 20
-  float sp = y > 20.0f ? y : log1pf(expf(y));
-  return y * tanhf(sp);
+  // y tanh(softplus(y)) = y n (n + 2) / (n (n + 2) + 2) with n = e^y; above torch's softplus threshold 20 it is y
+  if (y > 20.0f) return y;
+  const float n = __expf(y);
+  const float p = n * (n + 2.0f);
+  return y * __fdividef(p, p + 2.0f);
 }
 
 }  // namespace t2w

@@ -14,11 +14,45 @@
 
 namespace t2w {
 
+int pick_cfg(const GemmArgs& g);
+
 namespace {
 
 constexpr int BK = 64;  // K values per stage (128 bytes of bf16 per tile row)
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+
+template <int EPI>
+__device__ __forceinline__ void epilogue4(const GemmArgs& g, int m, int n, float (&v)[4]) {
+    if (n + 3 < g.N) {
+      const float4 bb = *(const float4*)(g.bias + n);
+      v[0] += bb.x; v[1] += bb.y; v[2] += bb.z; v[3] += bb.w;
+      if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) {
+        if (EPI == EPI_GELU_BF16) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+        }
+        uint2 o = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+        *(uint2*)((bf16_t*)g.C + (size_t)m * g.ldc + n) = o;
+      } else if (EPI == EPI_RESID_F32) {
+        float* hp = (float*)g.C + (size_t)m * g.ldc + n;
+        float4 h = *(float4*)hp;
+        const float4 gg = *(const float4*)(g.gate + n);
+        h.x += gg.x * v[0]; h.y += gg.y * v[1]; h.z += gg.z * v[2]; h.w += gg.w * v[3];
+        *(float4*)hp = h;
+      } else {
+        *(float4*)((float*)g.C + (size_t)m * g.ldc + n) = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    } else {
+      for (int e = 0; e < 4 && n + e < g.N; ++e) {
+        float x = v[e] + g.bias[n + e];
+        if (EPI == EPI_BF16) ((bf16_t*)g.C)[(size_t)m * g.ldc + n + e] = f2bf(x);
+        else if (EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[(size_t)m * g.ldc + n + e] = f2bf(gelu_tanh(x));
+        else if (EPI == EPI_RESID_F32) ((float*)g.C)[(size_t)m * g.ldc + n + e] += g.gate[n + e] * x;
+        else ((float*)g.C)[(size_t)m * g.ldc + n + e] = x;
+      }
+    }
+}
 
 template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
@@ -26,9 +60,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
   constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA blocks per wave
   constexpr int APASS = BM * 8 / NT, BPASS = BN * 8 / NT;
+  constexpr int STAGE = (BM + BN) * 8;  // uint4 per LDS stage
   static_assert(APASS * NT == BM * 8 && BPASS * NT == BN * 8, "tile / thread mismatch");
 
-  __shared__ uint4 lds[2][(BM + BN) * 8];
+  extern __shared__ uint4 lds_dyn[];  // two stages of STAGE uint4: [A tile BM x 8 | W tile BN x 8]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -86,9 +121,9 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   };
   auto lstore = [&](int s) {
 #pragma unroll
-    for (int p = 0; p < APASS; ++p) lds[s][swz(arow[p], achunk[p])] = ra[p];
+    for (int p = 0; p < APASS; ++p) lds_dyn[s * STAGE + swz(arow[p], achunk[p])] = ra[p];
 #pragma unroll
-    for (int p = 0; p < BPASS; ++p) lds[s][BM * 8 + swz(brow[p], bchunk[p])] = rb[p];
+    for (int p = 0; p < BPASS; ++p) lds_dyn[s * STAGE + BM * 8 + swz(brow[p], bchunk[p])] = rb[p];
   };
 
   f32x16 acc[TM][TN];
@@ -113,12 +148,12 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         int row = wm * WTM + i * 32 + (lane & 31);
-        af[i] = as_bf16x8(lds[s][swz(row, chunk)]);
+        af[i] = as_bf16x8(lds_dyn[s * STAGE + swz(row, chunk)]);
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         int row = wn * WTN + j * 32 + (lane & 31);
-        bfr[j] = as_bf16x8(lds[s][BM * 8 + swz(row, chunk)]);
+        bfr[j] = as_bf16x8(lds_dyn[s * STAGE + BM * 8 + swz(row, chunk)]);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -143,34 +178,128 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
-        if (n + 3 < g.N) {
-          const float4 bb = *(const float4*)(g.bias + n);
-          v[0] += bb.x; v[1] += bb.y; v[2] += bb.z; v[3] += bb.w;
-          if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) {
-            if (EPI == EPI_GELU_BF16) {
+        epilogue4<EPI>(g, m, n, v);
+      }
+    }
+  }
+}
+
+// Direct-to-LDS variant: every 16-byte chunk of the next K stage goes from global memory straight into its swizzled
+// LDS slot (global_load_lds_dwordx4: a wave writes 1 KB of LDS, lane l at byte 16 l of the block, so each lane loads the
+// chunk whose swizzled position is its own), with no VGPR staging; fragments of the next 16-wide K step are read while
+// the current one's MFMAs issue.  Rows past M / N are clamped to the last valid row (their results are never stored).
+template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_lds_kernel(GemmArgs g) {
+  constexpr int NT = 64 * WM * WN, NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int STAGE = (BM + BN) * 8;        // uint4 per stage
+  constexpr int ABLK = BM / 8, BBLK = BN / 8;  // 1 KB blocks (8 rows) per stage
+  constexpr int APW = ABLK / NW, BPW = BBLK / NW;
+  static_assert(APW * NW == ABLK && BPW * NW == BBLK, "blocks / waves mismatch");
+  extern __shared__ uint4 lds_dyn[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
+  const int nblk = gm * gn;
+  int b = blockIdx.x;
+  const int full = (nblk / 8) * 8;
+  if (b < full) b = (b % 8) * (nblk / 8) + b / 8;
+  const int mt = b / gn, nt = b % gn;
+  const int m0 = mt * BM, n0 = nt * BN;
+
+  // this lane's source chunk in each of its waves' 1 KB blocks: block row l/8, logical chunk (l%8) ^ (row & 7)
+  const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+  const bf16_t* asrc[APW];
+  const bf16_t* bsrc[BPW];
 #pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
-            }
-            uint2 o = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
-            *(uint2*)((bf16_t*)g.C + (size_t)m * g.ldc + n) = o;
-          } else if (EPI == EPI_RESID_F32) {
-            float* hp = (float*)g.C + (size_t)m * g.ldc + n;
-            float4 h = *(float4*)hp;
-            const float4 gg = *(const float4*)(g.gate + n);
-            h.x += gg.x * v[0]; h.y += gg.y * v[1]; h.z += gg.z * v[2]; h.w += gg.w * v[3];
-            *(float4*)hp = h;
-          } else {
-            *(float4*)((float*)g.C + (size_t)m * g.ldc + n) = make_float4(v[0], v[1], v[2], v[3]);
-          }
-        } else {
-          for (int e = 0; e < 4 && n + e < g.N; ++e) {
-            float x = v[e] + g.bias[n + e];
-            if (EPI == EPI_BF16) ((bf16_t*)g.C)[(size_t)m * g.ldc + n + e] = f2bf(x);
-            else if (EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[(size_t)m * g.ldc + n + e] = f2bf(gelu_tanh(x));
-            else if (EPI == EPI_RESID_F32) ((float*)g.C)[(size_t)m * g.ldc + n + e] += g.gate[n + e] * x;
-            else ((float*)g.C)[(size_t)m * g.ldc + n + e] = x;
-          }
-        }
+  for (int p = 0; p < APW; ++p) {
+    int m = m0 + (wave + p * NW) * 8 + lrow;
+    m = m < g.M ? m : g.M - 1;
+    asrc[p] = TAPS ? g.A + (size_t)g.a_src[m] * g.lda + lchunk * 8 : g.A + (size_t)m * g.lda + lchunk * 8;
+  }
+#pragma unroll
+  for (int p = 0; p < BPW; ++p) {
+    int n = n0 + (wave + p * NW) * 8 + lrow;
+    n = n < g.N ? n : g.N - 1;
+    bsrc[p] = g.B + (size_t)n * g.ldb + lchunk * 8;
+  }
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  auto issue = [&](int k0, int s) {
+    size_t aoff;
+    if (TAPS) {
+      const int tap = k0 / g.tapC;
+      aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);
+    } else {
+      aoff = k0;
+    }
+#pragma unroll
+    for (int p = 0; p < APW; ++p)
+      __builtin_amdgcn_global_load_lds((const void*)(asrc[p] + aoff), (lds_ptr_t)(lds_dyn + s * STAGE + (wave + p * NW) * 64), 16, 0, 0);
+#pragma unroll
+    for (int p = 0; p < BPW; ++p)
+      __builtin_amdgcn_global_load_lds((const void*)(bsrc[p] + k0), (lds_ptr_t)(lds_dyn + s * STAGE + BM * 8 + (wave + p * NW) * 64), 16, 0, 0);
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int KT = g.K / BK;
+  issue(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int s = kt & 1;
+    if (kt + 1 < KT) issue((kt + 1) * BK, s ^ 1);
+    const uint4* L = lds_dyn + s * STAGE;
+    bf16x8 af[2][TM], bfr[2][TN];
+    auto frag = [&](int kk, int buf) {
+      const int chunk = kk * 2 + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * WTM + i * 32 + (lane & 31);
+        af[buf][i] = as_bf16x8(L[swz(row, chunk)]);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int row = wn * WTN + j * 32 + (lane & 31);
+        bfr[buf][j] = as_bf16x8(L[BM * 8 + swz(row, chunk)]);
+      }
+    };
+    frag(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      if (kk + 1 < BK / 16) frag(kk + 1, (kk + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[kk & 1][j], af[kk & 1][i], acc[i][j], 0, 0, 0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * WTM + i * 32 + (lane & 31);
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * WTN + j * 32 + q * 8 + (lane >> 5) * 4;
+        if (n >= g.N) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
+        epilogue4<EPI>(g, m, n, v);
       }
     }
   }
@@ -179,29 +308,73 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
 template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
 hipError_t launch_cfg(const GemmArgs& g, hipStream_t st) {
   const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, TAPS>), dim3(gm * gn), dim3(64 * WM * WN), 0, st, g);
+  const size_t lds = 2 * (size_t)(BM + BN) * 8 * sizeof(uint4);
+  auto kern = gemm_kernel<BM, BN, WM, WN, EPI, TAPS>;
+  static bool attr_set = false;  // one attribute call per instantiation (host side, idempotent)
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(gm * gn), dim3(64 * WM * WN), lds, st, g);
   return hipGetLastError();
 }
 
+template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
+hipError_t launch_lds(const GemmArgs& g, hipStream_t st) {
+  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
+  const size_t lds = 2 * (size_t)(BM + BN) * 8 * sizeof(uint4);
+  auto kern = gemm_lds_kernel<BM, BN, WM, WN, EPI, TAPS>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(gm * gn), dim3(64 * WM * WN), lds, st, g);
+  return hipGetLastError();
+}
+
+// tile configurations: 0 = 128x128 (4 waves of 64x64), 1 = 256x128 (4 waves of 128x64), 2 = 128x256 (4 waves of 64x128),
+// 3 = 256x256 (4 waves of 128x128), 4 = 256x256 (8 waves of 128x64)
 template <int EPI, bool TAPS>
-hipError_t launch_epi(const GemmArgs& g, hipStream_t st) {
-  return launch_cfg<128, 128, 2, 2, EPI, TAPS>(g, st);
+hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
+  if (cfg < 0) cfg = pick_cfg(g);
+  switch (cfg) {
+    case 0: return launch_cfg<128, 128, 2, 2, EPI, TAPS>(g, st);
+    case 1: return launch_cfg<256, 128, 2, 2, EPI, TAPS>(g, st);
+    case 2: return launch_cfg<128, 256, 2, 2, EPI, TAPS>(g, st);
+    case 3: return launch_cfg<256, 256, 2, 2, EPI, TAPS>(g, st);
+    case 4: return launch_cfg<256, 256, 2, 4, EPI, TAPS>(g, st);
+    case 5: return launch_lds<256, 256, 2, 4, EPI, TAPS>(g, st);
+    case 6: return launch_lds<256, 256, 2, 2, EPI, TAPS>(g, st);
+    case 7: return launch_lds<256, 128, 2, 2, EPI, TAPS>(g, st);
+    case 8: return launch_lds<128, 128, 2, 2, EPI, TAPS>(g, st);
+    case 9: return launch_lds<256, 256, 4, 2, EPI, TAPS>(g, st);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st) {
+int pick_cfg(const GemmArgs& g) {
+  // 256x256 tiles of 8 waves (64x128 per wave) with direct-to-LDS loads once there are enough rows to fill them
+  if (g.M >= 1024 && g.N >= 256) return 9;
+  return 8;
+}
+
+hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
   const bool taps = g.a_src != nullptr;
   switch (epi * 2 + (taps ? 1 : 0)) {
-    case EPI_BF16 * 2: return launch_epi<EPI_BF16, false>(g, st);
-    case EPI_BF16 * 2 + 1: return launch_epi<EPI_BF16, true>(g, st);
-    case EPI_GELU_BF16 * 2: return launch_epi<EPI_GELU_BF16, false>(g, st);
-    case EPI_GELU_BF16 * 2 + 1: return launch_epi<EPI_GELU_BF16, true>(g, st);
-    case EPI_RESID_F32 * 2: return launch_epi<EPI_RESID_F32, false>(g, st);
-    case EPI_RESID_F32 * 2 + 1: return launch_epi<EPI_RESID_F32, true>(g, st);
-    case EPI_F32 * 2: return launch_epi<EPI_F32, false>(g, st);
-    case EPI_F32 * 2 + 1: return launch_epi<EPI_F32, true>(g, st);
+    case EPI_BF16 * 2: return launch_epi<EPI_BF16, false>(g, cfg, st);
+    case EPI_BF16 * 2 + 1: return launch_epi<EPI_BF16, true>(g, cfg, st);
+    case EPI_GELU_BF16 * 2: return launch_epi<EPI_GELU_BF16, false>(g, cfg, st);
+    case EPI_GELU_BF16 * 2 + 1: return launch_epi<EPI_GELU_BF16, true>(g, cfg, st);
+    case EPI_RESID_F32 * 2: return launch_epi<EPI_RESID_F32, false>(g, cfg, st);
+    case EPI_RESID_F32 * 2 + 1: return launch_epi<EPI_RESID_F32, true>(g, cfg, st);
+    case EPI_F32 * 2: return launch_epi<EPI_F32, false>(g, cfg, st);
+    case EPI_F32 * 2 + 1: return launch_epi<EPI_F32, true>(g, cfg, st);
   }
   return hipErrorInvalidValue;
 }

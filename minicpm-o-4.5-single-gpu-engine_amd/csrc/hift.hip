@@ -29,6 +29,34 @@ __device__ __forceinline__ float pre_act(float v, int pre, float slope, float a,
   return v;
 }
 
+// epilogue of a 32-row x 32-channel MFMA block: this lane's output row and channels co + q*8 + (lane/32)*4 + e
+__device__ __forceinline__ void conv_epilogue(const ConvDesc& c, int b, int out_row, int co_base, int lane, const f32x16& acc) {
+  const size_t row = (size_t)c.out_off[b] + (size_t)out_row;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int co = co_base + q * 8 + (lane >> 5) * 4 + e;
+      if (co >= c.Cout) continue;
+      float v = __fadd_rn(acc[q * 4 + e], c.bias[co]);
+      float* yp = c.y + row * c.ldy + co;
+      switch (c.epi) {
+        case EPI_STORE: *yp = v; break;
+        case EPI_ELU: *yp = v > 0.f ? v : expm1f(v); break;
+        case EPI_RES: *yp = __fadd_rn(v, c.res[row * c.ldy + co]); break;
+        case EPI_ADD_RES: *yp = __fadd_rn(*yp, __fadd_rn(v, c.res[row * c.ldy + co])); break;
+        case EPI_RES_MEAN: {
+          v = __fadd_rn(v, c.res[row * c.ldy + co]);
+          float* sp = c.sum + row * c.ldy + co;
+          if (c.sum_mode == 0) *sp = v;
+          else if (c.sum_mode == 1) *sp = __fadd_rn(*sp, v);
+          else *sp = __fdiv_rn(__fadd_rn(*sp, v), (float)c.sum_div);
+        } break;
+      }
+    }
+  }
+}
+
 __global__ void __launch_bounds__(256) conv_f32_kernel(ConvDesc c) {
   __shared__ float xs[CBM * CLD];
   __shared__ float ws[CBN * CLD];
@@ -79,32 +107,111 @@ __global__ void __launch_bounds__(256) conv_f32_kernel(ConvDesc c) {
       __syncthreads();
     }
   }
-  // lane: output row r0 + wm*32 + lane%32, channels co0 + wn*32 + (q*8) + (lane/32)*4 + e
   const int r = r0 + wm * 32 + (lane & 31);
   if (r > r_hi) return;
-  const size_t row = (size_t)c.out_off[b] + (size_t)(r * c.s_out + oo);
+  conv_epilogue(c, b, r * c.s_out + oo, co0 + wn * 32, lane, acc);
+}
+
+
+// bf16-MFMA convolution (fp32 activations in HBM, bf16 operands, fp32 accumulation) for stride-1 convs and the
+// polyphase transposed convs.  For a tile of BM output rows the input rows of every tap form one slab of
+// BM + (taps - 1) |d| rows: per 64-channel chunk the slab is staged once in LDS (activation applied, rounded to bf16)
+// and each tap's A fragments are the slab rows shifted by its offset; the tap's 64 x 64 weight tile is double-buffered.
+constexpr int HB_BN = 64, HB_MAXSPAN = 64;
+
+__device__ __forceinline__ int hswz(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+
+template <int BM>
+__global__ void __launch_bounds__(256) conv_bf16_kernel(ConvDesc c, const bf16_t* __restrict__ wbf) {
+  constexpr int WAVES_M = 4, WTM = BM / WAVES_M, TM = WTM / 32;  // 4 waves along time, each all 64 channels
+  constexpr int SLAB = BM + HB_MAXSPAN;
+  extern __shared__ uint4 hl[];  // slab [SLAB][8 chunks] then 2 weight tiles [64][8 chunks]
+  uint4* slab = hl;
+  uint4* wt = hl + SLAB * 8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
+  const int Tin = c.in_len[b], Tout = c.out_len[b];
+  const int oo = c.off_out[ph];
+  const int r_lo = oo >= 0 ? 0 : (-oo + c.s_out - 1) / c.s_out;
+  const int r_hi = Tout - 1 - oo < 0 ? -1 : (Tout - 1 - oo) / c.s_out;
+  const int r0 = r_lo + blockIdx.x * BM;
+  if (r0 > r_hi) return;
+  const int co0 = blockIdx.y * HB_BN;
+  const float* xb = c.x + (size_t)c.in_off[b] * c.ldx;
+  // tap j reads input row r + j d + off: the slab starts at r0 + min_j(j d) + off
+  const int dmin = c.d_in < 0 ? (c.taps - 1) * c.d_in : 0;
+  const int slab0 = r0 + dmin + c.off_in[ph];
+  const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
+  const int srows = BM + span;
+  const int cin_pad = (c.Cin + 63) & ~63;
+  const bf16_t* wph = wbf + ((size_t)ph * ((c.Cout + 63) & ~63) + co0) * c.taps * cin_pad;
+
+  f32x16 acc[TM][2];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int co = co0 + wn * 32 + q * 8 + (lane >> 5) * 4 + e;
-      if (co >= c.Cout) continue;
-      float v = __fadd_rn(acc[q * 4 + e], c.bias[co]);
-      float* yp = c.y + row * c.ldy + co;
-      switch (c.epi) {
-        case EPI_STORE: *yp = v; break;
-        case EPI_ELU: *yp = v > 0.f ? v : expm1f(v); break;
-        case EPI_RES: *yp = __fadd_rn(v, c.res[row * c.ldy + co]); break;
-        case EPI_ADD_RES: *yp = __fadd_rn(*yp, __fadd_rn(v, c.res[row * c.ldy + co])); break;
-        case EPI_RES_MEAN: {
-          v = __fadd_rn(v, c.res[row * c.ldy + co]);
-          float* sp = c.sum + row * c.ldy + co;
-          if (c.sum_mode == 0) *sp = v;
-          else if (c.sum_mode == 1) *sp = __fadd_rn(*sp, v);
-          else *sp = __fdiv_rn(__fadd_rn(*sp, v), (float)c.sum_div);
-        } break;
-      }
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  auto load_w = [&](int j, int c0, int buf) {  // 64 channels x 64 ci of tap j: 512 chunks, 2 per thread
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int idx = tid + u * 256, co = idx >> 3, ch = idx & 7;
+      wt[buf * 512 + hswz(co, ch)] = *(const uint4*)(wph + ((size_t)co * c.taps + j) * cin_pad + c0 + ch * 8);
     }
+  };
+  for (int c0 = 0; c0 < c.Cin; c0 += 64) {
+    __syncthreads();
+    // slab: srows x 64 channels, 8 channels (one 16-byte chunk) per item
+    for (int idx = tid; idx < srows * 8; idx += 256) {
+      const int sr = idx >> 3, ch = idx & 7;
+      const int in_row = slab0 + sr;
+      float v[8];
+      const bool rok = in_row >= 0 && in_row < Tin;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int ci = c0 + ch * 8 + e;
+        float x = 0.f;
+        if (rok && ci < c.Cin) {
+          x = xb[(size_t)in_row * c.ldx + ci];
+          if (c.pre) x = pre_act(x, c.pre, c.slope, c.alpha ? c.alpha[ci] : 0.f, c.inv ? c.inv[ci] : 0.f);
+        }
+        v[e] = x;
+      }
+      slab[hswz(sr, ch)] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+    }
+    load_w(0, c0, 0);
+    __syncthreads();
+    for (int j = 0; j < c.taps; ++j) {
+      const int buf = j & 1;
+      if (j + 1 < c.taps) load_w(j + 1, c0, buf ^ 1);
+      const int shift = j * c.d_in - dmin;  // slab row of output row r0 + i for this tap: i + shift
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int chunk = kk * 2 + (lane >> 5);
+        bf16x8 af[TM], wf[2];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int srow = wave * WTM + i * 32 + (lane & 31) + shift;
+          af[i] = as_bf16x8(slab[hswz(srow, chunk)]);
+        }
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) wf[jj] = as_bf16x8(wt[buf * 512 + hswz(jj * 32 + (lane & 31), chunk)]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[jj], af[i], acc[i][jj], 0, 0, 0);
+      }
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int r = r0 + wave * WTM + i * 32 + (lane & 31);
+    if (r > r_hi) continue;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) conv_epilogue(c, b, r * c.s_out + oo, co0 + jj * 32, lane, acc[i][jj]);
   }
 }
 
@@ -266,6 +373,24 @@ hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
   if (c.n_phase < 1 || c.n_phase > 8) return hipErrorInvalidValue;
   dim3 grid(cdiv(max_rows, CBM), cdiv(c.Cout, CBN), c.n_items * c.n_phase);
   hipLaunchKernelGGL(conv_f32_kernel, grid, dim3(256), 0, st, c);
+  return hipGetLastError();
+}
+
+hipError_t conv_bf16(const ConvDesc& c, const bf16_t* wbf, int max_rows, hipStream_t st) {
+  if (c.n_items <= 0 || max_rows <= 0) return hipSuccess;
+  if (c.n_phase < 1 || c.n_phase > 8 || c.s_in != 1) return hipErrorInvalidValue;
+  const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
+  if (span > HB_MAXSPAN) return hipErrorInvalidValue;
+  constexpr int BM = 128;
+  const size_t lds = ((size_t)(BM + HB_MAXSPAN) * 8 + 2 * 512) * sizeof(uint4);
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)conv_bf16_kernel<BM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  dim3 grid(cdiv(max_rows, BM), cdiv(c.Cout, HB_BN), c.n_items * c.n_phase);
+  hipLaunchKernelGGL(conv_bf16_kernel<BM>, grid, dim3(256), lds, st, c, wbf);
   return hipGetLastError();
 }
 

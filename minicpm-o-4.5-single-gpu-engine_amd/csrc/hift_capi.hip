@@ -99,6 +99,7 @@ size_t carve(const t2w_hift* h, const Lens& L, char* base, Bufs* b) {
 
 struct Ctx {
   const t2w_hift* h;
+  bool bf16;
   const int* plan;  // device: [class][off | len][n]
   int n;
   Lens L;
@@ -113,7 +114,7 @@ ConvDesc conv_desc(const Ctx& x, const t2w_conv& w, const float* in, int Cin, in
   ConvDesc c{};
   c.x = in; c.ldx = Cin; c.in_off = x.off(in_cls); c.in_len = x.len(in_cls);
   c.y = out; c.ldy = Cout; c.out_off = x.off(out_cls); c.out_len = x.len(out_cls);
-  c.w = w.w; c.bias = w.b; c.Cin = Cin; c.Cout = Cout; c.taps = k;
+  c.w = w.w; c.wbf = (const uint16_t*)w.wbf; c.bias = w.b; c.Cin = Cin; c.Cout = Cout; c.taps = k;
   c.s_in = s; c.d_in = dil; c.s_out = 1; c.n_phase = 1; c.off_in[0] = -p; c.off_out[0] = 0;
   c.pre = PRE_NONE; c.epi = EPI_STORE; c.n_items = x.n;
   return c;
@@ -121,7 +122,11 @@ ConvDesc conv_desc(const Ctx& x, const t2w_conv& w, const float* in, int Cin, in
 
 int run(const Ctx& x, const ConvDesc& c, int out_cls, const char* what) {
   const int mr = x.L.mx[out_cls] / c.s_out + 2;
-  H_CHECK(conv_f32(c, mr, x.st), what);
+  const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
+  if (x.bf16 && c.wbf && c.s_in == 1 && span <= 64)
+    H_CHECK(conv_bf16(c, c.wbf, mr, x.st), what);
+  else
+    H_CHECK(conv_f32(c, mr, x.st), what);
   return 0;
 }
 
@@ -204,10 +209,10 @@ size_t t2w_hift_workspace_bytes(const t2w_hift* h, int n, const int* frames) {
 
 int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* plan_dev, const float* mel, const float* noise,
                      const float* cache_source, int S, const float* f0_override, const float* source_override, float* speech,
-                     float* source, float* f0_out, void* workspace, size_t workspace_bytes, void* stream) {
+                     float* source, float* f0_out, void* workspace, size_t workspace_bytes, int decode_bf16, void* stream) {
   if (!h || n <= 0 || !frames || !plan_dev || !mel || !speech || !source) return t2w::set_error("bad hift arguments", hipSuccess);
   const t2w_hift_dims& d = h->d;
-  Ctx x{h, plan_dev, n, lens_of(d, n, frames), (hipStream_t)stream};
+  Ctx x{h, decode_bf16 != 0, plan_dev, n, lens_of(d, n, frames), (hipStream_t)stream};
   for (int i = 0; i < n; ++i)
     if (S > class_len(d, C_SMP, frames[i])) return t2w::set_error("source cache longer than a row", hipSuccess);
   if (S > 0 && !cache_source) return t2w::set_error("missing source cache", hipSuccess);
@@ -226,6 +231,7 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
       float* o = (l & 1) ? B.f0b : B.f0a;
       ConvDesc c = conv_desc(x, w.f0[l], cur, cin, C_T, o, d.f0_channels, C_T, 3, 1, 1, 1);
       c.epi = EPI_ELU;
+      c.wbf = nullptr;  // the f0 predictor stays fp32: its rounding integrates into the source phase
       if (run(x, c, C_T, "f0 conv")) return 1;
       cur = o;
       cin = d.f0_channels;
@@ -269,11 +275,11 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
       c.y = B.XN; c.ldy = cout;
       c.out_off = x.off(i == 2 ? C_S2P : cls);
       c.out_len = x.len(i == 2 ? C_S2P : cls);
-      c.w = w.ups[i].w; c.bias = w.ups[i].b; c.Cin = cin; c.Cout = cout; c.taps = (k + u - 1) / u;
+      c.w = w.ups[i].w; c.wbf = (const uint16_t*)w.ups[i].wbf; c.bias = w.ups[i].b; c.Cin = cin; c.Cout = cout; c.taps = (k + u - 1) / u;
       c.s_in = 1; c.d_in = -1; c.s_out = u; c.n_phase = u;
       for (int ph = 0; ph < u; ++ph) { c.off_in[ph] = 0; c.off_out[ph] = ph - p; }
       c.pre = PRE_LEAKY; c.slope = d.lrelu_slope; c.epi = EPI_STORE; c.n_items = n;
-      H_CHECK(conv_f32(c, x.L.mx[i == 2 ? C_S2P : cls] / u + 2, x.st), "ups");
+      if (run(x, c, i == 2 ? C_S2P : cls, "ups")) return 1;
       if (i == 2) H_CHECK(reflect_rows(B.XN, cout, x.off(C_S2), n, x.st), "reflection pad");
     }
     {  // source branch: downsampling conv of the source STFT, a ResBlock, added into the stage input

@@ -16,6 +16,7 @@ struct ConvDesc {
   float* y; int ldy;
   const int* out_off; const int* out_len;
   const float* w; const float* bias;  // w [n_phase, Cout, taps, Cin]
+  const uint16_t* wbf;                // bf16 weights for conv_bf16 (or null)
   int Cin, Cout, taps;
   int s_in, d_in, s_out;
   int n_phase;
@@ -26,6 +27,8 @@ struct ConvDesc {
 };
 
 hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st);
+// stride-1 / polyphase convs on bf16 MFMA; wbf: bf16 weights [n_phase, Cout padded to 64, taps, Cin padded to 64]
+hipError_t conv_bf16(const ConvDesc& c, const uint16_t* wbf, int max_rows, hipStream_t st);
 hipError_t f0_head(const float* x, int C, const float* w, const float* b, float* f0, int rows, hipStream_t st);
 hipError_t nsf_phase(const float* f0, const int* fr_off, const int* fr_len, int n_items, int harm, float sr, float scale, float* phase,
                      hipStream_t st);

@@ -24,7 +24,7 @@ struct GemmArgs {
   int M, N, K;         // K % 64 == 0
 };
 
-hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st);
+hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg = -1);  // cfg < 0: by shape
 
 // Per-token row kernels of the DiT block (H = hidden, one wave per token).
 hipError_t ln_mod(const float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H,

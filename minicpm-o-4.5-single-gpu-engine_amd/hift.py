@@ -24,8 +24,10 @@ def chunk_noise_seed(noise_seed: int, chunk: int) -> int:
 
 
 class HiFTModel:
-    def __init__(self, W: dict, cfg: HiFTConfig = HiFTConfig(), device: str = "cuda"):
+    def __init__(self, W: dict, cfg: HiFTConfig = HiFTConfig(), device: str = "cuda", decode_bf16: bool = False):
+        """``decode_bf16``: the decoder convs on bf16 MFMA (fp32 activations); f0 predictor and source stay fp32."""
         self.cfg, self.device = cfg, device
+        self.decode_bf16 = decode_bf16
         f32 = lambda t: t.to(device=device, dtype=torch.float32).contiguous()  # noqa: E731
         self._keep = []
 
@@ -34,8 +36,17 @@ class HiFTModel:
             self._keep.append(t)
             return t.data_ptr()
 
-        def conv(name):
-            return _lib.Conv(keep(W[name + ".weight"].permute(0, 2, 1)), keep(W[name + ".bias"]))
+        def keep_bf(w):  # [phases, Cout, taps, Cin] -> bf16, Cout and Cin zero-padded to multiples of 64
+            ph, co, tp, ci = w.shape
+            pad = torch.zeros(ph, -(-co // 64) * 64, tp, -(-ci // 64) * 64)
+            pad[:, :co, :, :ci] = w
+            t = pad.to(device=device, dtype=torch.bfloat16).contiguous()
+            self._keep.append(t)
+            return t.data_ptr()
+
+        def conv(name, bf=True):
+            w = W[name + ".weight"].permute(0, 2, 1).contiguous()  # [Cout, taps, Cin]
+            return _lib.Conv(keep(w), keep(W[name + ".bias"]), keep_bf(w[None]) if bf else None)
 
         def conv_t(name, u):
             w = W[name + ".weight"]  # [Cin, Cout, k]
@@ -47,7 +58,7 @@ class HiFTModel:
                     j = ph + m * u
                     if j < k:
                         wp[ph, :, m, :] = w[:, :, j].t()
-            return _lib.Conv(keep(wp), keep(W[name + ".bias"]))
+            return _lib.Conv(keep(wp), keep(W[name + ".bias"]), keep_bf(wp))
 
         def resblock(p):
             rb = _lib.ResBlock()
@@ -62,7 +73,7 @@ class HiFTModel:
 
         hw = _lib.HiftWeights()
         for i in range(cfg.f0_layers):
-            hw.f0[i] = conv(f"f0_predictor.condnet.{2 * i}")
+            hw.f0[i] = conv(f"f0_predictor.condnet.{2 * i}", bf=False)
         hw.f0_head_w = keep(W["f0_predictor.classifier.weight"][0])
         hw.f0_head_b = keep(W["f0_predictor.classifier.bias"])
         hw.src_w = keep(W["m_source.l_linear.weight"][0])
@@ -70,7 +81,7 @@ class HiFTModel:
         hw.conv_pre = conv("conv_pre")
         for i, u in enumerate(cfg.up_rates):
             hw.ups[i] = conv_t(f"ups.{i}", u)
-            hw.src_down[i] = conv(f"source_downs.{i}")
+            hw.src_down[i] = conv(f"source_downs.{i}", bf=False)
             hw.src_res[i] = resblock(f"source_resblocks.{i}")
         for i in range(9):
             hw.res[i] = resblock(f"resblocks.{i}")
@@ -131,7 +142,7 @@ class HiFTModel:
         cs = cache_source.contiguous().float() if (cache_source is not None and S > 0) else None
         _lib.check(L.t2w_hift_forward(self.handle, n, fr, plan_dev.data_ptr(), mel_tm.data_ptr(), noise_tm.data_ptr(), _lib.ptr(cs), S,
                                       _lib.ptr(f0_override), _lib.ptr(source_override), speech.data_ptr(), source.data_ptr(), _lib.ptr(f0),
-                                      ws.data_ptr(), ws.numel(), _lib.stream_handle()), "hift_forward")
+                                      ws.data_ptr(), ws.numel(), int(self.decode_bf16), _lib.stream_handle()), "hift_forward")
         return speech, source, f0
 
     @torch.inference_mode()

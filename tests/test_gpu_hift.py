@@ -86,3 +86,32 @@ def test_forward_noise_end_to_end_with_cache(dev, case):
     print("end-to-end speech rel-L2", e_sp, "source rel-L2", e_src)
     assert torch.equal(src[:, :, :3840].cpu(), cs)
     assert e_sp < 1e-2 and e_src < 1e-2
+
+
+def test_decoder_bf16_given_source(dev, case):
+    """The bf16-MFMA decoder (fp32 activations and accumulation) against the strict-fp32 oracle on the oracle's source:
+    the reference's reduced-precision HiFT bound, waveform rel-L2 <= 1e-2 (``tests/engine/test_hift_tf32.py:227``)."""
+    W, h, gm, mels, noise = case
+    gb = HiFTModel(W, HiFTConfig(), decode_bf16=True)
+    mel_tm, noise_tm = _packed(mels, noise)
+    srcs = [oh.source(h, m, torch.zeros(1, 1, 0), ri, nz) for m, (ri, nz) in zip(mels, noise)]
+    s_tm = torch.cat([s[0, 0] for s in srcs]).cuda()
+    sp, _, _ = gb.forward_packed(LENS, mel_tm, noise_tm, None, 0, source_override=s_tm)
+    ref = torch.cat([oh.decode(h, m, s)[0] for m, s in zip(mels, srcs)])
+    e = rel(sp.cpu(), ref)
+    print("bf16 decoder rel-L2 (oracle source)", e)
+    assert e < 1e-2
+
+
+def test_forward_bf16_end_to_end(dev, case):
+    W, h, gm, mels, noise = case
+    gb = HiFTModel(W, HiFTConfig(), decode_bf16=True)
+    g = torch.Generator().manual_seed(9)
+    mel = torch.randn(2, 80, 58, generator=g) * 2 - 5
+    cs = torch.randn(2, 1, 3840, generator=g) * 0.01
+    ri, nz = oh.hift_noise(9, [5, 6], 58 * 480)
+    sp, src = gb.forward_noise(mel.cuda(), cs.cuda(), ri.cuda(), nz.cuda())
+    rsp, rsrc = oh.forward_noise(h, mel, cs, ri, nz)
+    e = rel(sp.cpu(), rsp)
+    print("bf16 end-to-end speech rel-L2", e, "source", rel(src.cpu(), rsrc))
+    assert e < 1e-2
