@@ -7,7 +7,8 @@
 // earlier chunks (the chunk-causal mask of whole-sequence solves); cached frames are always visible.
 //
 // CDNA4 mapping: a workgroup of two waves owns 64 queries of one head; each wave 32 of them.  Keys come in tiles of
-// 32, gathered by slot id with 16-byte loads into registers one tile ahead, then stored to LDS: K row-major with the
+// 64 (two 32-key MFMA halves per barrier), gathered by slot id with 16-byte loads into registers one tile ahead (the
+// slot ids themselves two tiles ahead, so the dependent id -> key load chain is hidden), then stored to LDS: K row-major with the
 // 16-byte chunks XOR-swizzled by key, V transposed (d-major) with its keys permuted so that the probabilities the
 // score MFMA leaves in a lane are exactly the K-slice the P.V MFMA wants from that lane.  Scores are computed
 // transposed, S^T = K . Q^T (v_mfma_f32_32x32x16_bf16, the wave's Q fragment stays in registers), so each lane holds
@@ -25,8 +26,8 @@ constexpr float NEG = -1.0e30f;
 __device__ __forceinline__ int vpos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
 __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
-  __shared__ uint4 ks[2][32 * 8];   // [key][16-byte chunk ^ (key & 7)]
-  __shared__ uint4 vt[2][64 * 4];   // [d][16-byte chunk ^ ((d >> 1) & 3)] of 32 permuted keys
+  __shared__ uint4 ks[2][64 * 8];      // [key][16-byte chunk ^ (key & 7)], 64 keys
+  __shared__ uint4 vt[2][2][64 * 4];   // per 32-key half: [d][16-byte chunk ^ ((d >> 1) & 3)] of permuted keys
   const int tile = blockIdx.x, head = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = a.tiles[2 * tile];
@@ -51,44 +52,52 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
     for (int kk = 0; kk < 4; ++kk) qf[kk] = as_bf16x8(*(const uint4*)(qp + kk * 16));
   }
 
-  // key tiles: new keys [0, lim_max) then cached keys [T, kvlen), 32 at a time
-  const int n1 = (lim_max + 31) / 32, n2 = (kvlen - T + 31) / 32;
+  // key tiles of 64: new keys [0, lim_max), then cached keys [T, kvlen)
+  const int n1 = (lim_max + 63) / 64, n2 = (kvlen - T + 63) / 64;
   const int ntiles = n1 + n2;
-  // loader role: key lk = tid / 4 of the tile, 16-byte chunks 2 (tid % 4) and 2 (tid % 4) + 1 of its K and V rows
-  const int lk = tid >> 2, lc = (tid & 3) * 2;
-  uint4 rk[2], rv[2];
-  auto tile_base = [&](int t, int& kb, int& ke) {
-    if (t < n1) { kb = t * 32; ke = lim_max; }
-    else { kb = T + (t - n1) * 32; ke = kvlen; }
-  };
-  auto gload = [&](int t) {
-    int kb, ke;
-    tile_base(t, kb, ke);
-    const int k = kb + lk < ke ? kb + lk : kb;
-    const size_t slot = (size_t)a.kv_idx[kvoff + k];
-    const bf16_t* kp = a.k_pool + slot * H + head * 64 + lc * 8;
-    const bf16_t* vp = a.v_pool + slot * H + head * 64 + lc * 8;
-    rk[0] = *(const uint4*)kp;
-    rk[1] = *(const uint4*)(kp + 8);
-    rv[0] = *(const uint4*)vp;
-    rv[1] = *(const uint4*)(vp + 8);
-  };
-  auto lstore = [&](int s) {
-    ks[s][lk * 8 + ((lc) ^ (lk & 7))] = rk[0];
-    ks[s][lk * 8 + ((lc + 1) ^ (lk & 7))] = rk[1];
-    bf16_t* vb = (bf16_t*)vt[s];
-    const int p = vpos(lk);
+  // loader role: key lk of the tile, 16-byte chunks lc .. lc + 3 of its K and V rows
+  const int lk = tid >> 1, lc = (tid & 1) * 4;
+#define T2W_TILE_RANGE(t, kb, ke)                 \
+  if ((t) < n1) { kb = (t) * 64; ke = lim_max; }  \
+  else { kb = T + ((t) - n1) * 64; ke = kvlen; }
+#define T2W_SLOT_OF(t, out)                                   \
+  {                                                           \
+    int kb_, ke_;                                             \
+    T2W_TILE_RANGE(t, kb_, ke_)                               \
+    out = a.kv_idx[kvoff + (kb_ + lk < ke_ ? kb_ + lk : kb_)]; \
+  }
+  uint4 rk0, rk1, rk2, rk3, rv0, rv1, rv2, rv3;
+#define T2W_GLOAD(slot)                                                                 \
+  {                                                                                     \
+    const uint4* kp = (const uint4*)(a.k_pool + (size_t)(slot) * H + head * 64 + lc * 8); \
+    const uint4* vp = (const uint4*)(a.v_pool + (size_t)(slot) * H + head * 64 + lc * 8); \
+    rk0 = kp[0]; rk1 = kp[1]; rk2 = kp[2]; rk3 = kp[3];                                 \
+    rv0 = vp[0]; rv1 = vp[1]; rv2 = vp[2]; rv3 = vp[3];                                 \
+  }
+  const int vp_ = vpos(lk & 31);
+  auto vstore = [](bf16_t* vb, int p, int dbase, uint4 v) {  // 8 consecutive d of one key into the transposed tile
+    const uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
+    const uint32_t ws[4] = {w0, w1, w2, w3};
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const uint32_t w[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = (lc + u) * 8 + e;
-        const bf16_t val = (bf16_t)((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffff));
-        vb[d * 32 + (((p >> 3) ^ ((d >> 1) & 3)) << 3) + (p & 7)] = val;
-      }
+    for (int e = 0; e < 8; ++e) {
+      const int d = dbase + e;
+      const uint32_t wv = ws[e >> 1];
+      vb[d * 32 + (((p >> 3) ^ ((d >> 1) & 3)) << 3) + (p & 7)] = (bf16_t)((e & 1) ? (wv >> 16) : (wv & 0xffff));
     }
   };
+#define T2W_LSTORE(s)                                            \
+  {                                                              \
+    uint4* kr = ks[s] + lk * 8;                                  \
+    kr[(lc + 0) ^ (lk & 7)] = rk0;                               \
+    kr[(lc + 1) ^ (lk & 7)] = rk1;                               \
+    kr[(lc + 2) ^ (lk & 7)] = rk2;                               \
+    kr[(lc + 3) ^ (lk & 7)] = rk3;                               \
+    bf16_t* vb = (bf16_t*)vt[s][lk >> 5];                        \
+    vstore(vb, vp_, (lc + 0) * 8, rv0);                          \
+    vstore(vb, vp_, (lc + 1) * 8, rv1);                          \
+    vstore(vb, vp_, (lc + 2) * 8, rv2);                          \
+    vstore(vb, vp_, (lc + 3) * 8, rv3);                          \
+  }
 
   f32x16 o0, o1;
 #pragma unroll
@@ -96,67 +105,86 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
   float m = NEG, l = 0.f;
   const float sl2 = a.scale * 1.4426950408889634f;
 
+  int slot_next = 0;
   if (ntiles > 0) {
-    gload(0);
-    lstore(0);
+    int s0;
+    T2W_SLOT_OF(0, s0)
+    T2W_GLOAD(s0)
+    if (ntiles > 1) T2W_SLOT_OF(1, slot_next)
+    T2W_LSTORE(0)
   }
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const int s = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
+    if (t + 1 < ntiles) T2W_GLOAD(slot_next)
+    if (t + 2 < ntiles) T2W_SLOT_OF(t + 2, slot_next)
     if (active) {
       int kb, ke;
-      tile_base(t, kb, ke);
+      T2W_TILE_RANGE(t, kb, ke)
       const bool cached = t >= n1;
-      f32x16 sc;
+      // visible new keys of this query end at lim_me; cached keys at ke
+      const int lim = cached ? ke : min(ke, lim_me);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+      for (int sub = 0; sub < 2; ++sub) {
+        const int sb = kb + sub * 32;
+        if (sb < ke) {
+          f32x16 sc;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int chunk = kk * 2 + half;
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ks[s][col * 8 + (chunk ^ (col & 7))]), qf[kk], sc, 0, 0, 0);
-      }
-      // lane holds query col, keys kb + (r/4)*8 + half*4 + r%4
-      float mx = NEG;
-      bool vis[16];
+          for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+          const int krow = sub * 32 + col;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb + (r >> 2) * 8 + half * 4 + (r & 3);
-        vis[r] = key < ke && (cached || key < lim_me);
-        sc[r] = vis[r] ? sc[r] * sl2 : NEG;
-        mx = fmaxf(mx, sc[r]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mn = fmaxf(m, mx);
-      const float alpha = exp2f(m - mn);
-      float rs = 0.f;
-      float p[16];
+          for (int kk = 0; kk < 4; ++kk) {
+            const int chunk = kk * 2 + half;
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ks[s][krow * 8 + (chunk ^ (krow & 7))]), qf[kk], sc, 0, 0, 0);
+          }
+          // lane holds query col, keys sb + (r/4)*8 + half*4 + r%4; invisible keys score NEG
+          const int nvis = lim - (sb + half * 4);  // key offsets below nvis (relative to sb + half*4) are visible
+          float mx = NEG;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        p[r] = vis[r] ? exp2f(sc[r] - mn) : 0.f;
-        rs += p[r];
-      }
-      rs += __shfl_xor(rs, 32, 64);
-      l = l * alpha + rs;
-      m = mn;
+          for (int r = 0; r < 16; ++r) {
+            const int off = (r >> 2) * 8 + (r & 3);
+            sc[r] = off < nvis ? sc[r] * sl2 : NEG;
+            mx = fmaxf(mx, sc[r]);
+          }
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          const float mn = fmaxf(m, mx);
+          const float alpha = __builtin_amdgcn_exp2f(m - mn);
+          // a query whose keys are all invisible so far keeps m = NEG; its probabilities must stay 0
+          const float live = mn > 0.5f * NEG ? 1.0f : 0.0f;
+          float rs = 0.f;
+          float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) { o0[r] *= alpha; o1[r] *= alpha; }
+          for (int r = 0; r < 16; ++r) {
+            p[r] = __builtin_amdgcn_exp2f(sc[r] - mn) * live;
+            rs += p[r];
+          }
+          rs += __shfl_xor(rs, 32, 64);
+          l = l * alpha + rs;
+          m = mn;
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        union { uint4 u; bf16x8 b; } pf;
-        pf.u = make_uint4(pack2(p[8 * hh], p[8 * hh + 1]), pack2(p[8 * hh + 2], p[8 * hh + 3]), pack2(p[8 * hh + 4], p[8 * hh + 5]),
-                          pack2(p[8 * hh + 6], p[8 * hh + 7]));
-        const int chunk = hh * 2 + half;
-        const int d0 = col, d1 = 32 + col;
-        const uint4 v0 = vt[s][d0 * 4 + (chunk ^ ((d0 >> 1) & 3))];
-        const uint4 v1 = vt[s][d1 * 4 + (chunk ^ ((d1 >> 1) & 3))];
-        o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v0), pf.b, o0, 0, 0, 0);
-        o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v1), pf.b, o1, 0, 0, 0);
+          for (int r = 0; r < 16; ++r) { o0[r] *= alpha; o1[r] *= alpha; }
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            union { uint4 u; bf16x8 b; } pf;
+            pf.u = make_uint4(pack2(p[8 * hh], p[8 * hh + 1]), pack2(p[8 * hh + 2], p[8 * hh + 3]), pack2(p[8 * hh + 4], p[8 * hh + 5]),
+                              pack2(p[8 * hh + 6], p[8 * hh + 7]));
+            const int chunk = hh * 2 + half;
+            const int d0 = col, d1 = 32 + col;
+            const uint4 v0 = vt[s][sub][d0 * 4 + (chunk ^ ((d0 >> 1) & 3))];
+            const uint4 v1 = vt[s][sub][d1 * 4 + (chunk ^ ((d1 >> 1) & 3))];
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v0), pf.b, o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v1), pf.b, o1, 0, 0, 0);
+          }
+        }
       }
     }
-    if (t + 1 < ntiles) lstore(s ^ 1);
+    if (t + 1 < ntiles) T2W_LSTORE(s ^ 1)
     __syncthreads();
   }
+#undef T2W_TILE_RANGE
+#undef T2W_SLOT_OF
+#undef T2W_GLOAD
+#undef T2W_LSTORE
   if (!active || myq >= T) return;
   const float inv = 1.0f / l;
   bf16_t* op = a.out + (size_t)(start + myq) * H + head * 64;

@@ -265,7 +265,7 @@ int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, 
   if (K % 64) return fail("K must be a multiple of 64");
   if (epi < 0 || epi > 3) return fail("bad epilogue");
   if (a_src && (K % lda)) return fail("taps mode: K must be a multiple of lda");
-  if (tile > 9) return fail("bad tile configuration");
+  if (tile > 13) return fail("bad tile configuration");
   T2W_CHECK(gemm_bf16(gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K), epi, (hipStream_t)stream, tile), "gemm");
   return 0;
 }

@@ -20,7 +20,11 @@ namespace {
 
 constexpr int BK = 64;  // K values per stage (128 bytes of bf16 per tile row)
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+// 16-byte chunk c of tile row `row` lives at chunk c ^ ((row >> 1) & 7) of that row: 16 consecutive rows reading the same
+// chunk (a 16-lane LDS phase of a fragment read) then cover all 64 banks, and 8 consecutive lanes writing one row stay
+// within it.
+__device__ __forceinline__ int swz_key(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ swz_key(row)); }
 
 template <int EPI>
 __device__ __forceinline__ void epilogue4(const GemmArgs& g, int m, int n, float (&v)[4]) {
@@ -209,19 +213,23 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_lds_kernel(GemmArgs g) {
   const int mt = b / gn, nt = b % gn;
   const int m0 = mt * BM, n0 = nt * BN;
 
-  // this lane's source chunk in each of its waves' 1 KB blocks: block row l/8, logical chunk (l%8) ^ (row & 7)
-  const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+  // this lane's source chunk in each of its waves' 1 KB blocks: tile row blk*8 + l/8, logical chunk (l%8) ^ swz_key(row)
+  const int lrow = lane >> 3;
   const bf16_t* asrc[APW];
   const bf16_t* bsrc[BPW];
 #pragma unroll
   for (int p = 0; p < APW; ++p) {
-    int m = m0 + (wave + p * NW) * 8 + lrow;
+    const int trow = (wave + p * NW) * 8 + lrow;
+    const int lchunk = (lane & 7) ^ swz_key(trow);
+    int m = m0 + trow;
     m = m < g.M ? m : g.M - 1;
     asrc[p] = TAPS ? g.A + (size_t)g.a_src[m] * g.lda + lchunk * 8 : g.A + (size_t)m * g.lda + lchunk * 8;
   }
 #pragma unroll
   for (int p = 0; p < BPW; ++p) {
-    int n = n0 + (wave + p * NW) * 8 + lrow;
+    const int trow = (wave + p * NW) * 8 + lrow;
+    const int lchunk = (lane & 7) ^ swz_key(trow);
+    int n = n0 + trow;
     n = n < g.N ? n : g.N - 1;
     bsrc[p] = g.B + (size_t)n * g.ldb + lchunk * 8;
   }
@@ -305,6 +313,137 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_lds_kernel(GemmArgs g) {
   }
 }
 
+// Deep-pipelined direct-to-LDS variant: K stages of 32 (64-byte tile rows, 16-byte chunk c of row r at chunk
+// c ^ ((r >> 2) & 3): 16 consecutive rows reading one chunk cover all 64 banks), an NS-deep LDS ring with the loads of
+// stage kt + NS - 1 issued while stage kt computes, and a wait that only requires stage kt's own loads to have landed.
+__device__ __forceinline__ int swz32(int row, int chunk) { return row * 4 + (chunk ^ ((row >> 2) & 3)); }
+
+template <int LPT, int NS>
+__device__ __forceinline__ void wait_stage(bool tail) {
+  // outstanding loads are the stages after this one; vmcnt counts per-thread vector memory instructions in issue order
+  if (tail) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    constexpr int N = (NS - 2) * LPT;
+    static_assert(N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int EPI, bool TAPS>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_pipe_kernel(GemmArgs g) {
+  constexpr int BKP = 32;
+  constexpr int NT = 64 * WM * WN, NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int STAGE = (BM + BN) * 4;          // uint4 per stage
+  constexpr int ABLK = BM / 16, BBLK = BN / 16;  // 1 KB blocks (16 rows of 64 bytes)
+  constexpr int APW = ABLK / NW, BPW = BBLK / NW;
+  constexpr int LPT = APW + BPW;
+  static_assert(APW * NW == ABLK && BPW * NW == BBLK, "blocks / waves mismatch");
+  extern __shared__ uint4 lds_dyn[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
+  const int nblk = gm * gn;
+  int b = blockIdx.x;
+  const int full = (nblk / 8) * 8;
+  if (b < full) b = (b % 8) * (nblk / 8) + b / 8;
+  const int mt = b / gn, nt = b % gn;
+  const int m0 = mt * BM, n0 = nt * BN;
+
+  const int lrow = lane >> 2;  // row of the lane's chunk inside its 1 KB block (16 rows x 4 chunks)
+  const bf16_t* asrc[APW];
+  const bf16_t* bsrc[BPW];
+#pragma unroll
+  for (int p = 0; p < APW; ++p) {
+    const int trow = (wave + p * NW) * 16 + lrow;
+    const int lchunk = (lane & 3) ^ ((trow >> 2) & 3);
+    int m = m0 + trow;
+    m = m < g.M ? m : g.M - 1;
+    asrc[p] = TAPS ? g.A + (size_t)g.a_src[m] * g.lda + lchunk * 8 : g.A + (size_t)m * g.lda + lchunk * 8;
+  }
+#pragma unroll
+  for (int p = 0; p < BPW; ++p) {
+    const int trow = (wave + p * NW) * 16 + lrow;
+    const int lchunk = (lane & 3) ^ ((trow >> 2) & 3);
+    int n = n0 + trow;
+    n = n < g.N ? n : g.N - 1;
+    bsrc[p] = g.B + (size_t)n * g.ldb + lchunk * 8;
+  }
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  const int KT = g.K / BKP;
+#define T2W_ISSUE(kt_)                                                                                                          \
+  {                                                                                                                             \
+    const int k0 = (kt_) * BKP;                                                                                                 \
+    const int s_ = (kt_) % NS;                                                                                                  \
+    size_t aoff;                                                                                                                \
+    if (TAPS) {                                                                                                                 \
+      const int tap = k0 / g.tapC;                                                                                              \
+      aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);                                                                         \
+    } else {                                                                                                                    \
+      aoff = k0;                                                                                                                \
+    }                                                                                                                           \
+    _Pragma("unroll") for (int p = 0; p < APW; ++p) __builtin_amdgcn_global_load_lds(                                           \
+        (const void*)(asrc[p] + aoff), (lds_ptr_t)(lds_dyn + s_ * STAGE + (wave + p * NW) * 64), 16, 0, 0);                      \
+    _Pragma("unroll") for (int p = 0; p < BPW; ++p) __builtin_amdgcn_global_load_lds(                                           \
+        (const void*)(bsrc[p] + k0), (lds_ptr_t)(lds_dyn + s_ * STAGE + BM * 4 + (wave + p * NW) * 64), 16, 0, 0);               \
+  }
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p)
+    if (p < KT) T2W_ISSUE(p)
+  for (int kt = 0; kt < KT; ++kt) {
+    wait_stage<LPT, NS>(kt + NS - 2 >= KT);
+    __syncthreads();  // stage kt landed for every thread; stage kt - 1 (about to be refilled) is no longer read
+    if (kt + NS - 1 < KT) T2W_ISSUE(kt + NS - 1)
+    const uint4* L = lds_dyn + (kt % NS) * STAGE;
+    bf16x8 af[2][TM], bfr[2][TN];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int chunk = kk * 2 + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[kk][i] = as_bf16x8(L[swz32(wm * WTM + i * 32 + (lane & 31), chunk)]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bfr[kk][j] = as_bf16x8(L[BM * 4 + swz32(wn * WTN + j * 32 + (lane & 31), chunk)]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[kk][j], af[kk][i], acc[i][j], 0, 0, 0);
+  }
+#undef T2W_ISSUE
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * WTM + i * 32 + (lane & 31);
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * WTN + j * 32 + q * 8 + (lane >> 5) * 4;
+        if (n >= g.N) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
+        epilogue4<EPI>(g, m, n, v);
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
 hipError_t launch_cfg(const GemmArgs& g, hipStream_t st) {
   const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
@@ -335,6 +474,21 @@ hipError_t launch_lds(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int BM, int BN, int WM, int WN, int NS, int EPI, bool TAPS>
+hipError_t launch_pipe(const GemmArgs& g, hipStream_t st) {
+  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
+  const size_t lds = (size_t)NS * (BM + BN) * 4 * sizeof(uint4);
+  auto kern = gemm_pipe_kernel<BM, BN, WM, WN, NS, EPI, TAPS>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(gm * gn), dim3(64 * WM * WN), lds, st, g);
+  return hipGetLastError();
+}
+
 // tile configurations: 0 = 128x128 (4 waves of 64x64), 1 = 256x128 (4 waves of 128x64), 2 = 128x256 (4 waves of 64x128),
 // 3 = 256x256 (4 waves of 128x128), 4 = 256x256 (8 waves of 128x64)
 template <int EPI, bool TAPS>
@@ -351,6 +505,10 @@ hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
     case 7: return launch_lds<256, 128, 2, 2, EPI, TAPS>(g, st);
     case 8: return launch_lds<128, 128, 2, 2, EPI, TAPS>(g, st);
     case 9: return launch_lds<256, 256, 4, 2, EPI, TAPS>(g, st);
+    case 10: return launch_pipe<256, 256, 4, 2, 4, EPI, TAPS>(g, st);
+    case 11: return launch_pipe<256, 256, 2, 2, 4, EPI, TAPS>(g, st);
+    case 12: return launch_pipe<256, 256, 4, 2, 3, EPI, TAPS>(g, st);
+    case 13: return launch_pipe<256, 128, 4, 2, 4, EPI, TAPS>(g, st);
   }
   return hipErrorInvalidValue;
 }
