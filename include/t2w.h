@@ -123,8 +123,8 @@ int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const f
  * a_src non-null: conv taps mode, A row m = frames a_src[m] .. a_src[m] + K / lda - 1 of A (rows lda wide). */
 int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                   void* C, int ldc, int M, int N, int K, int epi, void* stream);
-/* t2w_gemm_bf16 with an explicit tile configuration (-1: chosen by shape; 0: 128x128, 1: 256x128, 2: 128x256,
- * 3: 256x256 of 4 waves, 4: 256x256 of 8 waves) for tile sweeps. */
+/* t2w_gemm_bf16 with an explicit tile configuration (-1: chosen by shape; 0: 128x128 of 4 waves, 1: 256x256 of
+ * 8 waves, 2: 256x128 of 8 waves) for tile sweeps.  K % 64 == 0, lda % 8 == 0 (taps mode: lda % 64 == 0). */
 int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                        void* C, int ldc, int M, int N, int K, int epi, int tile, void* stream);
 int t2w_ln_mod(const float* h, const float* shift, const float* scale1, float eps, void* out, int N, int H,

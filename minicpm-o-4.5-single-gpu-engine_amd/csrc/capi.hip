@@ -263,9 +263,10 @@ int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const
 int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate, void* C, int ldc,
                        int M, int N, int K, int epi, int tile, void* stream) {
   if (K % 64) return fail("K must be a multiple of 64");
+  if (lda % 8) return fail("lda must be a multiple of 8 (16-byte rows)");
   if (epi < 0 || epi > 3) return fail("bad epilogue");
-  if (a_src && (K % lda)) return fail("taps mode: K must be a multiple of lda");
-  if (tile > 13) return fail("bad tile configuration");
+  if (a_src && (K % lda || lda % 64)) return fail("taps mode: K must be a multiple of lda, lda of 64");
+  if (tile > 2) return fail("bad tile configuration");
   T2W_CHECK(gemm_bf16(gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K), epi, (hipStream_t)stream, tile), "gemm");
   return 0;
 }

@@ -1,10 +1,22 @@
 // bf16 MFMA GEMM for the DiT linears: C = epilogue(A[M,K] . W[N,K]^T + bias), fp32 accumulation.
 //
-// CDNA4 design: v_mfma_f32_32x32x16_bf16 tiles on wave64, LDS-staged A/W tiles of 64 K-values (128 B rows, 16-byte
-// chunks XOR-swizzled by row so the fragment reads of 32 consecutive rows spread over all banks), two LDS stages with
-// the next tile's global loads in flight during the MFMAs, XCD-aware block order.  The weight operand is passed to the
-// MFMA as its "A" side so each lane ends up holding four consecutive output columns (16-byte fp32 / 8-byte bf16
-// stores in the epilogue).
+// CDNA4 design.  A workgroup owns a BM x BN output tile; its waves own WTM x WTN sub-tiles made of
+// v_mfma_f32_32x32x16_bf16 blocks.  K advances in stages of 64 (128-byte tile rows).  Every stage is copied straight
+// from HBM/L2 into LDS with global_load_lds_dwordx4 (no register staging), 16-byte chunks XOR-swizzled by row so that
+// the fragment reads of 16 consecutive rows cover all 64 LDS banks.  Two LDS stages: the loads of stage k + 2 are issued
+// right after the barrier that retires stage k, and the first fragments of stage k + 1 are read before the last MFMAs
+// of stage k, so neither the load latency nor the post-barrier LDS latency sits in front of the matrix pipe.  The
+// fragment reads, the loads and the MFMAs of a stage are interleaved one by one (sched_group_barrier).
+//
+// The two stage buffers are separate __shared__ objects and the K loop is unrolled by two, so every LDS access names
+// its buffer at compile time.  Behind one dynamically indexed array the compiler cannot tell the fragment reads of one
+// stage from the in-flight DMA into the other and waits for all loads before every read, which serialises loads and
+// MFMAs.  For the same reason the loads are issued without a branch: at the end of K the free buffer is refilled with
+// the last stage (in bounds, never read).
+//
+// The weight operand is passed to the MFMA as its "A" side, so a lane ends up holding four consecutive output columns
+// of one row.  The epilogue stages each wave's accumulators through LDS and writes whole rows: 32 lanes cover 512
+// contiguous bytes of fp32 (or 256 of bf16), with bias, GELU or the gated fp32 residual applied on the way out.
 //
 // A operand modes: dense rows, or "taps" rows for the kernel-3 causal convs: row m of A is the three frames starting
 // at frame a_src[m] of a frame buffer whose rows are lda wide (no im2col copy in HBM; the host lays the two cached
@@ -26,489 +38,262 @@ constexpr int BK = 64;  // K values per stage (128 bytes of bf16 per tile row)
 __device__ __forceinline__ int swz_key(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ swz_key(row)); }
 
+// Output columns n .. n + 3 of one lane: bias (and gate) loaded once, before any output row is touched.
 template <int EPI>
-__device__ __forceinline__ void epilogue4(const GemmArgs& g, int m, int n, float (&v)[4]) {
-    if (n + 3 < g.N) {
-      const float4 bb = *(const float4*)(g.bias + n);
-      v[0] += bb.x; v[1] += bb.y; v[2] += bb.z; v[3] += bb.w;
-      if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) {
-        if (EPI == EPI_GELU_BF16) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
-        }
-        uint2 o = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
-        *(uint2*)((bf16_t*)g.C + (size_t)m * g.ldc + n) = o;
-      } else if (EPI == EPI_RESID_F32) {
-        float* hp = (float*)g.C + (size_t)m * g.ldc + n;
-        float4 h = *(float4*)hp;
-        const float4 gg = *(const float4*)(g.gate + n);
-        h.x += gg.x * v[0]; h.y += gg.y * v[1]; h.z += gg.z * v[2]; h.w += gg.w * v[3];
-        *(float4*)hp = h;
-      } else {
-        *(float4*)((float*)g.C + (size_t)m * g.ldc + n) = make_float4(v[0], v[1], v[2], v[3]);
-      }
-    } else {
-      for (int e = 0; e < 4 && n + e < g.N; ++e) {
-        float x = v[e] + g.bias[n + e];
-        if (EPI == EPI_BF16) ((bf16_t*)g.C)[(size_t)m * g.ldc + n + e] = f2bf(x);
-        else if (EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[(size_t)m * g.ldc + n + e] = f2bf(gelu_tanh(x));
-        else if (EPI == EPI_RESID_F32) ((float*)g.C)[(size_t)m * g.ldc + n + e] += g.gate[n + e] * x;
-        else ((float*)g.C)[(size_t)m * g.ldc + n + e] = x;
-      }
+struct Cols {
+  float4 bias, gate;
+  int n;
+  bool full;  // all four columns inside N
+  __device__ __forceinline__ Cols(const GemmArgs& g, int n_) : n(n_), full(n_ + 3 < g.N) {
+    bias = gate = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (full) {
+      bias = *(const float4*)(g.bias + n);
+      if (EPI == EPI_RESID_F32) gate = *(const float4*)(g.gate + n);
     }
-}
-
-template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
-  constexpr int NT = 64 * WM * WN;
-  constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
-  constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA blocks per wave
-  constexpr int APASS = BM * 8 / NT, BPASS = BN * 8 / NT;
-  constexpr int STAGE = (BM + BN) * 8;  // uint4 per LDS stage
-  static_assert(APASS * NT == BM * 8 && BPASS * NT == BN * 8, "tile / thread mismatch");
-
-  extern __shared__ uint4 lds_dyn[];  // two stages of STAGE uint4: [A tile BM x 8 | W tile BN x 8]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
-  const int nblk = gm * gn;
-  int b = blockIdx.x;
-  const int full = (nblk / 8) * 8;  // blocks b, b+8, .. run on one XCD: give each XCD a contiguous band of tiles
-  if (b < full) b = (b % 8) * (nblk / 8) + b / 8;
-  const int mt = b / gn, nt = b % gn;
-  const int m0 = mt * BM, n0 = nt * BN;
-
-  // per-thread global load sources (rows fixed over the K loop)
-  const bf16_t* asrc[APASS];
-  bool aok[APASS];
-  int arow[APASS], achunk[APASS];
+  }
+  // finished output of accumulator values a for full columns (h: the residual row's current values)
+  __device__ __forceinline__ float4 apply(float4 a, float4 h) const {
+    float v[4] = {a.x + bias.x, a.y + bias.y, a.z + bias.z, a.w + bias.w};
+    if (EPI == EPI_GELU_BF16) {
 #pragma unroll
-  for (int p = 0; p < APASS; ++p) {
-    int idx = tid + p * NT;
-    arow[p] = idx >> 3;
-    achunk[p] = idx & 7;
-    int m = m0 + arow[p];
-    aok[p] = m < g.M;
-    int mm = aok[p] ? m : 0;
-    if (TAPS)
-      asrc[p] = g.A + (size_t)g.a_src[mm] * g.lda + achunk[p] * 8;
+      for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+    }
+    if (EPI == EPI_RESID_F32) return make_float4(h.x + gate.x * v[0], h.y + gate.y * v[1], h.z + gate.z * v[2], h.w + gate.w * v[3]);
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+  __device__ __forceinline__ void put(const GemmArgs& g, int m, float4 o) const {
+    if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16)
+      *(uint2*)((bf16_t*)g.C + (size_t)m * g.ldc + n) = make_uint2(pack2(o.x, o.y), pack2(o.z, o.w));
     else
-      asrc[p] = g.A + (size_t)mm * g.lda + achunk[p] * 8;
+      *(float4*)((float*)g.C + (size_t)m * g.ldc + n) = o;
   }
-  const bf16_t* bsrc[BPASS];
-  bool bok[BPASS];
-  int brow[BPASS], bchunk[BPASS];
-#pragma unroll
-  for (int p = 0; p < BPASS; ++p) {
-    int idx = tid + p * NT;
-    brow[p] = idx >> 3;
-    bchunk[p] = idx & 7;
-    int n = n0 + brow[p];
-    bok[p] = n < g.N;
-    bsrc[p] = g.B + (size_t)(bok[p] ? n : 0) * g.ldb + bchunk[p] * 8;
-  }
-
-  uint4 ra[APASS], rb[BPASS];
-  auto gload = [&](int k0) {
-    size_t aoff;
-    if (TAPS) {
-      int tap = k0 / g.tapC;
-      aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);
-    } else {
-      aoff = k0;
-    }
-#pragma unroll
-    for (int p = 0; p < APASS; ++p) ra[p] = aok[p] ? *(const uint4*)(asrc[p] + aoff) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int p = 0; p < BPASS; ++p) rb[p] = bok[p] ? *(const uint4*)(bsrc[p] + k0) : make_uint4(0, 0, 0, 0);
-  };
-  auto lstore = [&](int s) {
-#pragma unroll
-    for (int p = 0; p < APASS; ++p) lds_dyn[s * STAGE + swz(arow[p], achunk[p])] = ra[p];
-#pragma unroll
-    for (int p = 0; p < BPASS; ++p) lds_dyn[s * STAGE + BM * 8 + swz(brow[p], bchunk[p])] = rb[p];
-  };
-
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  const int KT = g.K / BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int s = kt & 1;
-    if (kt + 1 < KT) gload((kt + 1) * BK);
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int chunk = kk * 2 + (lane >> 5);
-      bf16x8 af[TM], bfr[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        int row = wm * WTM + i * 32 + (lane & 31);
-        af[i] = as_bf16x8(lds_dyn[s * STAGE + swz(row, chunk)]);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        int row = wn * WTN + j * 32 + (lane & 31);
-        bfr[j] = as_bf16x8(lds_dyn[s * STAGE + BM * 8 + swz(row, chunk)]);
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < KT) lstore(s ^ 1);
-    __syncthreads();
-  }
-
-  // epilogue: lane holds row m = .. + lane%32 and columns n = .. + (r/4)*8 + (lane/32)*4 + r%4
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int m = m0 + wm * WTM + i * 32 + (lane & 31);
-    if (m >= g.M) continue;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * WTN + j * 32 + q * 8 + (lane >> 5) * 4;
-        if (n >= g.N) continue;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
-        epilogue4<EPI>(g, m, n, v);
-      }
+  // columns past N: element by element
+  __device__ __forceinline__ void put_partial(const GemmArgs& g, int m, float4 a) const {
+    const float v[4] = {a.x, a.y, a.z, a.w};
+    for (int e = 0; e < 4 && n + e < g.N; ++e) {
+      const float x = v[e] + g.bias[n + e];
+      const size_t o = (size_t)m * g.ldc + n + e;
+      if (EPI == EPI_BF16) ((bf16_t*)g.C)[o] = f2bf(x);
+      else if (EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[o] = f2bf(gelu_tanh(x));
+      else if (EPI == EPI_RESID_F32) ((float*)g.C)[o] += g.gate[n + e] * x;
+      else ((float*)g.C)[o] = x;
     }
   }
-}
+};
 
-// Direct-to-LDS variant: every 16-byte chunk of the next K stage goes from global memory straight into its swizzled
-// LDS slot (global_load_lds_dwordx4: a wave writes 1 KB of LDS, lane l at byte 16 l of the block, so each lane loads the
-// chunk whose swizzled position is its own), with no VGPR staging; fragments of the next 16-wide K step are read while
-// the current one's MFMAs issue.  Rows past M / N are clamped to the last valid row (their results are never stored).
-template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_lds_kernel(GemmArgs g) {
-  constexpr int NT = 64 * WM * WN, NW = WM * WN;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int STAGE = (BM + BN) * 8;        // uint4 per stage
-  constexpr int ABLK = BM / 8, BBLK = BN / 8;  // 1 KB blocks (8 rows) per stage
-  constexpr int APW = ABLK / NW, BPW = BBLK / NW;
-  static_assert(APW * NW == ABLK && BPW * NW == BBLK, "blocks / waves mismatch");
-  extern __shared__ uint4 lds_dyn[];
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
-  const int nblk = gm * gn;
-  int b = blockIdx.x;
-  const int full = (nblk / 8) * 8;
-  if (b < full) b = (b % 8) * (nblk / 8) + b / 8;
-  const int mt = b / gn, nt = b % gn;
-  const int m0 = mt * BM, n0 = nt * BN;
+template <int BM, int BN, int WM, int WN, bool TAPS>
+struct Tile {
+  static constexpr int NW = WM * WN;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave sub-tile
+  static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA blocks per wave
+  static constexpr int APW = BM / 8 / NW, BPW = BN / 8 / NW;  // 1 KB (8-row) load blocks per wave and stage
+  static_assert(APW * NW * 8 == BM && BPW * NW * 8 == BN, "tile rows / waves mismatch");
 
-  // this lane's source chunk in each of its waves' 1 KB blocks: tile row blk*8 + l/8, logical chunk (l%8) ^ swz_key(row)
-  const int lrow = lane >> 3;
   const bf16_t* asrc[APW];
   const bf16_t* bsrc[BPW];
+  const GemmArgs& g;
+  int lane, wave, wm, wn;
+
+  __device__ __forceinline__ Tile(const GemmArgs& g_, int m0, int n0) : g(g_) {
+    const int tid = threadIdx.x;
+    lane = tid & 63;
+    wave = tid >> 6;
+    wm = wave / WN;
+    wn = wave % WN;
+    // this lane's 16 bytes of each of its wave's load blocks: tile row blk * 8 + lane / 8, logical chunk (lane % 8) ^ key
+    const int lrow = lane >> 3;
 #pragma unroll
-  for (int p = 0; p < APW; ++p) {
-    const int trow = (wave + p * NW) * 8 + lrow;
-    const int lchunk = (lane & 7) ^ swz_key(trow);
-    int m = m0 + trow;
-    m = m < g.M ? m : g.M - 1;
-    asrc[p] = TAPS ? g.A + (size_t)g.a_src[m] * g.lda + lchunk * 8 : g.A + (size_t)m * g.lda + lchunk * 8;
-  }
+    for (int p = 0; p < APW; ++p) {
+      const int trow = (wave + p * NW) * 8 + lrow;
+      const int m = min(m0 + trow, g.M - 1);  // rows past M load row M - 1; their results are never stored
+      const int ch = (lane & 7) ^ swz_key(trow);
+      asrc[p] = TAPS ? g.A + (size_t)g.a_src[m] * g.lda + ch * 8 : g.A + (size_t)m * g.lda + ch * 8;
+    }
 #pragma unroll
-  for (int p = 0; p < BPW; ++p) {
-    const int trow = (wave + p * NW) * 8 + lrow;
-    const int lchunk = (lane & 7) ^ swz_key(trow);
-    int n = n0 + trow;
-    n = n < g.N ? n : g.N - 1;
-    bsrc[p] = g.B + (size_t)n * g.ldb + lchunk * 8;
+    for (int p = 0; p < BPW; ++p) {
+      const int trow = (wave + p * NW) * 8 + lrow;
+      bsrc[p] = g.B + (size_t)min(n0 + trow, g.N - 1) * g.ldb + ((lane & 7) ^ swz_key(trow)) * 8;
+    }
   }
-  typedef __attribute__((address_space(3))) void* lds_ptr_t;
-  auto issue = [&](int k0, int s) {
-    size_t aoff;
+
+  __device__ __forceinline__ void issue(uint4* la, uint4* lb, int kt) const {
+    const int k0 = kt * BK;
+    size_t aoff = k0;
     if (TAPS) {
-      const int tap = k0 / g.tapC;
+      const int tap = k0 / g.tapC;  // a stage never straddles two taps (tapC % 64 == 0)
       aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);
-    } else {
-      aoff = k0;
     }
 #pragma unroll
     for (int p = 0; p < APW; ++p)
-      __builtin_amdgcn_global_load_lds((const void*)(asrc[p] + aoff), (lds_ptr_t)(lds_dyn + s * STAGE + (wave + p * NW) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(asrc[p] + aoff), (lds_ptr_t)(la + (wave + p * NW) * 64), 16, 0, 0);
 #pragma unroll
     for (int p = 0; p < BPW; ++p)
-      __builtin_amdgcn_global_load_lds((const void*)(bsrc[p] + k0), (lds_ptr_t)(lds_dyn + s * STAGE + BM * 8 + (wave + p * NW) * 64), 16, 0, 0);
-  };
+      __builtin_amdgcn_global_load_lds((const void*)(bsrc[p] + k0), (lds_ptr_t)(lb + (wave + p * NW) * 64), 16, 0, 0);
+  }
 
-  f32x16 acc[TM][TN];
+  __device__ __forceinline__ void frag(const uint4* La, const uint4* Lb, int kk, bf16x8 (&af)[TM], bf16x8 (&bf)[TN]) const {
+    const int chunk = kk * 2 + (lane >> 5);
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(La[swz(wm * WTM + i * 32 + (lane & 31), chunk)]);
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+    for (int j = 0; j < TN; ++j) bf[j] = as_bf16x8(Lb[swz(wn * WTN + j * 32 + (lane & 31), chunk)]);
+  }
+
+  static __device__ __forceinline__ void mma(f32x16 (&acc)[TM][TN], const bf16x8 (&af)[TM], const bf16x8 (&bf)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+  }
+
+  // One K stage from buffers (La, Lb).  Stage kt + 1 must already be in flight into (Na, Nb); after the barrier the
+  // loads of stage kt + 2 go into (La, Lb).
+  __device__ __forceinline__ void stage(f32x16 (&acc)[TM][TN], bf16x8 (&af)[2][TM], bf16x8 (&bf)[2][TN], uint4* La,
+                                        uint4* Lb, const uint4* Na, const uint4* Nb, int kt, int KT) const {
+    constexpr int NV = APW + BPW, ND = TM + TN, NM = TM * TN;
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk) {
+      frag(La, Lb, kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
+      mma(acc, af[kk & 1], bf[kk & 1]);
+      // MFMA, fragment read, MFMA, ... then the remaining MFMAs
+#pragma unroll
+      for (int x = 0; x < ND; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+#pragma unroll
+      for (int x = ND; x < NM; ++x) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    // stage kt + 1 has landed (this wave's loads) and is visible (everyone's), and nobody reads (La, Lb) any more
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+    issue(La, Lb, min(kt + 2, KT - 1));
+    frag(Na, Nb, 0, af[0], bf[0]);
+    mma(acc, af[1], bf[1]);
+    // MFMA, load(s), fragment read(s), MFMA, ...
+    constexpr int VPM = (NV + NM - 1) / NM, DPM = (ND + NM - 1) / NM;
+#pragma unroll
+    for (int x = 0; x < NM; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (x * VPM < NV) __builtin_amdgcn_sched_group_barrier(0x020, VPM, 0);
+      if (x * DPM < ND) __builtin_amdgcn_sched_group_barrier(0x100, DPM, 0);
+    }
+  }
+
+  // Writes the wave's accumulators through its LDS slab st (32 x WTN fp32, chunks XOR-swizzled by row) so that each
+  // global access of the epilogue covers whole rows.  Rows go out in batches of RB read-back instructions whose
+  // residual loads are all in flight before the first store.
+  template <int EPI>
+  __device__ __forceinline__ void store(const f32x16 (&acc)[TM][TN], float4* st, int m0, int n0) const {
+    constexpr int CPR = WTN / 4;   // 16-byte chunks per slab row
+    constexpr int RPI = 64 / CPR;  // slab rows per read-back instruction
+    constexpr int NRB = 32 / RPI;  // read-back instructions per slab
+    constexpr int RB = NRB < 8 ? NRB : 8;
+    const int cc = lane % CPR;
+    const Cols<EPI> cols(g, n0 + wn * WTN + cc * 4);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = lane & 31;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = j * 8 + q * 2 + (lane >> 5);
+          st[r * CPR + (c ^ (r & (CPR - 1)))] =
+              make_float4(acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int b = 0; b < NRB; b += RB) {
+        float4 v[RB], h[RB];
+        int m[RB];
+#pragma unroll
+        for (int x = 0; x < RB; ++x) {
+          const int row = (b + x) * RPI + lane / CPR;
+          m[x] = m0 + wm * WTM + i * 32 + row;
+          v[x] = st[row * CPR + (cc ^ (row & (CPR - 1)))];
+          h[x] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (EPI == EPI_RESID_F32 && cols.full && m[x] < g.M) h[x] = *(const float4*)((const float*)g.C + (size_t)m[x] * g.ldc + cols.n);
+        }
+#pragma unroll
+        for (int x = 0; x < RB; ++x) {
+          if (m[x] >= g.M) continue;
+          if (cols.full) cols.put(g, m[x], cols.apply(v[x], h[x]));
+          else cols.put_partial(g, m[x], v[x]);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+  }
+};
+
+template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
+  using T = Tile<BM, BN, WM, WN, TAPS>;
+  __shared__ uint4 sA0[BM * 8], sA1[BM * 8], sB0[BN * 8], sB1[BN * 8];
+
+  // XCD-aware order: consecutive workgroups go to different XCDs, so the tiles of one XCD are a contiguous run (they
+  // share A rows and W columns in that XCD's L2)
+  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
+  const int nblk = gm * gn, full = (nblk / 8) * 8;
+  int b = blockIdx.x;
+  if (b < full) b = (b % 8) * (nblk / 8) + b / 8;
+  const int m0 = (b / gn) * BM, n0 = (b % gn) * BN;
+  T t(g, m0, n0);
+
+  f32x16 acc[T::TM][T::TN];
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  bf16x8 af[2][T::TM], bf[2][T::TN];
 
   const int KT = g.K / BK;
-  issue(0, 0);
+  t.issue(sA0, sB0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int s = kt & 1;
-    if (kt + 1 < KT) issue((kt + 1) * BK, s ^ 1);
-    const uint4* L = lds_dyn + s * STAGE;
-    bf16x8 af[2][TM], bfr[2][TN];
-    auto frag = [&](int kk, int buf) {
-      const int chunk = kk * 2 + (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int row = wm * WTM + i * 32 + (lane & 31);
-        af[buf][i] = as_bf16x8(L[swz(row, chunk)]);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int row = wn * WTN + j * 32 + (lane & 31);
-        bfr[buf][j] = as_bf16x8(L[BM * 8 + swz(row, chunk)]);
-      }
-    };
-    frag(0, 0);
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      if (kk + 1 < BK / 16) frag(kk + 1, (kk + 1) & 1);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[kk & 1][j], af[kk & 1][i], acc[i][j], 0, 0, 0);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+  t.issue(sA1, sB1, min(1, KT - 1));
+  t.frag(sA0, sB0, 0, af[0], bf[0]);
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    t.stage(acc, af, bf, sA0, sB0, sA1, sB1, kt, KT);
+    t.stage(acc, af, bf, sA1, sB1, sA0, sB0, kt + 1, KT);
   }
+  if (kt < KT) t.stage(acc, af, bf, sA0, sB0, sA1, sB1, kt, KT);
 
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int m = m0 + wm * WTM + i * 32 + (lane & 31);
-    if (m >= g.M) continue;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * WTN + j * 32 + q * 8 + (lane >> 5) * 4;
-        if (n >= g.N) continue;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
-        epilogue4<EPI>(g, m, n, v);
-      }
-    }
-  }
-}
-
-// Deep-pipelined direct-to-LDS variant: K stages of 32 (64-byte tile rows, 16-byte chunk c of row r at chunk
-// c ^ ((r >> 2) & 3): 16 consecutive rows reading one chunk cover all 64 banks), an NS-deep LDS ring with the loads of
-// stage kt + NS - 1 issued while stage kt computes, and a wait that only requires stage kt's own loads to have landed.
-__device__ __forceinline__ int swz32(int row, int chunk) { return row * 4 + (chunk ^ ((row >> 2) & 3)); }
-
-template <int LPT, int NS>
-__device__ __forceinline__ void wait_stage(bool tail) {
-  // outstanding loads are the stages after this one; vmcnt counts per-thread vector memory instructions in issue order
-  if (tail) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  } else {
-    constexpr int N = (NS - 2) * LPT;
-    static_assert(N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-  }
-}
-
-template <int BM, int BN, int WM, int WN, int NS, int EPI, bool TAPS>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_pipe_kernel(GemmArgs g) {
-  constexpr int BKP = 32;
-  constexpr int NT = 64 * WM * WN, NW = WM * WN;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int STAGE = (BM + BN) * 4;          // uint4 per stage
-  constexpr int ABLK = BM / 16, BBLK = BN / 16;  // 1 KB blocks (16 rows of 64 bytes)
-  constexpr int APW = ABLK / NW, BPW = BBLK / NW;
-  constexpr int LPT = APW + BPW;
-  static_assert(APW * NW == ABLK && BPW * NW == BBLK, "blocks / waves mismatch");
-  extern __shared__ uint4 lds_dyn[];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
-  const int nblk = gm * gn;
-  int b = blockIdx.x;
-  const int full = (nblk / 8) * 8;
-  if (b < full) b = (b % 8) * (nblk / 8) + b / 8;
-  const int mt = b / gn, nt = b % gn;
-  const int m0 = mt * BM, n0 = nt * BN;
-
-  const int lrow = lane >> 2;  // row of the lane's chunk inside its 1 KB block (16 rows x 4 chunks)
-  const bf16_t* asrc[APW];
-  const bf16_t* bsrc[BPW];
-#pragma unroll
-  for (int p = 0; p < APW; ++p) {
-    const int trow = (wave + p * NW) * 16 + lrow;
-    const int lchunk = (lane & 3) ^ ((trow >> 2) & 3);
-    int m = m0 + trow;
-    m = m < g.M ? m : g.M - 1;
-    asrc[p] = TAPS ? g.A + (size_t)g.a_src[m] * g.lda + lchunk * 8 : g.A + (size_t)m * g.lda + lchunk * 8;
-  }
-#pragma unroll
-  for (int p = 0; p < BPW; ++p) {
-    const int trow = (wave + p * NW) * 16 + lrow;
-    const int lchunk = (lane & 3) ^ ((trow >> 2) & 3);
-    int n = n0 + trow;
-    n = n < g.N ? n : g.N - 1;
-    bsrc[p] = g.B + (size_t)n * g.ldb + lchunk * 8;
-  }
-  typedef __attribute__((address_space(3))) void* lds_ptr_t;
-  const int KT = g.K / BKP;
-#define T2W_ISSUE(kt_)                                                                                                          \
-  {                                                                                                                             \
-    const int k0 = (kt_) * BKP;                                                                                                 \
-    const int s_ = (kt_) % NS;                                                                                                  \
-    size_t aoff;                                                                                                                \
-    if (TAPS) {                                                                                                                 \
-      const int tap = k0 / g.tapC;                                                                                              \
-      aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);                                                                         \
-    } else {                                                                                                                    \
-      aoff = k0;                                                                                                                \
-    }                                                                                                                           \
-    _Pragma("unroll") for (int p = 0; p < APW; ++p) __builtin_amdgcn_global_load_lds(                                           \
-        (const void*)(asrc[p] + aoff), (lds_ptr_t)(lds_dyn + s_ * STAGE + (wave + p * NW) * 64), 16, 0, 0);                      \
-    _Pragma("unroll") for (int p = 0; p < BPW; ++p) __builtin_amdgcn_global_load_lds(                                           \
-        (const void*)(bsrc[p] + k0), (lds_ptr_t)(lds_dyn + s_ * STAGE + BM * 4 + (wave + p * NW) * 64), 16, 0, 0);               \
-  }
-
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-#pragma unroll
-  for (int p = 0; p < NS - 1; ++p)
-    if (p < KT) T2W_ISSUE(p)
-  for (int kt = 0; kt < KT; ++kt) {
-    wait_stage<LPT, NS>(kt + NS - 2 >= KT);
-    __syncthreads();  // stage kt landed for every thread; stage kt - 1 (about to be refilled) is no longer read
-    if (kt + NS - 1 < KT) T2W_ISSUE(kt + NS - 1)
-    const uint4* L = lds_dyn + (kt % NS) * STAGE;
-    bf16x8 af[2][TM], bfr[2][TN];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int chunk = kk * 2 + (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < TM; ++i) af[kk][i] = as_bf16x8(L[swz32(wm * WTM + i * 32 + (lane & 31), chunk)]);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) bfr[kk][j] = as_bf16x8(L[BM * 4 + swz32(wn * WTN + j * 32 + (lane & 31), chunk)]);
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[kk][j], af[kk][i], acc[i][j], 0, 0, 0);
-  }
-#undef T2W_ISSUE
-
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int m = m0 + wm * WTM + i * 32 + (lane & 31);
-    if (m >= g.M) continue;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * WTN + j * 32 + q * 8 + (lane >> 5) * 4;
-        if (n >= g.N) continue;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
-        epilogue4<EPI>(g, m, n, v);
-      }
-    }
-  }
+  // retire the tail loads and every wave's last fragment reads before the stage buffers become epilogue slabs
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __syncthreads();
+  constexpr int SLAB = 32 * T::WTN / 4;  // float4 per wave slab
+  constexpr int CAPA = BM * 8 / SLAB, CAPB = BN * 8 / SLAB;
+  static_assert(2 * CAPA + 2 * CAPB >= T::NW, "epilogue slabs do not fit the stage buffers");
+  const int w = t.wave;
+  float4* st = w < CAPA ? (float4*)sA0 + w * SLAB
+             : w < 2 * CAPA ? (float4*)sA1 + (w - CAPA) * SLAB
+             : w < 2 * CAPA + CAPB ? (float4*)sB0 + (w - 2 * CAPA) * SLAB
+                                   : (float4*)sB1 + (w - 2 * CAPA - CAPB) * SLAB;
+  t.template store<EPI>(acc, st, m0, n0);
 }
 
 template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
-hipError_t launch_cfg(const GemmArgs& g, hipStream_t st) {
+hipError_t launch_tile(const GemmArgs& g, hipStream_t st) {
   const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
-  const size_t lds = 2 * (size_t)(BM + BN) * 8 * sizeof(uint4);
-  auto kern = gemm_kernel<BM, BN, WM, WN, EPI, TAPS>;
-  static bool attr_set = false;  // one attribute call per instantiation (host side, idempotent)
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  hipLaunchKernelGGL(kern, dim3(gm * gn), dim3(64 * WM * WN), lds, st, g);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, TAPS>), dim3(gm * gn), dim3(64 * WM * WN), 0, st, g);
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
-hipError_t launch_lds(const GemmArgs& g, hipStream_t st) {
-  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
-  const size_t lds = 2 * (size_t)(BM + BN) * 8 * sizeof(uint4);
-  auto kern = gemm_lds_kernel<BM, BN, WM, WN, EPI, TAPS>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  hipLaunchKernelGGL(kern, dim3(gm * gn), dim3(64 * WM * WN), lds, st, g);
-  return hipGetLastError();
-}
-
-template <int BM, int BN, int WM, int WN, int NS, int EPI, bool TAPS>
-hipError_t launch_pipe(const GemmArgs& g, hipStream_t st) {
-  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
-  const size_t lds = (size_t)NS * (BM + BN) * 4 * sizeof(uint4);
-  auto kern = gemm_pipe_kernel<BM, BN, WM, WN, NS, EPI, TAPS>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  hipLaunchKernelGGL(kern, dim3(gm * gn), dim3(64 * WM * WN), lds, st, g);
-  return hipGetLastError();
-}
-
-// tile configurations: 0 = 128x128 (4 waves of 64x64), 1 = 256x128 (4 waves of 128x64), 2 = 128x256 (4 waves of 64x128),
-// 3 = 256x256 (4 waves of 128x128), 4 = 256x256 (8 waves of 128x64)
+// tile configurations: 0 = 128x128 (4 waves of 64x64), 1 = 256x256 (8 waves of 64x128), 2 = 256x128 (8 waves of 64x64)
 template <int EPI, bool TAPS>
 hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
   if (cfg < 0) cfg = pick_cfg(g);
   switch (cfg) {
-    case 0: return launch_cfg<128, 128, 2, 2, EPI, TAPS>(g, st);
-    case 1: return launch_cfg<256, 128, 2, 2, EPI, TAPS>(g, st);
-    case 2: return launch_cfg<128, 256, 2, 2, EPI, TAPS>(g, st);
-    case 3: return launch_cfg<256, 256, 2, 2, EPI, TAPS>(g, st);
-    case 4: return launch_cfg<256, 256, 2, 4, EPI, TAPS>(g, st);
-    case 5: return launch_lds<256, 256, 2, 4, EPI, TAPS>(g, st);
-    case 6: return launch_lds<256, 256, 2, 2, EPI, TAPS>(g, st);
-    case 7: return launch_lds<256, 128, 2, 2, EPI, TAPS>(g, st);
-    case 8: return launch_lds<128, 128, 2, 2, EPI, TAPS>(g, st);
-    case 9: return launch_lds<256, 256, 4, 2, EPI, TAPS>(g, st);
-    case 10: return launch_pipe<256, 256, 4, 2, 4, EPI, TAPS>(g, st);
-    case 11: return launch_pipe<256, 256, 2, 2, 4, EPI, TAPS>(g, st);
-    case 12: return launch_pipe<256, 256, 4, 2, 3, EPI, TAPS>(g, st);
-    case 13: return launch_pipe<256, 128, 4, 2, 4, EPI, TAPS>(g, st);
+    case 0: return launch_tile<128, 128, 2, 2, EPI, TAPS>(g, st);
+    case 1: return launch_tile<256, 256, 4, 2, EPI, TAPS>(g, st);
+    case 2: return launch_tile<256, 128, 4, 2, EPI, TAPS>(g, st);
   }
   return hipErrorInvalidValue;
 }
@@ -516,9 +301,9 @@ hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
 }  // namespace
 
 int pick_cfg(const GemmArgs& g) {
-  // 256x256 tiles of 8 waves (64x128 per wave) with direct-to-LDS loads once there are enough rows to fill them
-  if (g.M >= 1024 && g.N >= 256) return 9;
-  return 8;
+  // 256x256 tiles once there are enough rows to fill them
+  if (g.M >= 1024 && g.N >= 256) return 1;
+  return 0;
 }
 
 hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
