@@ -127,6 +127,11 @@ int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const
  * 8 waves, 2: 256x128 of 8 waves) for tile sweeps.  K % 64 == 0, lda % 8 == 0 (taps mode: lda % 64 == 0). */
 int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                        void* C, int ldc, int M, int N, int K, int epi, int tile, void* stream);
+/* t2w_gemm_bf16 with a workspace for split-K partials (256-byte aligned; up to splits x M x N fp32): a call whose tile
+ * grid would leave most CUs idle (few rows) splits K over ~512 waves and reduces the partials in a fixed order. */
+int t2w_gemm_bf16_ws(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
+                     void* C, int ldc, int M, int N, int K, int epi, void* workspace, size_t workspace_bytes,
+                     void* stream);
 int t2w_ln_mod(const float* h, const float* shift, const float* scale1, float eps, void* out, int N, int H,
                void* stream);
 int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const float* kw, const float* kb, float eps,

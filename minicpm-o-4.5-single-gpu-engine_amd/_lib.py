@@ -77,6 +77,7 @@ _SIGS = {
     "t2w_dit_forward": (I, [P, C.POINTER(SolveArgs), I, P, P, P]),
     "t2w_gemm_bf16": (I, [P, I, P, P, P, P, P, I, I, I, I, I, P]),
     "t2w_gemm_bf16_tile": (I, [P, I, P, P, P, P, P, I, I, I, I, I, I, P]),
+    "t2w_gemm_bf16_ws": (I, [P, I, P, P, P, P, P, I, I, I, I, I, P, C.c_size_t, P]),
     "t2w_ln_mod": (I, [P, P, P, F, P, I, I, P]),
     "t2w_qk_norm_scatter": (I, [P, P, P, P, P, F, P, P, P, P, I, I, P]),
     "t2w_attention": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, F, P]),

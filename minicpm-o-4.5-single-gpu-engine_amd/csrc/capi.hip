@@ -53,7 +53,12 @@ namespace {
 
 struct Work {  // carve of the caller's workspace for n tokens, R rows
   bf16_t* a_in; float* x; float* h; bf16_t* abuf; bf16_t* big; bf16_t* q; bf16_t* ao; bf16_t* P; float* dphi;
+  float* part; size_t part_bytes;  // split-K partials of the GEMMs of calls with few tokens
 };
+
+// calls of up to this many tokens get a split-K partial area of SPLITK_BYTES
+constexpr int SPLITK_MAX_TOK = 1024;
+constexpr size_t SPLITK_BYTES = (size_t)16 << 20;
 
 size_t carve(const t2w_dit_dims& d, int N, int R, char* base, Work* w) {
   const int H = d.hidden, M = d.mel;
@@ -70,6 +75,8 @@ size_t carve(const t2w_dit_dims& d, int N, int R, char* base, Work* w) {
   t.ao = (bf16_t*)take((size_t)N * H * 2);
   t.P = (bf16_t*)take((size_t)(N + 2 * R) * H * 2);
   t.dphi = (float*)take((size_t)N * M * 4);
+  t.part_bytes = N <= SPLITK_MAX_TOK ? SPLITK_BYTES : 0;
+  t.part = t.part_bytes ? (float*)take(t.part_bytes) : nullptr;
   if (w) *w = t;
   return off;
 }
@@ -83,8 +90,10 @@ int check_model(const t2w_dit* m) {
 }
 
 GemmArgs gemm_args(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate, void* C,
-                   int ldc, int M, int N, int K) {
+                   int ldc, int M, int N, int K, const Work* w = nullptr) {
   GemmArgs g;
+  g.ws = w ? w->part : nullptr;
+  g.ws_bytes = w ? w->part_bytes : 0;
   g.A = (const bf16_t*)A;
   g.lda = lda;
   g.a_src = a_src;
@@ -106,7 +115,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
                   const float* fmods, float* dphi, hipStream_t st) {
   const t2w_dit_dims& d = m->d;
   const int N = a->n_tok, R = a->n_rows, H = d.hidden, F = d.ffn, M = d.mel, D = d.depth;
-  T2W_CHECK(gemm_bf16(gemm_args(w.a_in, 4 * M, nullptr, m->g.in_w, m->g.in_b, nullptr, w.h, H, N, H, 4 * M), EPI_F32, st), "in_proj");
+  T2W_CHECK(gemm_bf16(gemm_args(w.a_in, 4 * M, nullptr, m->g.in_w, m->g.in_b, nullptr, w.h, H, N, H, 4 * M, &w), EPI_F32, st), "in_proj");
   const long long cstride = (long long)d.steps * D * 4 * H;
   for (int b = 0; b < D; ++b) {
     const t2w_dit_block& k = m->blocks[b];
@@ -114,7 +123,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     const float *sh_a = md, *sc_a = md + H, *g_a = md + 2 * H, *sh_m = md + 3 * H, *sc_m = md + 4 * H, *g_m = md + 5 * H;
     const float *sh_c = md + 6 * H, *sc_c = md + 7 * H, *g_c = md + 8 * H;
     T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st), "ln_mod msa");
-    T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H), EPI_BF16, st), "qkv");
+    T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H, &w), EPI_BF16, st), "qkv");
     const size_t layer = (size_t)(step * D + b) * (size_t)a->pool_layer_stride;
     bf16_t* kp = (bf16_t*)a->k_pool + layer;
     bf16_t* vp = (bf16_t*)a->v_pool + layer;
@@ -124,7 +133,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     at.row_len = a->row_len; at.row_kv_off = a->row_kv_off; at.row_kv_len = a->row_kv_len; at.tiles = a->tiles;
     at.n_tiles = a->n_tiles; at.heads = d.heads; at.chunk = a->chunk; at.scale = 1.0f / sqrtf((float)d.head_dim);
     T2W_CHECK(attention(at, st), "attention");
-    T2W_CHECK(gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H), EPI_RESID_F32, st), "proj");
+    T2W_CHECK(gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F32, st), "proj");
     ConvPlace cp;
     cp.P = w.P; cp.tok_row = a->tok_row; cp.tok_pos = a->tok_pos; cp.row_start = a->row_start; cp.row_len = a->row_len;
     cp.rd = a->conv_rd; cp.wr = a->conv_wr; cp.cache_stride = cstride; cp.N = N; cp.R = R;
@@ -132,17 +141,17 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     cp.cache_base = cbase;
     cp.cache_out_base = cbase;
     T2W_CHECK(ln_mod_conv(w.h, sh_c, sc_c, d.eps_block, cp, H, st), "ln_mod_conv");
-    T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H), EPI_BF16, st), "conv1");
+    T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), EPI_BF16, st), "conv1");
     cp.cache_base = cbase + 2 * H;
     cp.cache_out_base = cbase + 2 * H;
     T2W_CHECK(ln_mish_conv(w.ao, k.cln_w, k.cln_b, d.eps_conv, cp, H, st), "ln_mish_conv");
-    T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H), EPI_RESID_F32, st), "conv2");
+    T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), EPI_RESID_F32, st), "conv2");
     T2W_CHECK(ln_mod(w.h, sh_m, sc_m, d.eps_block, w.abuf, N, H, st), "ln_mod mlp");
-    T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.fc1_w, k.fc1_b, nullptr, w.big, F, N, F, H), EPI_GELU_BF16, st), "fc1");
-    T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F), EPI_RESID_F32, st), "fc2");
+    T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.fc1_w, k.fc1_b, nullptr, w.big, F, N, F, H, &w), EPI_GELU_BF16, st), "fc1");
+    T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F32, st), "fc2");
   }
   T2W_CHECK(ln_mod(w.h, fmods, fmods + H, d.eps_final, w.abuf, N, H, st), "final norm");
-  T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, m->g.out_w, m->g.out_b, nullptr, dphi, M, N, M, H), EPI_F32, st), "final linear");
+  T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, m->g.out_w, m->g.out_b, nullptr, dphi, M, N, M, H, &w), EPI_F32, st), "final linear");
   return 0;
 }
 
@@ -268,6 +277,20 @@ int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, 
   if (a_src && (K % lda || lda % 64)) return fail("taps mode: K must be a multiple of lda, lda of 64");
   if (tile > 2) return fail("bad tile configuration");
   T2W_CHECK(gemm_bf16(gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K), epi, (hipStream_t)stream, tile), "gemm");
+  return 0;
+}
+
+int t2w_gemm_bf16_ws(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate, void* C,
+                     int ldc, int M, int N, int K, int epi, void* workspace, size_t workspace_bytes, void* stream) {
+  if (K % 64) return fail("K must be a multiple of 64");
+  if (lda % 8) return fail("lda must be a multiple of 8 (16-byte rows)");
+  if (epi < 0 || epi > 3) return fail("bad epilogue");
+  if (a_src && (K % lda || lda % 64)) return fail("taps mode: K must be a multiple of lda, lda of 64");
+  if (((uintptr_t)workspace & 255) != 0) return fail("workspace must be 256-byte aligned");
+  GemmArgs g = gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K);
+  g.ws = (float*)workspace;
+  g.ws_bytes = workspace ? workspace_bytes : 0;
+  T2W_CHECK(gemm_bf16(g, epi, (hipStream_t)stream, -1), "gemm");
   return 0;
 }
 

@@ -308,6 +308,15 @@ int pick_cfg(const GemmArgs& g) {
 
 hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
+  if (cfg < 0 && g.ws) {
+    // a grid of fewer than 128 tiles leaves most of the 256 CUs idle: split K instead
+    const int c = pick_cfg(g), bm = c == 0 ? 128 : 256, bn = c == 1 ? 256 : 128;
+    const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+    if (tiles < 128) {
+      const SplitPlan p = splitk_plan(g.M, g.N, g.K, g.ws_bytes);
+      if (p.splits > 1) return gemm_splitk(g, epi, p, g.ws, st);
+    }
+  }
   const bool taps = g.a_src != nullptr;
   switch (epi * 2 + (taps ? 1 : 0)) {
     case EPI_BF16 * 2: return launch_epi<EPI_BF16, false>(g, cfg, st);

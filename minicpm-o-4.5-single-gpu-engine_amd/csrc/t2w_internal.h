@@ -22,9 +22,19 @@ struct GemmArgs {
   void* C;
   int ldc;
   int M, N, K;         // K % 64 == 0
+  float* ws;           // split-K partials (null: tile kernels only)
+  size_t ws_bytes;
 };
 
-hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg = -1);  // cfg < 0: by shape
+// cfg < 0: by shape (split-K through g.ws when a tile grid would be too small to fill the chip)
+hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg = -1);
+
+struct SplitPlan {
+  int splits;  // 0: split-K not possible for this shape / workspace
+  int steps;   // 64-K steps per split
+};
+SplitPlan splitk_plan(int M, int N, int K, size_t ws_bytes);
+hipError_t gemm_splitk(const GemmArgs& g, int epi, const SplitPlan& p, float* part, hipStream_t st);
 
 // Per-token row kernels of the DiT block (H = hidden, one wave per token).
 hipError_t ln_mod(const float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H,

@@ -12,13 +12,17 @@ from conftest import rel
 pytestmark = pytest.mark.gpu
 
 
-def _gemm(A, W, bias, C_, epi, gate=None, a_src=None, lda=None, K=None):
+def _gemm(A, W, bias, C_, epi, gate=None, a_src=None, lda=None, K=None, ws=None):
     L = _lib.lib()
     M = C_.shape[0] if a_src is None else a_src.numel()
     N = W.shape[0]
     K = K or A.shape[1]
-    _lib.check(L.t2w_gemm_bf16(A.data_ptr(), lda or A.shape[1], _lib.ptr(a_src), W.data_ptr(), bias.data_ptr(), _lib.ptr(gate),
-                               C_.data_ptr(), C_.shape[1], M, N, K, epi, _lib.stream_handle()), "gemm")
+    if ws is None:
+        _lib.check(L.t2w_gemm_bf16(A.data_ptr(), lda or A.shape[1], _lib.ptr(a_src), W.data_ptr(), bias.data_ptr(), _lib.ptr(gate),
+                                   C_.data_ptr(), C_.shape[1], M, N, K, epi, _lib.stream_handle()), "gemm")
+    else:
+        _lib.check(L.t2w_gemm_bf16_ws(A.data_ptr(), lda or A.shape[1], _lib.ptr(a_src), W.data_ptr(), bias.data_ptr(), _lib.ptr(gate),
+                                      C_.data_ptr(), C_.shape[1], M, N, K, epi, ws.data_ptr(), ws.numel(), _lib.stream_handle()), "gemm")
     torch.cuda.synchronize()
 
 
@@ -46,6 +50,57 @@ def test_gemm_dense(dev, M, N, K, epi):
         out = torch.zeros(M, N, device=dev)
         _gemm(A, W, bias, out, 3)
         assert rel(out, ref) < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (37, 3072, 1024), (100, 1024, 2048), (100, 80, 1024), (300, 2048, 1024), (600, 1024, 320)])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_gemm_splitk(dev, M, N, K, epi):
+    """Calls with few rows split K over many waves (partials in the caller's workspace, fixed-order reduction):
+    parity with fp32 and bit-identical repeats."""
+    g = torch.Generator(device=dev).manual_seed(M + N + K + 5 * epi)
+    A = torch.randn(M, K, device=dev, generator=g).bfloat16()
+    W = (torch.randn(N, K, device=dev, generator=g) / K ** 0.5).bfloat16()
+    bias = torch.randn(N, device=dev, generator=g)
+    gate = torch.randn(N, device=dev, generator=g)
+    ws = torch.empty(16 << 20, dtype=torch.uint8, device=dev)
+    ref = A.float() @ W.float().t() + bias
+    if epi == 1:
+        ref = torch.nn.functional.gelu(ref, approximate="tanh")
+    outs = []
+    for _ in range(2):
+        if epi in (0, 1):
+            out = torch.full((M, N), 7.0, device=dev).bfloat16()
+        elif epi == 2:
+            out = torch.randn(M, N, device=dev, generator=torch.Generator(device=dev).manual_seed(9))
+            h0 = out.clone()
+        else:
+            out = torch.zeros(M, N, device=dev)
+        _gemm(A, W, bias, out, epi, gate=gate if epi == 2 else None, ws=ws)
+        outs.append(out)
+    if epi in (0, 1):
+        assert rel(outs[0].float(), ref) < 6e-3
+    elif epi == 2:
+        assert rel(outs[0], h0 + gate * ref) < 1e-5
+    else:
+        assert rel(outs[0], ref) < 1e-5
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_gemm_splitk_taps(dev):
+    """Split-K in taps mode (a streaming chunk's conv GEMM) equals the tile kernel's result for the same call."""
+    H, lens = 512, [50, 50]
+    g = torch.Generator(device=dev).manual_seed(3)
+    R, N = len(lens), sum(lens)
+    P = torch.randn(N + 2 * R, H, device=dev, generator=g).bfloat16()
+    Wfm = (torch.randn(H, 3 * H, device=dev, generator=g) / (3 * H) ** 0.5).bfloat16()
+    bias = torch.randn(H, device=dev, generator=g)
+    tok_row = [r for r, t in enumerate(lens) for _ in range(t)]
+    a_src = torch.tensor([i + 2 * r for i, r in enumerate(tok_row)], dtype=torch.int32, device=dev)
+    full = torch.cat([P[a_src.long() + j] for j in range(3)], 1).float()
+    ref = full @ Wfm.float().t() + bias
+    out = torch.zeros(N, H, device=dev)
+    _gemm(P, Wfm, bias, out, 3, a_src=a_src, lda=H, K=3 * H, ws=torch.empty(16 << 20, dtype=torch.uint8, device=dev))
+    assert rel(out, ref) < 1e-5
 
 
 @pytest.mark.parametrize("lens", [[5, 0, 1, 2, 3, 40, 0, 17, 1, 56], [400] * 3])
