@@ -2,9 +2,10 @@
 mel frames, chunk-causal attention with chunk 50), random-init weights, synthetic inputs resident in HBM.
 
 Prints one JSON line: mel frames/s of the 16 streams' output (value), audio-seconds/s, per-chunk p50 latency of a
-streaming chunk (300-frame cached prompt + 50 new frames, one stream, CFG pair, 10 steps, + HiFT), the roofline of
-the dominant kernel (the DiT's conv1 GEMM, timed with HIP events on its own stream) and the fp32 CPU oracle baseline
-timed on a bounded sample on this host.
+streaming chunk (300-frame cached prompt + 50 new frames, one stream, CFG pair, 10 steps, + HiFT), the ragged variant
+of the 16-stream workload (lengths uniform 150-450), HiFT alone (16 rows, 50-400 frames, fp32 and bf16 decoder), the
+roofline of the dominant kernel (the DiT's conv1 GEMM, timed with HIP events on its own stream) and the fp32 CPU
+oracle baseline timed on a bounded sample on this host.
 """
 
 from __future__ import annotations
@@ -50,6 +51,7 @@ def main() -> int:
     ap.add_argument("--no-hift", action="store_true")
     ap.add_argument("--latency-reps", type=int, default=20)
     ap.add_argument("--hift-fp32", action="store_true", help="HiFT decoder in strict fp32 (default: bf16 MFMA decoder)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the ragged-length and HiFT-alone measurements")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no sharding or collectives); use --gpus 1", file=sys.stderr)
@@ -67,7 +69,7 @@ def main() -> int:
     model = DiTModel(W, cfg)
     model.drop_table_weights()
     n, T = args.streams, args.frames
-    fd = FastDiT(model, n_slots=max(8192, 2 * n * T + 4096), max_streams=n + 2, use_graphs=True)
+    fd = FastDiT(model, n_slots=max(8192, 4 * n * 450 + 4096), max_streams=2 * n + 2, use_graphs=True)
     g = torch.Generator().manual_seed(2)
     mus = [torch.randn(cfg.mel, T, generator=g).to(dev) for _ in range(n)]
     spks = torch.randn(n, cfg.mel, generator=g).to(dev)
@@ -78,7 +80,7 @@ def main() -> int:
         from t2w_amd.hift import HiFTModel
 
         Wh = init_hift(HiFTConfig(), seed=3)
-        hift = HiFTModel(Wh, HiFTConfig(), decode_bf16=not args.hift_fp32)
+        hift = HiFTModel(Wh, HiFTConfig(), decode_bf16=not args.hift_fp32, use_graphs=True)
         hsrc = torch.zeros(n, 1, 0, device=dev)
         hnoise = hift.noise([1000 + i for i in range(n)], T * hift.cfg.upsample_scale)
 
@@ -156,6 +158,10 @@ def main() -> int:
                 ts.append(time.perf_counter() - a)
         lat = float(np.median(ts) * 1e3)
 
+    extra = {}
+    if not args.no_extra:
+        extra = extra_workloads(args, cfg, fd, spks, hift, Wh if hift is not None else None)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(W, T, args.chunk, hift_weights=Wh if hift is not None else None)
@@ -180,13 +186,74 @@ def main() -> int:
         "p50_chunk_latency_ms": lat,
         "dit_solve_ms": dit_dt * 1e3,
         "dit_mfma_frac": (gemm_f + attn_f) / dit_dt / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-        "roofline": {"bound": "mfma", "kernel": "gemm_lds_kernel<256,256,4,2,EPI_BF16,taps> (DiT conv1)", "achieved": k_tflops,
+        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<256,256,4,2,EPI_BF16,taps> (DiT conv1)", "achieved": k_tflops,
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": k_tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
                      "launch_ms": k_ms, "flops_per_launch": 2.0 * N * H * 3 * H},
         "cpu_baseline": cpu,
+        **extra,
     }
     print(json.dumps(res))
     return 0
+
+
+def extra_workloads(args, cfg, fd, spks, hift, Wh) -> dict:
+    """The ragged 16-stream workload (lengths uniform 150-450, seed 2; DiT solve + HiFT of the ragged mels) and HiFT
+    alone (16 rows of mel ~ N(-5, 2), lengths uniform 50-400, seed 3), each timed over args.steps calls after a
+    warm-up call."""
+    from t2w_amd.config import HiFTConfig
+    from t2w_amd.hift import HiFTModel
+
+    dev = "cuda"
+    n = args.streams
+    rng = np.random.default_rng(2)
+    lens = [int(x) for x in rng.integers(150, 451, size=n)]
+    g = torch.Generator().manual_seed(2)
+    mus = [torch.randn(cfg.mel, t, generator=g).to(dev) for t in lens]
+    caches = [fd.new_cache() for _ in range(n)]
+    hnz = None
+    if hift is not None:
+        ri, nz = hift.noise([2000 + i for i in range(n)], max(lens) * 480)
+        hnz = torch.cat([nz[i, : t * 480] for i, t in enumerate(lens)])
+
+    def ragged():
+        mels = fd.solve(caches, mus, spks, None, [False] * n, chunk=args.chunk)
+        if hift is not None:
+            hift.forward_packed(lens, torch.cat([m.t() for m in mels]), hnz, None, 0)
+
+    ragged()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ragged()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    for c in caches:
+        fd.release(c)
+    out = {"ragged_b32": {"mel_frames_per_s": sum(lens) / dt, "ms_per_step": dt * 1e3, "frames": sum(lens),
+                          "lengths": "uniform 150-450 (numpy default_rng(2))", "hift": hift is not None}}
+    if Wh is None:
+        return out
+    rng = np.random.default_rng(3)
+    hl = [int(x) for x in rng.integers(50, 401, size=16)]
+    g = torch.Generator().manual_seed(3)
+    mel_tm = torch.cat([torch.randn(t, cfg.mel, generator=g) * 2 - 5 for t in hl]).to(dev)
+    res = {"rows": 16, "lengths": "uniform 50-400 (numpy default_rng(3))", "frames": sum(hl)}
+    for tag, bf in (("fp32", False), ("bf16", True)):
+        hm = HiFTModel(Wh, HiFTConfig(), decode_bf16=bf, use_graphs=True)
+        ri, nz = hm.noise([3000 + i for i in range(16)], max(hl) * 480)
+        ntm = torch.cat([nz[i, : t * 480] for i, t in enumerate(hl)])
+        hm.forward_packed(hl, mel_tm, ntm, None, 0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            hm.forward_packed(hl, mel_tm, ntm, None, 0)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / args.steps
+        res[f"{tag}_samples_per_s"] = sum(hl) * 480 / dt
+        res[f"{tag}_ms_per_call"] = dt * 1e3
+        del hm
+    out["hift_alone"] = res
+    return out
 
 
 def cpu_baseline(W, T: int, chunk: int, hift_weights=None) -> dict:

@@ -24,10 +24,17 @@ def chunk_noise_seed(noise_seed: int, chunk: int) -> int:
 
 
 class HiFTModel:
-    def __init__(self, W: dict, cfg: HiFTConfig = HiFTConfig(), device: str = "cuda", decode_bf16: bool = False):
-        """``decode_bf16``: the decoder convs on bf16 MFMA (fp32 activations); f0 predictor and source stay fp32."""
+    def __init__(self, W: dict, cfg: HiFTConfig = HiFTConfig(), device: str = "cuda", decode_bf16: bool = False,
+                 use_graphs: bool = False, max_graphs: int = 32):
+        """``decode_bf16``: the decoder convs on bf16 MFMA (fp32 activations); f0 predictor and source stay fp32.
+        ``use_graphs``: calls without overrides replay one captured graph per (row lengths, source-cache length), the
+        role of ``HiFTGraphs`` (``engine/runtime/hift_graph.py:22-88``): inputs are copied into the graph's static
+        buffers, outputs are returned as copies; at most ``max_graphs`` graphs are kept (least recently used dropped)."""
         self.cfg, self.device = cfg, device
         self.decode_bf16 = decode_bf16
+        self.use_graphs, self.max_graphs = use_graphs, max_graphs
+        self.graphs: dict[tuple, dict] = {}
+        self.counts = {"graph": 0, "eager": 0}
         f32 = lambda t: t.to(device=device, dtype=torch.float32).contiguous()  # noqa: E731
         self._keep = []
 
@@ -100,6 +107,8 @@ class HiFTModel:
 
     def __del__(self):
         try:
+            for g in getattr(self, "graphs", {}).values():
+                _lib.lib().t2w_graph_destroy(g["graph"])
             if getattr(self, "handle", None) is not None:
                 _lib.lib().t2w_hift_destroy(self.handle)
         except Exception:
@@ -126,6 +135,9 @@ class HiFTModel:
                        f0_override=None, source_override=None, want_f0: bool = False):
         """Rows of ``frames[i]`` mel frames, packed time-major: mel [sum T, mel], noise [sum 480 T, dim], cache_source
         [n, S].  Returns (speech [sum 480 T], source [sum 480 T], f0 [sum T] or None)."""
+        if self.use_graphs and f0_override is None and source_override is None and not want_f0:
+            return self._forward_graph(frames, mel_tm, noise_tm, cache_source, S)
+        self.counts["eager"] += 1
         L = _lib.lib()
         n = len(frames)
         fr = (C.c_int * n)(*frames)
@@ -144,6 +156,52 @@ class HiFTModel:
                                       _lib.ptr(f0_override), _lib.ptr(source_override), speech.data_ptr(), source.data_ptr(), _lib.ptr(f0),
                                       ws.data_ptr(), ws.numel(), int(self.decode_bf16), _lib.stream_handle()), "hift_forward")
         return speech, source, f0
+
+    def _forward_graph(self, frames: list[int], mel_tm: torch.Tensor, noise_tm: torch.Tensor, cache_source, S: int):
+        L = _lib.lib()
+        key = (tuple(frames), S)
+        g = self.graphs.pop(key, None)
+        if g is None:
+            if len(self.graphs) >= self.max_graphs:
+                old = self.graphs.pop(next(iter(self.graphs)))
+                L.t2w_graph_destroy(old["graph"])
+            n = len(frames)
+            fr = (C.c_int * n)(*frames)
+            plan = (C.c_int * L.t2w_hift_plan_ints(n))()
+            _lib.check(L.t2w_hift_plan(self.handle, n, fr, plan), "hift_plan")
+            ns = sum(frames) * self.cfg.upsample_scale
+            dev = self.device
+            g = {"fr": fr, "plan": torch.from_numpy(np.ctypeslib.as_array(plan).copy()).to(dev),
+                 "mel": torch.empty(sum(frames), self.cfg.mel, device=dev), "noise": torch.empty(ns, self.dim, device=dev),
+                 "cs": torch.empty(n, S, device=dev) if S > 0 else None,
+                 "speech": torch.empty(ns, device=dev), "source": torch.empty(ns, device=dev),
+                 "ws": torch.empty(L.t2w_hift_workspace_bytes(self.handle, n, fr), dtype=torch.uint8, device=dev), "graph": None}
+        g["mel"].copy_(mel_tm)
+        g["noise"].copy_(noise_tm)
+        if S > 0:
+            g["cs"].copy_(cache_source.reshape(len(frames), S))
+        if g["graph"] is None:
+            cap = self._capture_stream()  # capture needs a non-default stream; replays go on the caller's
+            cap.wait_stream(torch.cuda.current_stream())
+            cst = cap.cuda_stream
+            _lib.check(L.t2w_graph_begin(cst), "graph_begin")
+            rc = L.t2w_hift_forward(self.handle, len(frames), g["fr"], g["plan"].data_ptr(), g["mel"].data_ptr(), g["noise"].data_ptr(),
+                                    _lib.ptr(g["cs"]), S, None, None, g["speech"].data_ptr(), g["source"].data_ptr(), None,
+                                    g["ws"].data_ptr(), g["ws"].numel(), int(self.decode_bf16), cst)
+            h = C.c_void_p()
+            rc2 = L.t2w_graph_end(cst, C.byref(h))
+            _lib.check(rc, "hift_forward (capture)")
+            _lib.check(rc2, "graph_end")
+            g["graph"] = h
+        self.graphs[key] = g  # most recently used last
+        _lib.check(L.t2w_graph_launch(g["graph"], _lib.stream_handle()), "graph_launch")
+        self.counts["graph"] += 1
+        return g["speech"].clone(), g["source"].clone(), None
+
+    def _capture_stream(self):
+        if getattr(self, "_cap", None) is None:
+            self._cap = torch.cuda.Stream()
+        return self._cap
 
     @torch.inference_mode()
     def forward_noise(self, mel: torch.Tensor, cache_source: torch.Tensor, rand_ini: torch.Tensor, noise: torch.Tensor):

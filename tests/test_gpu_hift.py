@@ -115,3 +115,24 @@ def test_forward_bf16_end_to_end(dev, case):
     e = rel(sp.cpu(), rsp)
     print("bf16 end-to-end speech rel-L2", e, "source", rel(src.cpu(), rsrc))
     assert e < 1e-2
+
+
+def test_hift_graphs_equal_eager():
+    """Graph replays (one graph per row lengths and source-cache length) equal eager calls bit for bit, replay after
+    replay with new inputs, eager work and synchronisations in between; a second key gets its own graph."""
+    W = init_hift(HiFTConfig(), seed=5)
+    eager = HiFTModel(W, HiFTConfig(), decode_bf16=True)
+    graphed = HiFTModel(W, HiFTConfig(), decode_bf16=True, use_graphs=True)
+    g = torch.Generator().manual_seed(8)
+    for rep, (lens, S) in enumerate([([58, 58], 3840), ([58, 58], 3840), ([50, 20, 7], 0), ([58, 58], 3840), ([50, 20, 7], 0)]):
+        mel = [torch.randn(t, 80, generator=g) * 2 - 5 for t in lens]
+        mel_tm = torch.cat(mel).cuda()
+        ri, nz = eager.noise([rep * 10 + i for i in range(len(lens))], max(lens) * 480)
+        noise_tm = torch.cat([nz[i, : t * 480] for i, t in enumerate(lens)])
+        cs = torch.randn(len(lens), S, generator=g).cuda() * 0.1 if S else None
+        sp_e, src_e, _ = eager.forward_packed(lens, mel_tm, noise_tm, cs, S)
+        torch.cuda.synchronize()
+        sp_g, src_g, _ = graphed.forward_packed(lens, mel_tm, noise_tm, cs, S)
+        torch.cuda.synchronize()
+        assert torch.equal(sp_e, sp_g) and torch.equal(src_e, src_g), (rep, lens)
+    assert graphed.counts["graph"] == 5 and len(graphed.graphs) == 2
