@@ -52,6 +52,7 @@ def main() -> int:
     ap.add_argument("--latency-reps", type=int, default=20)
     ap.add_argument("--hift-fp32", action="store_true", help="HiFT decoder in strict fp32 (default: bf16 MFMA decoder)")
     ap.add_argument("--no-extra", action="store_true", help="skip the ragged-length and HiFT-alone measurements")
+    ap.add_argument("--no-fp8", action="store_true", help="skip the fp8 (e4m3 weights, MX fp8 activations) measurement")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no sharding or collectives); use --gpus 1", file=sys.stderr)
@@ -66,7 +67,7 @@ def main() -> int:
     dev = "cuda"
     cfg = DiTConfig()
     W = init_dit(cfg, seed=2)
-    model = DiTModel(W, cfg)
+    model = DiTModel(W, cfg, fp8=not args.no_fp8)
     model.drop_table_weights()
     n, T = args.streams, args.frames
     fd = FastDiT(model, n_slots=max(8192, 4 * n * 450 + 4096), max_streams=2 * n + 2, use_graphs=True)
@@ -159,8 +160,11 @@ def main() -> int:
         lat = float(np.median(ts) * 1e3)
 
     extra = {}
+    if not args.no_fp8:
+        extra["fp8"] = fp8_workload(args, cfg, model, mus, spks, hift, hsrc if hift is not None else None,
+                                    hnoise if hift is not None else None, step)
     if not args.no_extra:
-        extra = extra_workloads(args, cfg, fd, spks, hift, Wh if hift is not None else None)
+        extra.update(extra_workloads(args, cfg, fd, spks, hift, Wh if hift is not None else None))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -194,6 +198,46 @@ def main() -> int:
     }
     print(json.dumps(res))
     return 0
+
+
+def fp8_workload(args, cfg, model, mus, spks, hift, hsrc, hnoise, bf16_step) -> dict:
+    """The same 16 x 400 workload with the block GEMMs on fp8 MFMA (e4m3 weights with per-output-channel scales, MX
+    fp8 activations); error of its mels against the bf16 solve's on identical inputs and weights."""
+    from t2w_amd.dit import FastDiT
+
+    n = len(mus)
+    T = int(mus[0].shape[1])
+    f8 = FastDiT(model, n_slots=max(8192, 2 * n * T + 4096), max_streams=n + 2, use_graphs=True, fp8=True)
+    caches = [f8.new_cache() for _ in range(n)]
+
+    def step():
+        mels = f8.solve(caches, mus, spks, None, [False] * n, chunk=args.chunk)
+        if hift is not None:
+            hift.forward_noise(torch.stack(mels), hsrc, *hnoise)
+        return mels
+
+    ref = bf16_step()
+    got = step()
+    torch.cuda.synchronize()
+    d = torch.cat([(a - b).flatten() for a, b in zip(got, ref)])
+    r = torch.cat([b.flatten() for b in ref])
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    t1 = time.perf_counter()
+    for _ in range(max(1, args.steps // 2)):
+        f8.solve(caches, mus, spks, None, [False] * n, chunk=args.chunk)
+    torch.cuda.synchronize()
+    dit_dt = (time.perf_counter() - t1) / max(1, args.steps // 2)
+    for c in caches:
+        f8.release(c)
+    del f8
+    return {"mel_frames_per_s": n * T / dt, "ms_per_step": dt * 1e3, "dit_solve_ms": dit_dt * 1e3,
+            "mel_rel_l2_vs_bf16": float(d.norm() / r.norm()), "mel_max_abs_vs_bf16": float(d.abs().max()),
+            "config": f"{n} streams x {T} frames, CFG B={2 * n}, chunk {args.chunk}, block GEMMs fp8 e4m3 / MX fp8, "
+                      "in_proj / final linear / attention bf16" + ("" if hift is None else " + HiFT")}
 
 
 def extra_workloads(args, cfg, fd, spks, hift, Wh) -> dict:

@@ -61,8 +61,22 @@ typedef struct {
   const float* dts;                           /* HOST pointer [steps]: Euler step sizes */
 } t2w_dit_globals;
 
+/* fp8 copies of a block's six GEMM weights (no counterpart in the reference; its fp8 convention of
+ * engine/runtime/fp8.py:15-37): OCP e4m3 codes with the same layouts as t2w_dit_block, and fp32 per-output-channel
+ * scales max|w_n| / 448. */
+typedef struct {
+  const void* qkv_w8; const float* qkv_ws;
+  const void* proj_w8; const float* proj_ws;
+  const void* c1_w8; const float* c1_ws;
+  const void* c2_w8; const float* c2_ws;
+  const void* fc1_w8; const float* fc1_ws;
+  const void* fc2_w8; const float* fc2_ws;
+} t2w_dit_block_fp8;
+
 int t2w_dit_create(const t2w_dit_dims* dims, t2w_dit** out);
 int t2w_dit_set_block(t2w_dit* m, int block, const t2w_dit_block* w);
+/* fp8 weights of a block; once every block has them, solves may set t2w_solve_args.fp8 */
+int t2w_dit_set_block_fp8(t2w_dit* m, int block, const t2w_dit_block_fp8* w);
 int t2w_dit_set_globals(t2w_dit* m, const t2w_dit_globals* g);
 void t2w_dit_destroy(t2w_dit* m);
 
@@ -108,8 +122,10 @@ typedef struct {
   void* conv_pool;          /* [row slots, steps, depth, 2, 2, H] bf16 */
   void* workspace;
   size_t workspace_bytes;
+  int fp8;                  /* 1: the block GEMMs on fp8 MFMA (e4m3 weights, MX fp8 activations; needs fp8 weights) */
 } t2w_solve_args;
 
+/* includes the fp8 activation buffers once the model has fp8 weights */
 size_t t2w_dit_workspace_bytes(const t2w_dit* m, int n_tok, int n_rows);
 int t2w_dit_solve(const t2w_dit* m, const t2w_solve_args* a, void* stream);
 /* One estimator evaluation at Euler step `step`'s key/value and conv-cache layers with the given tables
@@ -132,6 +148,14 @@ int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, 
 int t2w_gemm_bf16_ws(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                      void* C, int ldc, int M, int N, int K, int epi, void* workspace, size_t workspace_bytes,
                      void* stream);
+/* MX fp8 quantization (no counterpart in the reference; the fp8 weight convention of engine/runtime/fp8.py:15-37 with
+ * activations in 32-value K blocks): x [M, K] bf16 -> q [M, K] OCP e4m3 and scales [M, K / 32] E8M0, each block scaled
+ * by the smallest power of two that keeps its largest magnitude within 448.  K % 32 == 0. */
+int t2w_quant_mx8(const void* x, int ldx, int M, int K, void* q, int ldq, void* scales, void* stream);
+/* C = epilogue(dequant(A) . dequant(W)^T + bias) on fp8 MFMA: A [M, K] e4m3 with MX scales a_scale[row * a_sld + k / 32]
+ * (taps mode as t2w_gemm_bf16, rows = frames), W [N, K] e4m3 scaled per output channel by w_scale[N].  K % 128 == 0. */
+int t2w_gemm_fp8(const void* A, int lda, const int* a_src, const void* a_scale, int a_sld, const void* W, const float* w_scale,
+                 const float* bias, const float* gate, void* C, int ldc, int M, int N, int K, int epi, void* stream);
 int t2w_ln_mod(const float* h, const float* shift, const float* scale1, float eps, void* out, int N, int H,
                void* stream);
 int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const float* kw, const float* kb, float eps,

@@ -41,7 +41,12 @@ class SolveArgs(C.Structure):
     _fields_ = [(n, I) for n in ("n_tok", "n_rows", "half", "n_tiles", "chunk")] + \
                [(n, P) for n in ("x0", "stat", "in_rows", "out", "tok_row", "tok_pos", "a_src", "new_slot", "row_start", "row_len",
                                  "row_kv_off", "row_kv_len", "conv_rd", "conv_wr", "kv_idx", "tiles", "k_pool", "v_pool")] + \
-               [("pool_layer_stride", C.c_longlong), ("conv_pool", P), ("workspace", P), ("workspace_bytes", C.c_size_t)]
+               [("pool_layer_stride", C.c_longlong), ("conv_pool", P), ("workspace", P), ("workspace_bytes", C.c_size_t), ("fp8", I)]
+
+
+class DitBlockFp8(C.Structure):
+    _fields_ = [(n, P) for n in ("qkv_w8", "qkv_ws", "proj_w8", "proj_ws", "c1_w8", "c1_ws", "c2_w8", "c2_ws", "fc1_w8", "fc1_ws",
+                                 "fc2_w8", "fc2_ws")]
 
 
 class HiftDims(C.Structure):
@@ -78,6 +83,9 @@ _SIGS = {
     "t2w_gemm_bf16": (I, [P, I, P, P, P, P, P, I, I, I, I, I, P]),
     "t2w_gemm_bf16_tile": (I, [P, I, P, P, P, P, P, I, I, I, I, I, I, P]),
     "t2w_gemm_bf16_ws": (I, [P, I, P, P, P, P, P, I, I, I, I, I, P, C.c_size_t, P]),
+    "t2w_quant_mx8": (I, [P, I, I, I, P, I, P, P]),
+    "t2w_dit_set_block_fp8": (I, [P, I, P]),
+    "t2w_gemm_fp8": (I, [P, I, P, P, I, P, P, P, P, P, I, I, I, I, I, P]),
     "t2w_ln_mod": (I, [P, P, P, F, P, I, I, P]),
     "t2w_qk_norm_scatter": (I, [P, P, P, P, P, F, P, P, P, P, I, I, P]),
     "t2w_attention": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, F, P]),

@@ -187,6 +187,28 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
 #undef T2W_LSTORE
   if (!active || myq >= T) return;
   const float inv = 1.0f / l;
+  if (a.out8) {
+    // MX fp8: d 0-31 (o0) and 32-63 (o1) are the head's two blocks, each spread over this lane and its partner
+    float m0 = 0.f, m1 = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { m0 = fmaxf(m0, fabsf(o0[r])); m1 = fmaxf(m1, fabsf(o1[r])); }
+    m0 = fmaxf(m0, __shfl_xor(m0, 32, 64)) * inv;
+    m1 = fmaxf(m1, __shfl_xor(m1, 32, 64)) * inv;
+    const int e0 = mx_exp(m0), e1 = mx_exp(m1);
+    uint8_t* qp = a.out8 + (size_t)(start + myq) * H + head * 64;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = g * 8 + half * 4;
+      *(uint32_t*)(qp + d) = mx_pack4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv, e0);
+      *(uint32_t*)(qp + 32 + d) = mx_pack4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv, e1);
+    }
+    if (half == 0) {
+      uint8_t* sp = a.out8s + (size_t)(start + myq) * (H / 32) + head * 2;
+      sp[0] = (uint8_t)(e0 + 127);
+      sp[1] = (uint8_t)(e1 + 127);
+    }
+    return;
+  }
   bf16_t* op = a.out + (size_t)(start + myq) * H + head * 64;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {

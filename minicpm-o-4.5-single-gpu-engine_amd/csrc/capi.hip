@@ -44,6 +44,13 @@ struct t2w_dit {
   t2w_dit_dims d;
   std::vector<t2w_dit_block> blocks;
   std::vector<bool> block_set;
+  std::vector<t2w_dit_block_fp8> blocks8;
+  std::vector<bool> block8_set;
+  bool fp8_ready() const {
+    for (bool b : block8_set)
+      if (!b) return false;
+    return !block8_set.empty();
+  }
   t2w_dit_globals g;
   std::vector<float> dts;
   bool globals_set = false;
@@ -54,13 +61,16 @@ namespace {
 struct Work {  // carve of the caller's workspace for n tokens, R rows
   bf16_t* a_in; float* x; float* h; bf16_t* abuf; bf16_t* big; bf16_t* q; bf16_t* ao; bf16_t* P; float* dphi;
   float* part; size_t part_bytes;  // split-K partials of the GEMMs of calls with few tokens
+  // fp8 mode: MX fp8 activations (codes, block scales) of the qkv / fc1 inputs, the attention output, the conv frame
+  // buffer and the fc1 output
+  uint8_t *a8, *a8s, *o8, *o8s, *P8, *P8s, *b8, *b8s;
 };
 
 // calls of up to this many tokens get a split-K partial area of SPLITK_BYTES
 constexpr int SPLITK_MAX_TOK = 1024;
 constexpr size_t SPLITK_BYTES = (size_t)16 << 20;
 
-size_t carve(const t2w_dit_dims& d, int N, int R, char* base, Work* w) {
+size_t carve(const t2w_dit_dims& d, int N, int R, bool fp8, char* base, Work* w) {
   const int H = d.hidden, M = d.mel;
   const size_t bigc = (size_t)N * (size_t)(3 * H > d.ffn ? 3 * H : d.ffn);
   size_t off = 0;
@@ -77,6 +87,14 @@ size_t carve(const t2w_dit_dims& d, int N, int R, char* base, Work* w) {
   t.dphi = (float*)take((size_t)N * M * 4);
   t.part_bytes = N <= SPLITK_MAX_TOK ? SPLITK_BYTES : 0;
   t.part = t.part_bytes ? (float*)take(t.part_bytes) : nullptr;
+  t.a8 = t.a8s = t.o8 = t.o8s = t.P8 = t.P8s = t.b8 = t.b8s = nullptr;
+  if (fp8) {
+    const size_t F = (size_t)d.ffn, NP = (size_t)N + 2 * R;
+    t.a8 = (uint8_t*)take((size_t)N * H); t.a8s = (uint8_t*)take((size_t)N * H / 32);
+    t.o8 = (uint8_t*)take((size_t)N * H); t.o8s = (uint8_t*)take((size_t)N * H / 32);
+    t.P8 = (uint8_t*)take(NP * H); t.P8s = (uint8_t*)take(NP * H / 32);
+    t.b8 = (uint8_t*)take((size_t)N * F); t.b8s = (uint8_t*)take((size_t)N * F / 32);
+  }
   if (w) *w = t;
   return off;
 }
@@ -91,7 +109,7 @@ int check_model(const t2w_dit* m) {
 
 GemmArgs gemm_args(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate, void* C,
                    int ldc, int M, int N, int K, const Work* w = nullptr) {
-  GemmArgs g;
+  GemmArgs g{};
   g.ws = w ? w->part : nullptr;
   g.ws_bytes = w ? w->part_bytes : 0;
   g.A = (const bf16_t*)A;
@@ -110,6 +128,16 @@ GemmArgs gemm_args(const void* A, int lda, const int* a_src, const void* W, cons
   return g;
 }
 
+// fp8 GEMM: A as MX fp8 codes with block scales (rows a_sld apart), W as e4m3 codes with per-channel scales
+GemmArgs gemm8(const uint8_t* A, int lda, const int* a_src, const uint8_t* as, const void* W8, const float* ws,
+               const float* bias, const float* gate, void* C, int ldc, int M, int N, int K) {
+  GemmArgs g = gemm_args(A, lda, a_src, W8, bias, gate, C, ldc, M, N, K);
+  g.a_scale = as;
+  g.a_sld = lda / 32;
+  g.w_scale = ws;
+  return g;
+}
+
 // One estimator evaluation from w.a_in (bf16 [N, 4 mel]) to w.dphi (fp32 [N, mel]) at Euler step `step`.
 int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int step, const float* mods,
                   const float* fmods, float* dphi, hipStream_t st) {
@@ -117,13 +145,20 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
   const int N = a->n_tok, R = a->n_rows, H = d.hidden, F = d.ffn, M = d.mel, D = d.depth;
   T2W_CHECK(gemm_bf16(gemm_args(w.a_in, 4 * M, nullptr, m->g.in_w, m->g.in_b, nullptr, w.h, H, N, H, 4 * M, &w), EPI_F32, st), "in_proj");
   const long long cstride = (long long)d.steps * D * 4 * H;
+  const bool f8 = a->fp8 != 0;
   for (int b = 0; b < D; ++b) {
     const t2w_dit_block& k = m->blocks[b];
+    const t2w_dit_block_fp8* k8 = f8 ? &m->blocks8[b] : nullptr;
     const float* md = mods + (size_t)b * 9 * H;
     const float *sh_a = md, *sc_a = md + H, *g_a = md + 2 * H, *sh_m = md + 3 * H, *sc_m = md + 4 * H, *g_m = md + 5 * H;
     const float *sh_c = md + 6 * H, *sc_c = md + 7 * H, *g_c = md + 8 * H;
-    T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st), "ln_mod msa");
-    T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H, &w), EPI_BF16, st), "qkv");
+    if (f8) {
+      T2W_CHECK(ln_mod_mx8(w.h, sh_a, sc_a, d.eps_block, w.a8, w.a8s, N, H, st), "ln_mod msa");
+      T2W_CHECK(gemm_bf16(gemm8(w.a8, H, nullptr, w.a8s, k8->qkv_w8, k8->qkv_ws, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H), EPI_BF16, st), "qkv");
+    } else {
+      T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st), "ln_mod msa");
+      T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H, &w), EPI_BF16, st), "qkv");
+    }
     const size_t layer = (size_t)(step * D + b) * (size_t)a->pool_layer_stride;
     bf16_t* kp = (bf16_t*)a->k_pool + layer;
     bf16_t* vp = (bf16_t*)a->v_pool + layer;
@@ -132,23 +167,43 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     at.q = w.q; at.k_pool = kp; at.v_pool = vp; at.out = w.ao; at.kv_idx = a->kv_idx; at.row_start = a->row_start;
     at.row_len = a->row_len; at.row_kv_off = a->row_kv_off; at.row_kv_len = a->row_kv_len; at.tiles = a->tiles;
     at.n_tiles = a->n_tiles; at.heads = d.heads; at.chunk = a->chunk; at.scale = 1.0f / sqrtf((float)d.head_dim);
+    if (f8) { at.out8 = w.o8; at.out8s = w.o8s; }
     T2W_CHECK(attention(at, st), "attention");
-    T2W_CHECK(gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F32, st), "proj");
+    if (f8)
+      T2W_CHECK(gemm_bf16(gemm8(w.o8, H, nullptr, w.o8s, k8->proj_w8, k8->proj_ws, k.proj_b, g_a, w.h, H, N, H, H), EPI_RESID_F32, st), "proj");
+    else
+      T2W_CHECK(gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F32, st), "proj");
     ConvPlace cp;
     cp.P = w.P; cp.tok_row = a->tok_row; cp.tok_pos = a->tok_pos; cp.row_start = a->row_start; cp.row_len = a->row_len;
     cp.rd = a->conv_rd; cp.wr = a->conv_wr; cp.cache_stride = cstride; cp.N = N; cp.R = R;
+    if (f8) { cp.P8 = w.P8; cp.P8s = w.P8s; }
     bf16_t* cbase = (bf16_t*)a->conv_pool + ((size_t)(step * D + b) * 2) * 2 * H;
     cp.cache_base = cbase;
     cp.cache_out_base = cbase;
     T2W_CHECK(ln_mod_conv(w.h, sh_c, sc_c, d.eps_block, cp, H, st), "ln_mod_conv");
-    T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), EPI_BF16, st), "conv1");
+    if (f8)
+      T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c1_w8, k8->c1_ws, k.c1_b, nullptr, w.ao, H, N, H, 3 * H), EPI_BF16, st), "conv1");
+    else
+      T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), EPI_BF16, st), "conv1");
     cp.cache_base = cbase + 2 * H;
     cp.cache_out_base = cbase + 2 * H;
     T2W_CHECK(ln_mish_conv(w.ao, k.cln_w, k.cln_b, d.eps_conv, cp, H, st), "ln_mish_conv");
-    T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), EPI_RESID_F32, st), "conv2");
-    T2W_CHECK(ln_mod(w.h, sh_m, sc_m, d.eps_block, w.abuf, N, H, st), "ln_mod mlp");
-    T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.fc1_w, k.fc1_b, nullptr, w.big, F, N, F, H, &w), EPI_GELU_BF16, st), "fc1");
-    T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F32, st), "fc2");
+    if (f8)
+      T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c2_w8, k8->c2_ws, k.c2_b, g_c, w.h, H, N, H, 3 * H), EPI_RESID_F32, st), "conv2");
+    else
+      T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), EPI_RESID_F32, st), "conv2");
+    if (f8) {
+      T2W_CHECK(ln_mod_mx8(w.h, sh_m, sc_m, d.eps_block, w.a8, w.a8s, N, H, st), "ln_mod mlp");
+      GemmArgs g1 = gemm8(w.a8, H, nullptr, w.a8s, k8->fc1_w8, k8->fc1_ws, k.fc1_b, nullptr, w.b8, F, N, F, H);
+      g1.c_scale = w.b8s;
+      g1.c_sld = F / 32;
+      T2W_CHECK(gemm_bf16(g1, EPI_GELU_MX8, st), "fc1");
+      T2W_CHECK(gemm_bf16(gemm8(w.b8, F, nullptr, w.b8s, k8->fc2_w8, k8->fc2_ws, k.fc2_b, g_m, w.h, H, N, H, F), EPI_RESID_F32, st), "fc2");
+    } else {
+      T2W_CHECK(ln_mod(w.h, sh_m, sc_m, d.eps_block, w.abuf, N, H, st), "ln_mod mlp");
+      T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.fc1_w, k.fc1_b, nullptr, w.big, F, N, F, H, &w), EPI_GELU_BF16, st), "fc1");
+      T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F32, st), "fc2");
+    }
   }
   T2W_CHECK(ln_mod(w.h, fmods, fmods + H, d.eps_final, w.abuf, N, H, st), "final norm");
   T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, m->g.out_w, m->g.out_b, nullptr, dphi, M, N, M, H, &w), EPI_F32, st), "final linear");
@@ -159,7 +214,9 @@ int check_args(const t2w_dit* m, const t2w_solve_args* a) {
   if (check_model(m)) return 1;
   if (!a) return fail("null args");
   if (a->n_tok <= 0 || a->n_rows <= 0) return fail("empty call");
-  if (a->workspace_bytes < carve(m->d, a->n_tok, a->n_rows, nullptr, nullptr)) return fail("workspace too small");
+  if (a->fp8 && !m->fp8_ready()) return fail("fp8 solve needs fp8 weights for every block");
+  if (a->fp8 && (m->d.hidden % 128 || m->d.ffn % 128)) return fail("fp8 solve needs hidden and ffn multiples of 128");
+  if (a->workspace_bytes < carve(m->d, a->n_tok, a->n_rows, m->fp8_ready(), nullptr, nullptr)) return fail("workspace too small");
   if (a->chunk < 0) return fail("negative chunk");
   return 0;
 }
@@ -192,6 +249,20 @@ int t2w_dit_set_block(t2w_dit* m, int block, const t2w_dit_block* w) {
   if (!m || !w || block < 0 || block >= m->d.depth) return fail("bad block");
   m->blocks[block] = *w;
   m->block_set[block] = true;
+  return 0;
+}
+
+int t2w_dit_set_block_fp8(t2w_dit* m, int block, const t2w_dit_block_fp8* w) {
+  if (!m || !w || block < 0 || block >= m->d.depth) return fail("bad block");
+  if (!w->qkv_w8 || !w->qkv_ws || !w->proj_w8 || !w->proj_ws || !w->c1_w8 || !w->c1_ws || !w->c2_w8 || !w->c2_ws ||
+      !w->fc1_w8 || !w->fc1_ws || !w->fc2_w8 || !w->fc2_ws)
+    return fail("fp8 block weights incomplete");
+  if (m->blocks8.empty()) {
+    m->blocks8.resize(m->d.depth);
+    m->block8_set.assign(m->d.depth, false);
+  }
+  m->blocks8[block] = *w;
+  m->block8_set[block] = true;
   return 0;
 }
 
@@ -232,7 +303,7 @@ int t2w_dit_build_mods(const t2w_dit* m, const t2w_mod_weights* w, const float* 
 
 size_t t2w_dit_workspace_bytes(const t2w_dit* m, int n_tok, int n_rows) {
   if (!m) return 0;
-  return carve(m->d, n_tok, n_rows, nullptr, nullptr);
+  return carve(m->d, n_tok, n_rows, m->fp8_ready(), nullptr, nullptr);
 }
 
 int t2w_dit_solve(const t2w_dit* m, const t2w_solve_args* a, void* stream) {
@@ -241,7 +312,7 @@ int t2w_dit_solve(const t2w_dit* m, const t2w_solve_args* a, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   const t2w_dit_dims& d = m->d;
   Work w;
-  carve(d, a->n_tok, a->n_rows, (char*)a->workspace, &w);
+  carve(d, a->n_tok, a->n_rows, m->fp8_ready(), (char*)a->workspace, &w);
   T2W_CHECK(pack_inputs(a->x0, a->stat, w.a_in, w.x, a->half, d.mel, st), "pack_inputs");
   for (int s = 0; s < d.steps; ++s) {
     if (run_estimator(m, a, w, s, m->g.mods + (size_t)s * d.depth * 9 * d.hidden, m->g.final_mods + (size_t)s * 2 * d.hidden, w.dphi, st))
@@ -258,7 +329,7 @@ int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const f
   if (step < 0 || step >= m->d.steps) return fail("bad step");
   hipStream_t st = (hipStream_t)stream;
   Work w;
-  carve(m->d, a->n_tok, a->n_rows, (char*)a->workspace, &w);
+  carve(m->d, a->n_tok, a->n_rows, m->fp8_ready(), (char*)a->workspace, &w);
   T2W_CHECK(convert_rows_bf16(a->in_rows, w.a_in, (long long)a->n_tok * 4 * m->d.mel, st), "convert");
   if (run_estimator(m, a, w, step, mods, final_mods, a->out, st)) return 1;
   return 0;
@@ -291,6 +362,27 @@ int t2w_gemm_bf16_ws(const void* A, int lda, const int* a_src, const void* W, co
   g.ws = (float*)workspace;
   g.ws_bytes = workspace ? workspace_bytes : 0;
   T2W_CHECK(gemm_bf16(g, epi, (hipStream_t)stream, -1), "gemm");
+  return 0;
+}
+
+int t2w_quant_mx8(const void* x, int ldx, int M, int K, void* q, int ldq, void* scales, void* stream) {
+  if (K % 32 || ldx % 8 || ldq % 8) return fail("quant_mx8: K % 32, ldx % 8 and ldq % 8 must be 0");
+  T2W_CHECK(quant_mx8((const bf16_t*)x, ldx, M, K, (uint8_t*)q, ldq, (uint8_t*)scales, (hipStream_t)stream), "quant_mx8");
+  return 0;
+}
+
+int t2w_gemm_fp8(const void* A, int lda, const int* a_src, const void* a_scale, int a_sld, const void* W, const float* w_scale,
+                 const float* bias, const float* gate, void* C, int ldc, int M, int N, int K, int epi, void* stream) {
+  if (K % 128) return fail("fp8 gemm: K must be a multiple of 128");
+  if (lda % 16 || a_sld % 4) return fail("fp8 gemm: lda % 16 and a_sld % 4 must be 0");
+  if (epi < 0 || epi > 3) return fail("bad epilogue");
+  if (a_src && (K % lda || lda % 128)) return fail("fp8 taps mode: K must be a multiple of lda, lda of 128");
+  if (!a_scale || !w_scale) return fail("fp8 gemm: scales required");
+  GemmArgs g = gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K);
+  g.a_scale = (const uint8_t*)a_scale;
+  g.a_sld = a_sld;
+  g.w_scale = w_scale;
+  T2W_CHECK(gemm_bf16(g, epi, (hipStream_t)stream, -1), "gemm fp8");
   return 0;
 }
 

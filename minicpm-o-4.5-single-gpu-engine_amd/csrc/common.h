@@ -40,6 +40,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// MX fp8: OCP e4m3 values with one power-of-two (E8M0) scale per 32 consecutive K values.  The scale is the smallest
+// power of two that keeps the block's largest magnitude within e4m3's 448, so nothing clips: with amax = 1.m * 2^E and
+// 448 = 1.75 * 2^8, that exponent is E - 8, plus one when 1.m > 1.75.  Returns the unbiased exponent in [-126, 126].
+__device__ __forceinline__ int mx_exp(float amax) {
+  const uint32_t b = __float_as_uint(amax) & 0x7fffffffu;
+  if (b < 0x00800000u) return -126;  // zero or subnormal block
+  int e = (int)(b >> 23) - 127 - 8 + ((b & 0x7fffffu) > 0x600000u ? 1 : 0);
+  return e < -126 ? -126 : (e > 126 ? 126 : e);
+}
+
+// four values times 2^-se, clamped to +-448 and rounded to nearest even e4m3 (v_cvt_pk_fp8_f32), packed low byte first
+__device__ __forceinline__ uint32_t mx_pack4(float a, float b, float c, float d, int se) {
+  const float inv = __uint_as_float((uint32_t)(127 - se) << 23);
+  auto cl = [](float x) { return fminf(fmaxf(x, -448.0f), 448.0f); };
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(cl(a * inv), cl(b * inv), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(cl(c * inv), cl(d * inv), w, true);
+  return (uint32_t)w;
+}
+
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3), written as x / (1 + 2^(-2 u log2 e)): one exp2, one
   // reciprocal

@@ -51,6 +51,25 @@ __device__ __forceinline__ void store_packed(bf16_t* p, const uint32_t (&o)[VPL 
   }
 }
 
+// MX fp8 store of a row chunk: this lane's VPL values at c0 of a row; the 32-value block's maximum is reduced over its
+// 32 / VPL lanes, and the block's first lane writes the E8M0 scale byte
+template <int VPL>
+__device__ __forceinline__ void store_mx8(const float (&v)[VPL], uint8_t* qrow, uint8_t* srow, int c0) {
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) a = fmaxf(a, fabsf(v[i]));
+#pragma unroll
+  for (int o = 1; o < 32 / VPL; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  const int se = mx_exp(a);
+  uint32_t w[VPL / 4];
+#pragma unroll
+  for (int i = 0; i < VPL / 4; ++i) w[i] = mx_pack4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3], se);
+  if (VPL == 16) *(uint4*)(qrow + c0) = make_uint4(w[0], w[1], w[2], w[3]);
+  else if (VPL == 8) *(uint2*)(qrow + c0) = make_uint2(w[0], w[1]);
+  else *(uint32_t*)(qrow + c0) = w[0];
+  if ((c0 & 31) == 0) srow[c0 >> 5] = (uint8_t)(se + 127);
+}
+
 // LayerNorm statistics over a row spread across the wave: v -> (v - mean) * rstd
 template <int VPL>
 __device__ __forceinline__ void normalize(float (&v)[VPL], int H, float eps) {
@@ -69,9 +88,10 @@ __device__ __forceinline__ void normalize(float (&v)[VPL], int H, float eps) {
   for (int i = 0; i < VPL; ++i) v[i] *= rstd;
 }
 
+// out: bf16 [N, H]; or, with q non-null, MX fp8 codes q [N, H] and block scales qs [N, H / 32]
 template <int VPL>
 __global__ void __launch_bounds__(256) ln_mod_kernel(const float* h, const float* shift, const float* scale1, float eps,
-                                                     bf16_t* out, int N, int H) {
+                                                     bf16_t* out, uint8_t* q, uint8_t* qs, int N, int H) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -83,6 +103,10 @@ __global__ void __launch_bounds__(256) ln_mod_kernel(const float* h, const float
   load_f32<VPL>(shift + c0, sh);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) v[i] = v[i] * sc[i] + sh[i];
+  if (q) {
+    store_mx8<VPL>(v, q + (size_t)n * H, qs + (size_t)n * (H / 32), c0);
+    return;
+  }
   uint32_t o[VPL / 2];
   pack_bf<VPL>(v, o);
   store_packed<VPL>(out + (size_t)n * H + c0, o);
@@ -93,9 +117,11 @@ __global__ void __launch_bounds__(256) ln_mod_kernel(const float* h, const float
 // for rows of fewer than two tokens, produce the new cache from the old one (the reference's _conv_place and
 // _conv_row_cache, engine/runtime/dit_kernels.py:217-248).
 template <int VPL>
-__device__ __forceinline__ void place_token(const ConvPlace& cp, int n, int H, int c0, const uint32_t (&o)[VPL / 2]) {
+__device__ __forceinline__ void place_token(const ConvPlace& cp, int n, int H, int c0, const float (&v)[VPL], const uint32_t (&o)[VPL / 2]) {
   const int r = cp.tok_row[n], t = cp.tok_pos[n], T = cp.row_len[r];
-  store_packed<VPL>(cp.P + (size_t)(n + 2 * r + 2) * H + c0, o);
+  const size_t f = (size_t)(n + 2 * r + 2);
+  if (cp.P8) store_mx8<VPL>(v, cp.P8 + f * H, cp.P8s + f * (H / 32), c0);
+  else store_packed<VPL>(cp.P + f * H + c0, o);
   if (t >= T - 2) store_packed<VPL>(cp.cache_out_base + (size_t)cp.wr[r] * cp.cache_stride + (size_t)(t - T + 2) * H + c0, o);
 }
 
@@ -105,13 +131,24 @@ __device__ __forceinline__ void place_row(const ConvPlace& cp, int r, int H, int
   const bf16_t* ci = cp.cache_base + (size_t)cp.rd[r] * cp.cache_stride + c0;
   bf16_t* co = cp.cache_out_base + (size_t)cp.wr[r] * cp.cache_stride + c0;
   bf16_t* p = cp.P + (size_t)(s + 2 * r) * H + c0;
+  const size_t f = (size_t)(s + 2 * r);
 #pragma unroll
   for (int i = 0; i < VPL / 4; ++i) {
     uint2 a = *(const uint2*)(ci + 4 * i), b = *(const uint2*)(ci + H + 4 * i);
-    *(uint2*)(p + 4 * i) = a;
-    *(uint2*)(p + H + 4 * i) = b;
+    if (!cp.P8) {
+      *(uint2*)(p + 4 * i) = a;
+      *(uint2*)(p + H + 4 * i) = b;
+    }
     if (T == 1) *(uint2*)(co + 4 * i) = b;
     if (T == 0) { *(uint2*)(co + 4 * i) = a; *(uint2*)(co + H + 4 * i) = b; }
+  }
+  if (cp.P8) {  // the cached frames (kept bf16) enter the fp8 frame buffer quantized like the new ones
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float v[VPL];
+      load_bf<VPL>(ci + (size_t)j * H, v);
+      store_mx8<VPL>(v, cp.P8 + (f + j) * H, cp.P8s + (f + j) * (H / 32), c0);
+    }
   }
 }
 
@@ -131,7 +168,7 @@ __global__ void __launch_bounds__(256) ln_mod_conv_kernel(const float* h, const 
     for (int i = 0; i < VPL; ++i) v[i] = v[i] * sc[i] + sh[i];
     uint32_t o[VPL / 2];
     pack_bf<VPL>(v, o);
-    place_token<VPL>(cp, w, H, c0, o);
+    place_token<VPL>(cp, w, H, c0, v, o);
   } else if (w < cp.N + cp.R) {
     place_row<VPL>(cp, w - cp.N, H, c0);
   }
@@ -153,7 +190,7 @@ __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, cons
     for (int i = 0; i < VPL; ++i) v[i] = mish(v[i] * a[i] + b[i]);
     uint32_t o[VPL / 2];
     pack_bf<VPL>(v, o);
-    place_token<VPL>(cp, w, H, c0, o);
+    place_token<VPL>(cp, w, H, c0, v, o);
   } else if (w < cp.N + cp.R) {
     place_row<VPL>(cp, w - cp.N, H, c0);
   }
@@ -315,7 +352,14 @@ inline unsigned blocks_for(long long n, int per) { return (unsigned)((n + per - 
 
 hipError_t ln_mod(const float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H, hipStream_t st) {
   if (N <= 0) return hipSuccess;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, 4)), dim3(256), 0, st, h, shift, scale1, eps, out, N, H));
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, 4)), dim3(256), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H));
+  return hipGetLastError();
+}
+
+hipError_t ln_mod_mx8(const float* h, const float* shift, const float* scale1, float eps, uint8_t* q, uint8_t* qs, int N,
+                      int H, hipStream_t st) {
+  if (N <= 0) return hipSuccess;
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, 4)), dim3(256), 0, st, h, shift, scale1, eps, nullptr, q, qs, N, H));
   return hipGetLastError();
 }
 

@@ -18,6 +18,12 @@
 // of one row.  The epilogue stages each wave's accumulators through LDS and writes whole rows: 32 lanes cover 512
 // contiguous bytes of fp32 (or 256 of bf16), with bias, GELU or the gated fp32 residual applied on the way out.
 //
+// fp8 mode: A and W hold OCP e4m3 codes, so a 128-byte stage row carries 128 K values and the stage is two
+// v_mfma_scale_f32_32x32x64_f8f6f4 steps.  The MFMA applies A's MX block scales itself: a lane holds 16 bytes of each
+// 32-value K block of its row ([k0 + 16 h, +16) and [k0 + 32 + 16 h, +16) for lane half h) and supplies the scale byte
+// of block h, as E8M0.  The scale dwords of a stage (four blocks per row) are loaded with the stage; W's per-channel
+// scale multiplies the accumulator in the epilogue.
+//
 // A operand modes: dense rows, or "taps" rows for the kernel-3 causal convs: row m of A is the three frames starting
 // at frame a_src[m] of a frame buffer whose rows are lda wide (no im2col copy in HBM; the host lays the two cached
 // frames of every packed row in front of its frames).
@@ -41,20 +47,22 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk
 // Output columns n .. n + 3 of one lane: bias (and gate) loaded once, before any output row is touched.
 template <int EPI>
 struct Cols {
-  float4 bias, gate;
+  float4 bias, gate, wsc;
   int n;
   bool full;  // all four columns inside N
   __device__ __forceinline__ Cols(const GemmArgs& g, int n_) : n(n_), full(n_ + 3 < g.N) {
     bias = gate = make_float4(0.f, 0.f, 0.f, 0.f);
+    wsc = make_float4(1.f, 1.f, 1.f, 1.f);
     if (full) {
       bias = *(const float4*)(g.bias + n);
       if (EPI == EPI_RESID_F32) gate = *(const float4*)(g.gate + n);
+      if (g.w_scale) wsc = *(const float4*)(g.w_scale + n);
     }
   }
   // finished output of accumulator values a for full columns (h: the residual row's current values)
   __device__ __forceinline__ float4 apply(float4 a, float4 h) const {
-    float v[4] = {a.x + bias.x, a.y + bias.y, a.z + bias.z, a.w + bias.w};
-    if (EPI == EPI_GELU_BF16) {
+    float v[4] = {a.x * wsc.x + bias.x, a.y * wsc.y + bias.y, a.z * wsc.z + bias.z, a.w * wsc.w + bias.w};
+    if (EPI == EPI_GELU_BF16 || EPI == EPI_GELU_MX8) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
     }
@@ -71,7 +79,7 @@ struct Cols {
   __device__ __forceinline__ void put_partial(const GemmArgs& g, int m, float4 a) const {
     const float v[4] = {a.x, a.y, a.z, a.w};
     for (int e = 0; e < 4 && n + e < g.N; ++e) {
-      const float x = v[e] + g.bias[n + e];
+      const float x = v[e] * (g.w_scale ? g.w_scale[n + e] : 1.0f) + g.bias[n + e];
       const size_t o = (size_t)m * g.ldc + n + e;
       if (EPI == EPI_BF16) ((bf16_t*)g.C)[o] = f2bf(x);
       else if (EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[o] = f2bf(gelu_tanh(x));
@@ -82,17 +90,36 @@ struct Cols {
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
-template <int BM, int BN, int WM, int WN, bool TAPS>
+__device__ __forceinline__ i32x8 join8(uint4 a, uint4 b) {
+  i32x8 r;
+  r[0] = (int)a.x; r[1] = (int)a.y; r[2] = (int)a.z; r[3] = (int)a.w;
+  r[4] = (int)b.x; r[5] = (int)b.y; r[6] = (int)b.z; r[7] = (int)b.w;
+  return r;
+}
+
+template <bool FP8>
+struct FragT { typedef bf16x8 type; };
+template <>
+struct FragT<true> { typedef i32x8 type; };
+
+template <int BM, int BN, int WM, int WN, bool TAPS, bool FP8>
 struct Tile {
   static constexpr int NW = WM * WN;
   static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave sub-tile
   static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA blocks per wave
   static constexpr int APW = BM / 8 / NW, BPW = BN / 8 / NW;  // 1 KB (8-row) load blocks per wave and stage
+  static constexpr int ES = FP8 ? 1 : 2;              // bytes per element
+  static constexpr int BKE = BK * 2 / ES;             // K values per 128-byte stage row
+  static constexpr int NKK = FP8 ? 2 : 4;             // MFMA K steps per stage
+  static constexpr int NSC = FP8 ? TM : 1;            // scale dwords per lane and stage
   static_assert(APW * NW * 8 == BM && BPW * NW * 8 == BN, "tile rows / waves mismatch");
+  typedef typename FragT<FP8>::type frag_t;
 
-  const bf16_t* asrc[APW];
-  const bf16_t* bsrc[BPW];
+  const uint8_t* asrc[APW];
+  const uint8_t* bsrc[BPW];
+  const uint8_t* sbase[NSC];  // fp8: this lane's activation rows' scale rows
   const GemmArgs& g;
   int lane, wave, wm, wn;
 
@@ -104,74 +131,117 @@ struct Tile {
     wn = wave % WN;
     // this lane's 16 bytes of each of its wave's load blocks: tile row blk * 8 + lane / 8, logical chunk (lane % 8) ^ key
     const int lrow = lane >> 3;
+    const uint8_t* A = (const uint8_t*)g.A;
+    const uint8_t* B = (const uint8_t*)g.B;
 #pragma unroll
     for (int p = 0; p < APW; ++p) {
       const int trow = (wave + p * NW) * 8 + lrow;
       const int m = min(m0 + trow, g.M - 1);  // rows past M load row M - 1; their results are never stored
       const int ch = (lane & 7) ^ swz_key(trow);
-      asrc[p] = TAPS ? g.A + (size_t)g.a_src[m] * g.lda + ch * 8 : g.A + (size_t)m * g.lda + ch * 8;
+      asrc[p] = A + (size_t)(TAPS ? g.a_src[m] : m) * g.lda * ES + ch * 16;
     }
 #pragma unroll
     for (int p = 0; p < BPW; ++p) {
       const int trow = (wave + p * NW) * 8 + lrow;
-      bsrc[p] = g.B + (size_t)min(n0 + trow, g.N - 1) * g.ldb + ((lane & 7) ^ swz_key(trow)) * 8;
+      bsrc[p] = B + (size_t)min(n0 + trow, g.N - 1) * g.ldb * ES + ((lane & 7) ^ swz_key(trow)) * 16;
+    }
+    if (FP8) {
+#pragma unroll
+      for (int i = 0; i < NSC; ++i) {
+        const int m = min(m0 + wm * WTM + i * 32 + (lane & 31), g.M - 1);
+        sbase[i] = g.a_scale + (size_t)(TAPS ? g.a_src[m] : m) * g.a_sld;
+      }
     }
   }
 
-  __device__ __forceinline__ void issue(uint4* la, uint4* lb, int kt) const {
-    const int k0 = kt * BK;
-    size_t aoff = k0;
+  // loads of stage kt into (la, lb) and, in fp8 mode, its activation scale dwords into sd
+  __device__ __forceinline__ void issue(uint4* la, uint4* lb, uint32_t (&sd)[NSC], int kt) const {
+    const int k0 = kt * BKE;
+    size_t aoff = (size_t)k0 * ES;
+    int srow = 0, sblk = k0 / 32;
     if (TAPS) {
-      const int tap = k0 / g.tapC;  // a stage never straddles two taps (tapC % 64 == 0)
-      aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);
+      const int tap = k0 / g.tapC;  // a stage never straddles two taps (tapC % BKE == 0)
+      aoff = ((size_t)tap * g.lda + (k0 - tap * g.tapC)) * ES;
+      srow = tap;
+      sblk = (k0 - tap * g.tapC) / 32;
     }
 #pragma unroll
     for (int p = 0; p < APW; ++p)
       __builtin_amdgcn_global_load_lds((const void*)(asrc[p] + aoff), (lds_ptr_t)(la + (wave + p * NW) * 64), 16, 0, 0);
 #pragma unroll
     for (int p = 0; p < BPW; ++p)
-      __builtin_amdgcn_global_load_lds((const void*)(bsrc[p] + k0), (lds_ptr_t)(lb + (wave + p * NW) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(bsrc[p] + (size_t)k0 * ES), (lds_ptr_t)(lb + (wave + p * NW) * 64), 16, 0, 0);
+    if (FP8) {
+#pragma unroll
+      for (int i = 0; i < NSC; ++i) sd[i] = *(const uint32_t*)(sbase[i] + (size_t)srow * g.a_sld + sblk);
+    }
   }
 
-  __device__ __forceinline__ void frag(const uint4* La, const uint4* Lb, int kk, bf16x8 (&af)[TM], bf16x8 (&bf)[TN]) const {
-    const int chunk = kk * 2 + (lane >> 5);
+  __device__ __forceinline__ void frag(const uint4* La, const uint4* Lb, int kk, frag_t (&af)[TM], frag_t (&bf)[TN]) const {
+    if constexpr (FP8) {
+      const int c0 = kk * 4 + (lane >> 5);  // 16-byte pieces of the two 32-value blocks of this K step
 #pragma unroll
-    for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(La[swz(wm * WTM + i * 32 + (lane & 31), chunk)]);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) bf[j] = as_bf16x8(Lb[swz(wn * WTN + j * 32 + (lane & 31), chunk)]);
-  }
-
-  static __device__ __forceinline__ void mma(f32x16 (&acc)[TM][TN], const bf16x8 (&af)[TM], const bf16x8 (&bf)[TN]) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
-  }
-
-  // One K stage from buffers (La, Lb).  Stage kt + 1 must already be in flight into (Na, Nb); after the barrier the
-  // loads of stage kt + 2 go into (La, Lb).
-  __device__ __forceinline__ void stage(f32x16 (&acc)[TM][TN], bf16x8 (&af)[2][TM], bf16x8 (&bf)[2][TN], uint4* La,
-                                        uint4* Lb, const uint4* Na, const uint4* Nb, int kt, int KT) const {
-    constexpr int NV = APW + BPW, ND = TM + TN, NM = TM * TN;
-#pragma unroll
-    for (int kk = 0; kk < 3; ++kk) {
-      frag(La, Lb, kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
-      mma(acc, af[kk & 1], bf[kk & 1]);
-      // MFMA, fragment read, MFMA, ... then the remaining MFMAs
-#pragma unroll
-      for (int x = 0; x < ND; ++x) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WTM + i * 32 + (lane & 31);
+        af[i] = join8(La[swz(r, c0)], La[swz(r, c0 + 2)]);
       }
 #pragma unroll
-      for (int x = ND; x < NM; ++x) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn * WTN + j * 32 + (lane & 31);
+        bf[j] = join8(Lb[swz(r, c0)], Lb[swz(r, c0 + 2)]);
+      }
+    } else {
+      const int chunk = kk * 2 + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(La[swz(wm * WTM + i * 32 + (lane & 31), chunk)]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = as_bf16x8(Lb[swz(wn * WTN + j * 32 + (lane & 31), chunk)]);
+    }
+  }
+
+  __device__ __forceinline__ void mma(f32x16 (&acc)[TM][TN], const frag_t (&af)[TM], const frag_t (&bf)[TN],
+                                      const uint32_t (&sd)[NSC], int kk) const {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      if constexpr (FP8) {
+        const int sc = (int)((sd[i] >> (8 * (kk * 2 + (lane >> 5)))) & 255u);  // E8M0 of this lane's block
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[i][j], 0, 0, 0, 127, 0, sc);
+      } else {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // One K stage from buffers (La, Lb) with scales sd.  Stage kt + 1 must already be in flight into (Na, Nb); after the
+  // barrier the loads of stage kt + 2 go into (La, Lb, sd).
+  __device__ __forceinline__ void stage(f32x16 (&acc)[TM][TN], frag_t (&af)[2][TM], frag_t (&bf)[2][TN], uint4* La,
+                                        uint4* Lb, uint32_t (&sd)[NSC], const uint4* Na, const uint4* Nb, int kt, int KT) const {
+    constexpr int RPF = FP8 ? 2 : 1;  // LDS reads per fragment
+    constexpr int NV = APW + BPW + (FP8 ? NSC : 0), ND = (TM + TN) * RPF, NM = TM * TN;
+#pragma unroll
+    for (int kk = 0; kk < NKK - 1; ++kk) {
+      frag(La, Lb, kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
+      mma(acc, af[kk & 1], bf[kk & 1], sd, kk);
+      // MFMA, fragment read(s), MFMA, ... then the remaining MFMAs
+      constexpr int DPM = (ND + NM - 1) / NM;
+#pragma unroll
+      for (int x = 0; x < NM; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (x * DPM < ND) __builtin_amdgcn_sched_group_barrier(0x100, DPM, 0);
+      }
     }
     // stage kt + 1 has landed (this wave's loads) and is visible (everyone's), and nobody reads (La, Lb) any more
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __syncthreads();
-    issue(La, Lb, min(kt + 2, KT - 1));
+    uint32_t sl[NSC];
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) sl[i] = sd[i];
+    issue(La, Lb, sd, min(kt + 2, KT - 1));
     frag(Na, Nb, 0, af[0], bf[0]);
-    mma(acc, af[1], bf[1]);
+    mma(acc, af[(NKK - 1) & 1], bf[(NKK - 1) & 1], sl, NKK - 1);
     // MFMA, load(s), fragment read(s), MFMA, ...
     constexpr int VPM = (NV + NM - 1) / NM, DPM = (ND + NM - 1) / NM;
 #pragma unroll
@@ -219,9 +289,23 @@ struct Tile {
         }
 #pragma unroll
         for (int x = 0; x < RB; ++x) {
-          if (m[x] >= g.M) continue;
-          if (cols.full) cols.put(g, m[x], cols.apply(v[x], h[x]));
-          else cols.put_partial(g, m[x], v[x]);
+          if constexpr (EPI == EPI_GELU_MX8) {
+            // the 8 lanes holding this row's 32 consecutive columns share one block scale (N % 32 == 0)
+            const float4 o = cols.apply(v[x], h[x]);
+            float a = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
+            a = fmaxf(a, __shfl_xor(a, 1, 64));
+            a = fmaxf(a, __shfl_xor(a, 2, 64));
+            a = fmaxf(a, __shfl_xor(a, 4, 64));
+            const int se = mx_exp(a);
+            if (m[x] < g.M && cols.full) {
+              *(uint32_t*)((uint8_t*)g.C + (size_t)m[x] * g.ldc + cols.n) = mx_pack4(o.x, o.y, o.z, o.w, se);
+              if ((cc & 7) == 0) g.c_scale[(size_t)m[x] * g.c_sld + (cols.n >> 5)] = (uint8_t)(se + 127);
+            }
+          } else {
+            if (m[x] >= g.M) continue;
+            if (cols.full) cols.put(g, m[x], cols.apply(v[x], h[x]));
+            else cols.put_partial(g, m[x], v[x]);
+          }
         }
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -229,9 +313,9 @@ struct Tile {
   }
 };
 
-template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
+template <int BM, int BN, int WM, int WN, int EPI, bool TAPS, bool FP8>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
-  using T = Tile<BM, BN, WM, WN, TAPS>;
+  using T = Tile<BM, BN, WM, WN, TAPS, FP8>;
   __shared__ uint4 sA0[BM * 8], sA1[BM * 8], sB0[BN * 8], sB1[BN * 8];
 
   // XCD-aware order: consecutive workgroups go to different XCDs, so the tiles of one XCD are a contiguous run (they
@@ -250,20 +334,21 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
     for (int j = 0; j < T::TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  bf16x8 af[2][T::TM], bf[2][T::TN];
+  typename T::frag_t af[2][T::TM], bf[2][T::TN];
+  uint32_t sd0[T::NSC], sd1[T::NSC];  // fp8: activation scale dwords of the stages in buffers 0 and 1
 
-  const int KT = g.K / BK;
-  t.issue(sA0, sB0, 0);
+  const int KT = g.K / T::BKE;
+  t.issue(sA0, sB0, sd0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  t.issue(sA1, sB1, min(1, KT - 1));
+  t.issue(sA1, sB1, sd1, min(1, KT - 1));
   t.frag(sA0, sB0, 0, af[0], bf[0]);
   int kt = 0;
   for (; kt + 1 < KT; kt += 2) {
-    t.stage(acc, af, bf, sA0, sB0, sA1, sB1, kt, KT);
-    t.stage(acc, af, bf, sA1, sB1, sA0, sB0, kt + 1, KT);
+    t.stage(acc, af, bf, sA0, sB0, sd0, sA1, sB1, kt, KT);
+    t.stage(acc, af, bf, sA1, sB1, sd1, sA0, sB0, kt + 1, KT);
   }
-  if (kt < KT) t.stage(acc, af, bf, sA0, sB0, sA1, sB1, kt, KT);
+  if (kt < KT) t.stage(acc, af, bf, sA0, sB0, sd0, sA1, sB1, kt, KT);
 
   // retire the tail loads and every wave's last fragment reads before the stage buffers become epilogue slabs
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
@@ -282,7 +367,18 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
 template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
 hipError_t launch_tile(const GemmArgs& g, hipStream_t st) {
   const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, TAPS>), dim3(gm * gn), dim3(64 * WM * WN), 0, st, g);
+  if (g.w_scale) {
+    // fp8 fragments are twice as wide: 64x128 wave tiles would spill, so fp8 runs the 64x64-wave tiles only
+    if constexpr (BM / WM * BN / WN <= 64 * 64)
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, TAPS, true>), dim3(gm * gn), dim3(64 * WM * WN), 0, st, g);
+    else
+      return hipErrorInvalidValue;
+  } else {
+    if constexpr (EPI == EPI_GELU_MX8)
+      return hipErrorInvalidValue;  // fp8 output only follows fp8 GEMMs
+    else
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, TAPS, false>), dim3(gm * gn), dim3(64 * WM * WN), 0, st, g);
+  }
   return hipGetLastError();
 }
 
@@ -301,14 +397,14 @@ hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
 }  // namespace
 
 int pick_cfg(const GemmArgs& g) {
-  // 256x256 tiles once there are enough rows to fill them
-  if (g.M >= 1024 && g.N >= 256) return 1;
+  // 256x256 tiles (fp8: 256x128) once there are enough rows to fill them
+  if (g.M >= 1024 && g.N >= 256) return g.w_scale ? 2 : 1;
   return 0;
 }
 
 hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
-  if (cfg < 0 && g.ws) {
+  if (cfg < 0 && g.ws && !g.w_scale) {
     // a grid of fewer than 128 tiles leaves most of the 256 CUs idle: split K instead
     const int c = pick_cfg(g), bm = c == 0 ? 128 : 256, bn = c == 1 ? 256 : 128;
     const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
@@ -327,6 +423,9 @@ hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
     case EPI_RESID_F32 * 2 + 1: return launch_epi<EPI_RESID_F32, true>(g, cfg, st);
     case EPI_F32 * 2: return launch_epi<EPI_F32, false>(g, cfg, st);
     case EPI_F32 * 2 + 1: return launch_epi<EPI_F32, true>(g, cfg, st);
+    case EPI_GELU_MX8 * 2:
+      if (!g.w_scale || !g.c_scale || g.N % 32) return hipErrorInvalidValue;
+      return launch_epi<EPI_GELU_MX8, false>(g, cfg, st);
   }
   return hipErrorInvalidValue;
 }

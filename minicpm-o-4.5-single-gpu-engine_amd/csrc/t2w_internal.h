@@ -8,7 +8,8 @@ namespace t2w {
 
 typedef uint16_t bf16_t;
 
-enum Epi { EPI_BF16 = 0, EPI_GELU_BF16 = 1, EPI_RESID_F32 = 2, EPI_F32 = 3 };
+// EPI_GELU_MX8: GELU, then MX fp8 codes to C (bytes, ldc) and block scales to c_scale (N % 32 == 0)
+enum Epi { EPI_BF16 = 0, EPI_GELU_BF16 = 1, EPI_RESID_F32 = 2, EPI_F32 = 3, EPI_GELU_MX8 = 4 };
 
 struct GemmArgs {
   const bf16_t* A;     // dense: A[m * lda + k]; taps: A[(a_src[m] + k / tapC) * lda + k % tapC]
@@ -24,6 +25,13 @@ struct GemmArgs {
   int M, N, K;         // K % 64 == 0
   float* ws;           // split-K partials (null: tile kernels only)
   size_t ws_bytes;
+  // fp8 mode (w_scale non-null): A and B hold OCP e4m3 codes (lda, ldb, K in elements = bytes); A's MX scales are
+  // a_scale[row * a_sld + k / 32] (E8M0; taps mode: row = frame), W row n is scaled by w_scale[n] in the epilogue
+  const uint8_t* a_scale;
+  int a_sld;
+  const float* w_scale;
+  uint8_t* c_scale;    // EPI_GELU_MX8: output block scales c_scale[m * c_sld + n / 32]
+  int c_sld;
 };
 
 // cfg < 0: by shape (split-K through g.ws when a tile grid would be too small to fill the chip)
@@ -34,11 +42,17 @@ struct SplitPlan {
   int steps;   // 64-K steps per split
 };
 SplitPlan splitk_plan(int M, int N, int K, size_t ws_bytes);
+
+// MX fp8 quantization: x [M, K] bf16 (rows ldx apart) -> q [M, K] e4m3 (rows ldq apart), s [M, K / 32] E8M0; K % 32 == 0
+hipError_t quant_mx8(const bf16_t* x, int ldx, int M, int K, uint8_t* q, int ldq, uint8_t* s, hipStream_t st);
 hipError_t gemm_splitk(const GemmArgs& g, int epi, const SplitPlan& p, float* part, hipStream_t st);
 
 // Per-token row kernels of the DiT block (H = hidden, one wave per token).
 hipError_t ln_mod(const float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H,
                   hipStream_t st);
+// ln_mod with MX fp8 output: codes q [N, H], block scales qs [N, H / 32]
+hipError_t ln_mod_mx8(const float* h, const float* shift, const float* scale1, float eps, uint8_t* q, uint8_t* qs, int N,
+                      int H, hipStream_t st);
 
 struct ConvPlace {   // where the normed frames of a causal conv go (the padded frame buffer and the conv caches)
   bf16_t* P;          // [N + 2 R, H]: per row r its two cached frames, then its T_r frames
@@ -52,6 +66,8 @@ struct ConvPlace {   // where the normed frames of a causal conv go (the padded 
   const int* wr;
   long long cache_stride;    // elements between row slots
   int N, R;
+  uint8_t* P8 = nullptr;     // fp8 mode: the frame buffer as MX fp8 codes [N + 2 R, H] (P unused)
+  uint8_t* P8s = nullptr;    // and its block scales [N + 2 R, H / 32]
 };
 
 hipError_t ln_mod_conv(const float* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H,
@@ -75,6 +91,8 @@ struct AttnArgs {
   const int* tiles;       // [n_tiles, 2]: (row, first query position) of each 64-query tile
   int n_tiles, heads, chunk;  // chunk > 0: a new frame sees new frames of its own and earlier chunks only
   float scale;
+  uint8_t* out8 = nullptr;   // fp8 mode: MX fp8 codes [tokens, H] (out unused) and block scales [tokens, H / 32]
+  uint8_t* out8s = nullptr;
 };
 hipError_t attention(const AttnArgs& a, hipStream_t st);
 

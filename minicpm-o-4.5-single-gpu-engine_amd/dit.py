@@ -44,10 +44,20 @@ def freq_table(freq: int, max_period: float = 10000.0) -> torch.Tensor:
     return torch.exp(-np.log(max_period) * torch.arange(0, half, dtype=torch.float32) / half)
 
 
-class DiTModel:
-    """Weights on the GPU (bf16 GEMM operands, fp32 biases / norm affines) and the per-step adaLN tables."""
+def quantize_e4m3(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-channel fp8 weights (the reference's fp8 convention, ``engine/runtime/fp8.py:15-37``): scale
+    max|w_n| / 448, codes = round-to-nearest-even e4m3 of w / scale.  w [N, K] -> (uint8 codes [N, K], fp32 scales [N])."""
+    wf = w.float()
+    sc = (wf.abs().amax(dim=1) / 448.0).clamp_min(1e-30)
+    q = (wf / sc[:, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+    return q.contiguous(), sc.contiguous()
 
-    def __init__(self, W: dict, cfg: DiTConfig = DiTConfig(), device: str = "cuda"):
+
+class DiTModel:
+    """Weights on the GPU (bf16 GEMM operands, fp32 biases / norm affines) and the per-step adaLN tables.  With
+    ``fp8`` the six block GEMMs also get e4m3 weights (per-output-channel scales) for fp8 solves."""
+
+    def __init__(self, W: dict, cfg: DiTConfig = DiTConfig(), device: str = "cuda", fp8: bool = False):
         self.cfg, self.device = cfg, device
         H, D = cfg.hidden, cfg.depth
         bf = lambda t: t.to(device=device, dtype=torch.bfloat16).contiguous()  # noqa: E731
@@ -80,6 +90,24 @@ class DiTModel:
         for b, blk in enumerate(self.blocks):
             s = _lib.DitBlock(*[blk[n].data_ptr() for n, _ in _lib.DitBlock._fields_])
             _lib.check(L.t2w_dit_set_block(h, b, C.byref(s)), "set_block")
+        self.fp8 = fp8
+        self.blocks8 = []
+        if fp8:
+            for b in range(D):
+                p = f"blocks.{b}."
+                a = p + "attn."
+                src = {"qkv": torch.cat([W[a + "to_q.weight"], W[a + "to_k.weight"], W[a + "to_v.weight"]]),
+                       "proj": W[a + "proj.weight"],
+                       "c1": W[p + "conv.block.1.weight"].permute(0, 2, 1).reshape(H, -1),
+                       "c2": W[p + "conv.block.6.weight"].permute(0, 2, 1).reshape(H, -1),
+                       "fc1": W[p + "mlp.fc1.weight"], "fc2": W[p + "mlp.fc2.weight"]}
+                blk8 = {}
+                for k, w in src.items():
+                    q, sc = quantize_e4m3(w.to(device))
+                    blk8[k + "_w8"], blk8[k + "_ws"] = q, sc
+                self.blocks8.append(blk8)
+                s8 = _lib.DitBlockFp8(*[blk8[n].data_ptr() for n, _ in _lib.DitBlockFp8._fields_])
+                _lib.check(L.t2w_dit_set_block_fp8(h, b, C.byref(s8)), "set_block_fp8")
         self.ts, self.dts = t_schedule(cfg.steps)
         # timestep / adaLN tables of the schedule, computed on the GPU from fp32 copies of those weights
         self._mod_w = {"freqs": f32(freq_table(cfg.freq)), "te0_w": f32(W["t_embedder.mlp.0.weight"]), "te0_b": f32(W["t_embedder.mlp.0.bias"]),
@@ -209,7 +237,11 @@ def advance_row(r: FastRow, new: list[int], keep: bool, keep_len: int) -> list[i
 class FastDiT:
     """The packed ragged CFG Euler solve over per-request caches (``FastDiT`` of ``engine/runtime/dit_fast.py``)."""
 
-    def __init__(self, model: DiTModel, n_slots: int = 32768, max_streams: int = 96, use_graphs: bool = False):
+    def __init__(self, model: DiTModel, n_slots: int = 32768, max_streams: int = 96, use_graphs: bool = False, fp8: bool = False):
+        """``fp8``: solves run the block GEMMs on fp8 MFMA (the model must have been built with fp8 weights)."""
+        if fp8 and not model.fp8:
+            raise ValueError("fp8 solves need a DiTModel built with fp8=True")
+        self.fp8 = fp8
         cfg = model.cfg
         self.model, self.cfg, self.device = model, cfg, model.device
         S, D, H = cfg.steps, cfg.depth, cfg.hidden
@@ -277,7 +309,7 @@ class FastDiT:
         return _lib.SolveArgs(p["n_tok"], p["n_rows"], p["half"], p["n_tiles"], int(chunk), _lib.ptr(x0), _lib.ptr(stat), _lib.ptr(in_rows),
                               out.data_ptr(), tp(0), tp(1), tp(2), tp(3), tp(4), tp(5), tp(6), tp(7), tp(8), tp(9), tp(11), tp(10),
                               self.k_pool.data_ptr(), self.v_pool.data_ptr(), self.n_slots * H, self.conv_pool.data_ptr(),
-                              ws.data_ptr(), ws.numel())
+                              ws.data_ptr(), ws.numel(), int(self.fp8))
 
     @staticmethod
     def _tables(p: dict, device) -> torch.Tensor:
@@ -330,7 +362,7 @@ class FastDiT:
             _lib.check(L.t2w_dit_solve(self.model.handle, C.byref(a), st), "dit_solve")
             self.counts["eager"] += 1
             return out
-        key = (N, R, p["n_tiles"], chunk)
+        key = (N, R, p["n_tiles"], chunk, self.fp8)
         flat = np.concatenate([np.asarray(x, dtype=np.int32) for x in p["parts"]])
         g = self.graphs.get(key)
         if g is not None and g["tables"].numel() < flat.size:  # more cached keys than this graph's table holds

@@ -111,3 +111,51 @@ def test_chunk_causal_whole_sequence(dev, tiny):
     errs = [rel(a.cpu(), b) for a, b in zip(got, ref)]
     print("chunk-causal rel-L2", errs)
     assert max(errs) < TOL
+
+
+FP8_TOL = 5e-2  # fp8 (e4m3 weights, MX fp8 activations) against the bf16 result: the bound stated for config 5
+
+
+def _solve_once(model, fp8: bool, Ts, seed: int, chunk: int):
+    fd = FastDiT(model, n_slots=4096, max_streams=4, fp8=fp8)
+    g = torch.Generator().manual_seed(seed)
+    caches = [fd.new_cache() for _ in Ts]
+    mus = [torch.randn(80, t, generator=g).cuda() for t in Ts]
+    spks = torch.randn(len(Ts), 80, generator=g).cuda()
+    out = fd.solve(caches, mus, spks, None, [False] * len(Ts), chunk=chunk)
+    for c in caches:
+        fd.release(c)
+    return [o.cpu() for o in out]
+
+
+def test_fp8_solve_vs_bf16_full_size(dev):
+    """Config-5 form at the full model size: 10-step CFG solve with fp8 block GEMMs against the bf16 solve."""
+    W = init_dit(DiTConfig(), seed=4)
+    model = DiTModel(W, DiTConfig(), fp8=True)
+    Ts = [200, 130]
+    b = _solve_once(model, False, Ts, 4, 50)
+    f = _solve_once(model, True, Ts, 4, 50)
+    e = max(rel(x, y) for x, y in zip(f, b))
+    print("fp8 vs bf16 mel rel-L2", e, "max-abs", max(float((x - y).abs().max()) for x, y in zip(f, b)))
+    assert e < FP8_TOL
+
+
+def test_fp8_streaming_vs_oracle(dev):
+    """fp8 streaming windows with caches (small model) against the fp32 oracle, same structure as the bf16 case."""
+    W = init_dit(TINY, seed=12)
+    model = DiTModel(W, TINY, fp8=True)
+    d = od.dims_of(W, steps=TINY.steps)
+    fd = FastDiT(model, n_slots=4096, max_streams=4, fp8=True)
+    g = torch.Generator().manual_seed(2)
+    caches = [fd.new_cache(keep=30)]
+    refc = [od.empty_cache(d, keep=30)]
+    spks = torch.randn(1, 80, generator=g)
+    errs = []
+    for w, T in enumerate([30, 50, 50]):
+        mus = [torch.randn(80, T, generator=g)]
+        conds = [torch.randn(80, T, generator=g)] if w == 0 else None
+        ref = od.solve(W, d, W["rand_noise"], refc, mus, spks, conds, [True])
+        got = fd.solve(caches, [m.cuda() for m in mus], spks.cuda(), [c.cuda() for c in conds] if conds else None, [True])
+        errs.append(rel(got[0].cpu(), ref[0]))
+    print("fp8 streaming vs oracle rel-L2 per window", errs)
+    assert max(errs) < FP8_TOL

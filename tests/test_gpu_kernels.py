@@ -8,6 +8,7 @@ import torch
 import t2w_amd  # noqa: F401
 from t2w_amd import _lib
 from conftest import rel
+from oracle import fp8 as of
 
 pytestmark = pytest.mark.gpu
 
@@ -208,3 +209,88 @@ def test_attention_paged_block_causal(dev, chunk):
         s = s.masked_fill(~vis[None], float("-inf"))
         ref = (torch.softmax(s, -1) @ vv).transpose(0, 1).reshape(t, H)
         assert rel(out[row_start[r]:row_start[r] + t].float(), ref) < 1e-2, r
+
+
+def test_quant_mx8_matches_oracle(dev):
+    """The device MX quantizer equals the restatement bit for bit (codes and block scales), zero blocks and a wide
+    dynamic range included."""
+    L = _lib.lib()
+    g = torch.Generator().manual_seed(4)
+    M, K = 77, 1024
+    x = (torch.randn(M, K, generator=g) * torch.exp(torch.randn(M, K // 32, generator=g) * 4).repeat_interleave(32, dim=1)).bfloat16()
+    x[3, 64:96] = 0
+    x[5, :32] = 448.0
+    xd = x.to(dev)
+    q = torch.empty(M, K, dtype=torch.uint8, device=dev)
+    s = torch.empty(M, K // 32, dtype=torch.uint8, device=dev)
+    _lib.check(L.t2w_quant_mx8(xd.data_ptr(), K, M, K, q.data_ptr(), K, s.data_ptr(), _lib.stream_handle()), "quant")
+    torch.cuda.synchronize()
+    qo, so = of.quantize_mx(x)
+    assert torch.equal(s.cpu(), so)
+    assert torch.equal(q.cpu(), qo)
+
+
+def _fp8_operands(dev, M, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(M, K, generator=g).bfloat16()
+    W = torch.randn(N, K, generator=g) / K ** 0.5
+    qa, sa = of.quantize_mx(A)
+    qw, sw = of.quantize_weight(W)
+    return (qa.to(dev), sa.to(dev), qw.to(dev), sw.to(dev), of.dequantize_mx(qa, sa), of.dequantize_weight(qw, sw), A, W,
+            torch.randn(N, generator=g).to(dev), torch.randn(N, generator=g).to(dev))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 128), (100, 1024, 1024), (333, 80, 1024), (1300, 1024, 2048), (2048, 3072, 1024)])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_gemm_fp8(dev, M, N, K, epi):
+    """fp8 MFMA GEMM against fp32 matmul of the dequantized operands (the quantization itself is the restatement's).
+    The fp8 MFMA sums its 64 products at a precision measured at ~6e-5 of the largest output on random e4m3 data, hence
+    1e-4 where bf16 GEMMs are held to 1e-5."""
+    L = _lib.lib()
+    qa, sa, qw, sw, Ad, Wd, A, W, bias, gate = _fp8_operands(dev, M, N, K, M + N + K + epi)
+    ref = Ad.to(dev) @ Wd.to(dev).t() + bias
+    if epi == 1:
+        ref = torch.nn.functional.gelu(ref, approximate="tanh")
+    if epi in (0, 1):
+        out = torch.full((M, N), 7.0, device=dev).bfloat16()
+    elif epi == 2:
+        out = torch.randn(M, N, device=dev)
+        h0 = out.clone()
+    else:
+        out = torch.zeros(M, N, device=dev)
+    _lib.check(L.t2w_gemm_fp8(qa.data_ptr(), K, None, sa.data_ptr(), K // 32, qw.data_ptr(), sw.data_ptr(), bias.data_ptr(),
+                              gate.data_ptr() if epi == 2 else None, out.data_ptr(), N, M, N, K, epi, _lib.stream_handle()), "gemm_fp8")
+    torch.cuda.synchronize()
+    if epi in (0, 1):
+        assert rel(out.float(), ref) < 6e-3
+    elif epi == 2:
+        assert rel(out, h0 + gate * ref) < 1e-4
+    else:
+        assert rel(out, ref) < 1e-4
+        # and against the unquantized bf16 product: the fp8 rounding error itself
+        exact = A.float().to(dev) @ W.to(dev).t() + bias
+        assert rel(out, exact) < 6e-2
+
+
+def test_gemm_fp8_taps(dev):
+    """fp8 taps mode: the block scales of a row come from its three frames."""
+    L = _lib.lib()
+    H, lens = 256, [50, 7, 300]
+    R, N = len(lens), sum(lens)
+    g = torch.Generator().manual_seed(9)
+    frames = torch.randn(N + 2 * R, H, generator=g).bfloat16()  # padded frame buffer [frames, H]
+    qa, sa = of.quantize_mx(frames)
+    Ad = of.dequantize_mx(qa, sa)
+    qw, sw = of.quantize_weight(torch.randn(H, 3 * H, generator=g) / (3 * H) ** 0.5)
+    Wd = of.dequantize_weight(qw, sw)
+    qa, sa, qw, sw = qa.to(dev), sa.to(dev), qw.to(dev), sw.to(dev)
+    bias = torch.randn(H, generator=g).to(dev)
+    tok_row = [r for r, t in enumerate(lens) for _ in range(t)]
+    a_src = torch.tensor([i + 2 * r for i, r in enumerate(tok_row)], dtype=torch.int32, device=dev)
+    full = torch.cat([Ad.to(dev)[a_src.long() + j] for j in range(3)], 1)
+    ref = full @ Wd.to(dev).t() + bias
+    out = torch.zeros(N, H, device=dev)
+    _lib.check(L.t2w_gemm_fp8(qa.data_ptr(), H, a_src.data_ptr(), sa.data_ptr(), H // 32, qw.data_ptr(), sw.data_ptr(), bias.data_ptr(),
+                              None, out.data_ptr(), H, N, H, 3 * H, 3, _lib.stream_handle()), "gemm_fp8 taps")
+    torch.cuda.synchronize()
+    assert rel(out, ref) < 1e-4
