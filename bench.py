@@ -53,6 +53,8 @@ def main() -> int:
     ap.add_argument("--hift-fp32", action="store_true", help="HiFT decoder in strict fp32 (default: bf16 MFMA decoder)")
     ap.add_argument("--no-extra", action="store_true", help="skip the ragged-length and HiFT-alone measurements")
     ap.add_argument("--no-fp8", action="store_true", help="skip the fp8 (e4m3 weights, MX fp8 activations) measurement")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the conv1 GEMM launches, after three 256 MiB calibration copies (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no sharding or collectives); use --gpus 1", file=sys.stderr)
@@ -61,6 +63,12 @@ def main() -> int:
     import t2w_amd  # noqa: F401
     from t2w_amd import _lib
     from t2w_amd.config import DiTConfig, HiFTConfig
+
+    if args.roofline_only:
+        k_ms, k_tf, k_fl = conv1_roofline(DiTConfig(), args.streams, args.frames, calibrate=True)
+        print(json.dumps({"kernel": "gemm_kernel<256,256,4,2,EPI_BF16,taps> (DiT conv1)", "launch_ms": k_ms, "tflops": k_tf,
+                          "calibration_copy_bytes": 2 * (256 << 20)}))
+        return 0
     from t2w_amd.dit import DiTModel, FastDiT
     from t2w_amd.weights import init_dit, init_hift
 
@@ -111,30 +119,7 @@ def main() -> int:
     torch.cuda.synchronize()
     dit_dt = (time.perf_counter() - t1) / max(1, args.steps // 2)
 
-    # dominant kernel: the conv1 GEMM (taps mode, bf16 out) at this workload's shape, HIP events on its own stream
-    H, N = cfg.hidden, 2 * n * T
-    R = 2 * n
-    P = torch.randn(N + 2 * R, H, device=dev).bfloat16()
-    Wc = (torch.randn(H, 3 * H, device=dev) * 0.02).bfloat16()
-    bc = torch.zeros(H, device=dev)
-    tok_row = np.repeat(np.arange(R), T)
-    a_src = torch.from_numpy((np.arange(N) + 2 * tok_row).astype(np.int32)).to(dev)
-    out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())  # operands were written on the default stream
-    L = _lib.lib()
-    with torch.cuda.stream(s):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 20
-        for _ in range(3):
-            _lib.check(L.t2w_gemm_bf16(P.data_ptr(), H, a_src.data_ptr(), Wc.data_ptr(), bc.data_ptr(), None, out.data_ptr(), H, N, H, 3 * H, 0, s.cuda_stream))
-        e0.record(s)
-        for _ in range(reps):
-            _lib.check(L.t2w_gemm_bf16(P.data_ptr(), H, a_src.data_ptr(), Wc.data_ptr(), bc.data_ptr(), None, out.data_ptr(), H, N, H, 3 * H, 0, s.cuda_stream))
-        e1.record(s)
-    s.synchronize()
-    k_ms = e0.elapsed_time(e1) / reps
-    k_tflops = 2.0 * N * H * 3 * H / (k_ms * 1e-3) / 1e12
+    k_ms, k_tflops, k_flops = conv1_roofline(cfg, n, T)
 
     # per-chunk latency: one stream, 300-frame prompt cached, 50 new frames, CFG pair, 10 steps, + HiFT of the window
     lat = None
@@ -191,13 +176,66 @@ def main() -> int:
         "dit_solve_ms": dit_dt * 1e3,
         "dit_mfma_frac": (gemm_f + attn_f) / dit_dt / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "roofline": {"bound": "mfma", "kernel": "gemm_kernel<256,256,4,2,EPI_BF16,taps> (DiT conv1)", "achieved": k_tflops,
-                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": k_tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
-                     "launch_ms": k_ms, "flops_per_launch": 2.0 * N * H * 3 * H},
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": k_tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": pmc_traffic(),
+                     "launch_ms": k_ms, "flops_per_launch": k_flops},
         "cpu_baseline": cpu,
         **extra,
     }
     print(json.dumps(res))
     return 0
+
+
+def conv1_roofline(cfg, n: int, T: int, calibrate: bool = False) -> tuple[float, float, float]:
+    """The dominant kernel alone: the DiT's conv1 GEMM (taps mode, bf16 out) at the workload's shape, 20 launches timed
+    with HIP events on its own stream.  calibrate: first three plain 256 MiB device copies (torch copy_), the known-size
+    reference for the HBM byte counters of a rocprofv3 --pmc run of this same command."""
+    from t2w_amd import _lib
+
+    dev = "cuda"
+    if calibrate:
+        src = torch.ones(64 << 20, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    H, N = cfg.hidden, 2 * n * T
+    R = 2 * n
+    P = torch.randn(N + 2 * R, H, device=dev).bfloat16()
+    Wc = (torch.randn(H, 3 * H, device=dev) * 0.02).bfloat16()
+    bc = torch.zeros(H, device=dev)
+    tok_row = np.repeat(np.arange(R), T)
+    a_src = torch.from_numpy((np.arange(N) + 2 * tok_row).astype(np.int32)).to(dev)
+    out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())  # operands were written on the default stream
+    L = _lib.lib()
+    with torch.cuda.stream(s):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        for _ in range(3):
+            _lib.check(L.t2w_gemm_bf16(P.data_ptr(), H, a_src.data_ptr(), Wc.data_ptr(), bc.data_ptr(), None, out.data_ptr(), H, N, H, 3 * H, 0, s.cuda_stream))
+        e0.record(s)
+        for _ in range(reps):
+            _lib.check(L.t2w_gemm_bf16(P.data_ptr(), H, a_src.data_ptr(), Wc.data_ptr(), bc.data_ptr(), None, out.data_ptr(), H, N, H, 3 * H, 0, s.cuda_stream))
+        e1.record(s)
+    s.synchronize()
+    k_ms = e0.elapsed_time(e1) / reps
+    flops = 2.0 * N * H * 3 * H
+    return k_ms, flops / (k_ms * 1e-3) / 1e12, flops
+
+
+def pmc_traffic() -> float | None:
+    """HBM bytes per launch of the conv1 GEMM as measured by the committed rocprofv3 --pmc summary (FETCH_SIZE +
+    WRITE_SIZE of the GEMM dispatches, each scaled by the same counter's reading on a plain copy of known size), or
+    None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gemm_conv1_b32x400_pmc.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def fp8_workload(args, cfg, model, mus, spks, hift, hsrc, hnoise, bf16_step) -> dict:
