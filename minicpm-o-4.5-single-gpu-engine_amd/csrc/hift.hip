@@ -114,20 +114,65 @@ __global__ void __launch_bounds__(256) conv_f32_kernel(ConvDesc c) {
 
 
 // bf16-MFMA convolution (fp32 activations in HBM, bf16 operands, fp32 accumulation) for stride-1 convs and the
-// polyphase transposed convs.  For a tile of BM output rows the input rows of every tap form one slab of
-// BM + (taps - 1) |d| rows: per 64-channel chunk the slab is staged once in LDS (activation applied, rounded to bf16)
-// and each tap's A fragments are the slab rows shifted by its offset; the tap's 64 x 64 weight tile is double-buffered.
+// polyphase transposed convs.  A workgroup owns BM output rows x 64 output channels; its four waves own BM / 4 rows
+// each.  For every 64-channel input chunk the input rows of all taps form one slab of BM + (taps - 1) |d| rows, staged
+// once in LDS (two 16-byte fp32 loads per thread and row segment, activation applied with the hardware sine, rounded
+// to bf16, 16-byte chunks XOR-swizzled by row); each tap then reads the slab rows shifted by its offset, so the tap loop
+// has no barrier.  Weight fragments come straight from L2 into registers, the next tap's loaded while this tap's MFMAs
+// run.  The epilogue stages each wave's 32-row blocks through LDS and works on whole rows (16-byte accesses).
 constexpr int HB_BN = 64, HB_MAXSPAN = 64;
 
 __device__ __forceinline__ int hswz(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
 
+__device__ __forceinline__ float pre_fast(float v, int pre, float slope, float a, float inv) {
+  if (pre == PRE_LEAKY) return v > 0.f ? v : v * slope;
+  if (pre == PRE_SNAKE) {
+    const float s = __sinf(v * a);
+    return v + inv * (s * s);
+  }
+  return v;
+}
+
+// epilogue of four consecutive channels co .. co + 3 of one output row (all inside Cout)
+__device__ __forceinline__ void conv_epilogue4(const ConvDesc& c, size_t row, int co, float4 a) {
+  const float4 bb = *(const float4*)(c.bias + co);
+  float v[4] = {__fadd_rn(a.x, bb.x), __fadd_rn(a.y, bb.y), __fadd_rn(a.z, bb.z), __fadd_rn(a.w, bb.w)};
+  float* yp = c.y + row * c.ldy + co;
+  if (c.epi == EPI_STORE) {
+    *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
+  } else if (c.epi == EPI_ELU) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.f ? v[e] : expm1f(v[e]);
+    *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    const float4 r = *(const float4*)(c.res + row * c.ldy + co);
+    v[0] = __fadd_rn(v[0], r.x); v[1] = __fadd_rn(v[1], r.y); v[2] = __fadd_rn(v[2], r.z); v[3] = __fadd_rn(v[3], r.w);
+    if (c.epi == EPI_RES) {
+      *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
+    } else if (c.epi == EPI_ADD_RES) {
+      const float4 y = *(const float4*)yp;
+      *(float4*)yp = make_float4(__fadd_rn(y.x, v[0]), __fadd_rn(y.y, v[1]), __fadd_rn(y.z, v[2]), __fadd_rn(y.w, v[3]));
+    } else {  // EPI_RES_MEAN
+      float* sp = c.sum + row * c.ldy + co;
+      if (c.sum_mode == 0) {
+        *(float4*)sp = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+        const float4 t = *(const float4*)sp;
+        float o[4] = {__fadd_rn(t.x, v[0]), __fadd_rn(t.y, v[1]), __fadd_rn(t.z, v[2]), __fadd_rn(t.w, v[3])};
+        if (c.sum_mode == 2) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = __fdiv_rn(o[e], (float)c.sum_div);
+        }
+        *(float4*)sp = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+}
+
 template <int BM>
-__global__ void __launch_bounds__(256) conv_bf16_kernel(ConvDesc c, const bf16_t* __restrict__ wbf) {
-  constexpr int WAVES_M = 4, WTM = BM / WAVES_M, TM = WTM / 32;  // 4 waves along time, each all 64 channels
-  constexpr int SLAB = BM + HB_MAXSPAN;
-  extern __shared__ uint4 hl[];  // slab [SLAB][8 chunks] then 2 weight tiles [64][8 chunks]
-  uint4* slab = hl;
-  uint4* wt = hl + SLAB * 8;
+__global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf16_t* __restrict__ wbf) {
+  constexpr int WTM = BM / 4, TM = WTM / 32;  // 4 waves along time, each all 64 channels
+  extern __shared__ uint4 hl[];               // slab [BM + span][8 chunks]; later the epilogue's fp32 blocks
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
   const int Tin = c.in_len[b], Tout = c.out_len[b];
@@ -145,6 +190,8 @@ __global__ void __launch_bounds__(256) conv_bf16_kernel(ConvDesc c, const bf16_t
   const int srows = BM + span;
   const int cin_pad = (c.Cin + 63) & ~63;
   const bf16_t* wph = wbf + ((size_t)ph * ((c.Cout + 63) & ~63) + co0) * c.taps * cin_pad;
+  // wave-uniform count of this wave's 32-row blocks that hold output rows
+  const int live = min(TM, max(0, (r_hi - (r0 + wave * WTM)) / 32 + 1));
 
   f32x16 acc[TM][2];
 #pragma unroll
@@ -154,64 +201,118 @@ __global__ void __launch_bounds__(256) conv_bf16_kernel(ConvDesc c, const bf16_t
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  auto load_w = [&](int j, int c0, int buf) {  // 64 channels x 64 ci of tap j: 512 chunks, 2 per thread
+  // this lane's weight fragments of tap j: channel rows co0 + jj * 32 + lane % 32, K chunk kk * 2 + lane / 32
+  auto load_w = [&](int j, int c0, bf16x8 (&w)[4][2]) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int idx = tid + u * 256, co = idx >> 3, ch = idx & 7;
-      wt[buf * 512 + hswz(co, ch)] = *(const uint4*)(wph + ((size_t)co * c.taps + j) * cin_pad + c0 + ch * 8);
-    }
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+        w[kk][jj] = as_bf16x8(*(const uint4*)(wph + ((size_t)(jj * 32 + (lane & 31)) * c.taps + j) * cin_pad + c0 + kk * 16 + (lane >> 5) * 8));
   };
+  const int sch = tid & 7;  // this thread's 8-channel chunk of the slab rows
   for (int c0 = 0; c0 < c.Cin; c0 += 64) {
-    __syncthreads();
-    // slab: srows x 64 channels, 8 channels (one 16-byte chunk) per item
-    for (int idx = tid; idx < srows * 8; idx += 256) {
-      const int sr = idx >> 3, ch = idx & 7;
+    __syncthreads();  // the previous chunk's slab is no longer read
+    const int ci = c0 + sch * 8;
+    float al[8], iv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      al[e] = (c.pre == PRE_SNAKE && ci + e < c.Cin) ? c.alpha[ci + e] : 0.f;
+      iv[e] = (c.pre == PRE_SNAKE && ci + e < c.Cin) ? c.inv[ci + e] : 0.f;
+    }
+    for (int sr = tid >> 3; sr < srows; sr += 32) {
       const int in_row = slab0 + sr;
       float v[8];
-      const bool rok = in_row >= 0 && in_row < Tin;
+      if (in_row >= 0 && in_row < Tin && ci + 8 <= c.Cin) {
+        const float4 u0 = *(const float4*)(xb + (size_t)in_row * c.ldx + ci);
+        const float4 u1 = *(const float4*)(xb + (size_t)in_row * c.ldx + ci + 4);
+        v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w; v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int ci = c0 + ch * 8 + e;
-        float x = 0.f;
-        if (rok && ci < c.Cin) {
-          x = xb[(size_t)in_row * c.ldx + ci];
-          if (c.pre) x = pre_act(x, c.pre, c.slope, c.alpha ? c.alpha[ci] : 0.f, c.inv ? c.inv[ci] : 0.f);
+        for (int e = 0; e < 8; ++e) v[e] = pre_fast(v[e], c.pre, c.slope, al[e], iv[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float x = 0.f;
+          if (in_row >= 0 && in_row < Tin && ci + e < c.Cin) x = pre_fast(xb[(size_t)in_row * c.ldx + ci + e], c.pre, c.slope, al[e], iv[e]);
+          v[e] = x;
         }
-        v[e] = x;
       }
-      slab[hswz(sr, ch)] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+      hl[hswz(sr, sch)] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
     }
-    load_w(0, c0, 0);
+    bf16x8 wa[4][2], wb[4][2];
+    load_w(0, c0, wa);
     __syncthreads();
     for (int j = 0; j < c.taps; ++j) {
-      const int buf = j & 1;
-      if (j + 1 < c.taps) load_w(j + 1, c0, buf ^ 1);
+      if (j + 1 < c.taps) load_w(j + 1, c0, wb);
       const int shift = j * c.d_in - dmin;  // slab row of output row r0 + i for this tap: i + shift
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const int chunk = kk * 2 + (lane >> 5);
-        bf16x8 af[TM], wf[2];
+        bf16x8 af[TM];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(hl[hswz(wave * WTM + i * 32 + (lane & 31) + shift, chunk)]);
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-          const int srow = wave * WTM + i * 32 + (lane & 31) + shift;
-          af[i] = as_bf16x8(slab[hswz(srow, chunk)]);
+          if (i >= live) break;
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[kk][jj], af[i], acc[i][jj], 0, 0, 0);
         }
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) wf[jj] = as_bf16x8(wt[buf * 512 + hswz(jj * 32 + (lane & 31), chunk)]);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[jj], af[i], acc[i][jj], 0, 0, 0);
       }
-      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) wa[kk][jj] = wb[kk][jj];
     }
   }
+
+  // epilogue: each wave stages one 32-row x 64-channel block at a time (fp32, 16 chunks of 4 channels per row,
+  // chunk c at c ^ (row & 15)), then reads it back four rows per instruction
+  __syncthreads();
+  float4* st = (float4*)hl + wave * (32 * 16);
+  const int ncols = min(HB_BN, c.Cout - co0);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int r = r0 + wave * WTM + i * 32 + (lane & 31);
-    if (r > r_hi) continue;
+    if (i >= live) break;
+    const int t = lane & 31;
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) conv_epilogue(c, b, r * c.s_out + oo, co0 + jj * 32, lane, acc[i][jj]);
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c4 = jj * 8 + q * 2 + (lane >> 5);
+        st[t * 16 + (c4 ^ (t & 15))] = make_float4(acc[i][jj][q * 4], acc[i][jj][q * 4 + 1], acc[i][jj][q * 4 + 2], acc[i][jj][q * 4 + 3]);
+      }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int row = rr * 4 + (lane >> 4), c4 = lane & 15;
+      const int r = r0 + wave * WTM + i * 32 + row;
+      const float4 v = st[row * 16 + (c4 ^ (row & 15))];
+      if (r > r_hi || c4 * 4 >= ncols) continue;
+      const size_t orow = (size_t)c.out_off[b] + (size_t)(r * c.s_out + oo);
+      if (c4 * 4 + 3 < ncols) {
+        conv_epilogue4(c, orow, co0 + c4 * 4, v);
+      } else {  // the last channels of a Cout that is not a multiple of 4
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        for (int e = 0; e < 4 && c4 * 4 + e < ncols; ++e) {
+          const int co = co0 + c4 * 4 + e;
+          float x = __fadd_rn(vv[e], c.bias[co]);
+          float* yp = c.y + orow * c.ldy + co;
+          if (c.epi == EPI_STORE) *yp = x;
+          else if (c.epi == EPI_ELU) *yp = x > 0.f ? x : expm1f(x);
+          else {
+            x = __fadd_rn(x, c.res[orow * c.ldy + co]);
+            if (c.epi == EPI_RES) *yp = x;
+            else if (c.epi == EPI_ADD_RES) *yp = __fadd_rn(*yp, x);
+            else {
+              float* sp = c.sum + orow * c.ldy + co;
+              if (c.sum_mode == 0) *sp = x;
+              else if (c.sum_mode == 1) *sp = __fadd_rn(*sp, x);
+              else *sp = __fdiv_rn(__fadd_rn(*sp, x), (float)c.sum_div);
+            }
+          }
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 }
 
@@ -376,21 +477,36 @@ hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
   return hipGetLastError();
 }
 
+// LDS of a BM-row tile: the slab, and at least the epilogue's four 32-row x 64-channel fp32 blocks
+size_t conv_bf16_lds(int BM) {
+  const size_t slab = (size_t)(BM + HB_MAXSPAN) * 8 * sizeof(uint4), epi = 4 * 32 * 16 * sizeof(float4);
+  return slab > epi ? slab : epi;
+}
+
 hipError_t conv_bf16(const ConvDesc& c, const bf16_t* wbf, int max_rows, hipStream_t st) {
   if (c.n_items <= 0 || max_rows <= 0) return hipSuccess;
-  if (c.n_phase < 1 || c.n_phase > 8 || c.s_in != 1) return hipErrorInvalidValue;
+  if (c.n_phase < 1 || c.n_phase > 8 || c.s_in != 1 || c.ldx % 4 || c.ldy % 4) return hipErrorInvalidValue;
   const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
   if (span > HB_MAXSPAN) return hipErrorInvalidValue;
-  constexpr int BM = 128;
-  const size_t lds = ((size_t)(BM + HB_MAXSPAN) * 8 + 2 * 512) * sizeof(uint4);
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)conv_bf16_kernel<BM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr = true;
+  // 512-row tiles when there are enough of them for the chip, else 128
+  const long tiles512 = (long)cdiv(max_rows, 512) * cdiv(c.Cout, HB_BN) * c.n_items * c.n_phase;
+  if (tiles512 >= 256) {
+    constexpr int BM = 512;
+    const size_t lds = conv_bf16_lds(BM);
+    static bool attr = false;
+    if (!attr) {
+      hipError_t e = hipFuncSetAttribute((const void*)conv_bf16_kernel<BM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+      attr = true;
+    }
+    dim3 grid(cdiv(max_rows, BM), cdiv(c.Cout, HB_BN), c.n_items * c.n_phase);
+    hipLaunchKernelGGL(conv_bf16_kernel<BM>, grid, dim3(256), lds, st, c, wbf);
+  } else {
+    constexpr int BM = 128;
+    const size_t lds = conv_bf16_lds(BM);
+    dim3 grid(cdiv(max_rows, BM), cdiv(c.Cout, HB_BN), c.n_items * c.n_phase);
+    hipLaunchKernelGGL(conv_bf16_kernel<BM>, grid, dim3(256), lds, st, c, wbf);
   }
-  dim3 grid(cdiv(max_rows, BM), cdiv(c.Cout, HB_BN), c.n_items * c.n_phase);
-  hipLaunchKernelGGL(conv_bf16_kernel<BM>, grid, dim3(256), lds, st, c, wbf);
   return hipGetLastError();
 }
 

@@ -123,7 +123,7 @@ ConvDesc conv_desc(const Ctx& x, const t2w_conv& w, const float* in, int Cin, in
 int run(const Ctx& x, const ConvDesc& c, int out_cls, const char* what) {
   const int mr = x.L.mx[out_cls] / c.s_out + 2;
   const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
-  if (x.bf16 && c.wbf && c.s_in == 1 && span <= 64)
+  if (x.bf16 && c.wbf && c.s_in == 1 && span <= 64 && c.ldx % 4 == 0 && c.ldy % 4 == 0)
     H_CHECK(conv_bf16(c, c.wbf, mr, x.st), what);
   else
     H_CHECK(conv_f32(c, mr, x.st), what);
