@@ -152,17 +152,25 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     const float* md = mods + (size_t)b * 9 * H;
     const float *sh_a = md, *sc_a = md + H, *g_a = md + 2 * H, *sh_m = md + 3 * H, *sc_m = md + 4 * H, *g_m = md + 5 * H;
     const float *sh_c = md + 6 * H, *sc_c = md + 7 * H, *g_c = md + 8 * H;
-    if (f8) {
-      T2W_CHECK(ln_mod_mx8(w.h, sh_a, sc_a, d.eps_block, w.a8, w.a8s, N, H, st), "ln_mod msa");
-      T2W_CHECK(gemm_bf16(gemm8(w.a8, H, nullptr, w.a8s, k8->qkv_w8, k8->qkv_ws, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H), EPI_BF16, st), "qkv");
-    } else {
-      T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st), "ln_mod msa");
-      T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H, &w), EPI_BF16, st), "qkv");
-    }
     const size_t layer = (size_t)(step * D + b) * (size_t)a->pool_layer_stride;
     bf16_t* kp = (bf16_t*)a->k_pool + layer;
     bf16_t* vp = (bf16_t*)a->v_pool + layer;
-    T2W_CHECK(qk_norm_scatter(w.big, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, w.q, kp, vp, a->new_slot, N, d.heads, st), "qk_norm");
+    GemmArgs gq;
+    if (f8) {
+      T2W_CHECK(ln_mod_mx8(w.h, sh_a, sc_a, d.eps_block, w.a8, w.a8s, N, H, st), "ln_mod msa");
+      gq = gemm8(w.a8, H, nullptr, w.a8s, k8->qkv_w8, k8->qkv_ws, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H);
+    } else {
+      T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st), "ln_mod msa");
+      gq = gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H, &w);
+    }
+    if (!gemm_splits(gq) && H % 256 == 0) {
+      // per-head q / k LayerNorm and the key / value scatter in the projection's epilogue
+      gq.qk = QkvOut{w.q, kp, vp, a->new_slot, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, H};
+      T2W_CHECK(gemm_bf16(gq, EPI_QKV, st), "qkv");
+    } else {
+      T2W_CHECK(gemm_bf16(gq, EPI_BF16, st), "qkv");
+      T2W_CHECK(qk_norm_scatter(w.big, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, w.q, kp, vp, a->new_slot, N, d.heads, st), "qk_norm");
+    }
     AttnArgs at;
     at.q = w.q; at.k_pool = kp; at.v_pool = vp; at.out = w.ao; at.kv_idx = a->kv_idx; at.row_start = a->row_start;
     at.row_len = a->row_len; at.row_kv_off = a->row_kv_off; at.row_kv_len = a->row_kv_len; at.tiles = a->tiles;

@@ -40,6 +40,16 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// sum over the 16 lanes of a DPP row (lanes 16 r .. 16 r + 15), every lane gets it: quad swaps, then half-row and
+// row mirrors (each step pairs a lane with one not yet summed in); VALU only, no LDS
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)); // row_half_mirror
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)); // row_mirror
+  return v;
+}
+
 // MX fp8: OCP e4m3 values with one power-of-two (E8M0) scale per 32 consecutive K values.  The scale is the smallest
 // power of two that keeps the block's largest magnitude within e4m3's 448, so nothing clips: with amax = 1.m * 2^E and
 // 448 = 1.75 * 2^8, that exponent is E - 8, plus one when 1.m > 1.75.  Returns the unbiased exponent in [-126, 126].

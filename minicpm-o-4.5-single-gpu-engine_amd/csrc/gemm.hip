@@ -263,6 +263,17 @@ struct Tile {
     constexpr int RB = NRB < 8 ? NRB : 8;
     const int cc = lane % CPR;
     const Cols<EPI> cols(g, n0 + wn * WTN + cc * 4);
+    // EPI_QKV: this lane's part (q, k, v), column and head offset, and the LayerNorm affine of its four columns
+    int qpart = 0, qcol = 0;
+    float4 qlw = make_float4(0.f, 0.f, 0.f, 0.f), qlb = qlw;
+    if constexpr (EPI == EPI_QKV) {
+      qpart = cols.n / g.qk.H;
+      qcol = cols.n - qpart * g.qk.H;
+      if (qpart < 2) {
+        qlw = *(const float4*)((qpart ? g.qk.kw : g.qk.qw) + (qcol & 63));
+        qlb = *(const float4*)((qpart ? g.qk.kb : g.qk.qb) + (qcol & 63));
+      }
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int r = lane & 31;
@@ -278,7 +289,7 @@ struct Tile {
 #pragma unroll
       for (int b = 0; b < NRB; b += RB) {
         float4 v[RB], h[RB];
-        int m[RB];
+        int m[RB], slot[RB];
 #pragma unroll
         for (int x = 0; x < RB; ++x) {
           const int row = (b + x) * RPI + lane / CPR;
@@ -286,10 +297,34 @@ struct Tile {
           v[x] = st[row * CPR + (cc ^ (row & (CPR - 1)))];
           h[x] = make_float4(0.f, 0.f, 0.f, 0.f);
           if (EPI == EPI_RESID_F32 && cols.full && m[x] < g.M) h[x] = *(const float4*)((const float*)g.C + (size_t)m[x] * g.ldc + cols.n);
+          slot[x] = 0;
+          if (EPI == EPI_QKV && qpart > 0 && m[x] < g.M) slot[x] = g.qk.slots[m[x]];
         }
 #pragma unroll
         for (int x = 0; x < RB; ++x) {
-          if constexpr (EPI == EPI_GELU_MX8) {
+          if constexpr (EPI == EPI_QKV) {
+            // the 16 lanes (one DPP row) holding this row's 64 columns of one head: heads are 64-aligned in the tile
+            const QkvOut& o = g.qk;
+            float y[4] = {v[x].x * cols.wsc.x + cols.bias.x, v[x].y * cols.wsc.y + cols.bias.y,
+                          v[x].z * cols.wsc.z + cols.bias.z, v[x].w * cols.wsc.w + cols.bias.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(y[e]));  // the projection is rounded to bf16 first
+            if (qpart < 2) {
+              const float mean = row16_sum(y[0] + y[1] + y[2] + y[3]) * (1.0f / 64.0f);
+              float q = 0.f;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) { y[e] -= mean; q += y[e] * y[e]; }
+              const float rstd = rsqrtf(row16_sum(q) * (1.0f / 64.0f) + o.eps);
+              y[0] = y[0] * rstd * qlw.x + qlb.x;
+              y[1] = y[1] * rstd * qlw.y + qlb.y;
+              y[2] = y[2] * rstd * qlw.z + qlb.z;
+              y[3] = y[3] * rstd * qlw.w + qlb.w;
+            }
+            if (m[x] < g.M) {
+              bf16_t* dst = qpart == 0 ? o.q_out + (size_t)m[x] * o.H : (qpart == 1 ? o.k_pool : o.v_pool) + (size_t)slot[x] * o.H;
+              *(uint2*)(dst + qcol) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+            }
+          } else if constexpr (EPI == EPI_GELU_MX8) {
             // the 8 lanes holding this row's 32 consecutive columns share one block scale (N % 32 == 0)
             const float4 o = cols.apply(v[x], h[x]);
             float a = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
@@ -397,21 +432,28 @@ hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
 }  // namespace
 
 int pick_cfg(const GemmArgs& g) {
-  // 256x256 tiles (fp8: 256x128) once there are enough rows to fill them
-  if (g.M >= 1024 && g.N >= 256) return g.w_scale ? 2 : 1;
-  return 0;
+  // 256x256 tiles (fp8: 256x128) once there are enough rows to fill them; for the wide projections the narrower
+  // tiles measured faster at 12800 rows (qkv, N = 3072: 256x128 105 us vs 114; fc1, N = 2048: 128x128 85 us vs 95)
+  if (g.M < 1024 || g.N < 256) return 0;
+  if (g.w_scale) return 2;
+  if (g.N >= 3072) return 2;
+  if (g.N >= 2048) return 0;
+  return 1;
+}
+
+bool gemm_splits(const GemmArgs& g) {
+  if (!g.ws || g.w_scale || g.M <= 0) return false;
+  // a grid of fewer than 128 tiles leaves most of the 256 CUs idle: split K instead
+  const int c = pick_cfg(g), bm = c == 0 ? 128 : 256, bn = c == 1 ? 256 : 128;
+  const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+  return tiles < 128 && splitk_plan(g.M, g.N, g.K, g.ws_bytes).splits > 1;
 }
 
 hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
-  if (cfg < 0 && g.ws && !g.w_scale) {
-    // a grid of fewer than 128 tiles leaves most of the 256 CUs idle: split K instead
-    const int c = pick_cfg(g), bm = c == 0 ? 128 : 256, bn = c == 1 ? 256 : 128;
-    const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
-    if (tiles < 128) {
-      const SplitPlan p = splitk_plan(g.M, g.N, g.K, g.ws_bytes);
-      if (p.splits > 1) return gemm_splitk(g, epi, p, g.ws, st);
-    }
+  if (cfg < 0 && gemm_splits(g)) {
+    if (epi == EPI_QKV || epi == EPI_GELU_MX8) return hipErrorInvalidValue;  // tile-path epilogues
+    return gemm_splitk(g, epi, splitk_plan(g.M, g.N, g.K, g.ws_bytes), g.ws, st);
   }
   const bool taps = g.a_src != nullptr;
   switch (epi * 2 + (taps ? 1 : 0)) {
@@ -426,6 +468,9 @@ hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
     case EPI_GELU_MX8 * 2:
       if (!g.w_scale || !g.c_scale || g.N % 32) return hipErrorInvalidValue;
       return launch_epi<EPI_GELU_MX8, false>(g, cfg, st);
+    case EPI_QKV * 2:
+      if (g.N != 3 * g.qk.H || g.qk.H % 256) return hipErrorInvalidValue;
+      return launch_epi<EPI_QKV, false>(g, cfg, st);
   }
   return hipErrorInvalidValue;
 }

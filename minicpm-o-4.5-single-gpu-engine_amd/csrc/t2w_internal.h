@@ -9,7 +9,19 @@ namespace t2w {
 typedef uint16_t bf16_t;
 
 // EPI_GELU_MX8: GELU, then MX fp8 codes to C (bytes, ldc) and block scales to c_scale (N % 32 == 0)
-enum Epi { EPI_BF16 = 0, EPI_GELU_BF16 = 1, EPI_RESID_F32 = 2, EPI_F32 = 3, EPI_GELU_MX8 = 4 };
+// EPI_QKV: the attention projection (N = 3 H): q and k rounded to bf16, per-head LayerNorm + affine, q to its token
+// row of q_out, k and v to the token's key slot of the pools (fields qk.*); tile path only
+enum Epi { EPI_BF16 = 0, EPI_GELU_BF16 = 1, EPI_RESID_F32 = 2, EPI_F32 = 3, EPI_GELU_MX8 = 4, EPI_QKV = 5 };
+
+struct QkvOut {
+  bf16_t* q_out;        // [M, H]
+  bf16_t* k_pool;       // [slots, H]
+  bf16_t* v_pool;
+  const int* slots;     // [M] key slot of each token
+  const float *qw, *qb, *kw, *kb;  // [64] each
+  float eps;
+  int H;
+};
 
 struct GemmArgs {
   const bf16_t* A;     // dense: A[m * lda + k]; taps: A[(a_src[m] + k / tapC) * lda + k % tapC]
@@ -32,10 +44,12 @@ struct GemmArgs {
   const float* w_scale;
   uint8_t* c_scale;    // EPI_GELU_MX8: output block scales c_scale[m * c_sld + n / 32]
   int c_sld;
+  QkvOut qk;           // EPI_QKV
 };
 
 // cfg < 0: by shape (split-K through g.ws when a tile grid would be too small to fill the chip)
 hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg = -1);
+bool gemm_splits(const GemmArgs& g);  // whether gemm_bf16 (cfg < 0) takes the split-K path for g
 
 struct SplitPlan {
   int splits;  // 0: split-K not possible for this shape / workspace
