@@ -33,6 +33,7 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
   const int row = a.tiles[2 * tile];
   const int q0 = a.tiles[2 * tile + 1];
   const int T = a.row_len[row];
+  if (q0 >= T) return;  // a filler tile past its row's end (padded tile lists): the whole workgroup leaves together
   const int start = a.row_start[row], kvoff = a.row_kv_off[row], kvlen = a.row_kv_len[row];
   const int H = a.heads * 64;
   const int half = lane >> 5, col = lane & 31;

@@ -217,6 +217,93 @@ def plan_call(rows: list[FastRow], Ts: list[int], new: list[list[int]], keep: li
     return {"n_tok": o, "n_rows": 2 * n, "half": o // 2, "n_tiles": len(tiles) // 2, "parts": parts, "new": new, "rows": rows}
 
 
+ROW_BUCKETS = (2, 4, 8, 16, 32, 64)  # request rows (both CFG halves) of a graph bucket, padding rows excluded
+MAX_GRAPH_T = 56  # frames per row of the streaming windows the row buckets are sized for
+SETUP_TOKENS = 4096  # row buckets up to SETUP_ROWS also take whole-prompt setups up to this many tokens
+SETUP_ROWS = 8
+
+
+def token_buckets(rb: int) -> list[int]:
+    """Token buckets (both halves) of row bucket ``rb`` (``token_buckets``, ``engine/runtime/dit_fast.py:43-55``):
+    multiples of 128 below 512, then of 256, up to the bucket's top (``MAX_GRAPH_T`` frames per row, at least
+    ``SETUP_TOKENS`` for small buckets), which is a bucket itself."""
+    top = max(rb * MAX_GRAPH_T, SETUP_TOKENS if rb <= SETUP_ROWS else 0)
+    return [b for b in list(range(128, 512, 128)) + list(range(512, top, 256)) if b < top] + [top]
+
+
+def bucket_of(n_rows: int, n_tok: int) -> tuple[int, int] | None:
+    """The smallest row bucket holding ``n_rows`` request rows with a token bucket for ``n_tok`` tokens, and that token
+    bucket (``FastDiT._bucket``, ``engine/runtime/dit_fast.py:212-221``); None when no bucket fits."""
+    for rb in ROW_BUCKETS:
+        if rb >= n_rows:
+            nb = next((b for b in token_buckets(rb) if b >= n_tok), None)
+            if nb is not None:
+                return rb, nb
+    return None
+
+
+def bucket_tiles(rb: int, nb: int) -> int:
+    """Attention tiles of a bucket's graph: a half's real rows of T_i tokens take sum ceil(T_i / 64) tiles, at most
+    (tokens + 63 rows) / 64, so tokens / 64 + rows per half (the padding row included) covers every call."""
+    return 2 * ((nb // 2 + 63) // 64 + rb // 2 + 1)
+
+
+def pad_plan(p: dict, rb: int, nb: int, kv_scratch: int, cnn_scratch: int) -> dict:
+    """Pads a call's plan to bucket ``(rb, nb)`` (the layout of ``FastDiT._plan``, ``engine/runtime/dit_fast.py:223-263``):
+    each CFG half holds its request rows, ``rb / 2 - n`` empty rows and one padding row carrying the half's
+    ``nb / 2 - half`` padding tokens.  Padding tokens have zero inputs, write their keys and values to one scratch slot
+    and attend to it alone; empty and padding rows read and write the scratch conv-cache slot; their outputs are
+    discarded.  No real row reads padding data, since every kernel works within a token or a row.  The attention tile
+    list is filled up to ``bucket_tiles`` with tiles past a row's end, which the kernel skips."""
+    tok_row, tok_pos, _, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, kv = p["parts"]
+    n = p["n_rows"] // 2
+    hr, half_b = rb // 2 + 1, nb // 2
+    pad = half_b - p["half"]
+    row_tiles: dict[int, list[int]] = {}
+    for i in range(0, len(tiles), 2):
+        row_tiles.setdefault(tiles[i], []).append(tiles[i + 1])
+    out = [[] for _ in range(12)]
+    t_row, t_pos, _, t_slot, t_start, t_len, t_kvo, t_kvl, t_rd, t_wr, t_tiles, t_kv = out
+    o = 0
+    for h in range(2):  # cond half, then uncond half
+        for j in range(hr):
+            r_new = h * hr + j
+            if j < n:  # a request row
+                r = h * n + j
+                s0, T = row_start[r], lens[r]
+                t_pos += tok_pos[s0:s0 + T]
+                t_slot += new_slot[s0:s0 + T]
+                t_kvo.append(len(t_kv))
+                t_kv += kv[kv_off[r]:kv_off[r] + kv_len[r]]
+                t_kvl.append(kv_len[r])
+                t_rd.append(rd[r])
+                t_wr.append(wr[r])
+                q0s = row_tiles.get(r, [])
+            else:  # empty rows, then the padding row
+                T = pad if j == hr - 1 else 0
+                t_pos += list(range(T))
+                t_slot += [kv_scratch] * T
+                t_kvo.append(len(t_kv))
+                t_kv += [kv_scratch] * T
+                t_kvl.append(T)
+                t_rd.append(cnn_scratch)
+                t_wr.append(cnn_scratch)
+                q0s = list(range(0, T, 64))
+            t_row += [r_new] * T
+            t_tiles += [v for q0 in q0s for v in (r_new, q0)]
+            t_start.append(o)
+            t_len.append(T)
+            o += T
+    n_tiles = bucket_tiles(rb, nb)
+    if len(t_tiles) // 2 > n_tiles:
+        raise AssertionError("attention tiles beyond the bucket's bound")
+    t_tiles += [hr - 1, 1 << 30] * (n_tiles - len(t_tiles) // 2)
+    out[2] = [i + 2 * r for i, r in enumerate(t_row)]
+    q = dict(p)
+    q.update({"n_tok": o, "n_rows": 2 * hr, "half": half_b, "n_tiles": n_tiles, "parts": out, "real_half": p["half"]})
+    return q
+
+
 def advance_row(r: FastRow, new: list[int], keep: bool, keep_len: int) -> list[int]:
     """After a solve: a kept window's slots join the row as ``[new, cache]`` (the reference's concatenation order), then
     the order is trimmed to its first ``keep_len`` and last 100 entries (``engine/runtime/dit_fast.py:480-490``) and
@@ -234,18 +321,31 @@ def advance_row(r: FastRow, new: list[int], keep: bool, keep_len: int) -> list[i
     return freed
 
 
+def _pad_halves(x: torch.Tensor, real: int, padded: int) -> torch.Tensor:
+    """Conditional-token rows [real, C] padded with zero rows to [padded, C] (the padding rows come last)."""
+    if padded == real:
+        return x
+    return torch.cat([x, x.new_zeros(padded - real, x.shape[1])])
+
+
 class FastDiT:
     """The packed ragged CFG Euler solve over per-request caches (``FastDiT`` of ``engine/runtime/dit_fast.py``)."""
 
-    def __init__(self, model: DiTModel, n_slots: int = 32768, max_streams: int = 96, use_graphs: bool = False, fp8: bool = False):
-        """``fp8``: solves run the block GEMMs on fp8 MFMA (the model must have been built with fp8 weights)."""
+    def __init__(self, model: DiTModel, n_slots: int = 32768, max_streams: int = 96, use_graphs: bool = False, fp8: bool = False,
+                 buckets: bool = True):
+        """``fp8``: solves run the block GEMMs on fp8 MFMA (the model must have been built with fp8 weights).
+        ``buckets`` (with ``use_graphs``): a call that fits a (rows, tokens) bucket is padded to it, so that one captured
+        graph serves every call of the bucket; other calls (and every call without ``buckets``) take a graph keyed by
+        their exact shape."""
+        self.buckets = buckets
         if fp8 and not model.fp8:
             raise ValueError("fp8 solves need a DiTModel built with fp8=True")
         self.fp8 = fp8
         cfg = model.cfg
         self.model, self.cfg, self.device = model, cfg, model.device
         S, D, H = cfg.steps, cfg.depth, cfg.hidden
-        self.pool = SlotPool(n_slots)
+        self.pool = SlotPool(n_slots - 1)
+        self.kv_scratch = n_slots - 1  # key slot written by padding tokens, outside the pool
         self.n_slots = n_slots
         self.k_pool = torch.zeros(S * D, n_slots, H, dtype=torch.bfloat16, device=self.device)
         self.v_pool = torch.zeros_like(self.k_pool)
@@ -362,6 +462,13 @@ class FastDiT:
             _lib.check(L.t2w_dit_solve(self.model.handle, C.byref(a), st), "dit_solve")
             self.counts["eager"] += 1
             return out
+        real_half = p["half"]
+        bucket = bucket_of(R, N) if self.buckets else None
+        if bucket is not None:
+            p = pad_plan(p, *bucket, self.kv_scratch, self.cnn_scratch)
+            x0 = _pad_halves(x0, real_half, p["half"])
+            stat = _pad_halves(stat, real_half, p["half"])
+            N, R = p["n_tok"], p["n_rows"]
         key = (N, R, p["n_tiles"], chunk, self.fp8)
         flat = np.concatenate([np.asarray(x, dtype=np.int32) for x in p["parts"]])
         g = self.graphs.get(key)
@@ -369,7 +476,7 @@ class FastDiT:
             L.t2w_graph_destroy(g["graph"])
             g = None
         if g is None:
-            g = {"tables": torch.zeros(flat.size + 8192, dtype=torch.int32, device=self.device), "x0": torch.empty_like(x0),
+            g = {"tables": torch.zeros(flat.size + max(8192, flat.size), dtype=torch.int32, device=self.device), "x0": torch.empty_like(x0),
                  "stat": torch.empty_like(stat), "out": torch.empty(p["half"], self.cfg.mel, device=self.device),
                  "ws": torch.empty(L.t2w_dit_workspace_bytes(self.model.handle, N, R), dtype=torch.uint8, device=self.device),
                  "graph": None}
@@ -391,7 +498,7 @@ class FastDiT:
             g["graph"] = h
         _lib.check(L.t2w_graph_launch(g["graph"], st), "graph_launch")
         self.counts["graph"] += 1
-        return g["out"].clone()
+        return g["out"][:real_half].clone()
 
     def _capture_stream(self):
         if getattr(self, "_cap", None) is None:

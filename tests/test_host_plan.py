@@ -3,7 +3,7 @@
 import pytest
 
 import t2w_amd  # noqa: F401
-from t2w_amd.dit import FastRow, SlotPool, advance_row, plan_call
+from t2w_amd.dit import FastRow, SlotPool, advance_row, bucket_of, bucket_tiles, pad_plan, plan_call, token_buckets
 from oracle import dit as od
 
 
@@ -24,6 +24,50 @@ def test_plan_tables_are_consistent():
     covered = sorted((r, q) for r, q0 in zip(tiles[::2], tiles[1::2]) for q in range(q0, min(q0 + 64, lens[r])))
     assert covered == sorted((r, q) for r in range(4) for q in range(lens[r]))
     assert set(rd).isdisjoint(set(wr))
+
+
+def test_bucket_table():
+    """Row buckets of 2..64 request rows, token buckets (both halves) in steps of 128 below 512 and 256 above, up to 56
+    frames per row (at least 4096 tokens for up to 8 rows); calls beyond the largest bucket have none."""
+    assert token_buckets(2)[:6] == [128, 256, 384, 512, 768, 1024] and token_buckets(2)[-1] == 4096
+    assert token_buckets(16)[-2:] == [768, 896] and token_buckets(64)[-1] == 3584
+    assert bucket_of(4, 220) == (4, 256) and bucket_of(4, 256) == (4, 256) and bucket_of(3, 257) == (4, 384)
+    assert bucket_of(2, 5000) is None and bucket_of(6, 4000) == (8, 4096) and bucket_of(10, 4000) is None
+    assert bucket_of(10, 900) == (32, 1024) and bucket_of(64, 3584) == (64, 3584) and bucket_of(66, 10) is None
+
+
+@pytest.mark.parametrize("Ts,keep", [([70, 1], [True, False]), ([64, 128, 5], [True, True, False]), ([50], [True])])
+def test_padded_plan_keeps_every_real_row(Ts, keep):
+    n = len(Ts)
+    rows = [FastRow(order=list(range(1000 * r, 1000 * r + 7 * r)), cnn=(2 * r, 2 * r + 1), cur=r % 2) for r in range(2 * n)]
+    new = [list(range(100000 + 1000 * r, 100000 + 1000 * r + Ts[r % n])) for r in range(2 * n)]
+    p = plan_call(rows, Ts, new, keep, cnn_scratch=99)
+    rb, nb = bucket_of(2 * n, p["n_tok"])
+    q = pad_plan(p, rb, nb, kv_scratch=77, cnn_scratch=99)
+    hr = rb // 2 + 1
+    tok_row, tok_pos, a_src, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, kv = q["parts"]
+    P = p["parts"]
+    assert q["n_rows"] == 2 * hr and q["n_tok"] == nb and q["half"] == nb // 2 and len(tok_row) == nb
+    assert sum(lens[:hr]) == sum(lens[hr:]) == nb // 2
+    assert a_src == [i + 2 * r for i, r in enumerate(tok_row)]
+    for h in range(2):
+        for j in range(hr):
+            r = h * hr + j
+            s, T = row_start[r], lens[r]
+            assert tok_row[s:s + T] == [r] * T and tok_pos[s:s + T] == list(range(T))
+            if j < n:  # a request row: the same tables as unpadded
+                o = h * n + j
+                assert T == P[5][o] and new_slot[s:s + T] == P[3][P[4][o]:P[4][o] + T]
+                assert kv[kv_off[r]:kv_off[r] + kv_len[r]] == P[11][P[6][o]:P[6][o] + P[7][o]]
+                assert (rd[r], wr[r]) == (P[8][o], P[9][o])
+            else:  # empty rows, then the padding row: scratch slots only
+                assert T == (0 if j < hr - 1 else nb // 2 - p["half"])
+                assert new_slot[s:s + T] == [77] * T and kv[kv_off[r]:kv_off[r] + kv_len[r]] == [77] * T
+                assert rd[r] == wr[r] == 99
+    assert q["n_tiles"] == len(tiles) // 2 == bucket_tiles(rb, nb)
+    live = [(r, q0) for r, q0 in zip(tiles[::2], tiles[1::2]) if q0 < lens[r]]
+    covered = sorted((r, t) for r, q0 in live for t in range(q0, min(q0 + 64, lens[r])))
+    assert covered == sorted((r, t) for r in range(2 * hr) for t in range(lens[r]))
 
 
 @pytest.mark.parametrize("keep_len", [0, 40, 300])
