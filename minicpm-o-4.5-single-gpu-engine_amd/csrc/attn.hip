@@ -103,8 +103,9 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
   f32x16 o0, o1;
 #pragma unroll
   for (int r = 0; r < 16; ++r) { o0[r] = 0.f; o1[r] = 0.f; }
-  float m = NEG, l = 0.f;
+  float m = NEG, l = 0.f;  // running max (raw score units) and sum
   const float sl2 = a.scale * 1.4426950408889634f;
+  const int lim_w0 = a.chunk > 0 ? min(T, (qpos0 / a.chunk + 1) * a.chunk) : T;  // the wave's first query's limit
 
   int slot_next = 0;
   if (ntiles > 0) {
@@ -123,59 +124,80 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
       int kb, ke;
       T2W_TILE_RANGE(t, kb, ke)
       const bool cached = t >= n1;
-      // visible new keys of this query end at lim_me; cached keys at ke
+      // visible new keys of this query end at lim_me; cached keys at ke.  lim_lo: the wave's smallest limit (its first
+      // query's: limits grow with the position), for the all-visible test
       const int lim = cached ? ke : min(ke, lim_me);
+      const int lim_lo = cached ? ke : min(ke, lim_w0);
+      const bool two = kb + 32 < ke;  // the second 32-key half holds keys
+      // scores of both halves first: one max, one rescale and one exponent pass per 64 keys
+      f32x16 sc[2];
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
-        const int sb = kb + sub * 32;
-        if (sb < ke) {
-          f32x16 sc;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+        for (int r = 0; r < 16; ++r) sc[sub][r] = 0.f;
+        if (sub == 0 || two) {
           const int krow = sub * 32 + col;
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) {
             const int chunk = kk * 2 + half;
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ks[s][krow * 8 + (chunk ^ (krow & 7))]), qf[kk], sc, 0, 0, 0);
+            sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ks[s][krow * 8 + (chunk ^ (krow & 7))]), qf[kk], sc[sub], 0, 0, 0);
           }
-          // lane holds query col, keys sb + (r/4)*8 + half*4 + r%4; invisible keys score NEG
-          const int nvis = lim - (sb + half * 4);  // key offsets below nvis (relative to sb + half*4) are visible
-          float mx = NEG;
+        }
+      }
+      // lane holds query col, keys kb + sub * 32 + (r/4)*8 + half*4 + r%4; invisible keys score -inf (raw units)
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const int sb = kb + sub * 32;
+        if (sb + 32 > lim_lo || (sub == 1 && !two)) {  // wave-uniform: some key of this half is invisible to some query
+          const int nvis = lim - (sb + half * 4);
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int off = (r >> 2) * 8 + (r & 3);
-            sc[r] = off < nvis ? sc[r] * sl2 : NEG;
-            mx = fmaxf(mx, sc[r]);
+            sc[sub][r] = off < nvis ? sc[sub][r] : -__builtin_inff();
           }
-          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-          const float mn = fmaxf(m, mx);
-          const float alpha = __builtin_amdgcn_exp2f(m - mn);
-          // a query whose keys are all invisible so far keeps m = NEG; its probabilities must stay 0
-          const float live = mn > 0.5f * NEG ? 1.0f : 0.0f;
-          float rs = 0.f;
-          float p[16];
+        }
+      }
+      float mx = -__builtin_inff();
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            p[r] = __builtin_amdgcn_exp2f(sc[r] - mn) * live;
-            rs += p[r];
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // m starts at a finite -1e30: keys all invisible so far give exp2(-inf) = 0 and leave m, l and o alone
+      const float mn = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f((m - mn) * sl2);
+      const float mb = -mn * sl2;
+      // probabilities, packed to bf16 as they are made (the P.V operands), their fp32 sum on the side
+      float rs = 0.f;
+      uint4 pf[2][2];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          float e[8];
+#pragma unroll
+          for (int x = 0; x < 8; ++x) {
+            e[x] = __builtin_amdgcn_exp2f(fmaf(sc[sub][8 * hh + x], sl2, mb));
+            rs += e[x];
           }
-          rs += __shfl_xor(rs, 32, 64);
-          l = l * alpha + rs;
-          m = mn;
+          pf[sub][hh] = make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
+        }
+      rs += __shfl_xor(rs, 32, 64);
+      l = l * alpha + rs;
+      m = mn;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // the running max moved for some query of the wave
 #pragma unroll
-          for (int r = 0; r < 16; ++r) { o0[r] *= alpha; o1[r] *= alpha; }
+        for (int r = 0; r < 16; ++r) { o0[r] *= alpha; o1[r] *= alpha; }
+      }
 #pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            union { uint4 u; bf16x8 b; } pf;
-            pf.u = make_uint4(pack2(p[8 * hh], p[8 * hh + 1]), pack2(p[8 * hh + 2], p[8 * hh + 3]), pack2(p[8 * hh + 4], p[8 * hh + 5]),
-                              pack2(p[8 * hh + 6], p[8 * hh + 7]));
-            const int chunk = hh * 2 + half;
-            const int d0 = col, d1 = 32 + col;
-            const uint4 v0 = vt[s][sub][d0 * 4 + (chunk ^ ((d0 >> 1) & 3))];
-            const uint4 v1 = vt[s][sub][d1 * 4 + (chunk ^ ((d1 >> 1) & 3))];
-            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v0), pf.b, o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v1), pf.b, o1, 0, 0, 0);
-          }
+      for (int sub = 0; sub < 2; ++sub) {
+        if (sub == 1 && !two) break;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int chunk = hh * 2 + half;
+          const int d0 = col, d1 = 32 + col;
+          const uint4 v0 = vt[s][sub][d0 * 4 + (chunk ^ ((d0 >> 1) & 3))];
+          const uint4 v1 = vt[s][sub][d1 * 4 + (chunk ^ ((d1 >> 1) & 3))];
+          o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v0), as_bf16x8(pf[sub][hh]), o0, 0, 0, 0);
+          o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v1), as_bf16x8(pf[sub][hh]), o1, 0, 0, 0);
         }
       }
     }
