@@ -432,12 +432,12 @@ hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
 }  // namespace
 
 int pick_cfg(const GemmArgs& g) {
-  // 256x256 tiles (fp8: 256x128) once there are enough rows to fill them; for the wide projections the narrower
-  // tiles measured faster at 12800 rows (qkv, N = 3072: 256x128 105 us vs 114; fc1, N = 2048: 128x128 85 us vs 95)
+  // 256x256 tiles (fp8: 256x128) once there are enough rows to fill them; for qkv (N = 3072) 256x128 measured faster
+  // at 12800 rows (105 us vs 114).  fc1 (N = 2048, GELU) takes 256x256 since its epilogue uses the hardware reciprocal
+  // (DiT solve 143.5 -> 142.0 ms against 128x128)
   if (g.M < 1024 || g.N < 256) return 0;
   if (g.w_scale) return 2;
   if (g.N >= 3072) return 2;
-  if (g.N >= 2048) return 0;
   return 1;
 }
 
