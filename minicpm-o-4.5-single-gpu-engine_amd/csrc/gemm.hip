@@ -451,6 +451,7 @@ bool gemm_splits(const GemmArgs& g) {
 
 hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
+  if (cfg < 0 && gemm_small_fits(g, epi)) return gemm_small(g, epi, st);
   if (cfg < 0 && gemm_splits(g)) {
     if (epi == EPI_QKV || epi == EPI_GELU_MX8) return hipErrorInvalidValue;  // tile-path epilogues
     return gemm_splitk(g, epi, splitk_plan(g.M, g.N, g.K, g.ws_bytes), g.ws, st);

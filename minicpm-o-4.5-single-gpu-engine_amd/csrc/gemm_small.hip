@@ -1,0 +1,134 @@
+// bf16 MFMA GEMM for calls with very few rows (a streaming chunk: ~100 tokens), in one kernel.
+//
+// At ~100 rows the time of a GEMM is the weight stream plus fixed per-kernel costs, and a split-K pass followed by a
+// separate reduce kernel pays those costs twice and moves fp32 partials through HBM.  Here a workgroup of 16 waves
+// owns 32 output columns x 32 rows and splits K over its waves: each wave loads its (at most three) 64-K steps of the
+// W rows and activation rows straight into registers, all loads in flight before the first MFMA (64 contiguous bytes
+// per lane and step, seen by the MFMA as four 16-K slices of the same K permutation on both sides), then leaves its
+// 32x32 fp32 block in LDS.  After one barrier the block is summed over the waves in wave order (deterministic) and the
+// epilogue (bias, GELU, gated fp32 residual) writes four consecutive columns per lane.
+//
+// MFMA roles: W is the A operand (its 32 rows are output columns n0 ..), the activations the B operand (32 token
+// rows), so a lane's four consecutive accumulator registers are four consecutive output columns of one token.
+#include "common.h"
+#include "t2w_internal.h"
+
+namespace t2w {
+
+namespace {
+
+constexpr int GS_WAVES = 16;  // waves per workgroup, sharing K
+constexpr int GS_MAXSTEPS = 3;  // 64-K steps per wave: K <= 16 * 3 * 64 = 3072
+
+template <bool TAPS, int EPI>
+__global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
+  __shared__ float4 red[GS_WAVES][4][64];  // per wave: its 32x32 block in register order (quad q, lane)
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
+  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
+  const int KS = g.K / 64;
+  const int s0 = w * KS / GS_WAVES, s1 = (w + 1) * KS / GS_WAVES;  // this wave's steps (possibly none)
+  const bf16_t* wrow = g.B + (size_t)min(n0 + c, g.N - 1) * g.ldb + h * 32;
+  const int m = min(m0 + c, g.M - 1);  // rows past M load row M - 1; their results are never stored
+  const bf16_t* arow = g.A + (size_t)(TAPS ? g.a_src[m] : m) * g.lda + h * 32;
+
+  uint4 wf[GS_MAXSTEPS][4], af[GS_MAXSTEPS][4];
+#pragma unroll
+  for (int t = 0; t < GS_MAXSTEPS; ++t) {
+    if (s0 + t < s1) {
+      const int k0 = (s0 + t) * 64;
+      size_t aoff = k0;
+      if (TAPS) {
+        const int tap = k0 / g.tapC;  // a 64-K step never straddles two taps (tapC % 64 == 0)
+        aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        wf[t][kk] = *(const uint4*)(wrow + k0 + kk * 8);
+        af[t][kk] = *(const uint4*)(arow + aoff + kk * 8);
+      }
+    }
+  }
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int t = 0; t < GS_MAXSTEPS; ++t)
+    if (s0 + t < s1) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wf[t][kk]), as_bf16x8(af[t][kk]), acc, 0, 0, 0);
+    }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) red[w][q][lane] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+  __syncthreads();
+
+  // one float4 (four columns of one row) per thread of the first four waves, summed over the waves in order
+  if (tid >= 256) return;
+  const int q = tid >> 6, l = tid & 63;
+  float4 a = red[0][q][l];
+#pragma unroll
+  for (int x = 1; x < GS_WAVES; ++x) {
+    const float4 b = red[x][q][l];
+    a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+  }
+  // lane l of the MFMA holds token m0 + l % 32 and columns n0 + q * 8 + (l / 32) * 4 + 0..3
+  const int mo = m0 + (l & 31), n = n0 + q * 8 + (l >> 5) * 4;
+  if (mo >= g.M || n >= g.N) return;
+  const float v[4] = {a.x, a.y, a.z, a.w};
+  if (n + 3 < g.N) {
+    const float4 b = *(const float4*)(g.bias + n);
+    float o[4] = {v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
+    const size_t off = (size_t)mo * g.ldc + n;
+    if (EPI == EPI_GELU_BF16) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = gelu_tanh(o[e]);
+    }
+    if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) {
+      *(uint2*)((bf16_t*)g.C + off) = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
+    } else if (EPI == EPI_RESID_F32) {
+      const float4 gt = *(const float4*)(g.gate + n);
+      float4* hp = (float4*)((float*)g.C + off);
+      const float4 hv = *hp;
+      *hp = make_float4(hv.x + gt.x * o[0], hv.y + gt.y * o[1], hv.z + gt.z * o[2], hv.w + gt.w * o[3]);
+    } else {
+      *(float4*)((float*)g.C + off) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+    return;
+  }
+  for (int e = 0; e < 4 && n + e < g.N; ++e) {  // the last columns of an N that is not a multiple of 4
+    float x = v[e] + g.bias[n + e];
+    const size_t off = (size_t)mo * g.ldc + n + e;
+    if (EPI == EPI_GELU_BF16) x = gelu_tanh(x);
+    if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[off] = f2bf(x);
+    else if (EPI == EPI_RESID_F32) ((float*)g.C)[off] += g.gate[n + e] * x;
+    else ((float*)g.C)[off] = x;
+  }
+}
+
+template <int EPI>
+hipError_t launch_small(const GemmArgs& g, hipStream_t st) {
+  const dim3 grid((g.N + 31) / 32, (g.M + 31) / 32);
+  if (g.a_src) hipLaunchKernelGGL((gemm_small_kernel<true, EPI>), grid, dim3(64 * GS_WAVES), 0, st, g);
+  else hipLaunchKernelGGL((gemm_small_kernel<false, EPI>), grid, dim3(64 * GS_WAVES), 0, st, g);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_small_fits(const GemmArgs& g, int epi) {
+  return g.M > 0 && g.M <= GEMM_SMALL_MAX_M && !g.w_scale && epi <= EPI_F32 && g.K % 64 == 0 &&
+         g.K <= GS_WAVES * GS_MAXSTEPS * 64 && g.lda % 8 == 0 && g.ldb % 8 == 0 && g.ldc % 4 == 0 &&
+         (!g.a_src || g.tapC % 64 == 0);
+}
+
+hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st) {
+  if (!gemm_small_fits(g, epi)) return hipErrorInvalidValue;
+  switch (epi) {
+    case EPI_BF16: return launch_small<EPI_BF16>(g, st);
+    case EPI_GELU_BF16: return launch_small<EPI_GELU_BF16>(g, st);
+    case EPI_RESID_F32: return launch_small<EPI_RESID_F32>(g, st);
+    case EPI_F32: return launch_small<EPI_F32>(g, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace t2w
