@@ -25,11 +25,14 @@ constexpr float NEG = -1.0e30f;
 // key k of a 32-key tile -> its column in the transposed V tile: bits 2 and 3 swapped
 __device__ __forceinline__ int vpos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
-__global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
-  __shared__ uint4 ks[2][64 * 8];      // [key][16-byte chunk ^ (key & 7)], 64 keys
-  __shared__ uint4 vt[2][2][64 * 4];   // per 32-key half: [d][16-byte chunk ^ ((d >> 1) & 3)] of permuted keys
+// KS > 1 (few workgroups, e.g. a streaming chunk): KS groups of two waves share the 64 queries and take every KS-th
+// key tile each; their softmax states (max, sum, output) are merged through LDS at the end.
+template <int KS>
+__global__ void __launch_bounds__(128 * KS) attn_kernel(AttnArgs a) {
+  __shared__ uint4 ks[KS][2][64 * 8];      // [key][16-byte chunk ^ (key & 7)], 64 keys
+  __shared__ uint4 vt[KS][2][2][64 * 4];   // per 32-key half: [d][16-byte chunk ^ ((d >> 1) & 3)] of permuted keys
   const int tile = blockIdx.x, head = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int gi = threadIdx.x >> 7, tid = threadIdx.x & 127, lane = tid & 63, wave = tid >> 6;
   const int row = a.tiles[2 * tile];
   const int q0 = a.tiles[2 * tile + 1];
   const int T = a.row_len[row];
@@ -88,12 +91,12 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
   };
 #define T2W_LSTORE(s)                                            \
   {                                                              \
-    uint4* kr = ks[s] + lk * 8;                                  \
+    uint4* kr = ks[gi][s] + lk * 8;                              \
     kr[(lc + 0) ^ (lk & 7)] = rk0;                               \
     kr[(lc + 1) ^ (lk & 7)] = rk1;                               \
     kr[(lc + 2) ^ (lk & 7)] = rk2;                               \
     kr[(lc + 3) ^ (lk & 7)] = rk3;                               \
-    bf16_t* vb = (bf16_t*)vt[s][lk >> 5];                        \
+    bf16_t* vb = (bf16_t*)vt[gi][s][lk >> 5];                    \
     vstore(vb, vp_, (lc + 0) * 8, rv0);                          \
     vstore(vb, vp_, (lc + 1) * 8, rv1);                          \
     vstore(vb, vp_, (lc + 2) * 8, rv2);                          \
@@ -107,20 +110,22 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
   const float sl2 = a.scale * 1.4426950408889634f;
   const int lim_w0 = a.chunk > 0 ? min(T, (qpos0 / a.chunk + 1) * a.chunk) : T;  // the wave's first query's limit
 
+  // group gi takes tiles gi, gi + KS, ...; every group runs the same number of iterations (the barriers are shared)
+  const int niter = (ntiles + KS - 1) / KS;
   int slot_next = 0;
-  if (ntiles > 0) {
+  if (gi < ntiles) {
     int s0;
-    T2W_SLOT_OF(0, s0)
+    T2W_SLOT_OF(gi, s0)
     T2W_GLOAD(s0)
-    if (ntiles > 1) T2W_SLOT_OF(1, slot_next)
+    if (gi + KS < ntiles) T2W_SLOT_OF(gi + KS, slot_next)
     T2W_LSTORE(0)
   }
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int s = t & 1;
-    if (t + 1 < ntiles) T2W_GLOAD(slot_next)
-    if (t + 2 < ntiles) T2W_SLOT_OF(t + 2, slot_next)
-    if (active) {
+  for (int it = 0; it < niter; ++it) {
+    const int s = it & 1, t = it * KS + gi;
+    if (t + KS < ntiles) T2W_GLOAD(slot_next)
+    if (t + 2 * KS < ntiles) T2W_SLOT_OF(t + 2 * KS, slot_next)
+    if (active && t < ntiles) {
       int kb, ke;
       T2W_TILE_RANGE(t, kb, ke)
       const bool cached = t >= n1;
@@ -140,7 +145,7 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) {
             const int chunk = kk * 2 + half;
-            sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ks[s][krow * 8 + (chunk ^ (krow & 7))]), qf[kk], sc[sub], 0, 0, 0);
+            sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ks[gi][s][krow * 8 + (chunk ^ (krow & 7))]), qf[kk], sc[sub], 0, 0, 0);
           }
         }
       }
@@ -194,20 +199,50 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
         for (int hh = 0; hh < 2; ++hh) {
           const int chunk = hh * 2 + half;
           const int d0 = col, d1 = 32 + col;
-          const uint4 v0 = vt[s][sub][d0 * 4 + (chunk ^ ((d0 >> 1) & 3))];
-          const uint4 v1 = vt[s][sub][d1 * 4 + (chunk ^ ((d1 >> 1) & 3))];
+          const uint4 v0 = vt[gi][s][sub][d0 * 4 + (chunk ^ ((d0 >> 1) & 3))];
+          const uint4 v1 = vt[gi][s][sub][d1 * 4 + (chunk ^ ((d1 >> 1) & 3))];
           o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v0), as_bf16x8(pf[sub][hh]), o0, 0, 0, 0);
           o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v1), as_bf16x8(pf[sub][hh]), o1, 0, 0, 0);
         }
       }
     }
-    if (t + 1 < ntiles) T2W_LSTORE(s ^ 1)
+    if (t + KS < ntiles) T2W_LSTORE(s ^ 1)
     __syncthreads();
   }
 #undef T2W_TILE_RANGE
 #undef T2W_SLOT_OF
 #undef T2W_GLOAD
 #undef T2W_LSTORE
+  if constexpr (KS > 1) {
+    // merge: groups 1.. leave (max, sum, output) per lane in their (now free) tile buffers, group 0 folds them in
+    // group order, rescaling each by 2^((m_g - m*) scale)
+    // per wave: o0 in the group's K buffers (16 x 64 floats), o1, m and l in its V buffers (18 x 64 floats)
+    float* xk = (float*)ks[gi] + wave * (16 * 64);
+    float* xv = (float*)vt[gi] + wave * (18 * 64);
+    if (gi > 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { xk[r * 64 + lane] = o0[r]; xv[r * 64 + lane] = o1[r]; }
+      xv[16 * 64 + lane] = m;
+      xv[17 * 64 + lane] = l;
+    }
+    __syncthreads();
+    if (gi > 0) return;
+#pragma unroll
+    for (int g2 = 1; g2 < KS; ++g2) {
+      const float* yk = (const float*)ks[g2] + wave * (16 * 64);
+      const float* yv = (const float*)vt[g2] + wave * (18 * 64);
+      const float mg = yv[16 * 64 + lane], lg = yv[17 * 64 + lane];
+      const float mn = fmaxf(m, mg);
+      const float fa = __builtin_amdgcn_exp2f((m - mn) * sl2), fb = __builtin_amdgcn_exp2f((mg - mn) * sl2);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        o0[r] = o0[r] * fa + yk[r * 64 + lane] * fb;
+        o1[r] = o1[r] * fa + yv[r * 64 + lane] * fb;
+      }
+      l = l * fa + lg * fb;
+      m = mn;
+    }
+  }
   if (!active || myq >= T) return;
   const float inv = 1.0f / l;
   if (a.out8) {
@@ -245,7 +280,11 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a) {
 
 hipError_t attention(const AttnArgs& a, hipStream_t st) {
   if (a.n_tiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_kernel, dim3(a.n_tiles, a.heads), dim3(128), 0, st, a);
+  // a grid of fewer workgroups than CUs (a streaming chunk) splits each workgroup's key tiles over four wave groups
+  if (a.n_tiles * a.heads < 256)
+    hipLaunchKernelGGL(attn_kernel<4>, dim3(a.n_tiles, a.heads), dim3(512), 0, st, a);
+  else
+    hipLaunchKernelGGL(attn_kernel<1>, dim3(a.n_tiles, a.heads), dim3(128), 0, st, a);
   return hipGetLastError();
 }
 

@@ -164,14 +164,16 @@ def test_qk_norm_scatter(dev):
 
 
 @pytest.mark.parametrize("chunk", [0, 50, 7])
-def test_attention_paged_block_causal(dev, chunk):
-    """Rows of new frames with cached keys in scattered slots; mask: cached keys always visible, new keys by chunk."""
+@pytest.mark.parametrize("rep", [1, 9])
+def test_attention_paged_block_causal(dev, chunk, rep):
+    """Rows of new frames with cached keys in scattered slots; mask: cached keys always visible, new keys by chunk.
+    rep 1: 32 workgroups (the key tiles of each split over four wave groups and merged); rep 9: 288 (one group)."""
     L = _lib.lib()
     g = torch.Generator(device=dev).manual_seed(9 + chunk)
-    heads, n_slots = 4, 4096
+    heads, n_slots = 4, 8192
     H = heads * 64
-    lens = [50, 1, 0, 130, 64, 65]
-    cached = [300, 0, 7, 0, 100, 33]
+    lens = [50, 1, 0, 130, 64, 65] * rep
+    cached = [300, 0, 7, 0, 100, 33] * rep
     N = sum(lens)
     q = torch.randn(N, H, device=dev, generator=g).bfloat16()
     kp = torch.randn(n_slots, H, device=dev, generator=g).bfloat16()
