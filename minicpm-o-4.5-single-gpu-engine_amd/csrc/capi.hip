@@ -163,9 +163,9 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
       T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st), "ln_mod msa");
       gq = gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H, &w);
     }
-    if (!gemm_splits(gq) && H % 256 == 0) {
+    gq.qk = QkvOut{w.q, kp, vp, a->new_slot, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, H};
+    if (gemm_small_fits(gq, EPI_QKV) || (!gemm_splits(gq) && H % 256 == 0)) {
       // per-head q / k LayerNorm and the key / value scatter in the projection's epilogue
-      gq.qk = QkvOut{w.q, kp, vp, a->new_slot, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, H};
       T2W_CHECK(gemm_bf16(gq, EPI_QKV, st), "qkv");
     } else {
       T2W_CHECK(gemm_bf16(gq, EPI_BF16, st), "qkv");

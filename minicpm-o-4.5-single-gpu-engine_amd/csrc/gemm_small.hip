@@ -104,6 +104,82 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
   }
 }
 
+// The qkv projection (N = 3 H) for few rows, with the per-head q / k LayerNorm and the key / value scatter fused:
+// 64 columns (one head of q, k or v) x 32 rows per workgroup, K split over the 16 waves (one 64-K step each, so
+// K <= 1024).  The block summed over the waves goes row-major through LDS, where the 16 lanes of one DPP row hold a
+// row's 64 columns: bias, rounding to bf16 (the projection's own precision), LayerNorm + affine for q and k, then q
+// to its token row and k, v to the token's key slot.
+__global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_qkv_kernel(GemmArgs g) {
+  __shared__ float4 red[GS_WAVES][2][4][64];  // per wave: two 32x32 blocks (column tiles) in register order
+  __shared__ float rowm[32][68];               // the summed 32 x 64 block, row-major (padded rows)
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
+  const int n0 = blockIdx.x * 64, m0 = blockIdx.y * 32;
+  const int KS = g.K / 64;
+  const int s0 = w * KS / GS_WAVES, s1 = (w + 1) * KS / GS_WAVES;  // at most one step
+  const int m = min(m0 + c, g.M - 1);
+  f32x16 acc[2];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[ct][r] = 0.0f;
+  if (s0 < s1) {
+    const int k0 = s0 * 64;
+    uint4 wf[2][4], af[4];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const bf16_t* wrow = g.B + (size_t)min(n0 + ct * 32 + c, g.N - 1) * g.ldb + h * 32 + k0;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) wf[ct][kk] = *(const uint4*)(wrow + kk * 8);
+    }
+    const bf16_t* arow = g.A + (size_t)m * g.lda + h * 32 + k0;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) af[kk] = *(const uint4*)(arow + kk * 8);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wf[ct][kk]), as_bf16x8(af[kk]), acc[ct], 0, 0, 0);
+  }
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[w][ct][q][lane] = make_float4(acc[ct][4 * q], acc[ct][4 * q + 1], acc[ct][4 * q + 2], acc[ct][4 * q + 3]);
+  __syncthreads();
+  if (tid < 512) {  // sum over the waves in order; lane l holds token m0 + l % 32, columns ct * 32 + q * 8 + (l / 32) * 4 + 0..3
+    const int ct = tid >> 8, q = (tid >> 6) & 3, l = tid & 63;
+    float4 a = red[0][ct][q][l];
+#pragma unroll
+    for (int x = 1; x < GS_WAVES; ++x) {
+      const float4 b = red[x][ct][q][l];
+      a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+    }
+    *(float4*)&rowm[l & 31][ct * 32 + q * 8 + (l >> 5) * 4] = a;
+  }
+  __syncthreads();
+  if (tid >= 512) return;
+  const QkvOut& o = g.qk;
+  const int r = tid >> 4, c4 = (tid & 15) * 4;  // 16 consecutive lanes (a DPP row) per token row
+  const float4 a = *(const float4*)&rowm[r][c4];
+  const float4 b = *(const float4*)(g.bias + n0 + c4);
+  float y[4] = {bf2f(f2bf(a.x + b.x)), bf2f(f2bf(a.y + b.y)), bf2f(f2bf(a.z + b.z)), bf2f(f2bf(a.w + b.w))};
+  const int part = n0 / o.H, hc = n0 - part * o.H + c4;  // q, k or v; column within the part
+  if (part < 2) {
+    const float mean = row16_sum(y[0] + y[1] + y[2] + y[3]) * (1.0f / 64.0f);
+    float var = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { y[e] -= mean; var += y[e] * y[e]; }
+    const float rstd = rsqrtf(row16_sum(var) * (1.0f / 64.0f) + o.eps);
+    const float4 lw = *(const float4*)((part ? o.kw : o.qw) + c4), lb = *(const float4*)((part ? o.kb : o.qb) + c4);
+    y[0] = y[0] * rstd * lw.x + lb.x;
+    y[1] = y[1] * rstd * lw.y + lb.y;
+    y[2] = y[2] * rstd * lw.z + lb.z;
+    y[3] = y[3] * rstd * lw.w + lb.w;
+  }
+  const int mo = m0 + r;
+  if (mo >= g.M) return;
+  bf16_t* dst = part == 0 ? o.q_out + (size_t)mo * o.H : (part == 1 ? o.k_pool : o.v_pool) + (size_t)o.slots[mo] * o.H;
+  *(uint2*)(dst + hc) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+}
+
 template <int EPI>
 hipError_t launch_small(const GemmArgs& g, hipStream_t st) {
   const dim3 grid((g.N + 31) / 32, (g.M + 31) / 32);
@@ -115,6 +191,9 @@ hipError_t launch_small(const GemmArgs& g, hipStream_t st) {
 }  // namespace
 
 bool gemm_small_fits(const GemmArgs& g, int epi) {
+  if (epi == EPI_QKV)
+    return g.M > 0 && g.M <= GEMM_SMALL_MAX_M && !g.w_scale && !g.a_src && g.K % 64 == 0 && g.K <= GS_WAVES * 64 &&
+           g.qk.H % 64 == 0 && g.N == 3 * g.qk.H && g.lda % 8 == 0 && g.ldb % 8 == 0;
   return g.M > 0 && g.M <= GEMM_SMALL_MAX_M && !g.w_scale && epi <= EPI_F32 && g.K % 64 == 0 &&
          g.K <= GS_WAVES * GS_MAXSTEPS * 64 && g.lda % 8 == 0 && g.ldb % 8 == 0 && g.ldc % 4 == 0 &&
          (!g.a_src || g.tapC % 64 == 0);
@@ -127,6 +206,9 @@ hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st) {
     case EPI_GELU_BF16: return launch_small<EPI_GELU_BF16>(g, st);
     case EPI_RESID_F32: return launch_small<EPI_RESID_F32>(g, st);
     case EPI_F32: return launch_small<EPI_F32>(g, st);
+    case EPI_QKV:
+      hipLaunchKernelGGL(gemm_small_qkv_kernel, dim3(g.N / 64, (g.M + 31) / 32), dim3(64 * GS_WAVES), 0, st, g);
+      return hipGetLastError();
   }
   return hipErrorInvalidValue;
 }

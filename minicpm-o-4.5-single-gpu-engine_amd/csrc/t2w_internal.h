@@ -51,9 +51,9 @@ struct GemmArgs {
 hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg = -1);
 bool gemm_splits(const GemmArgs& g);  // whether gemm_bf16 (cfg < 0) takes the split-K path for g
 
-// One-kernel GEMM for calls of at most GEMM_SMALL_MAX_M rows (K split over the waves of a workgroup, reduced in LDS);
-// plain epilogues only (EPI_BF16 .. EPI_F32), K % 64 == 0, K <= 3072, ldc % 4 == 0.  gemm_bf16 (cfg < 0) takes it
-// whenever it fits.
+// One-kernel GEMM for calls of at most GEMM_SMALL_MAX_M rows (K split over the waves of a workgroup, reduced in LDS):
+// plain epilogues (EPI_BF16 .. EPI_F32; K % 64 == 0, K <= 3072, ldc % 4 == 0) and EPI_QKV (dense A, K <= 1024,
+// N = 3 qk.H, qk.H % 64 == 0).  gemm_bf16 (cfg < 0) takes it whenever it fits.
 constexpr int GEMM_SMALL_MAX_M = 128;
 bool gemm_small_fits(const GemmArgs& g, int epi);
 hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st);
