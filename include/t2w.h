@@ -136,7 +136,9 @@ int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const f
 /* ---------------------------------------------------------------- kernel-level entry points (tests, benchmarks) */
 
 /* C = A . W^T + bias; epi 0: bf16 out, 1: GELU-tanh bf16 out, 2: C(fp32) += gate * (.), 3: fp32 out.
- * a_src non-null: conv taps mode, A row m = frames a_src[m] .. a_src[m] + K / lda - 1 of A (rows lda wide). */
+ * a_src non-null: conv taps mode, A row m = frames a_src[m] .. a_src[m] + K / lda - 1 of A (rows lda wide).
+ * Calls of at most 128 rows (K <= 3072, ldc % 4 == 0) run as one kernel that splits K over the waves of a workgroup;
+ * larger ones on the tile GEMM. */
 int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                   void* C, int ldc, int M, int N, int K, int epi, void* stream);
 /* t2w_gemm_bf16 with an explicit tile configuration (-1: chosen by shape; 0: 128x128 of 4 waves, 1: 256x256 of
