@@ -29,324 +29,13 @@
 // frames of every packed row in front of its frames).
 #include "common.h"
 #include "t2w_internal.h"
+#include "gemm_tile.h"
 
 namespace t2w {
 
 int pick_cfg(const GemmArgs& g);
 
 namespace {
-
-constexpr int BK = 64;  // K values per stage (128 bytes of bf16 per tile row)
-
-// 16-byte chunk c of tile row `row` lives at chunk c ^ ((row >> 1) & 7) of that row: 16 consecutive rows reading the same
-// chunk (a 16-lane LDS phase of a fragment read) then cover all 64 banks, and 8 consecutive lanes writing one row stay
-// within it.
-__device__ __forceinline__ int swz_key(int row) { return (row >> 1) & 7; }
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ swz_key(row)); }
-
-// Output columns n .. n + 3 of one lane: bias (and gate) loaded once, before any output row is touched.
-template <int EPI>
-struct Cols {
-  float4 bias, gate, wsc;
-  int n;
-  bool full;  // all four columns inside N
-  __device__ __forceinline__ Cols(const GemmArgs& g, int n_) : n(n_), full(n_ + 3 < g.N) {
-    bias = gate = make_float4(0.f, 0.f, 0.f, 0.f);
-    wsc = make_float4(1.f, 1.f, 1.f, 1.f);
-    if (full) {
-      bias = *(const float4*)(g.bias + n);
-      if (EPI == EPI_RESID_F32) gate = *(const float4*)(g.gate + n);
-      if (g.w_scale) wsc = *(const float4*)(g.w_scale + n);
-    }
-  }
-  // finished output of accumulator values a for full columns (h: the residual row's current values)
-  __device__ __forceinline__ float4 apply(float4 a, float4 h) const {
-    float v[4] = {a.x * wsc.x + bias.x, a.y * wsc.y + bias.y, a.z * wsc.z + bias.z, a.w * wsc.w + bias.w};
-    if (EPI == EPI_GELU_BF16 || EPI == EPI_GELU_MX8) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
-    }
-    if (EPI == EPI_RESID_F32) return make_float4(h.x + gate.x * v[0], h.y + gate.y * v[1], h.z + gate.z * v[2], h.w + gate.w * v[3]);
-    return make_float4(v[0], v[1], v[2], v[3]);
-  }
-  __device__ __forceinline__ void put(const GemmArgs& g, int m, float4 o) const {
-    if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16)
-      *(uint2*)((bf16_t*)g.C + (size_t)m * g.ldc + n) = make_uint2(pack2(o.x, o.y), pack2(o.z, o.w));
-    else
-      *(float4*)((float*)g.C + (size_t)m * g.ldc + n) = o;
-  }
-  // columns past N: element by element
-  __device__ __forceinline__ void put_partial(const GemmArgs& g, int m, float4 a) const {
-    const float v[4] = {a.x, a.y, a.z, a.w};
-    for (int e = 0; e < 4 && n + e < g.N; ++e) {
-      const float x = v[e] * (g.w_scale ? g.w_scale[n + e] : 1.0f) + g.bias[n + e];
-      const size_t o = (size_t)m * g.ldc + n + e;
-      if (EPI == EPI_BF16) ((bf16_t*)g.C)[o] = f2bf(x);
-      else if (EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[o] = f2bf(gelu_tanh(x));
-      else if (EPI == EPI_RESID_F32) ((float*)g.C)[o] += g.gate[n + e] * x;
-      else ((float*)g.C)[o] = x;
-    }
-  }
-};
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef int i32x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ i32x8 join8(uint4 a, uint4 b) {
-  i32x8 r;
-  r[0] = (int)a.x; r[1] = (int)a.y; r[2] = (int)a.z; r[3] = (int)a.w;
-  r[4] = (int)b.x; r[5] = (int)b.y; r[6] = (int)b.z; r[7] = (int)b.w;
-  return r;
-}
-
-template <bool FP8>
-struct FragT { typedef bf16x8 type; };
-template <>
-struct FragT<true> { typedef i32x8 type; };
-
-template <int BM, int BN, int WM, int WN, bool TAPS, bool FP8>
-struct Tile {
-  static constexpr int NW = WM * WN;
-  static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave sub-tile
-  static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA blocks per wave
-  static constexpr int APW = BM / 8 / NW, BPW = BN / 8 / NW;  // 1 KB (8-row) load blocks per wave and stage
-  static constexpr int ES = FP8 ? 1 : 2;              // bytes per element
-  static constexpr int BKE = BK * 2 / ES;             // K values per 128-byte stage row
-  static constexpr int NKK = FP8 ? 2 : 4;             // MFMA K steps per stage
-  static constexpr int NSC = FP8 ? TM : 1;            // scale dwords per lane and stage
-  static_assert(APW * NW * 8 == BM && BPW * NW * 8 == BN, "tile rows / waves mismatch");
-  typedef typename FragT<FP8>::type frag_t;
-
-  const uint8_t* asrc[APW];
-  const uint8_t* bsrc[BPW];
-  const uint8_t* sbase[NSC];  // fp8: this lane's activation rows' scale rows
-  const GemmArgs& g;
-  int lane, wave, wm, wn;
-
-  __device__ __forceinline__ Tile(const GemmArgs& g_, int m0, int n0) : g(g_) {
-    const int tid = threadIdx.x;
-    lane = tid & 63;
-    wave = tid >> 6;
-    wm = wave / WN;
-    wn = wave % WN;
-    // this lane's 16 bytes of each of its wave's load blocks: tile row blk * 8 + lane / 8, logical chunk (lane % 8) ^ key
-    const int lrow = lane >> 3;
-    const uint8_t* A = (const uint8_t*)g.A;
-    const uint8_t* B = (const uint8_t*)g.B;
-#pragma unroll
-    for (int p = 0; p < APW; ++p) {
-      const int trow = (wave + p * NW) * 8 + lrow;
-      const int m = min(m0 + trow, g.M - 1);  // rows past M load row M - 1; their results are never stored
-      const int ch = (lane & 7) ^ swz_key(trow);
-      asrc[p] = A + (size_t)(TAPS ? g.a_src[m] : m) * g.lda * ES + ch * 16;
-    }
-#pragma unroll
-    for (int p = 0; p < BPW; ++p) {
-      const int trow = (wave + p * NW) * 8 + lrow;
-      bsrc[p] = B + (size_t)min(n0 + trow, g.N - 1) * g.ldb * ES + ((lane & 7) ^ swz_key(trow)) * 16;
-    }
-    if (FP8) {
-#pragma unroll
-      for (int i = 0; i < NSC; ++i) {
-        const int m = min(m0 + wm * WTM + i * 32 + (lane & 31), g.M - 1);
-        sbase[i] = g.a_scale + (size_t)(TAPS ? g.a_src[m] : m) * g.a_sld;
-      }
-    }
-  }
-
-  // loads of stage kt into (la, lb) and, in fp8 mode, its activation scale dwords into sd
-  __device__ __forceinline__ void issue(uint4* la, uint4* lb, uint32_t (&sd)[NSC], int kt) const {
-    const int k0 = kt * BKE;
-    size_t aoff = (size_t)k0 * ES;
-    int srow = 0, sblk = k0 / 32;
-    if (TAPS) {
-      const int tap = k0 / g.tapC;  // a stage never straddles two taps (tapC % BKE == 0)
-      aoff = ((size_t)tap * g.lda + (k0 - tap * g.tapC)) * ES;
-      srow = tap;
-      sblk = (k0 - tap * g.tapC) / 32;
-    }
-#pragma unroll
-    for (int p = 0; p < APW; ++p)
-      __builtin_amdgcn_global_load_lds((const void*)(asrc[p] + aoff), (lds_ptr_t)(la + (wave + p * NW) * 64), 16, 0, 0);
-#pragma unroll
-    for (int p = 0; p < BPW; ++p)
-      __builtin_amdgcn_global_load_lds((const void*)(bsrc[p] + (size_t)k0 * ES), (lds_ptr_t)(lb + (wave + p * NW) * 64), 16, 0, 0);
-    if (FP8) {
-#pragma unroll
-      for (int i = 0; i < NSC; ++i) sd[i] = *(const uint32_t*)(sbase[i] + (size_t)srow * g.a_sld + sblk);
-    }
-  }
-
-  __device__ __forceinline__ void frag(const uint4* La, const uint4* Lb, int kk, frag_t (&af)[TM], frag_t (&bf)[TN]) const {
-    if constexpr (FP8) {
-      const int c0 = kk * 4 + (lane >> 5);  // 16-byte pieces of the two 32-value blocks of this K step
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * WTM + i * 32 + (lane & 31);
-        af[i] = join8(La[swz(r, c0)], La[swz(r, c0 + 2)]);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = wn * WTN + j * 32 + (lane & 31);
-        bf[j] = join8(Lb[swz(r, c0)], Lb[swz(r, c0 + 2)]);
-      }
-    } else {
-      const int chunk = kk * 2 + (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(La[swz(wm * WTM + i * 32 + (lane & 31), chunk)]);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = as_bf16x8(Lb[swz(wn * WTN + j * 32 + (lane & 31), chunk)]);
-    }
-  }
-
-  __device__ __forceinline__ void mma(f32x16 (&acc)[TM][TN], const frag_t (&af)[TM], const frag_t (&bf)[TN],
-                                      const uint32_t (&sd)[NSC], int kk) const {
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      if constexpr (FP8) {
-        const int sc = (int)((sd[i] >> (8 * (kk * 2 + (lane >> 5)))) & 255u);  // E8M0 of this lane's block
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[i][j], 0, 0, 0, 127, 0, sc);
-      } else {
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
-      }
-    }
-  }
-
-  // One K stage from buffers (La, Lb) with scales sd.  Stage kt + 1 must already be in flight into (Na, Nb); after the
-  // barrier the loads of stage kt + 2 go into (La, Lb, sd).
-  __device__ __forceinline__ void stage(f32x16 (&acc)[TM][TN], frag_t (&af)[2][TM], frag_t (&bf)[2][TN], uint4* La,
-                                        uint4* Lb, uint32_t (&sd)[NSC], const uint4* Na, const uint4* Nb, int kt, int KT) const {
-    constexpr int RPF = FP8 ? 2 : 1;  // LDS reads per fragment
-    constexpr int NV = APW + BPW + (FP8 ? NSC : 0), ND = (TM + TN) * RPF, NM = TM * TN;
-#pragma unroll
-    for (int kk = 0; kk < NKK - 1; ++kk) {
-      frag(La, Lb, kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
-      mma(acc, af[kk & 1], bf[kk & 1], sd, kk);
-      // MFMA, fragment read(s), MFMA, ... then the remaining MFMAs
-      constexpr int DPM = (ND + NM - 1) / NM;
-#pragma unroll
-      for (int x = 0; x < NM; ++x) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (x * DPM < ND) __builtin_amdgcn_sched_group_barrier(0x100, DPM, 0);
-      }
-    }
-    // stage kt + 1 has landed (this wave's loads) and is visible (everyone's), and nobody reads (La, Lb) any more
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    __syncthreads();
-    uint32_t sl[NSC];
-#pragma unroll
-    for (int i = 0; i < NSC; ++i) sl[i] = sd[i];
-    issue(La, Lb, sd, min(kt + 2, KT - 1));
-    frag(Na, Nb, 0, af[0], bf[0]);
-    mma(acc, af[(NKK - 1) & 1], bf[(NKK - 1) & 1], sl, NKK - 1);
-    // MFMA, load(s), fragment read(s), MFMA, ...
-    constexpr int VPM = (NV + NM - 1) / NM, DPM = (ND + NM - 1) / NM;
-#pragma unroll
-    for (int x = 0; x < NM; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (x * VPM < NV) __builtin_amdgcn_sched_group_barrier(0x020, VPM, 0);
-      if (x * DPM < ND) __builtin_amdgcn_sched_group_barrier(0x100, DPM, 0);
-    }
-  }
-
-  // Writes the wave's accumulators through its LDS slab st (32 x WTN fp32, chunks XOR-swizzled by row) so that each
-  // global access of the epilogue covers whole rows.  Rows go out in batches of RB read-back instructions whose
-  // residual loads are all in flight before the first store.
-  template <int EPI>
-  __device__ __forceinline__ void store(const f32x16 (&acc)[TM][TN], float4* st, int m0, int n0) const {
-    constexpr int CPR = WTN / 4;   // 16-byte chunks per slab row
-    constexpr int RPI = 64 / CPR;  // slab rows per read-back instruction
-    constexpr int NRB = 32 / RPI;  // read-back instructions per slab
-    constexpr int RB = NRB < 8 ? NRB : 8;
-    const int cc = lane % CPR;
-    const Cols<EPI> cols(g, n0 + wn * WTN + cc * 4);
-    // EPI_QKV: this lane's part (q, k, v), column and head offset, and the LayerNorm affine of its four columns
-    int qpart = 0, qcol = 0;
-    float4 qlw = make_float4(0.f, 0.f, 0.f, 0.f), qlb = qlw;
-    if constexpr (EPI == EPI_QKV) {
-      qpart = cols.n / g.qk.H;
-      qcol = cols.n - qpart * g.qk.H;
-      if (qpart < 2) {
-        qlw = *(const float4*)((qpart ? g.qk.kw : g.qk.qw) + (qcol & 63));
-        qlb = *(const float4*)((qpart ? g.qk.kb : g.qk.qb) + (qcol & 63));
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int r = lane & 31;
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int c = j * 8 + q * 2 + (lane >> 5);
-          st[r * CPR + (c ^ (r & (CPR - 1)))] =
-              make_float4(acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
-        }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-      for (int b = 0; b < NRB; b += RB) {
-        float4 v[RB], h[RB];
-        int m[RB], slot[RB];
-#pragma unroll
-        for (int x = 0; x < RB; ++x) {
-          const int row = (b + x) * RPI + lane / CPR;
-          m[x] = m0 + wm * WTM + i * 32 + row;
-          v[x] = st[row * CPR + (cc ^ (row & (CPR - 1)))];
-          h[x] = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (EPI == EPI_RESID_F32 && cols.full && m[x] < g.M) h[x] = *(const float4*)((const float*)g.C + (size_t)m[x] * g.ldc + cols.n);
-          slot[x] = 0;
-          if (EPI == EPI_QKV && qpart > 0 && m[x] < g.M) slot[x] = g.qk.slots[m[x]];
-        }
-#pragma unroll
-        for (int x = 0; x < RB; ++x) {
-          if constexpr (EPI == EPI_QKV) {
-            // the 16 lanes (one DPP row) holding this row's 64 columns of one head: heads are 64-aligned in the tile
-            const QkvOut& o = g.qk;
-            float y[4] = {v[x].x * cols.wsc.x + cols.bias.x, v[x].y * cols.wsc.y + cols.bias.y,
-                          v[x].z * cols.wsc.z + cols.bias.z, v[x].w * cols.wsc.w + cols.bias.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(y[e]));  // the projection is rounded to bf16 first
-            if (qpart < 2) {
-              const float mean = row16_sum(y[0] + y[1] + y[2] + y[3]) * (1.0f / 64.0f);
-              float q = 0.f;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) { y[e] -= mean; q += y[e] * y[e]; }
-              const float rstd = rsqrtf(row16_sum(q) * (1.0f / 64.0f) + o.eps);
-              y[0] = y[0] * rstd * qlw.x + qlb.x;
-              y[1] = y[1] * rstd * qlw.y + qlb.y;
-              y[2] = y[2] * rstd * qlw.z + qlb.z;
-              y[3] = y[3] * rstd * qlw.w + qlb.w;
-            }
-            if (m[x] < g.M) {
-              bf16_t* dst = qpart == 0 ? o.q_out + (size_t)m[x] * o.H : (qpart == 1 ? o.k_pool : o.v_pool) + (size_t)slot[x] * o.H;
-              *(uint2*)(dst + qcol) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
-            }
-          } else if constexpr (EPI == EPI_GELU_MX8) {
-            // the 8 lanes holding this row's 32 consecutive columns share one block scale (N % 32 == 0)
-            const float4 o = cols.apply(v[x], h[x]);
-            float a = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
-            a = fmaxf(a, __shfl_xor(a, 1, 64));
-            a = fmaxf(a, __shfl_xor(a, 2, 64));
-            a = fmaxf(a, __shfl_xor(a, 4, 64));
-            const int se = mx_exp(a);
-            if (m[x] < g.M && cols.full) {
-              *(uint32_t*)((uint8_t*)g.C + (size_t)m[x] * g.ldc + cols.n) = mx_pack4(o.x, o.y, o.z, o.w, se);
-              if ((cc & 7) == 0) g.c_scale[(size_t)m[x] * g.c_sld + (cols.n >> 5)] = (uint8_t)(se + 127);
-            }
-          } else {
-            if (m[x] >= g.M) continue;
-            if (cols.full) cols.put(g, m[x], cols.apply(v[x], h[x]));
-            else cols.put_partial(g, m[x], v[x]);
-          }
-        }
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
-  }
-};
 
 template <int BM, int BN, int WM, int WN, int EPI, bool TAPS, bool FP8>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
