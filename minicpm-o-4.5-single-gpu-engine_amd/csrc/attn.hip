@@ -31,7 +31,12 @@ template <int KS>
 __global__ void __launch_bounds__(128 * KS) attn_kernel(AttnArgs a) {
   __shared__ uint4 ks[KS][2][64 * 8];      // [key][16-byte chunk ^ (key & 7)], 64 keys
   __shared__ uint4 vt[KS][2][2][64 * 4];   // per 32-key half: [d][16-byte chunk ^ ((d >> 1) & 3)] of permuted keys
-  const int tile = blockIdx.x, head = blockIdx.y;
+  // XCD-aware order: consecutive workgroups go to different XCDs, so each XCD takes a contiguous run of (head, tile)
+  // pairs; the query tiles of one row and head then share that row's keys and values in one L2
+  const int nblk = gridDim.x * gridDim.y, full = (nblk / 8) * 8;
+  int lin = blockIdx.y * gridDim.x + blockIdx.x;
+  if (lin < full) lin = (lin % 8) * (nblk / 8) + lin / 8;
+  const int tile = lin % gridDim.x, head = lin / gridDim.x;
   const int gi = threadIdx.x >> 7, tid = threadIdx.x & 127, lane = tid & 63, wave = tid >> 6;
   const int row = a.tiles[2 * tile];
   const int q0 = a.tiles[2 * tile + 1];

@@ -1,24 +1,15 @@
 // Per-token row kernels of the DiT block and the Euler/CFG update.
 //
-// One wave64 per token row: each lane holds H / 64 consecutive values (64 contiguous bytes of fp32 for H = 1024), so a
-// row is read with fully coalesced 16-byte loads and the LayerNorm statistics are two wave reductions.  Norm statistics
-// and modulation are fp32 (the reference's ``dit_kernels.py`` keeps norm math in fp32); outputs that feed an MFMA GEMM
-// are rounded once to bf16.
+// One wave64 per token row: each lane holds H / 64 values of the row, four consecutive ones per 256 columns, so every
+// access instruction covers a contiguous run of the row and the LayerNorm statistics are two wave reductions.  Norm
+// statistics and modulation are fp32 (the reference's ``dit_kernels.py`` keeps norm math in fp32); outputs that feed an
+// MFMA GEMM are rounded once to bf16.
 #include "common.h"
 #include "t2w_internal.h"
 
 namespace t2w {
 
 namespace {
-
-template <int VPL>
-__device__ __forceinline__ void load_f32(const float* p, float (&v)[VPL]) {
-#pragma unroll
-  for (int i = 0; i < VPL / 4; ++i) {
-    float4 x = *(const float4*)(p + 4 * i);
-    v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
-  }
-}
 
 template <int VPL>
 __device__ __forceinline__ void load_bf(const bf16_t* p, float (&v)[VPL]) {
@@ -51,23 +42,75 @@ __device__ __forceinline__ void store_packed(bf16_t* p, const uint32_t (&o)[VPL 
   }
 }
 
-// MX fp8 store of a row chunk: this lane's VPL values at c0 of a row; the 32-value block's maximum is reduced over its
-// 32 / VPL lanes, and the block's first lane writes the E8M0 scale byte
+// Whole-row access of the LayerNorm kernels: a lane holds groups of G consecutive values, value i at column
+// (i / G) * 64 G + lane * G + i % G, so every load or store instruction of the wave covers one contiguous run of the
+// row.  G = 4 suits rows read as fp32 (1 KB per instruction), G = 8 rows read as bf16 (16 bytes per lane).
+template <int G>
+__device__ __forceinline__ int row_col(int k, int lane) { return k * 64 * G + lane * G; }
+
+template <int VPL, int G>
+__device__ __forceinline__ void row_load_f32(const float* row, int lane, float (&v)[VPL]) {
+#pragma unroll
+  for (int k = 0; k < VPL / G; ++k)
+#pragma unroll
+    for (int j = 0; j < G / 4; ++j) {
+      const float4 x = *(const float4*)(row + row_col<G>(k, lane) + 4 * j);
+      float* d = v + k * G + 4 * j;
+      d[0] = x.x; d[1] = x.y; d[2] = x.z; d[3] = x.w;
+    }
+}
+
+// raw bf16 words of a row (G / 2 per group)
+template <int VPL, int G>
+__device__ __forceinline__ void row_load_words(const bf16_t* row, int lane, uint32_t (&w)[VPL / 2]) {
+#pragma unroll
+  for (int k = 0; k < VPL / G; ++k) {
+    const bf16_t* p = row + row_col<G>(k, lane);
+    if (G == 8) {
+      const uint4 x = *(const uint4*)p;
+      w[4 * k] = x.x; w[4 * k + 1] = x.y; w[4 * k + 2] = x.z; w[4 * k + 3] = x.w;
+    } else {
+      const uint2 x = *(const uint2*)p;
+      w[2 * k] = x.x; w[2 * k + 1] = x.y;
+    }
+  }
+}
+
 template <int VPL>
-__device__ __forceinline__ void store_mx8(const float (&v)[VPL], uint8_t* qrow, uint8_t* srow, int c0) {
-  float a = 0.f;
+__device__ __forceinline__ void words_to_f32(const uint32_t (&w)[VPL / 2], float (&v)[VPL]) {
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) a = fmaxf(a, fabsf(v[i]));
+  for (int j = 0; j < VPL / 2; ++j) { v[2 * j] = lo2f(w[j]); v[2 * j + 1] = hi2f(w[j]); }
+}
+
+template <int VPL, int G>
+__device__ __forceinline__ void row_store_bf(bf16_t* row, int lane, const uint32_t (&o)[VPL / 2]) {
 #pragma unroll
-  for (int o = 1; o < 32 / VPL; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-  const int se = mx_exp(a);
-  uint32_t w[VPL / 4];
+  for (int k = 0; k < VPL / G; ++k) {
+    bf16_t* p = row + row_col<G>(k, lane);
+    if (G == 8) *(uint4*)p = make_uint4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
+    else *(uint2*)p = make_uint2(o[2 * k], o[2 * k + 1]);
+  }
+}
+
+// MX fp8 store of a whole row: a 32-value block is 32 / G consecutive lanes' groups; its maximum is reduced over them
+// and the block's first lane writes the E8M0 scale byte
+template <int VPL, int G>
+__device__ __forceinline__ void row_store_mx8(const float (&v)[VPL], uint8_t* qrow, uint8_t* srow, int lane) {
 #pragma unroll
-  for (int i = 0; i < VPL / 4; ++i) w[i] = mx_pack4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3], se);
-  if (VPL == 16) *(uint4*)(qrow + c0) = make_uint4(w[0], w[1], w[2], w[3]);
-  else if (VPL == 8) *(uint2*)(qrow + c0) = make_uint2(w[0], w[1]);
-  else *(uint32_t*)(qrow + c0) = w[0];
-  if ((c0 & 31) == 0) srow[c0 >> 5] = (uint8_t)(se + 127);
+  for (int k = 0; k < VPL / G; ++k) {
+    const float* x = v + k * G;
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < G; ++j) a = fmaxf(a, fabsf(x[j]));
+#pragma unroll
+    for (int o = 1; o < 32 / G; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    const int se = mx_exp(a);
+    const int c = row_col<G>(k, lane);
+    const uint32_t w0 = mx_pack4(x[0], x[1], x[2], x[3], se);
+    if (G == 8) *(uint2*)(qrow + c) = make_uint2(w0, mx_pack4(x[4], x[5], x[6], x[7], se));
+    else *(uint32_t*)(qrow + c) = w0;
+    if ((lane & (32 / G - 1)) == 0) srow[c >> 5] = (uint8_t)(se + 127);
+  }
 }
 
 // LayerNorm statistics over a row spread across the wave: v -> (v - mean) * rstd
@@ -95,60 +138,59 @@ __global__ void __launch_bounds__(256) ln_mod_kernel(const float* h, const float
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
-  const int c0 = lane * VPL;
   float v[VPL], sc[VPL], sh[VPL];
-  load_f32<VPL>(h + (size_t)n * H + c0, v);
+  row_load_f32<VPL, 4>(h + (size_t)n * H, lane, v);
   normalize<VPL>(v, H, eps);
-  load_f32<VPL>(scale1 + c0, sc);
-  load_f32<VPL>(shift + c0, sh);
+  row_load_f32<VPL, 4>(scale1, lane, sc);
+  row_load_f32<VPL, 4>(shift, lane, sh);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) v[i] = v[i] * sc[i] + sh[i];
   if (q) {
-    store_mx8<VPL>(v, q + (size_t)n * H, qs + (size_t)n * (H / 32), c0);
+    row_store_mx8<VPL, 4>(v, q + (size_t)n * H, qs + (size_t)n * (H / 32), lane);
     return;
   }
   uint32_t o[VPL / 2];
   pack_bf<VPL>(v, o);
-  store_packed<VPL>(out + (size_t)n * H + c0, o);
+  row_store_bf<VPL, 4>(out + (size_t)n * H, lane, o);
 }
 
 // Frame f of token n (position t of row r, T frames) in the padded buffer is n + 2 r + 2; it is also the row's new
 // cache frame t - T + 2 when t >= T - 2.  Row programs copy the two cached frames in front of the row's frames and,
 // for rows of fewer than two tokens, produce the new cache from the old one (the reference's _conv_place and
 // _conv_row_cache, engine/runtime/dit_kernels.py:217-248).
-template <int VPL>
-__device__ __forceinline__ void place_token(const ConvPlace& cp, int n, int H, int c0, const float (&v)[VPL], const uint32_t (&o)[VPL / 2]) {
+template <int VPL, int G>
+__device__ __forceinline__ void place_token(const ConvPlace& cp, int n, int H, int lane, const float (&v)[VPL], const uint32_t (&o)[VPL / 2]) {
   const int r = cp.tok_row[n], t = cp.tok_pos[n], T = cp.row_len[r];
   const size_t f = (size_t)(n + 2 * r + 2);
-  if (cp.P8) store_mx8<VPL>(v, cp.P8 + f * H, cp.P8s + f * (H / 32), c0);
-  else store_packed<VPL>(cp.P + f * H + c0, o);
-  if (t >= T - 2) store_packed<VPL>(cp.cache_out_base + (size_t)cp.wr[r] * cp.cache_stride + (size_t)(t - T + 2) * H + c0, o);
+  if (cp.P8) row_store_mx8<VPL, G>(v, cp.P8 + f * H, cp.P8s + f * (H / 32), lane);
+  else row_store_bf<VPL, G>(cp.P + f * H, lane, o);
+  if (t >= T - 2) row_store_bf<VPL, G>(cp.cache_out_base + (size_t)cp.wr[r] * cp.cache_stride + (size_t)(t - T + 2) * H, lane, o);
 }
 
-template <int VPL>
-__device__ __forceinline__ void place_row(const ConvPlace& cp, int r, int H, int c0) {
+// both cached frames are loaded before the first store (the frame buffer and the caches are distinct memory)
+template <int VPL, int G>
+__device__ __forceinline__ void place_row(const ConvPlace& cp, int r, int H, int lane) {
   const int s = cp.row_start[r], T = cp.row_len[r];
-  const bf16_t* ci = cp.cache_base + (size_t)cp.rd[r] * cp.cache_stride + c0;
-  bf16_t* co = cp.cache_out_base + (size_t)cp.wr[r] * cp.cache_stride + c0;
-  bf16_t* p = cp.P + (size_t)(s + 2 * r) * H + c0;
+  const bf16_t* ci = cp.cache_base + (size_t)cp.rd[r] * cp.cache_stride;
+  bf16_t* co = cp.cache_out_base + (size_t)cp.wr[r] * cp.cache_stride;
   const size_t f = (size_t)(s + 2 * r);
-#pragma unroll
-  for (int i = 0; i < VPL / 4; ++i) {
-    uint2 a = *(const uint2*)(ci + 4 * i), b = *(const uint2*)(ci + H + 4 * i);
-    if (!cp.P8) {
-      *(uint2*)(p + 4 * i) = a;
-      *(uint2*)(p + H + 4 * i) = b;
-    }
-    if (T == 1) *(uint2*)(co + 4 * i) = b;
-    if (T == 0) { *(uint2*)(co + 4 * i) = a; *(uint2*)(co + H + 4 * i) = b; }
-  }
+  uint32_t a[VPL / 2], b[VPL / 2];
+  row_load_words<VPL, G>(ci, lane, a);
+  row_load_words<VPL, G>(ci + H, lane, b);
   if (cp.P8) {  // the cached frames (kept bf16) enter the fp8 frame buffer quantized like the new ones
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float v[VPL];
-      load_bf<VPL>(ci + (size_t)j * H, v);
-      store_mx8<VPL>(v, cp.P8 + (f + j) * H, cp.P8s + (f + j) * (H / 32), c0);
-    }
+    float v[VPL];
+    words_to_f32<VPL>(a, v);
+    row_store_mx8<VPL, G>(v, cp.P8 + f * H, cp.P8s + f * (H / 32), lane);
+    words_to_f32<VPL>(b, v);
+    row_store_mx8<VPL, G>(v, cp.P8 + (f + 1) * H, cp.P8s + (f + 1) * (H / 32), lane);
+  } else {
+    row_store_bf<VPL, G>(cp.P + f * H, lane, a);
+    row_store_bf<VPL, G>(cp.P + (f + 1) * H, lane, b);
+  }
+  if (T == 1) row_store_bf<VPL, G>(co, lane, b);
+  if (T == 0) {
+    row_store_bf<VPL, G>(co, lane, a);
+    row_store_bf<VPL, G>(co + H, lane, b);
   }
 }
 
@@ -157,20 +199,19 @@ __global__ void __launch_bounds__(256) ln_mod_conv_kernel(const float* h, const 
                                                           ConvPlace cp, int H) {
   const int lane = threadIdx.x & 63;
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int c0 = lane * VPL;
   if (w < cp.N) {
     float v[VPL], sc[VPL], sh[VPL];
-    load_f32<VPL>(h + (size_t)w * H + c0, v);
+    row_load_f32<VPL, 4>(h + (size_t)w * H, lane, v);
     normalize<VPL>(v, H, eps);
-    load_f32<VPL>(scale1 + c0, sc);
-    load_f32<VPL>(shift + c0, sh);
+    row_load_f32<VPL, 4>(scale1, lane, sc);
+    row_load_f32<VPL, 4>(shift, lane, sh);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) v[i] = v[i] * sc[i] + sh[i];
     uint32_t o[VPL / 2];
     pack_bf<VPL>(v, o);
-    place_token<VPL>(cp, w, H, c0, v, o);
+    place_token<VPL, 4>(cp, w, H, lane, v, o);
   } else if (w < cp.N + cp.R) {
-    place_row<VPL>(cp, w - cp.N, H, c0);
+    place_row<VPL, 4>(cp, w - cp.N, H, lane);
   }
 }
 
@@ -179,20 +220,22 @@ __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, cons
                                                            ConvPlace cp, int H) {
   const int lane = threadIdx.x & 63;
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int c0 = lane * VPL;
   if (w < cp.N) {
+    constexpr int G = VPL >= 8 ? 8 : 4;  // the row comes in as bf16
     float v[VPL], a[VPL], b[VPL];
-    load_bf<VPL>(y + (size_t)w * H + c0, v);
+    uint32_t wv[VPL / 2];
+    row_load_words<VPL, G>(y + (size_t)w * H, lane, wv);
+    words_to_f32<VPL>(wv, v);
     normalize<VPL>(v, H, eps);
-    load_f32<VPL>(lw + c0, a);
-    load_f32<VPL>(lb + c0, b);
+    row_load_f32<VPL, G>(lw, lane, a);
+    row_load_f32<VPL, G>(lb, lane, b);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) v[i] = mish(v[i] * a[i] + b[i]);
     uint32_t o[VPL / 2];
     pack_bf<VPL>(v, o);
-    place_token<VPL>(cp, w, H, c0, v, o);
+    place_token<VPL, G>(cp, w, H, lane, v, o);
   } else if (w < cp.N + cp.R) {
-    place_row<VPL>(cp, w - cp.N, H, c0);
+    place_row<VPL, VPL >= 8 ? 8 : 4>(cp, w - cp.N, H, lane);
   }
 }
 

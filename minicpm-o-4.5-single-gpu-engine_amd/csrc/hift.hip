@@ -133,8 +133,17 @@ __device__ __forceinline__ float pre_fast(float v, int pre, float slope, float a
   return v;
 }
 
-// epilogue of four consecutive channels co .. co + 3 of one output row (all inside Cout)
-__device__ __forceinline__ void conv_epilogue4(const ConvDesc& c, size_t row, int co, float4 a) {
+// the tensors the epilogue of four channels reads before it writes: the residual (r) and the output or the running
+// sum it accumulates into (t); loaded ahead so that a batch of rows has all its loads in flight
+__device__ __forceinline__ void conv_epilogue4_loads(const ConvDesc& c, size_t row, int co, float4& r, float4& t) {
+  if (c.epi == EPI_RES || c.epi == EPI_ADD_RES || c.epi == EPI_RES_MEAN) r = *(const float4*)(c.res + row * c.ldy + co);
+  if (c.epi == EPI_ADD_RES) t = *(const float4*)(c.y + row * c.ldy + co);
+  if (c.epi == EPI_RES_MEAN && c.sum_mode != 0) t = *(const float4*)(c.sum + row * c.ldy + co);
+}
+
+// epilogue of four consecutive channels co .. co + 3 of one output row (all inside Cout), with its loads already done
+// (r, t as conv_epilogue4_loads left them)
+__device__ __forceinline__ void conv_epilogue4_pre(const ConvDesc& c, size_t row, int co, float4 a, float4 r, float4 t) {
   const float4 bb = *(const float4*)(c.bias + co);
   float v[4] = {__fadd_rn(a.x, bb.x), __fadd_rn(a.y, bb.y), __fadd_rn(a.z, bb.z), __fadd_rn(a.w, bb.w)};
   float* yp = c.y + row * c.ldy + co;
@@ -145,25 +154,52 @@ __device__ __forceinline__ void conv_epilogue4(const ConvDesc& c, size_t row, in
     for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.f ? v[e] : expm1f(v[e]);
     *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
   } else {
-    const float4 r = *(const float4*)(c.res + row * c.ldy + co);
     v[0] = __fadd_rn(v[0], r.x); v[1] = __fadd_rn(v[1], r.y); v[2] = __fadd_rn(v[2], r.z); v[3] = __fadd_rn(v[3], r.w);
     if (c.epi == EPI_RES) {
       *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
     } else if (c.epi == EPI_ADD_RES) {
-      const float4 y = *(const float4*)yp;
-      *(float4*)yp = make_float4(__fadd_rn(y.x, v[0]), __fadd_rn(y.y, v[1]), __fadd_rn(y.z, v[2]), __fadd_rn(y.w, v[3]));
+      *(float4*)yp = make_float4(__fadd_rn(t.x, v[0]), __fadd_rn(t.y, v[1]), __fadd_rn(t.z, v[2]), __fadd_rn(t.w, v[3]));
     } else {  // EPI_RES_MEAN
       float* sp = c.sum + row * c.ldy + co;
       if (c.sum_mode == 0) {
         *(float4*)sp = make_float4(v[0], v[1], v[2], v[3]);
       } else {
-        const float4 t = *(const float4*)sp;
         float o[4] = {__fadd_rn(t.x, v[0]), __fadd_rn(t.y, v[1]), __fadd_rn(t.z, v[2]), __fadd_rn(t.w, v[3])};
         if (c.sum_mode == 2) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) o[e] = __fdiv_rn(o[e], (float)c.sum_div);
         }
         *(float4*)sp = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+}
+
+// conv_epilogue4 with its own loads
+__device__ __forceinline__ void conv_epilogue4(const ConvDesc& c, size_t row, int co, float4 a) {
+  float4 r, t;
+  conv_epilogue4_loads(c, row, co, r, t);
+  conv_epilogue4_pre(c, row, co, a, r, t);
+}
+
+// the last n < 4 channels co .. co + n - 1 of a Cout that is not a multiple of 4, element by element
+__device__ __forceinline__ void conv_epilogue_part(const ConvDesc& c, size_t orow, int co0, int n, float4 v) {
+  const float vv[4] = {v.x, v.y, v.z, v.w};
+  for (int e = 0; e < 4 && e < n; ++e) {
+    const int co = co0 + e;
+    float x = __fadd_rn(vv[e], c.bias[co]);
+    float* yp = c.y + orow * c.ldy + co;
+    if (c.epi == EPI_STORE) *yp = x;
+    else if (c.epi == EPI_ELU) *yp = x > 0.f ? x : expm1f(x);
+    else {
+      x = __fadd_rn(x, c.res[orow * c.ldy + co]);
+      if (c.epi == EPI_RES) *yp = x;
+      else if (c.epi == EPI_ADD_RES) *yp = __fadd_rn(*yp, x);
+      else {
+        float* sp = c.sum + orow * c.ldy + co;
+        if (c.sum_mode == 0) *sp = x;
+        else if (c.sum_mode == 1) *sp = __fadd_rn(*sp, x);
+        else *sp = __fdiv_rn(__fadd_rn(*sp, x), (float)c.sum_div);
       }
     }
   }
@@ -219,24 +255,53 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
       al[e] = (c.pre == PRE_SNAKE && ci + e < c.Cin) ? c.alpha[ci + e] : 0.f;
       iv[e] = (c.pre == PRE_SNAKE && ci + e < c.Cin) ? c.inv[ci + e] : 0.f;
     }
-    for (int sr = tid >> 3; sr < srows; sr += 32) {
-      const int in_row = slab0 + sr;
+    // slab row sr from its two loaded float4 (row inside the input, all 8 channels inside Cin), or element by element
+    auto put_fast = [&](int sr, float4 u0, float4 u1) {
+      float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = pre_fast(v[e], c.pre, c.slope, al[e], iv[e]);
+      hl[hswz(sr, sch)] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+    };
+    auto put_edge = [&](int sr, int in_row) {
       float v[8];
-      if (in_row >= 0 && in_row < Tin && ci + 8 <= c.Cin) {
-        const float4 u0 = *(const float4*)(xb + (size_t)in_row * c.ldx + ci);
-        const float4 u1 = *(const float4*)(xb + (size_t)in_row * c.ldx + ci + 4);
-        v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w; v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = pre_fast(v[e], c.pre, c.slope, al[e], iv[e]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float x = 0.f;
-          if (in_row >= 0 && in_row < Tin && ci + e < c.Cin) x = pre_fast(xb[(size_t)in_row * c.ldx + ci + e], c.pre, c.slope, al[e], iv[e]);
-          v[e] = x;
-        }
+      for (int e = 0; e < 8; ++e) {
+        float xv = 0.f;
+        if (in_row >= 0 && in_row < Tin && ci + e < c.Cin) xv = pre_fast(xb[(size_t)in_row * c.ldx + ci + e], c.pre, c.slope, al[e], iv[e]);
+        v[e] = xv;
       }
       hl[hswz(sr, sch)] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+    };
+    if constexpr (BM < 512) {  // one slab row at a time: the small tile keeps its register budget (4 waves per SIMD)
+      for (int sr = tid >> 3; sr < srows; sr += 32) {
+        const int in_row = slab0 + sr;
+        if (in_row >= 0 && in_row < Tin && ci + 8 <= c.Cin)
+          put_fast(sr, *(const float4*)(xb + (size_t)in_row * c.ldx + ci), *(const float4*)(xb + (size_t)in_row * c.ldx + ci + 4));
+        else
+          put_edge(sr, in_row);
+      }
+    } else {  // SU slab rows per thread and pass, all their loads in flight before the first one is used
+      constexpr int SU = 4;
+      for (int sr0 = tid >> 3; sr0 < srows; sr0 += 32 * SU) {
+        float4 u[SU][2];
+        bool fast[SU];
+#pragma unroll
+        for (int x = 0; x < SU; ++x) {
+          const int sr = sr0 + 32 * x, in_row = slab0 + sr;
+          fast[x] = sr < srows && in_row >= 0 && in_row < Tin && ci + 8 <= c.Cin;
+          if (fast[x]) {
+            u[x][0] = *(const float4*)(xb + (size_t)in_row * c.ldx + ci);
+            u[x][1] = *(const float4*)(xb + (size_t)in_row * c.ldx + ci + 4);
+          }
+        }
+#pragma unroll
+        for (int x = 0; x < SU; ++x) {
+          const int sr = sr0 + 32 * x;
+          if (sr >= srows) break;
+          if (fast[x]) put_fast(sr, u[x][0], u[x][1]);
+          else put_edge(sr, slab0 + sr);
+        }
+      }
     }
     bf16x8 wa[4][2], wb[4][2];
     load_w(0, c0, wa);
@@ -281,35 +346,38 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
         st[t * 16 + (c4 ^ (t & 15))] = make_float4(acc[i][jj][q * 4], acc[i][jj][q * 4 + 1], acc[i][jj][q * 4 + 2], acc[i][jj][q * 4 + 3]);
       }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int c4 = lane & 15;
+    if constexpr (BM < 512) {
 #pragma unroll
-    for (int rr = 0; rr < 8; ++rr) {
-      const int row = rr * 4 + (lane >> 4), c4 = lane & 15;
-      const int r = r0 + wave * WTM + i * 32 + row;
-      const float4 v = st[row * 16 + (c4 ^ (row & 15))];
-      if (r > r_hi || c4 * 4 >= ncols) continue;
-      const size_t orow = (size_t)c.out_off[b] + (size_t)(r * c.s_out + oo);
-      if (c4 * 4 + 3 < ncols) {
-        conv_epilogue4(c, orow, co0 + c4 * 4, v);
-      } else {  // the last channels of a Cout that is not a multiple of 4
-        const float vv[4] = {v.x, v.y, v.z, v.w};
-        for (int e = 0; e < 4 && c4 * 4 + e < ncols; ++e) {
-          const int co = co0 + c4 * 4 + e;
-          float x = __fadd_rn(vv[e], c.bias[co]);
-          float* yp = c.y + orow * c.ldy + co;
-          if (c.epi == EPI_STORE) *yp = x;
-          else if (c.epi == EPI_ELU) *yp = x > 0.f ? x : expm1f(x);
-          else {
-            x = __fadd_rn(x, c.res[orow * c.ldy + co]);
-            if (c.epi == EPI_RES) *yp = x;
-            else if (c.epi == EPI_ADD_RES) *yp = __fadd_rn(*yp, x);
-            else {
-              float* sp = c.sum + orow * c.ldy + co;
-              if (c.sum_mode == 0) *sp = x;
-              else if (c.sum_mode == 1) *sp = __fadd_rn(*sp, x);
-              else *sp = __fdiv_rn(__fadd_rn(*sp, x), (float)c.sum_div);
-            }
-          }
-        }
+      for (int rr = 0; rr < 8; ++rr) {
+        const int row = rr * 4 + (lane >> 4);
+        const int r = r0 + wave * WTM + i * 32 + row;
+        const float4 v = st[row * 16 + (c4 ^ (row & 15))];
+        if (r > r_hi || c4 * 4 >= ncols) continue;
+        const size_t orow = (size_t)c.out_off[b] + (size_t)(r * c.s_out + oo);
+        if (c4 * 4 + 3 < ncols) conv_epilogue4(c, orow, co0 + c4 * 4, v);
+        else conv_epilogue_part(c, orow, co0 + c4 * 4, ncols - c4 * 4, v);
+      }
+    } else {
+      // the eight rows of this lane: every residual / accumulator load in flight before the first store
+      float4 vv4[8], rr4[8], tt4[8];
+#pragma unroll
+      for (int rr = 0; rr < 8; ++rr) {
+        const int row = rr * 4 + (lane >> 4);
+        const int r = r0 + wave * WTM + i * 32 + row;
+        vv4[rr] = st[row * 16 + (c4 ^ (row & 15))];
+        rr4[rr] = tt4[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r <= r_hi && c4 * 4 + 3 < ncols)
+          conv_epilogue4_loads(c, (size_t)c.out_off[b] + (size_t)(r * c.s_out + oo), co0 + c4 * 4, rr4[rr], tt4[rr]);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 8; ++rr) {
+        const int row = rr * 4 + (lane >> 4);
+        const int r = r0 + wave * WTM + i * 32 + row;
+        if (r > r_hi || c4 * 4 >= ncols) continue;
+        const size_t orow = (size_t)c.out_off[b] + (size_t)(r * c.s_out + oo);
+        if (c4 * 4 + 3 < ncols) conv_epilogue4_pre(c, orow, co0 + c4 * 4, vv4[rr], rr4[rr], tt4[rr]);
+        else conv_epilogue_part(c, orow, co0 + c4 * 4, ncols - c4 * 4, vv4[rr]);
       }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
