@@ -138,11 +138,12 @@ int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const f
 /* C = A . W^T + bias; epi 0: bf16 out, 1: GELU-tanh bf16 out, 2: C(fp32) += gate * (.), 3: fp32 out.
  * a_src non-null: conv taps mode, A row m = frames a_src[m] .. a_src[m] + K / lda - 1 of A (rows lda wide).
  * Calls of at most 128 rows (K <= 3072, ldc % 4 == 0) run as one kernel that splits K over the waves of a workgroup;
- * larger ones on the tile GEMM. */
+ * larger ones on the tile GEMM (bf16 outputs: ldc % 8 == 0 and C 16-byte aligned there). */
 int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                   void* C, int ldc, int M, int N, int K, int epi, void* stream);
 /* t2w_gemm_bf16 with an explicit tile configuration (-1: chosen by shape; 0: 128x128 of 4 waves, 1: 256x256 of
- * 8 waves, 2: 256x128 of 8 waves) for tile sweeps.  K % 64 == 0, lda % 8 == 0 (taps mode: lda % 64 == 0). */
+ * 8 waves, 2: 256x128 of 8 waves, 3: 256x256 of 4 waves on a four-stage LDS ring, K % 128 == 0) for tile sweeps.
+ * K % 64 == 0, lda % 8 == 0 (taps mode: lda % 64 == 0). */
 int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                        void* C, int ldc, int M, int N, int K, int epi, int tile, void* stream);
 /* t2w_gemm_bf16 with a workspace for split-K partials (256-byte aligned; up to splits x M x N fp32): a call whose tile

@@ -141,10 +141,16 @@ bool gemm_splits(const GemmArgs& g) {
 hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
   if (cfg < 0 && gemm_small_fits(g, epi)) return gemm_small(g, epi, st);
+  // the tile epilogues store bf16 rows 16 bytes per lane
+  const bool bf16_out = epi == EPI_BF16 || epi == EPI_GELU_BF16;
+  if (bf16_out && (g.ldc % 8 || ((size_t)g.C & 15)) && !(cfg < 0 && gemm_splits(g))) return hipErrorInvalidValue;
   if (cfg < 0 && gemm_splits(g)) {
     if (epi == EPI_QKV || epi == EPI_GELU_MX8) return hipErrorInvalidValue;  // tile-path epilogues
     return gemm_splitk(g, epi, splitk_plan(g.M, g.N, g.K, g.ws_bytes), g.ws, st);
   }
+  // the four-wave ring on request only: on its own its main loop is the faster one, but with the DiT's epilogues
+  // (gated fp32 residual, q/k LayerNorm scatter) four waves hide less of the epilogue's memory traffic than eight
+  if (cfg == 3) return gemm_ring(g, epi, st);
   const bool taps = g.a_src != nullptr;
   switch (epi * 2 + (taps ? 1 : 0)) {
     case EPI_BF16 * 2: return launch_epi<EPI_BF16, false>(g, cfg, st);

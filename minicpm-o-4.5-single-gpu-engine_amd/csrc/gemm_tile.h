@@ -77,6 +77,128 @@ struct FragT { typedef bf16x8 type; };
 template <>
 struct FragT<true> { typedef i32x8 type; };
 
+// Writes one wave's accumulators (a WTM x WTN block at rows mw.., columns nw..; acc[i][j] = MFMA block (i, j), lane l
+// holding column nw + j * 32 + q * 8 + (l / 32) * 4 + (0..3) of row mw + i * 32 + l % 32 in registers q * 4 ..) through
+// its LDS slab st (32 x WTN fp32, 16-byte chunks XOR-swizzled by row) so that each global access of the epilogue covers
+// whole rows.  bf16 outputs go out 16 bytes per lane (8 columns); the others 4 columns per lane, in batches of RB
+// read-back instructions whose residual loads are all in flight before the first store.  bf16 outputs need
+// ldc % 8 == 0 and a 16-byte aligned C (gemm_bf16 checks).
+template <int EPI, int TM, int TN, int WTM, int WTN>
+__device__ __forceinline__ void tile_store(const GemmArgs& g, const f32x16 (&acc)[TM][TN], float4* st, int mw, int nw, int lane) {
+  constexpr int CPR = WTN / 4;   // 16-byte chunks per slab row
+  constexpr int RPI = 64 / CPR;  // slab rows per read-back instruction
+  constexpr int NRB = 32 / RPI;  // read-back instructions per slab
+  constexpr int RB = NRB < 8 ? NRB : 8;
+  constexpr bool WIDE = (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) && WTN % 8 == 0;
+  constexpr int CW = WTN / 8, RW = 64 / CW;  // wide: lanes per slab row, slab rows per instruction
+  const int cc = WIDE ? (lane % CW) * 2 : lane % CPR;
+  const Cols<EPI> cols(g, nw + cc * 4);
+  const Cols<EPI> cols2(g, nw + cc * 4 + 4);  // wide: the lane's second four columns
+  // EPI_QKV: this lane's part (q, k, v), column and head offset, and the LayerNorm affine of its four columns
+  int qpart = 0, qcol = 0;
+  float4 qlw = make_float4(0.f, 0.f, 0.f, 0.f), qlb = qlw;
+  if constexpr (EPI == EPI_QKV) {
+    qpart = cols.n / g.qk.H;
+    qcol = cols.n - qpart * g.qk.H;
+    if (qpart < 2) {
+      qlw = *(const float4*)((qpart ? g.qk.kw : g.qk.qw) + (qcol & 63));
+      qlb = *(const float4*)((qpart ? g.qk.kb : g.qk.qb) + (qcol & 63));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    {
+      const int r = lane & 31;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = j * 8 + q * 2 + (lane >> 5);
+          st[r * CPR + (c ^ (r & (CPR - 1)))] =
+              make_float4(acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if constexpr (WIDE) {
+#pragma unroll
+      for (int b = 0; b < 32 / RW; ++b) {
+        const int row = b * RW + lane / CW;
+        const int m = mw + i * 32 + row;
+        const float4 v0 = st[row * CPR + (cc ^ (row & (CPR - 1)))];
+        const float4 v1 = st[row * CPR + ((cc + 1) ^ (row & (CPR - 1)))];
+        if (m >= g.M) continue;
+        if (cols2.full) {
+          const float4 o0 = cols.apply(v0, v0), o1 = cols2.apply(v1, v1);
+          *(uint4*)((bf16_t*)g.C + (size_t)m * g.ldc + cols.n) =
+              make_uint4(pack2(o0.x, o0.y), pack2(o0.z, o0.w), pack2(o1.x, o1.y), pack2(o1.z, o1.w));
+        } else {
+          cols.put_partial(g, m, v0);
+          cols2.put_partial(g, m, v1);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < NRB; b += RB) {
+        float4 v[RB], h[RB];
+        int m[RB], slot[RB];
+#pragma unroll
+        for (int x = 0; x < RB; ++x) {
+          const int row = (b + x) * RPI + lane / CPR;
+          m[x] = mw + i * 32 + row;
+          v[x] = st[row * CPR + (cc ^ (row & (CPR - 1)))];
+          h[x] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (EPI == EPI_RESID_F32 && cols.full && m[x] < g.M) h[x] = *(const float4*)((const float*)g.C + (size_t)m[x] * g.ldc + cols.n);
+          slot[x] = 0;
+          if (EPI == EPI_QKV && qpart > 0 && m[x] < g.M) slot[x] = g.qk.slots[m[x]];
+        }
+#pragma unroll
+        for (int x = 0; x < RB; ++x) {
+          if constexpr (EPI == EPI_QKV) {
+            // the 16 lanes (one DPP row) holding this row's 64 columns of one head: heads are 64-aligned in the tile
+            const QkvOut& o = g.qk;
+            float y[4] = {v[x].x * cols.wsc.x + cols.bias.x, v[x].y * cols.wsc.y + cols.bias.y,
+                          v[x].z * cols.wsc.z + cols.bias.z, v[x].w * cols.wsc.w + cols.bias.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(y[e]));  // the projection is rounded to bf16 first
+            if (qpart < 2) {
+              const float mean = row16_sum(y[0] + y[1] + y[2] + y[3]) * (1.0f / 64.0f);
+              float q = 0.f;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) { y[e] -= mean; q += y[e] * y[e]; }
+              const float rstd = rsqrtf(row16_sum(q) * (1.0f / 64.0f) + o.eps);
+              y[0] = y[0] * rstd * qlw.x + qlb.x;
+              y[1] = y[1] * rstd * qlw.y + qlb.y;
+              y[2] = y[2] * rstd * qlw.z + qlb.z;
+              y[3] = y[3] * rstd * qlw.w + qlb.w;
+            }
+            if (m[x] < g.M) {
+              bf16_t* dst = qpart == 0 ? o.q_out + (size_t)m[x] * o.H : (qpart == 1 ? o.k_pool : o.v_pool) + (size_t)slot[x] * o.H;
+              *(uint2*)(dst + qcol) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+            }
+          } else if constexpr (EPI == EPI_GELU_MX8) {
+            // the 8 lanes holding this row's 32 consecutive columns share one block scale (N % 32 == 0)
+            const float4 o = cols.apply(v[x], h[x]);
+            float a = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
+            a = fmaxf(a, __shfl_xor(a, 1, 64));
+            a = fmaxf(a, __shfl_xor(a, 2, 64));
+            a = fmaxf(a, __shfl_xor(a, 4, 64));
+            const int se = mx_exp(a);
+            if (m[x] < g.M && cols.full) {
+              *(uint32_t*)((uint8_t*)g.C + (size_t)m[x] * g.ldc + cols.n) = mx_pack4(o.x, o.y, o.z, o.w, se);
+              if ((cc & 7) == 0) g.c_scale[(size_t)m[x] * g.c_sld + (cols.n >> 5)] = (uint8_t)(se + 127);
+            }
+          } else {
+            if (m[x] >= g.M) continue;
+            if (cols.full) cols.put(g, m[x], cols.apply(v[x], h[x]));
+            else cols.put_partial(g, m[x], v[x]);
+          }
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+}
+
 template <int BM, int BN, int WM, int WN, bool TAPS, bool FP8>
 struct Tile {
   static constexpr int NW = WM * WN;
@@ -225,99 +347,9 @@ struct Tile {
     }
   }
 
-  // Writes the wave's accumulators through its LDS slab st (32 x WTN fp32, chunks XOR-swizzled by row) so that each
-  // global access of the epilogue covers whole rows.  Rows go out in batches of RB read-back instructions whose
-  // residual loads are all in flight before the first store.
   template <int EPI>
   __device__ __forceinline__ void store(const f32x16 (&acc)[TM][TN], float4* st, int m0, int n0) const {
-    constexpr int CPR = WTN / 4;   // 16-byte chunks per slab row
-    constexpr int RPI = 64 / CPR;  // slab rows per read-back instruction
-    constexpr int NRB = 32 / RPI;  // read-back instructions per slab
-    constexpr int RB = NRB < 8 ? NRB : 8;
-    const int cc = lane % CPR;
-    const Cols<EPI> cols(g, n0 + wn * WTN + cc * 4);
-    // EPI_QKV: this lane's part (q, k, v), column and head offset, and the LayerNorm affine of its four columns
-    int qpart = 0, qcol = 0;
-    float4 qlw = make_float4(0.f, 0.f, 0.f, 0.f), qlb = qlw;
-    if constexpr (EPI == EPI_QKV) {
-      qpart = cols.n / g.qk.H;
-      qcol = cols.n - qpart * g.qk.H;
-      if (qpart < 2) {
-        qlw = *(const float4*)((qpart ? g.qk.kw : g.qk.qw) + (qcol & 63));
-        qlb = *(const float4*)((qpart ? g.qk.kb : g.qk.qb) + (qcol & 63));
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int r = lane & 31;
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int c = j * 8 + q * 2 + (lane >> 5);
-          st[r * CPR + (c ^ (r & (CPR - 1)))] =
-              make_float4(acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
-        }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-      for (int b = 0; b < NRB; b += RB) {
-        float4 v[RB], h[RB];
-        int m[RB], slot[RB];
-#pragma unroll
-        for (int x = 0; x < RB; ++x) {
-          const int row = (b + x) * RPI + lane / CPR;
-          m[x] = m0 + wm * WTM + i * 32 + row;
-          v[x] = st[row * CPR + (cc ^ (row & (CPR - 1)))];
-          h[x] = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (EPI == EPI_RESID_F32 && cols.full && m[x] < g.M) h[x] = *(const float4*)((const float*)g.C + (size_t)m[x] * g.ldc + cols.n);
-          slot[x] = 0;
-          if (EPI == EPI_QKV && qpart > 0 && m[x] < g.M) slot[x] = g.qk.slots[m[x]];
-        }
-#pragma unroll
-        for (int x = 0; x < RB; ++x) {
-          if constexpr (EPI == EPI_QKV) {
-            // the 16 lanes (one DPP row) holding this row's 64 columns of one head: heads are 64-aligned in the tile
-            const QkvOut& o = g.qk;
-            float y[4] = {v[x].x * cols.wsc.x + cols.bias.x, v[x].y * cols.wsc.y + cols.bias.y,
-                          v[x].z * cols.wsc.z + cols.bias.z, v[x].w * cols.wsc.w + cols.bias.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(y[e]));  // the projection is rounded to bf16 first
-            if (qpart < 2) {
-              const float mean = row16_sum(y[0] + y[1] + y[2] + y[3]) * (1.0f / 64.0f);
-              float q = 0.f;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) { y[e] -= mean; q += y[e] * y[e]; }
-              const float rstd = rsqrtf(row16_sum(q) * (1.0f / 64.0f) + o.eps);
-              y[0] = y[0] * rstd * qlw.x + qlb.x;
-              y[1] = y[1] * rstd * qlw.y + qlb.y;
-              y[2] = y[2] * rstd * qlw.z + qlb.z;
-              y[3] = y[3] * rstd * qlw.w + qlb.w;
-            }
-            if (m[x] < g.M) {
-              bf16_t* dst = qpart == 0 ? o.q_out + (size_t)m[x] * o.H : (qpart == 1 ? o.k_pool : o.v_pool) + (size_t)slot[x] * o.H;
-              *(uint2*)(dst + qcol) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
-            }
-          } else if constexpr (EPI == EPI_GELU_MX8) {
-            // the 8 lanes holding this row's 32 consecutive columns share one block scale (N % 32 == 0)
-            const float4 o = cols.apply(v[x], h[x]);
-            float a = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
-            a = fmaxf(a, __shfl_xor(a, 1, 64));
-            a = fmaxf(a, __shfl_xor(a, 2, 64));
-            a = fmaxf(a, __shfl_xor(a, 4, 64));
-            const int se = mx_exp(a);
-            if (m[x] < g.M && cols.full) {
-              *(uint32_t*)((uint8_t*)g.C + (size_t)m[x] * g.ldc + cols.n) = mx_pack4(o.x, o.y, o.z, o.w, se);
-              if ((cc & 7) == 0) g.c_scale[(size_t)m[x] * g.c_sld + (cols.n >> 5)] = (uint8_t)(se + 127);
-            }
-          } else {
-            if (m[x] >= g.M) continue;
-            if (cols.full) cols.put(g, m[x], cols.apply(v[x], h[x]));
-            else cols.put_partial(g, m[x], v[x]);
-          }
-        }
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
+    tile_store<EPI, TM, TN, WTM, WTN>(g, acc, st, m0 + wm * WTM, n0 + wn * WTN, lane);
   }
 };
 

@@ -58,6 +58,12 @@ constexpr int GEMM_SMALL_MAX_M = 128;
 bool gemm_small_fits(const GemmArgs& g, int epi);
 hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st);
 
+// Four-wave 256 x 256 tile GEMM with a four-stage LDS ring (gemm_ring.hip): bf16 operands, every epilogue but
+// EPI_GELU_MX8, K % 128 == 0, lda % 8 == 0, ldb % 8 == 0 (taps: tapC % 32 == 0, frames within 4 GB of A).
+// gemm_bf16 runs it when cfg 3 asks for it.
+bool gemm_ring_fits(const GemmArgs& g, int epi);
+hipError_t gemm_ring(const GemmArgs& g, int epi, hipStream_t st);
+
 struct SplitPlan {
   int splits;  // 0: split-K not possible for this shape / workspace
   int steps;   // 64-K steps per split

@@ -50,6 +50,22 @@ def test_estimator_forward_config1(dev, full):
     assert e < TOL
 
 
+def test_estimator_forward_3000_tokens(dev, full):
+    """One estimator forward with 3000 tokens (B=2 rows, T=1500, t=0.3): the qkv projection (with the fused q/k
+    LayerNorm and key/value scatter) runs on the four-wave ring GEMM, the other projections on split-K."""
+    W, model = full
+    fd = FastDiT(model, n_slots=4096, max_streams=2)
+    g = torch.Generator().manual_seed(3)
+    x, mu = torch.randn(2, 80, 1500, generator=g), torch.randn(2, 80, 1500, generator=g)
+    spk = torch.randn(2, 80, generator=g)
+    cond = torch.randn(2, 80, 1500, generator=g) * 0.5
+    ref = od.estimator_forward(W, od.dims_of(W), x, mu, torch.full((2,), 0.3), spk, cond)
+    got = fd.estimator_forward(x.cuda(), mu.cuda(), 0.3, spk.cuda(), cond.cuda()).cpu()
+    e = rel(got, ref)
+    print("3000-token estimator rel-L2", e, "max-abs", float((got - ref).abs().max()))
+    assert e < TOL
+
+
 def _stream_case(W, model, graphs: bool, buckets: bool = False, outs: list | None = None, stats: dict | None = None):
     d = od.dims_of(W, steps=TINY.steps)
     fd = FastDiT(model, n_slots=4096, max_streams=4, use_graphs=graphs, buckets=buckets)

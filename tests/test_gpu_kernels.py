@@ -53,6 +53,34 @@ def test_gemm_dense(dev, M, N, K, epi):
         assert rel(out, ref) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(1100, 640, 1024), (2048, 3072, 1024), (1300, 1024, 3072), (300, 256, 128)])
+@pytest.mark.parametrize("tile", [1, 3])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_gemm_tiles(dev, M, N, K, tile, epi):
+    """Explicit tile configurations (1: eight waves of 64 x 128; 3: four waves of 128 x 128 on the LDS ring) with
+    ragged rows and columns against fp32."""
+    L = _lib.lib()
+    g = torch.Generator(device=dev).manual_seed(M + N * 3 + K * 5 + epi)
+    A = torch.randn(M, K, device=dev, generator=g).bfloat16()
+    W = (torch.randn(N, K, device=dev, generator=g) / K ** 0.5).bfloat16()
+    bias = torch.randn(N, device=dev, generator=g)
+    gate = torch.randn(N, device=dev, generator=g)
+    ref = A.float() @ W.float().t() + bias
+    if epi in (0, 1):
+        out = torch.full((M, N), 7.0, device=dev).bfloat16()
+        if epi == 1:
+            ref = torch.nn.functional.gelu(ref, approximate="tanh")
+    elif epi == 2:
+        out = torch.randn(M, N, device=dev, generator=g)
+        ref = out + gate * ref
+    else:
+        out = torch.zeros(M, N, device=dev)
+    _lib.check(L.t2w_gemm_bf16_tile(A.data_ptr(), K, None, W.data_ptr(), bias.data_ptr(), gate.data_ptr() if epi == 2 else None,
+                                    out.data_ptr(), N, M, N, K, epi, tile, _lib.stream_handle()), "gemm tile")
+    torch.cuda.synchronize()
+    assert rel(out.float(), ref) < (6e-3 if epi in (0, 1) else 1e-5)
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (37, 3072, 1024), (100, 1024, 2048), (100, 80, 1024), (300, 2048, 1024), (600, 1024, 320)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 def test_gemm_splitk(dev, M, N, K, epi):
@@ -104,10 +132,11 @@ def test_gemm_splitk_taps(dev):
     assert rel(out, ref) < 1e-5
 
 
-@pytest.mark.parametrize("lens", [[5, 0, 1, 2, 3, 40, 0, 17, 1, 56], [400] * 3])
-def test_gemm_conv_taps(dev, lens):
+@pytest.mark.parametrize("lens,tile", [([5, 0, 1, 2, 3, 40, 0, 17, 1, 56], -1), ([400] * 3, -1), ([400] * 3, 1), ([400] * 3, 3),
+                                       ([5, 0, 300, 2, 3, 400, 0, 17, 1, 560], 3)])
+def test_gemm_conv_taps(dev, lens, tile):
     """Taps mode: row m reads three consecutive frames starting at a_src[m] of the padded frame buffer; equals a
-    kernel-3 conv over [2 cached frames | row frames] (F.conv1d, fp32)."""
+    kernel-3 conv over [2 cached frames | row frames] (F.conv1d, fp32).  tile: as chosen by shape (-1) or explicit."""
     H = 256
     g = torch.Generator(device=dev).manual_seed(11)
     R, N = len(lens), sum(lens)
@@ -118,7 +147,12 @@ def test_gemm_conv_taps(dev, lens):
     tok_row = [r for r, t in enumerate(lens) for _ in range(t)]
     a_src = torch.tensor([i + 2 * r for i, r in enumerate(tok_row)], dtype=torch.int32, device=dev)
     out = torch.zeros(N, H, device=dev)
-    _gemm(P, Wfm, bias, out, 3, a_src=a_src, lda=H, K=3 * H)
+    if tile < 0:
+        _gemm(P, Wfm, bias, out, 3, a_src=a_src, lda=H, K=3 * H)
+    else:
+        _lib.check(_lib.lib().t2w_gemm_bf16_tile(P.data_ptr(), H, a_src.data_ptr(), Wfm.data_ptr(), bias.data_ptr(), None, out.data_ptr(), H,
+                                                 N, H, 3 * H, 3, tile, _lib.stream_handle()), "gemm tile")
+        torch.cuda.synchronize()
     refs, o = [], 0
     for r, t in enumerate(lens):
         if t:
