@@ -1,5 +1,6 @@
 // The eight-wave tile machinery of the bf16 / fp8 MFMA GEMM (gemm.hip): LDS swizzle, epilogue columns and the Tile
-// (loads, fragments, MFMAs, K stage, row-coalesced epilogue), shared with the four-wave kernel (gemm4d.hip).
+// (loads, fragments, MFMAs, K stage), and the row-coalesced epilogue tile_store shared with the four-wave ring kernel
+// (gemm_ring.hip).
 #pragma once
 
 #include "common.h"
