@@ -28,7 +28,7 @@ __device__ __forceinline__ int vpos(int k) { return (k & ~12) | ((k & 4) << 1) |
 // KS > 1 (few workgroups, e.g. a streaming chunk): KS groups of two waves share the 64 queries and take every KS-th
 // key tile each; their softmax states (max, sum, output) are merged through LDS at the end.
 template <int KS>
-__global__ void __launch_bounds__(128 * KS) attn_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
   __shared__ uint4 ks[KS][2][64 * 8];      // [key][16-byte chunk ^ (key & 7)], 64 keys
   __shared__ uint4 vt[KS][2][2][64 * 4];   // per 32-key half: [d][16-byte chunk ^ ((d >> 1) & 3)] of permuted keys
   // XCD-aware order: consecutive workgroups go to different XCDs, so each XCD takes a contiguous run of (head, tile)
@@ -75,13 +75,15 @@ __global__ void __launch_bounds__(128 * KS) attn_kernel(AttnArgs a) {
     T2W_TILE_RANGE(t, kb_, ke_)                               \
     out = a.kv_idx[kvoff + (kb_ + lk < ke_ ? kb_ + lk : kb_)]; \
   }
-  uint4 rk0, rk1, rk2, rk3, rv0, rv1, rv2, rv3;
-#define T2W_GLOAD(slot)                                                                 \
+  // two register sets (a, b) of one tile each: the loads of tile t + 2 KS are issued while tile t is multiplied and
+  // tile t + KS (loaded one step earlier) goes to LDS
+  uint4 rk0a, rk1a, rk2a, rk3a, rv0a, rv1a, rv2a, rv3a, rk0b, rk1b, rk2b, rk3b, rv0b, rv1b, rv2b, rv3b;
+#define T2W_GLOAD(slot, X)                                                         \
   {                                                                                     \
     const uint4* kp = (const uint4*)(a.k_pool + (size_t)(slot) * H + head * 64 + lc * 8); \
     const uint4* vp = (const uint4*)(a.v_pool + (size_t)(slot) * H + head * 64 + lc * 8); \
-    rk0 = kp[0]; rk1 = kp[1]; rk2 = kp[2]; rk3 = kp[3];                                 \
-    rv0 = vp[0]; rv1 = vp[1]; rv2 = vp[2]; rv3 = vp[3];                                 \
+    rk0##X = kp[0]; rk1##X = kp[1]; rk2##X = kp[2]; rk3##X = kp[3];                     \
+    rv0##X = vp[0]; rv1##X = vp[1]; rv2##X = vp[2]; rv3##X = vp[3];                     \
   }
   const int vp_ = vpos(lk & 31);
   auto vstore = [](bf16_t* vb, int p, int dbase, uint4 v) {  // 8 consecutive d of one key into the transposed tile
@@ -94,18 +96,18 @@ __global__ void __launch_bounds__(128 * KS) attn_kernel(AttnArgs a) {
       vb[d * 32 + (((p >> 3) ^ ((d >> 1) & 3)) << 3) + (p & 7)] = (bf16_t)((e & 1) ? (wv >> 16) : (wv & 0xffff));
     }
   };
-#define T2W_LSTORE(s)                                            \
+#define T2W_LSTORE(s, X)                                         \
   {                                                              \
     uint4* kr = ks[gi][s] + lk * 8;                              \
-    kr[(lc + 0) ^ (lk & 7)] = rk0;                               \
-    kr[(lc + 1) ^ (lk & 7)] = rk1;                               \
-    kr[(lc + 2) ^ (lk & 7)] = rk2;                               \
-    kr[(lc + 3) ^ (lk & 7)] = rk3;                               \
+    kr[(lc + 0) ^ (lk & 7)] = rk0##X;                           \
+    kr[(lc + 1) ^ (lk & 7)] = rk1##X;                           \
+    kr[(lc + 2) ^ (lk & 7)] = rk2##X;                           \
+    kr[(lc + 3) ^ (lk & 7)] = rk3##X;                           \
     bf16_t* vb = (bf16_t*)vt[gi][s][lk >> 5];                    \
-    vstore(vb, vp_, (lc + 0) * 8, rv0);                          \
-    vstore(vb, vp_, (lc + 1) * 8, rv1);                          \
-    vstore(vb, vp_, (lc + 2) * 8, rv2);                          \
-    vstore(vb, vp_, (lc + 3) * 8, rv3);                          \
+    vstore(vb, vp_, (lc + 0) * 8, rv0##X);                      \
+    vstore(vb, vp_, (lc + 1) * 8, rv1##X);                      \
+    vstore(vb, vp_, (lc + 2) * 8, rv2##X);                      \
+    vstore(vb, vp_, (lc + 3) * 8, rv3##X);                      \
   }
 
   f32x16 o0, o1;
@@ -121,15 +123,18 @@ __global__ void __launch_bounds__(128 * KS) attn_kernel(AttnArgs a) {
   if (gi < ntiles) {
     int s0;
     T2W_SLOT_OF(gi, s0)
-    T2W_GLOAD(s0)
-    if (gi + KS < ntiles) T2W_SLOT_OF(gi + KS, slot_next)
-    T2W_LSTORE(0)
+    T2W_GLOAD(s0, a)
+    T2W_LSTORE(0, a)
   }
+  if (gi + KS < ntiles) {
+    int s1;
+    T2W_SLOT_OF(gi + KS, s1)
+    T2W_GLOAD(s1, b)
+  }
+  if (gi + 2 * KS < ntiles) T2W_SLOT_OF(gi + 2 * KS, slot_next)
   __syncthreads();
-  for (int it = 0; it < niter; ++it) {
-    const int s = it & 1, t = it * KS + gi;
-    if (t + KS < ntiles) T2W_GLOAD(slot_next)
-    if (t + 2 * KS < ntiles) T2W_SLOT_OF(t + 2 * KS, slot_next)
+  // one key tile t from LDS buffer s: scores, online softmax, P.V
+  auto tile_step = [&](const int t, const int s) {
     if (active && t < ntiles) {
       int kb, ke;
       T2W_TILE_RANGE(t, kb, ke)
@@ -211,8 +216,25 @@ __global__ void __launch_bounds__(128 * KS) attn_kernel(AttnArgs a) {
         }
       }
     }
-    if (t + KS < ntiles) T2W_LSTORE(s ^ 1)
-    __syncthreads();
+  };
+  // unrolled by two so that each step names its register sets at compile time
+  for (int it = 0; it < niter; it += 2) {
+    {
+      const int t = it * KS + gi;
+      if (t + 2 * KS < ntiles) T2W_GLOAD(slot_next, a)
+      if (t + 3 * KS < ntiles) T2W_SLOT_OF(t + 3 * KS, slot_next)
+      tile_step(t, 0);
+      if (t + KS < ntiles) T2W_LSTORE(1, b)
+      __syncthreads();
+    }
+    if (it + 1 < niter) {
+      const int t = (it + 1) * KS + gi;
+      if (t + 2 * KS < ntiles) T2W_GLOAD(slot_next, b)
+      if (t + 3 * KS < ntiles) T2W_SLOT_OF(t + 3 * KS, slot_next)
+      tile_step(t, 1);
+      if (t + KS < ntiles) T2W_LSTORE(0, a)
+      __syncthreads();
+    }
   }
 #undef T2W_TILE_RANGE
 #undef T2W_SLOT_OF

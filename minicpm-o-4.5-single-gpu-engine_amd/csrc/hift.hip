@@ -207,7 +207,11 @@ __device__ __forceinline__ void conv_epilogue_part(const ConvDesc& c, size_t oro
 
 template <int BM>
 __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf16_t* __restrict__ wbf) {
-  constexpr int WTM = BM / 4, TM = WTM / 32;  // 4 waves along time, each all 64 channels
+  constexpr int NWV = 4, RPP = 32;              // waves; slab rows per pass of the block (8 threads per row)
+  constexpr int WTM = BM / NWV, TM = WTM / 32;  // NWV waves along time, each all 64 channels
+  // loads batched across rows (slab fill, epilogue) in the 512-row tile (2 waves per SIMD, registers to spare); the
+  // 128-row tile keeps 4 waves per SIMD.  Measured: 256-row tiles at 3 waves per SIMD were 10% slower in all.
+  constexpr bool BATCH = BM >= 512;
   extern __shared__ uint4 hl[];               // slab [BM + span][8 chunks]; later the epilogue's fp32 blocks
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
@@ -272,8 +276,8 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
       }
       hl[hswz(sr, sch)] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
     };
-    if constexpr (BM < 512) {  // one slab row at a time: the small tile keeps its register budget (4 waves per SIMD)
-      for (int sr = tid >> 3; sr < srows; sr += 32) {
+    if constexpr (!BATCH) {  // one slab row at a time: keeps the register budget of 4 waves per SIMD
+      for (int sr = tid >> 3; sr < srows; sr += RPP) {
         const int in_row = slab0 + sr;
         if (in_row >= 0 && in_row < Tin && ci + 8 <= c.Cin)
           put_fast(sr, *(const float4*)(xb + (size_t)in_row * c.ldx + ci), *(const float4*)(xb + (size_t)in_row * c.ldx + ci + 4));
@@ -282,12 +286,12 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
       }
     } else {  // SU slab rows per thread and pass, all their loads in flight before the first one is used
       constexpr int SU = 4;
-      for (int sr0 = tid >> 3; sr0 < srows; sr0 += 32 * SU) {
+      for (int sr0 = tid >> 3; sr0 < srows; sr0 += RPP * SU) {
         float4 u[SU][2];
         bool fast[SU];
 #pragma unroll
         for (int x = 0; x < SU; ++x) {
-          const int sr = sr0 + 32 * x, in_row = slab0 + sr;
+          const int sr = sr0 + RPP * x, in_row = slab0 + sr;
           fast[x] = sr < srows && in_row >= 0 && in_row < Tin && ci + 8 <= c.Cin;
           if (fast[x]) {
             u[x][0] = *(const float4*)(xb + (size_t)in_row * c.ldx + ci);
@@ -296,7 +300,7 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
         }
 #pragma unroll
         for (int x = 0; x < SU; ++x) {
-          const int sr = sr0 + 32 * x;
+          const int sr = sr0 + RPP * x;
           if (sr >= srows) break;
           if (fast[x]) put_fast(sr, u[x][0], u[x][1]);
           else put_edge(sr, slab0 + sr);
@@ -347,7 +351,7 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
       }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     const int c4 = lane & 15;
-    if constexpr (BM < 512) {
+    if constexpr (!BATCH) {
 #pragma unroll
       for (int rr = 0; rr < 8; ++rr) {
         const int row = rr * 4 + (lane >> 4);
@@ -545,7 +549,7 @@ hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
   return hipGetLastError();
 }
 
-// LDS of a BM-row tile: the slab, and at least the epilogue's four 32-row x 64-channel fp32 blocks
+// LDS of a BM-row tile: the slab, and at least the epilogue's 32-row x 64-channel fp32 block per wave
 size_t conv_bf16_lds(int BM) {
   const size_t slab = (size_t)(BM + HB_MAXSPAN) * 8 * sizeof(uint4), epi = 4 * 32 * 16 * sizeof(float4);
   return slab > epi ? slab : epi;
