@@ -48,7 +48,15 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   const int nblk = gm * gn, full = (nblk / 8) * 8;
   int b = blockIdx.x;
   if (b < full) b = (b % 8) * (nblk / 8) + b / 8;
-  const int m0 = (b / gn) * BM, n0 = (b % gn) * BN;
+  // wide grids (more than 8 column tiles, e.g. qkv) walk groups of 4 row tiles column by column, so that the tiles
+  // one XCD runs at a time share 4 A row blocks and 8 W column blocks instead of all W columns of one row block
+  int mb = b / gn, nb = b % gn;
+  if (gn > 8) {
+    const int grp = b / (4 * gn), rows = min(4, gm - grp * 4), r = b - grp * 4 * gn;
+    mb = grp * 4 + r % rows;
+    nb = r / rows;
+  }
+  const int m0 = mb * BM, n0 = nb * BN;
   T t(g, m0, n0);
 
   f32x16 acc[T::TM][T::TN];
