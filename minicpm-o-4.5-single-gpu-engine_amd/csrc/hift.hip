@@ -388,6 +388,242 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
   }
 }
 
+// Small grids (a streaming window: one item of a few thousand samples) leave most CUs idle with whole-slab tiles, and
+// each tile's tap loop is a chain of weight-load latencies.  Here a workgroup of CS_WAVES waves owns 32 output rows x
+// 64 output channels and splits the (tap, 64-channel input chunk) steps over its waves: per step a lane loads 32
+// input channels of its row straight into registers (activation applied, rounded to bf16) and the 32 matching weights
+// of each of its two output-channel rows, the next step's loads issued before this step's MFMAs; the waves' 32 x 64
+// fp32 blocks are summed through LDS in wave order (deterministic) and the epilogue writes four channels per thread.
+// MFMA roles as in the small-row GEMM: the weights are the A operand (32 output channels), the activations the B
+// operand (32 output rows); both sides see the same K permutation (lane half h supplies channels h * 32 + kk * 8 ..).
+constexpr int CS_WAVES = 8;
+
+__global__ void __launch_bounds__(64 * CS_WAVES) conv_bf16_split_kernel(ConvDesc c, const bf16_t* __restrict__ wbf) {
+  __shared__ float4 red[CS_WAVES][2][4][64];  // per wave: its two 32x32 blocks in register order
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, cl = lane & 31;
+  const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
+  const int Tin = c.in_len[b], Tout = c.out_len[b];
+  const int oo = c.off_out[ph];
+  const int r_lo = oo >= 0 ? 0 : (-oo + c.s_out - 1) / c.s_out;
+  const int r_hi = Tout - 1 - oo < 0 ? -1 : (Tout - 1 - oo) / c.s_out;
+  const int r0 = r_lo + blockIdx.x * 32;
+  if (r0 > r_hi) return;  // the whole workgroup leaves together
+  const int co0 = blockIdx.y * HB_BN;
+  const float* xb = c.x + (size_t)c.in_off[b] * c.ldx;
+  const int cin_pad = (c.Cin + 63) & ~63, nch = cin_pad / 64;
+  const bf16_t* wph = wbf + ((size_t)ph * ((c.Cout + 63) & ~63) + co0) * c.taps * cin_pad;
+  const int NS = c.taps * nch;
+  const int s0 = w * NS / CS_WAVES, s1 = (w + 1) * NS / CS_WAVES;  // this wave's steps (possibly none)
+  const int r = r0 + cl;
+
+  // step s: tap j = s / nch, channels cc .. cc + 63 with cc = (s % nch) * 64; this lane's 32 of them: cc + h * 32 ..
+  auto load = [&](int st, float4 (&xv)[8], uint4 (&wv)[2][4]) {
+    const int j = st / nch, cc = (st - j * nch) * 64 + h * 32;
+    const int in_row = r + j * c.d_in + c.off_in[ph];
+    const bool rok = r <= r_hi && in_row >= 0 && in_row < Tin;
+    const float* xp = xb + (size_t)(rok ? in_row : 0) * c.ldx + cc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (rok && cc + e * 4 + 3 < c.Cin) xv[e] = *(const float4*)(xp + e * 4);
+      else {
+        float t[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t[u] = (rok && cc + e * 4 + u < c.Cin) ? xp[e * 4 + u] : 0.f;
+        xv[e] = make_float4(t[0], t[1], t[2], t[3]);
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        wv[jj][kk] = *(const uint4*)(wph + ((size_t)(jj * 32 + cl) * c.taps + j) * cin_pad + cc + kk * 8);
+  };
+  // activation (zero inputs stay zero: the padding rows and channels of the reference's zero-padded conv) and bf16
+  auto mma = [&](int st, const float4 (&xv)[8], const uint4 (&wv)[2][4], f32x16 (&acc)[2]) {
+    const int j = st / nch, cc = (st - j * nch) * 64 + h * 32;
+    const int in_row = r + j * c.d_in + c.off_in[ph];
+    const bool rok = r <= r_hi && in_row >= 0 && in_row < Tin;
+    const bool snake4 = c.pre == PRE_SNAKE && cc + 31 < c.Cin;  // the lane's 32 Snake parameters as float4s
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      float v[8] = {xv[2 * kk].x, xv[2 * kk].y, xv[2 * kk].z, xv[2 * kk].w, xv[2 * kk + 1].x, xv[2 * kk + 1].y, xv[2 * kk + 1].z, xv[2 * kk + 1].w};
+      float al[8], in[8];
+      if (snake4) {
+        const float4 a0 = *(const float4*)(c.alpha + cc + kk * 8), a1 = *(const float4*)(c.alpha + cc + kk * 8 + 4);
+        const float4 i0 = *(const float4*)(c.inv + cc + kk * 8), i1 = *(const float4*)(c.inv + cc + kk * 8 + 4);
+        al[0] = a0.x; al[1] = a0.y; al[2] = a0.z; al[3] = a0.w; al[4] = a1.x; al[5] = a1.y; al[6] = a1.z; al[7] = a1.w;
+        in[0] = i0.x; in[1] = i0.y; in[2] = i0.z; in[3] = i0.w; in[4] = i1.x; in[5] = i1.y; in[6] = i1.z; in[7] = i1.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int ci = cc + kk * 8 + e;
+          al[e] = (c.pre == PRE_SNAKE && ci < c.Cin) ? c.alpha[ci] : 0.f;
+          in[e] = (c.pre == PRE_SNAKE && ci < c.Cin) ? c.inv[ci] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool ok = rok && cc + kk * 8 + e < c.Cin;
+        v[e] = ok ? pre_fast(v[e], c.pre, c.slope, al[e], in[e]) : 0.f;
+      }
+      const uint4 xq = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) acc[jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wv[jj][kk]), as_bf16x8(xq), acc[jj], 0, 0, 0);
+    }
+  };
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[jj][i] = 0.f;
+  float4 xa[8], xb2[8];
+  uint4 wa[2][4], wb2[2][4];
+  // two register sets named at compile time: the loop runs two steps per pass
+  if (s0 < s1) load(s0, xa, wa);
+  for (int st = s0; st < s1; st += 2) {
+    if (st + 1 < s1) load(st + 1, xb2, wb2);
+    mma(st, xa, wa, acc);
+    if (st + 1 < s1) {
+      if (st + 2 < s1) load(st + 2, xa, wa);
+      mma(st + 1, xb2, wb2, acc);
+    }
+  }
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[w][jj][q][lane] = make_float4(acc[jj][4 * q], acc[jj][4 * q + 1], acc[jj][4 * q + 2], acc[jj][4 * q + 3]);
+  __syncthreads();
+
+  // one float4 (four channels of one row) per thread, summed over the waves in order
+  const int jj = tid >> 8, q = (tid >> 6) & 3, l = tid & 63;
+  float4 sum = red[0][jj][q][l];
+#pragma unroll
+  for (int x = 1; x < CS_WAVES; ++x) {
+    const float4 v = red[x][jj][q][l];
+    sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
+  }
+  // lane l of the MFMA holds output row r0 + l % 32 and channels co0 + jj * 32 + q * 8 + (l / 32) * 4 + 0..3
+  const int ro = r0 + (l & 31), cn = jj * 32 + q * 8 + (l >> 5) * 4;
+  const int ncols = min(HB_BN, c.Cout - co0);
+  if (ro > r_hi || cn >= ncols) return;
+  const size_t orow = (size_t)c.out_off[b] + (size_t)(ro * c.s_out + oo);
+  if (cn + 3 < ncols) conv_epilogue4(c, orow, co0 + cn, sum);
+  else conv_epilogue_part(c, orow, co0 + cn, ncols - cn, sum);
+}
+
+// The fp32 convolution for small grids (the f0 predictor of a streaming window: ~50 frames x 512 channels), on the
+// same plan as conv_bf16_split_kernel: 32 output rows x 64 output channels per workgroup, the (tap, 32-channel input
+// chunk) steps split over the waves, operands straight into registers with the next step's loads in flight, fp32 MFMA
+// (v_mfma_f32_32x32x2f32; lane half h supplies channels h * 16 + u of MFMA u on both sides), blocks summed in LDS in
+// wave order.
+__global__ void __launch_bounds__(64 * CS_WAVES) conv_f32_split_kernel(ConvDesc c) {
+  __shared__ float4 red[CS_WAVES][2][4][64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, cl = lane & 31;
+  const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
+  const int Tin = c.in_len[b], Tout = c.out_len[b];
+  const int oo = c.off_out[ph];
+  const int r_lo = oo >= 0 ? 0 : (-oo + c.s_out - 1) / c.s_out;
+  const int r_hi = Tout - 1 - oo < 0 ? -1 : (Tout - 1 - oo) / c.s_out;
+  const int r0 = r_lo + blockIdx.x * 32;
+  if (r0 > r_hi) return;
+  const int co0 = blockIdx.y * 64;
+  const float* xb = c.x + (size_t)c.in_off[b] * c.ldx;
+  const float* wph = c.w + (size_t)ph * c.Cout * c.taps * c.Cin;
+  const int nch = (c.Cin + 31) / 32, NS = c.taps * nch;
+  const int s0 = w * NS / CS_WAVES, s1 = (w + 1) * NS / CS_WAVES;
+  const int r = r0 + cl;
+  const bool vec = c.Cin % 4 == 0 && c.ldx % 4 == 0;  // 16-byte loads of whole 4-channel groups
+
+  // step s: tap j = s / nch, this lane's channels cc .. cc + 15 with cc = (s % nch) * 32 + h * 16, activation applied
+  auto load = [&](int st, float4 (&xv)[4], float4 (&wv)[2][4]) {
+    const int j = st / nch, cc = (st - j * nch) * 32 + h * 16;
+    const int in_row = r * c.s_in + j * c.d_in + c.off_in[ph];
+    const bool rok = r <= r_hi && in_row >= 0 && in_row < Tin;
+    const float* xp = xb + (size_t)(rok ? in_row : 0) * c.ldx + cc;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (vec && rok && cc + e * 4 + 3 < c.Cin) xv[e] = *(const float4*)(xp + e * 4);
+      else {
+        float t[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t[u] = (rok && cc + e * 4 + u < c.Cin) ? xp[e * 4 + u] : 0.f;
+        xv[e] = make_float4(t[0], t[1], t[2], t[3]);
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int co = co0 + jj * 32 + cl;
+      const float* wp = wph + ((size_t)(co < c.Cout ? co : 0) * c.taps + j) * c.Cin + cc;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (vec && co < c.Cout && cc + e * 4 + 3 < c.Cin) wv[jj][e] = *(const float4*)(wp + e * 4);
+        else {
+          float t[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) t[u] = (co < c.Cout && cc + e * 4 + u < c.Cin) ? wp[e * 4 + u] : 0.f;
+          wv[jj][e] = make_float4(t[0], t[1], t[2], t[3]);
+        }
+      }
+    }
+  };
+  auto mma = [&](int st, const float4 (&xv)[4], const float4 (&wv)[2][4], f32x16 (&acc)[2]) {
+    const int j = st / nch, cc = (st - j * nch) * 32 + h * 16;
+    const int in_row = r * c.s_in + j * c.d_in + c.off_in[ph];
+    const bool rok = r <= r_hi && in_row >= 0 && in_row < Tin;
+    const float xs[16] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w,
+                          xv[2].x, xv[2].y, xv[2].z, xv[2].w, xv[3].x, xv[3].y, xv[3].z, xv[3].w};
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int ci = cc + u;
+      const bool ok = rok && ci < c.Cin;
+      float v = xs[u];
+      if (c.pre && ok) v = pre_act(v, c.pre, c.slope, c.alpha ? c.alpha[ci] : 0.f, c.inv ? c.inv[ci] : 0.f);
+      v = ok ? v : 0.f;
+      const float4* w0 = wv[0];
+      const float4* w1 = wv[1];
+      const float a0 = (u & 3) == 0 ? w0[u >> 2].x : (u & 3) == 1 ? w0[u >> 2].y : (u & 3) == 2 ? w0[u >> 2].z : w0[u >> 2].w;
+      const float a1 = (u & 3) == 0 ? w1[u >> 2].x : (u & 3) == 1 ? w1[u >> 2].y : (u & 3) == 2 ? w1[u >> 2].z : w1[u >> 2].w;
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, v, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, v, acc[1], 0, 0, 0);
+    }
+  };
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[jj][i] = 0.f;
+  float4 xa[4], xb2[4], wa[2][4], wb2[2][4];
+  if (s0 < s1) load(s0, xa, wa);
+  for (int st = s0; st < s1; st += 2) {
+    if (st + 1 < s1) load(st + 1, xb2, wb2);
+    mma(st, xa, wa, acc);
+    if (st + 1 < s1) {
+      if (st + 2 < s1) load(st + 2, xa, wa);
+      mma(st + 1, xb2, wb2, acc);
+    }
+  }
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[w][jj][q][lane] = make_float4(acc[jj][4 * q], acc[jj][4 * q + 1], acc[jj][4 * q + 2], acc[jj][4 * q + 3]);
+  __syncthreads();
+  const int jj = tid >> 8, q = (tid >> 6) & 3, l = tid & 63;
+  float4 sum = red[0][jj][q][l];
+#pragma unroll
+  for (int x = 1; x < CS_WAVES; ++x) {
+    const float4 v = red[x][jj][q][l];
+    sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
+  }
+  const int ro = r0 + (l & 31), cn = jj * 32 + q * 8 + (l >> 5) * 4;
+  const int ncols = min(64, c.Cout - co0);
+  if (ro > r_hi || cn >= ncols) return;
+  const size_t orow = (size_t)c.out_off[b] + (size_t)(ro * c.s_out + oo);
+  if (cn + 3 < ncols) conv_epilogue4(c, orow, co0 + cn, sum);
+  else conv_epilogue_part(c, orow, co0 + cn, ncols - cn, sum);
+}
+
 // f0 = |w . x + b| per frame (one wave per frame row, Linear(C -> 1) then abs)
 __global__ void __launch_bounds__(256) f0_head_kernel(const float* x, int C, const float* w, const float* b, float* f0, int rows) {
   const int lane = threadIdx.x & 63;
@@ -544,6 +780,13 @@ inline unsigned cdiv(long long a, long long b) { return (unsigned)((a + b - 1) /
 hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
   if (c.n_items <= 0 || max_rows <= 0) return hipSuccess;
   if (c.n_phase < 1 || c.n_phase > 8) return hipErrorInvalidValue;
+  // grids that would keep fewer than half the CUs busy: 32-row tiles with the taps and channels split over the waves
+  const long tiles = (long)cdiv(max_rows, CBM) * cdiv(c.Cout, CBN) * c.n_items * c.n_phase;
+  if (tiles < 128) {
+    dim3 grid(cdiv(max_rows, 32), cdiv(c.Cout, 64), c.n_items * c.n_phase);
+    hipLaunchKernelGGL(conv_f32_split_kernel, grid, dim3(64 * CS_WAVES), 0, st, c);
+    return hipGetLastError();
+  }
   dim3 grid(cdiv(max_rows, CBM), cdiv(c.Cout, CBN), c.n_items * c.n_phase);
   hipLaunchKernelGGL(conv_f32_kernel, grid, dim3(256), 0, st, c);
   return hipGetLastError();
@@ -560,9 +803,14 @@ hipError_t conv_bf16(const ConvDesc& c, const bf16_t* wbf, int max_rows, hipStre
   if (c.n_phase < 1 || c.n_phase > 8 || c.s_in != 1 || c.ldx % 4 || c.ldy % 4) return hipErrorInvalidValue;
   const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
   if (span > HB_MAXSPAN) return hipErrorInvalidValue;
-  // 512-row tiles when there are enough of them for the chip, else 128
+  // 512-row tiles when there are enough of them for the chip, 128 when those fill at least half of it, else 32-row
+  // tiles with the taps split over the waves
   const long tiles512 = (long)cdiv(max_rows, 512) * cdiv(c.Cout, HB_BN) * c.n_items * c.n_phase;
-  if (tiles512 >= 256) {
+  const long tiles128 = (long)cdiv(max_rows, 128) * cdiv(c.Cout, HB_BN) * c.n_items * c.n_phase;
+  if (tiles128 < 128) {
+    dim3 grid(cdiv(max_rows, 32), cdiv(c.Cout, HB_BN), c.n_items * c.n_phase);
+    hipLaunchKernelGGL(conv_bf16_split_kernel, grid, dim3(64 * CS_WAVES), 0, st, c, wbf);
+  } else if (tiles512 >= 256) {
     constexpr int BM = 512;
     const size_t lds = conv_bf16_lds(BM);
     static bool attr = false;
