@@ -129,12 +129,12 @@ hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
 }  // namespace
 
 int pick_cfg(const GemmArgs& g) {
-  // 256x256 tiles (fp8: 256x128) once there are enough rows to fill them; for qkv (N = 3072) 256x128 measured faster
-  // at 12800 rows (105 us vs 114).  fc1 (N = 2048, GELU) takes 256x256 since its epilogue uses the hardware reciprocal
-  // (DiT solve 143.5 -> 142.0 ms against 128x128)
+  // 256x256 tiles (fp8: 256x128) once there are enough rows to fill them.  qkv (N = 3072) took 256x128 while its
+  // epilogue wrote 4 columns per lane (105 us vs 114 at 12800 rows); with 16-byte stores 256x256 is the faster one
+  // (DiT solve 132.1 -> 129.6 ms on the same box).  fc1 (N = 2048, GELU) takes 256x256 since its epilogue uses the
+  // hardware reciprocal (DiT solve 143.5 -> 142.0 ms against 128x128)
   if (g.M < 1024 || g.N < 256) return 0;
   if (g.w_scale) return 2;
-  if (g.N >= 3072) return 2;
   return 1;
 }
 

@@ -90,20 +90,24 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const f32x16 (&acc
   constexpr int RPI = 64 / CPR;  // slab rows per read-back instruction
   constexpr int NRB = 32 / RPI;  // read-back instructions per slab
   constexpr int RB = NRB < 8 ? NRB : 8;
-  constexpr bool WIDE = (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) && WTN % 8 == 0;
+  constexpr bool WIDE = (EPI == EPI_BF16 || EPI == EPI_GELU_BF16 || EPI == EPI_QKV) && WTN % 8 == 0;
   constexpr int CW = WTN / 8, RW = 64 / CW;  // wide: lanes per slab row, slab rows per instruction
   const int cc = WIDE ? (lane % CW) * 2 : lane % CPR;
   const Cols<EPI> cols(g, nw + cc * 4);
   const Cols<EPI> cols2(g, nw + cc * 4 + 4);  // wide: the lane's second four columns
   // EPI_QKV: this lane's part (q, k, v), column and head offset, and the LayerNorm affine of its four columns
   int qpart = 0, qcol = 0;
-  float4 qlw = make_float4(0.f, 0.f, 0.f, 0.f), qlb = qlw;
+  float4 qlw = make_float4(0.f, 0.f, 0.f, 0.f), qlb = qlw, qlw2 = qlw, qlb2 = qlw;  // wide: 8 columns
   if constexpr (EPI == EPI_QKV) {
     qpart = cols.n / g.qk.H;
     qcol = cols.n - qpart * g.qk.H;
     if (qpart < 2) {
       qlw = *(const float4*)((qpart ? g.qk.kw : g.qk.qw) + (qcol & 63));
       qlb = *(const float4*)((qpart ? g.qk.kb : g.qk.qb) + (qcol & 63));
+      if (WIDE) {
+        qlw2 = *(const float4*)((qpart ? g.qk.kw : g.qk.qw) + (qcol & 63) + 4);
+        qlb2 = *(const float4*)((qpart ? g.qk.kb : g.qk.qb) + (qcol & 63) + 4);
+      }
     }
   }
 #pragma unroll
@@ -120,7 +124,57 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const f32x16 (&acc
         }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if constexpr (WIDE) {
+    if constexpr (WIDE && EPI == EPI_QKV) {
+      // the 8 lanes holding one row's 64 columns of one head (heads are 64-aligned in the tile): bias, bf16 rounding,
+      // LayerNorm + affine for q and k (sums over the 8 lanes), q to its row, k and v to the token's key slot; the
+      // batch's slot ids are loaded before its first store
+      constexpr int NB = 32 / RW;
+      const QkvOut& o = g.qk;
+      float4 a0[NB], a1[NB];
+      int slot[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int row = b * RW + lane / CW;
+        const int m = mw + i * 32 + row;
+        a0[b] = st[row * CPR + (cc ^ (row & (CPR - 1)))];
+        a1[b] = st[row * CPR + ((cc + 1) ^ (row & (CPR - 1)))];
+        slot[b] = qpart > 0 && m < g.M ? o.slots[m] : 0;
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int m = mw + i * 32 + b * RW + lane / CW;
+        float y[8] = {a0[b].x * cols.wsc.x + cols.bias.x, a0[b].y * cols.wsc.y + cols.bias.y,
+                      a0[b].z * cols.wsc.z + cols.bias.z, a0[b].w * cols.wsc.w + cols.bias.w,
+                      a1[b].x * cols2.wsc.x + cols2.bias.x, a1[b].y * cols2.wsc.y + cols2.bias.y,
+                      a1[b].z * cols2.wsc.z + cols2.bias.z, a1[b].w * cols2.wsc.w + cols2.bias.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = bf2f(f2bf(y[e]));  // the projection is rounded to bf16 first
+        if (qpart < 2) {
+          float sm = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sm += y[e];
+          sm += __shfl_xor(sm, 1, 64);
+          sm += __shfl_xor(sm, 2, 64);
+          sm += __shfl_xor(sm, 4, 64);
+          const float mean = sm * (1.0f / 64.0f);
+          float q = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) { y[e] -= mean; q += y[e] * y[e]; }
+          q += __shfl_xor(q, 1, 64);
+          q += __shfl_xor(q, 2, 64);
+          q += __shfl_xor(q, 4, 64);
+          const float rstd = rsqrtf(q * (1.0f / 64.0f) + o.eps);
+          const float lw[8] = {qlw.x, qlw.y, qlw.z, qlw.w, qlw2.x, qlw2.y, qlw2.z, qlw2.w};
+          const float lb[8] = {qlb.x, qlb.y, qlb.z, qlb.w, qlb2.x, qlb2.y, qlb2.z, qlb2.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) y[e] = y[e] * rstd * lw[e] + lb[e];
+        }
+        if (m < g.M) {
+          bf16_t* dst = qpart == 0 ? o.q_out + (size_t)m * o.H : (qpart == 1 ? o.k_pool : o.v_pool) + (size_t)slot[b] * o.H;
+          *(uint4*)(dst + qcol) = make_uint4(pack2(y[0], y[1]), pack2(y[2], y[3]), pack2(y[4], y[5]), pack2(y[6], y[7]));
+        }
+      }
+    } else if constexpr (WIDE) {
 #pragma unroll
       for (int b = 0; b < 32 / RW; ++b) {
         const int row = b * RW + lane / CW;
