@@ -2,6 +2,7 @@
 // capture.  No allocation happens in any compute call: the caller passes a workspace of t2w_dit_workspace_bytes().
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -138,6 +139,40 @@ GemmArgs gemm8(const uint8_t* A, int lda, const int* a_src, const uint8_t* as, c
   return g;
 }
 
+// K splits of the deferred GEMMs of a call of N tokens (0: no deferral): enough workgroups to occupy the 256 CUs, at
+// most 4 (the row kernels' limit), and the sums must fit the partial area.  Taken only when every deferred GEMM fits the
+// small-row kernel.
+int defer_splits(const t2w_dit_dims& d, int N, const Work& w) {
+  const int H = d.hidden;
+  if (N > GEMM_SMALL_MAX_M || !w.part) return 0;
+  const int tiles = ((N + 31) / 32) * ((H + 31) / 32);
+  const int S = std::min(4, 256 / tiles);
+  if (S < 2 || (size_t)S * N * H * 4 > w.part_bytes) return 0;
+  GemmArgs g{};
+  g.M = N; g.N = H; g.lda = H; g.ldb = H; g.ldc = H; g.splits = S;
+  for (int K : {H, 3 * H, d.ffn}) {
+    g.K = K;
+    g.ldb = K;
+    g.lda = K == 3 * H ? H : K;
+    g.a_src = K == 3 * H ? (const int*)&w : nullptr;  // taps mode (only the pointer's presence is checked)
+    g.tapC = H;
+    if (!gemm_small_fits(g, EPI_PART)) return 0;
+  }
+  return S;
+}
+
+// g (its bias and gate excepted) as a K-split GEMM into the partial area; the returned Pend finishes it
+Pend gemm_deferred(GemmArgs g, int S, const Work& w, hipStream_t st, hipError_t* err) {
+  Pend p;
+  p.part = w.part; p.S = S; p.stride = (size_t)g.M * g.N; p.ld = g.N; p.bias = g.bias; p.gate = g.gate;
+  g.C = w.part;
+  g.ldc = g.N;
+  g.splits = S;
+  g.c_split = p.stride;
+  *err = gemm_small(g, EPI_PART, st);
+  return p;
+}
+
 // One estimator evaluation from w.a_in (bf16 [N, 4 mel]) to w.dphi (fp32 [N, mel]) at Euler step `step`.
 int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int step, const float* mods,
                   const float* fmods, float* dphi, hipStream_t st) {
@@ -146,6 +181,11 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
   T2W_CHECK(gemm_bf16(gemm_args(w.a_in, 4 * M, nullptr, m->g.in_w, m->g.in_b, nullptr, w.h, H, N, H, 4 * M, &w), EPI_F32, st), "in_proj");
   const long long cstride = (long long)d.steps * D * 4 * H;
   const bool f8 = a->fp8 != 0;
+  // Calls of few tokens: the gated-residual GEMMs and conv1 split K over several workgroups per tile and the row
+  // kernel that reads their result next finishes their epilogue (pend: the result it has to finish).
+  const int S = f8 ? 0 : defer_splits(d, N, w);
+  Pend pend;
+  hipError_t perr = hipSuccess;
   for (int b = 0; b < D; ++b) {
     const t2w_dit_block& k = m->blocks[b];
     const t2w_dit_block_fp8* k8 = f8 ? &m->blocks8[b] : nullptr;
@@ -160,7 +200,8 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
       T2W_CHECK(ln_mod_mx8(w.h, sh_a, sc_a, d.eps_block, w.a8, w.a8s, N, H, st), "ln_mod msa");
       gq = gemm8(w.a8, H, nullptr, w.a8s, k8->qkv_w8, k8->qkv_ws, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H);
     } else {
-      T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st), "ln_mod msa");
+      T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st, pend), "ln_mod msa");
+      pend = Pend();
       gq = gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H, &w);
     }
     gq.qk = QkvOut{w.q, kp, vp, a->new_slot, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, H};
@@ -179,8 +220,12 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     T2W_CHECK(attention(at, st), "attention");
     if (f8)
       T2W_CHECK(gemm_bf16(gemm8(w.o8, H, nullptr, w.o8s, k8->proj_w8, k8->proj_ws, k.proj_b, g_a, w.h, H, N, H, H), EPI_RESID_F32, st), "proj");
-    else
+    else if (S) {
+      pend = gemm_deferred(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), S, w, st, &perr);
+      T2W_CHECK(perr, "proj");
+    } else {
       T2W_CHECK(gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F32, st), "proj");
+    }
     ConvPlace cp;
     cp.P = w.P; cp.tok_row = a->tok_row; cp.tok_pos = a->tok_pos; cp.row_start = a->row_start; cp.row_len = a->row_len;
     cp.rd = a->conv_rd; cp.wr = a->conv_wr; cp.cache_stride = cstride; cp.N = N; cp.R = R;
@@ -188,18 +233,28 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     bf16_t* cbase = (bf16_t*)a->conv_pool + ((size_t)(step * D + b) * 2) * 2 * H;
     cp.cache_base = cbase;
     cp.cache_out_base = cbase;
-    T2W_CHECK(ln_mod_conv(w.h, sh_c, sc_c, d.eps_block, cp, H, st), "ln_mod_conv");
-    if (f8)
+    T2W_CHECK(ln_mod_conv(w.h, sh_c, sc_c, d.eps_block, cp, H, st, pend), "ln_mod_conv");
+    pend = Pend();
+    if (f8) {
       T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c1_w8, k8->c1_ws, k.c1_b, nullptr, w.ao, H, N, H, 3 * H), EPI_BF16, st), "conv1");
-    else
+    } else if (S) {
+      pend = gemm_deferred(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), S, w, st, &perr);
+      T2W_CHECK(perr, "conv1");
+    } else {
       T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), EPI_BF16, st), "conv1");
+    }
     cp.cache_base = cbase + 2 * H;
     cp.cache_out_base = cbase + 2 * H;
-    T2W_CHECK(ln_mish_conv(w.ao, k.cln_w, k.cln_b, d.eps_conv, cp, H, st), "ln_mish_conv");
-    if (f8)
+    T2W_CHECK(ln_mish_conv(w.ao, k.cln_w, k.cln_b, d.eps_conv, cp, H, st, pend), "ln_mish_conv");
+    pend = Pend();
+    if (f8) {
       T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c2_w8, k8->c2_ws, k.c2_b, g_c, w.h, H, N, H, 3 * H), EPI_RESID_F32, st), "conv2");
-    else
+    } else if (S) {
+      pend = gemm_deferred(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), S, w, st, &perr);
+      T2W_CHECK(perr, "conv2");
+    } else {
       T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), EPI_RESID_F32, st), "conv2");
+    }
     if (f8) {
       T2W_CHECK(ln_mod_mx8(w.h, sh_m, sc_m, d.eps_block, w.a8, w.a8s, N, H, st), "ln_mod mlp");
       GemmArgs g1 = gemm8(w.a8, H, nullptr, w.a8s, k8->fc1_w8, k8->fc1_ws, k.fc1_b, nullptr, w.b8, F, N, F, H);
@@ -208,12 +263,18 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
       T2W_CHECK(gemm_bf16(g1, EPI_GELU_MX8, st), "fc1");
       T2W_CHECK(gemm_bf16(gemm8(w.b8, F, nullptr, w.b8s, k8->fc2_w8, k8->fc2_ws, k.fc2_b, g_m, w.h, H, N, H, F), EPI_RESID_F32, st), "fc2");
     } else {
-      T2W_CHECK(ln_mod(w.h, sh_m, sc_m, d.eps_block, w.abuf, N, H, st), "ln_mod mlp");
+      T2W_CHECK(ln_mod(w.h, sh_m, sc_m, d.eps_block, w.abuf, N, H, st, pend), "ln_mod mlp");
+      pend = Pend();
       T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.fc1_w, k.fc1_b, nullptr, w.big, F, N, F, H, &w), EPI_GELU_BF16, st), "fc1");
-      T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F32, st), "fc2");
+      if (S) {
+        pend = gemm_deferred(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), S, w, st, &perr);
+        T2W_CHECK(perr, "fc2");
+      } else {
+        T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F32, st), "fc2");
+      }
     }
   }
-  T2W_CHECK(ln_mod(w.h, fmods, fmods + H, d.eps_final, w.abuf, N, H, st), "final norm");
+  T2W_CHECK(ln_mod(w.h, fmods, fmods + H, d.eps_final, w.abuf, N, H, st, pend), "final norm");
   T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, m->g.out_w, m->g.out_b, nullptr, dphi, M, N, M, H, &w), EPI_F32, st), "final linear");
   return 0;
 }
@@ -396,7 +457,7 @@ int t2w_gemm_fp8(const void* A, int lda, const int* a_src, const void* a_scale, 
 }
 
 int t2w_ln_mod(const float* h, const float* shift, const float* scale1, float eps, void* out, int N, int H, void* stream) {
-  T2W_CHECK(ln_mod(h, shift, scale1, eps, (bf16_t*)out, N, H, (hipStream_t)stream), "ln_mod");
+  T2W_CHECK(ln_mod(const_cast<float*>(h), shift, scale1, eps, (bf16_t*)out, N, H, (hipStream_t)stream), "ln_mod");  // h only read
   return 0;
 }
 

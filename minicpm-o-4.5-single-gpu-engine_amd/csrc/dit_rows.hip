@@ -60,6 +60,49 @@ __device__ __forceinline__ void row_load_f32(const float* row, int lane, float (
     }
 }
 
+template <int VPL, int G>
+__device__ __forceinline__ void row_store_f32(float* row, int lane, const float (&v)[VPL]) {
+#pragma unroll
+  for (int k = 0; k < VPL / G; ++k)
+#pragma unroll
+    for (int j = 0; j < G / 4; ++j) {
+      const float* x = v + k * G + 4 * j;
+      *(float4*)(row + row_col<G>(k, lane) + 4 * j) = make_float4(x[0], x[1], x[2], x[3]);
+    }
+}
+
+// The pending GEMM's value of row n (sum of its K splits in split order, then + bias), G-grouped like row_load_f32;
+// all splits' loads are issued before the first add (at most 4 splits).
+template <int VPL, int G>
+__device__ __forceinline__ void pend_value(const Pend& pd, int n, int lane, float (&p)[VPL]) {
+  float t[3][VPL], b[VPL];
+  const float* r = pd.part + (size_t)n * pd.ld;
+  row_load_f32<VPL, G>(r, lane, p);
+#pragma unroll
+  for (int s = 1; s < 4; ++s)
+    if (s < pd.S) row_load_f32<VPL, G>(r + s * pd.stride, lane, t[s - 1]);
+  row_load_f32<VPL, G>(pd.bias, lane, b);
+#pragma unroll
+  for (int s = 1; s < 4; ++s)
+    if (s < pd.S) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) p[i] += t[s - 1][i];
+    }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) p[i] += b[i];
+}
+
+// h row n (in v) += gate * pending value, stored back to h (the gated residual epilogue of the GEMM, in its order)
+template <int VPL, int G>
+__device__ __forceinline__ void pend_resid(const Pend& pd, float* hrow, int n, int lane, float (&v)[VPL]) {
+  float p[VPL], gt[VPL];
+  pend_value<VPL, G>(pd, n, lane, p);
+  row_load_f32<VPL, G>(pd.gate, lane, gt);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) v[i] += gt[i] * p[i];
+  row_store_f32<VPL, G>(hrow, lane, v);
+}
+
 // raw bf16 words of a row (G / 2 per group)
 template <int VPL, int G>
 __device__ __forceinline__ void row_load_words(const bf16_t* row, int lane, uint32_t (&w)[VPL / 2]) {
@@ -133,13 +176,14 @@ __device__ __forceinline__ void normalize(float (&v)[VPL], int H, float eps) {
 
 // out: bf16 [N, H]; or, with q non-null, MX fp8 codes q [N, H] and block scales qs [N, H / 32]
 template <int VPL>
-__global__ void __launch_bounds__(256) ln_mod_kernel(const float* h, const float* shift, const float* scale1, float eps,
-                                                     bf16_t* out, uint8_t* q, uint8_t* qs, int N, int H) {
+__global__ void __launch_bounds__(256) ln_mod_kernel(float* h, const float* shift, const float* scale1, float eps,
+                                                     bf16_t* out, uint8_t* q, uint8_t* qs, int N, int H, Pend pd) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   float v[VPL], sc[VPL], sh[VPL];
   row_load_f32<VPL, 4>(h + (size_t)n * H, lane, v);
+  if (pd.part) pend_resid<VPL, 4>(pd, h + (size_t)n * H, n, lane, v);
   normalize<VPL>(v, H, eps);
   row_load_f32<VPL, 4>(scale1, lane, sc);
   row_load_f32<VPL, 4>(shift, lane, sh);
@@ -195,13 +239,14 @@ __device__ __forceinline__ void place_row(const ConvPlace& cp, int r, int H, int
 }
 
 template <int VPL>
-__global__ void __launch_bounds__(256) ln_mod_conv_kernel(const float* h, const float* shift, const float* scale1, float eps,
-                                                          ConvPlace cp, int H) {
+__global__ void __launch_bounds__(256) ln_mod_conv_kernel(float* h, const float* shift, const float* scale1, float eps,
+                                                          ConvPlace cp, int H, Pend pd) {
   const int lane = threadIdx.x & 63;
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w < cp.N) {
     float v[VPL], sc[VPL], sh[VPL];
     row_load_f32<VPL, 4>(h + (size_t)w * H, lane, v);
+    if (pd.part) pend_resid<VPL, 4>(pd, h + (size_t)w * H, w, lane, v);
     normalize<VPL>(v, H, eps);
     row_load_f32<VPL, 4>(scale1, lane, sc);
     row_load_f32<VPL, 4>(shift, lane, sh);
@@ -217,15 +262,21 @@ __global__ void __launch_bounds__(256) ln_mod_conv_kernel(const float* h, const 
 
 template <int VPL>
 __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, const float* lw, const float* lb, float eps,
-                                                           ConvPlace cp, int H) {
+                                                           ConvPlace cp, int H, Pend pd) {
   const int lane = threadIdx.x & 63;
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w < cp.N) {
     constexpr int G = VPL >= 8 ? 8 : 4;  // the row comes in as bf16
     float v[VPL], a[VPL], b[VPL];
-    uint32_t wv[VPL / 2];
-    row_load_words<VPL, G>(y + (size_t)w * H, lane, wv);
-    words_to_f32<VPL>(wv, v);
+    if (pd.part) {  // the pending conv GEMM's value, rounded to bf16 as its own epilogue would
+      pend_value<VPL, G>(pd, w, lane, v);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) v[i] = bf2f(f2bf(v[i]));
+    } else {
+      uint32_t wv[VPL / 2];
+      row_load_words<VPL, G>(y + (size_t)w * H, lane, wv);
+      words_to_f32<VPL>(wv, v);
+    }
     normalize<VPL>(v, H, eps);
     row_load_f32<VPL, G>(lw, lane, a);
     row_load_f32<VPL, G>(lb, lane, b);
@@ -393,28 +444,35 @@ inline unsigned blocks_for(long long n, int per) { return (unsigned)((n + per - 
     default: return hipErrorInvalidValue;  \
   }
 
-hipError_t ln_mod(const float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H, hipStream_t st) {
+hipError_t ln_mod(float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H, hipStream_t st,
+                  const Pend& pd) {
   if (N <= 0) return hipSuccess;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, 4)), dim3(256), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H));
+  if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, 4)), dim3(256), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H, pd));
   return hipGetLastError();
 }
 
 hipError_t ln_mod_mx8(const float* h, const float* shift, const float* scale1, float eps, uint8_t* q, uint8_t* qs, int N,
                       int H, hipStream_t st) {
   if (N <= 0) return hipSuccess;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, 4)), dim3(256), 0, st, h, shift, scale1, eps, nullptr, q, qs, N, H));
+  // nothing pending: h is only read
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, 4)), dim3(256), 0, st, const_cast<float*>(h), shift, scale1, eps, nullptr, q, qs, N, H, Pend()));
   return hipGetLastError();
 }
 
-hipError_t ln_mod_conv(const float* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H, hipStream_t st) {
+hipError_t ln_mod_conv(float* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H, hipStream_t st,
+                       const Pend& pd) {
   if (cp.N + cp.R <= 0) return hipSuccess;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_conv_kernel<V>, dim3(blocks_for(cp.N + cp.R, 4)), dim3(256), 0, st, h, shift, scale1, eps, cp, H));
+  if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_conv_kernel<V>, dim3(blocks_for(cp.N + cp.R, 4)), dim3(256), 0, st, h, shift, scale1, eps, cp, H, pd));
   return hipGetLastError();
 }
 
-hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float eps, const ConvPlace& cp, int H, hipStream_t st) {
+hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float eps, const ConvPlace& cp, int H, hipStream_t st,
+                        const Pend& pd) {
   if (cp.N + cp.R <= 0) return hipSuccess;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mish_conv_kernel<V>, dim3(blocks_for(cp.N + cp.R, 4)), dim3(256), 0, st, y, w, b, eps, cp, H));
+  if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mish_conv_kernel<V>, dim3(blocks_for(cp.N + cp.R, 4)), dim3(256), 0, st, y, w, b, eps, cp, H, pd));
   return hipGetLastError();
 }
 

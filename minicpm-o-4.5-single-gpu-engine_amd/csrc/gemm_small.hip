@@ -8,6 +8,11 @@
 // 32x32 fp32 block in LDS.  After one barrier the block is summed over the waves in wave order (deterministic) and the
 // epilogue (bias, GELU, gated fp32 residual) writes four consecutive columns per lane.
 //
+// A workgroup moves its W and activation rows through one CU, and a CU's load throughput (not HBM) is what bounds
+// these calls: ~100 rows x K = 3072 (conv taps) is 384 KB per workgroup on 128 CUs.  EPI_PART therefore also splits K
+// over g.splits workgroups per tile (grid z), so that all CUs share the bytes, and leaves the sum of the splits, the
+// bias and the gated residual to the row kernel that reads the result next (Pend).
+//
 // MFMA roles: W is the A operand (its 32 rows are output columns n0 ..), the activations the B operand (32 token
 // rows), so a lane's four consecutive accumulator registers are four consecutive output columns of one token.
 #include "common.h"
@@ -25,8 +30,10 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
   __shared__ float4 red[GS_WAVES][4][64];  // per wave: its 32x32 block in register order (quad q, lane)
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
   const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
-  const int KS = g.K / 64;
-  const int s0 = w * KS / GS_WAVES, s1 = (w + 1) * KS / GS_WAVES;  // this wave's steps (possibly none)
+  const int KT = g.K / 64, z = blockIdx.z, S = gridDim.z;
+  const int kb = z * KT / S, KS = (z + 1) * KT / S - kb;  // this workgroup's K split
+  const int nw = blockDim.x >> 6;
+  const int s0 = kb + w * KS / nw, s1 = kb + (w + 1) * KS / nw;  // this wave's steps (possibly none)
   const bf16_t* wrow = g.B + (size_t)min(n0 + c, g.N - 1) * g.ldb + h * 32;
   const int m = min(m0 + c, g.M - 1);  // rows past M load row M - 1; their results are never stored
   const bf16_t* arow = g.A + (size_t)(TAPS ? g.a_src[m] : m) * g.lda + h * 32;
@@ -66,7 +73,7 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
   const int q = tid >> 6, l = tid & 63;
   float4 a = red[0][q][l];
 #pragma unroll
-  for (int x = 1; x < GS_WAVES; ++x) {
+  for (int x = 1; x < nw; ++x) {
     const float4 b = red[x][q][l];
     a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
   }
@@ -74,7 +81,12 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
   const int mo = m0 + (l & 31), n = n0 + q * 8 + (l >> 5) * 4;
   if (mo >= g.M || n >= g.N) return;
   const float v[4] = {a.x, a.y, a.z, a.w};
+  float* part = (float*)g.C + (size_t)z * g.c_split;  // EPI_PART: this split's sums
   if (n + 3 < g.N) {
+    if (EPI == EPI_PART) {
+      *(float4*)(part + (size_t)mo * g.ldc + n) = a;
+      return;
+    }
     const float4 b = *(const float4*)(g.bias + n);
     float o[4] = {v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
     const size_t off = (size_t)mo * g.ldc + n;
@@ -95,8 +107,9 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
     return;
   }
   for (int e = 0; e < 4 && n + e < g.N; ++e) {  // the last columns of an N that is not a multiple of 4
-    float x = v[e] + g.bias[n + e];
+    float x = v[e] + (EPI == EPI_PART ? 0.f : g.bias[n + e]);
     const size_t off = (size_t)mo * g.ldc + n + e;
+    if (EPI == EPI_PART) { part[off] = v[e]; continue; }
     if (EPI == EPI_GELU_BF16) x = gelu_tanh(x);
     if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[off] = f2bf(x);
     else if (EPI == EPI_RESID_F32) ((float*)g.C)[off] += g.gate[n + e] * x;
@@ -182,9 +195,12 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_qkv_kernel(GemmArgs 
 
 template <int EPI>
 hipError_t launch_small(const GemmArgs& g, hipStream_t st) {
-  const dim3 grid((g.N + 31) / 32, (g.M + 31) / 32);
-  if (g.a_src) hipLaunchKernelGGL((gemm_small_kernel<true, EPI>), grid, dim3(64 * GS_WAVES), 0, st, g);
-  else hipLaunchKernelGGL((gemm_small_kernel<false, EPI>), grid, dim3(64 * GS_WAVES), 0, st, g);
+  const int S = EPI == EPI_PART ? g.splits : 1;
+  // waves per workgroup: one per 64-K step up to 16 (at least the 4 that run the epilogue)
+  const int nwv = max(4, min(GS_WAVES, (g.K / 64) / S));
+  const dim3 grid((g.N + 31) / 32, (g.M + 31) / 32, S);
+  if (g.a_src) hipLaunchKernelGGL((gemm_small_kernel<true, EPI>), grid, dim3(64 * nwv), 0, st, g);
+  else hipLaunchKernelGGL((gemm_small_kernel<false, EPI>), grid, dim3(64 * nwv), 0, st, g);
   return hipGetLastError();
 }
 
@@ -194,7 +210,8 @@ bool gemm_small_fits(const GemmArgs& g, int epi) {
   if (epi == EPI_QKV)
     return g.M > 0 && g.M <= GEMM_SMALL_MAX_M && !g.w_scale && !g.a_src && g.K % 64 == 0 && g.K <= GS_WAVES * 64 &&
            g.qk.H % 64 == 0 && g.N == 3 * g.qk.H && g.lda % 8 == 0 && g.ldb % 8 == 0;
-  return g.M > 0 && g.M <= GEMM_SMALL_MAX_M && !g.w_scale && epi <= EPI_F32 && g.K % 64 == 0 &&
+  if (epi == EPI_PART && (g.splits < 1 || g.splits > 4 || g.splits > g.K / 64)) return false;
+  return g.M > 0 && g.M <= GEMM_SMALL_MAX_M && !g.w_scale && (epi <= EPI_F32 || epi == EPI_PART) && g.K % 64 == 0 &&
          g.K <= GS_WAVES * GS_MAXSTEPS * 64 && g.lda % 8 == 0 && g.ldb % 8 == 0 && g.ldc % 4 == 0 &&
          (!g.a_src || g.tapC % 64 == 0);
 }
@@ -206,6 +223,7 @@ hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st) {
     case EPI_GELU_BF16: return launch_small<EPI_GELU_BF16>(g, st);
     case EPI_RESID_F32: return launch_small<EPI_RESID_F32>(g, st);
     case EPI_F32: return launch_small<EPI_F32>(g, st);
+    case EPI_PART: return launch_small<EPI_PART>(g, st);
     case EPI_QKV:
       hipLaunchKernelGGL(gemm_small_qkv_kernel, dim3(g.N / 64, (g.M + 31) / 32), dim3(64 * GS_WAVES), 0, st, g);
       return hipGetLastError();

@@ -11,7 +11,9 @@ typedef uint16_t bf16_t;
 // EPI_GELU_MX8: GELU, then MX fp8 codes to C (bytes, ldc) and block scales to c_scale (N % 32 == 0)
 // EPI_QKV: the attention projection (N = 3 H): q and k rounded to bf16, per-head LayerNorm + affine, q to its token
 // row of q_out, k and v to the token's key slot of the pools (fields qk.*); tile path only
-enum Epi { EPI_BF16 = 0, EPI_GELU_BF16 = 1, EPI_RESID_F32 = 2, EPI_F32 = 3, EPI_GELU_MX8 = 4, EPI_QKV = 5 };
+// EPI_PART (small-row GEMM only): K split over `splits` workgroups per tile, split z writes its fp32 sum without bias
+// to C + z * c_split (rows ldc apart); a row kernel that takes the sums as a Pend finishes the GEMM's epilogue
+enum Epi { EPI_BF16 = 0, EPI_GELU_BF16 = 1, EPI_RESID_F32 = 2, EPI_F32 = 3, EPI_GELU_MX8 = 4, EPI_QKV = 5, EPI_PART = 6 };
 
 struct QkvOut {
   bf16_t* q_out;        // [M, H]
@@ -45,6 +47,19 @@ struct GemmArgs {
   uint8_t* c_scale;    // EPI_GELU_MX8: output block scales c_scale[m * c_sld + n / 32]
   int c_sld;
   QkvOut qk;           // EPI_QKV
+  int splits;          // EPI_PART: K splits (1..4)
+  size_t c_split;      // EPI_PART: elements between the splits' sums
+};
+
+// K-split sums of a GEMM whose epilogue is left to the next row kernel (EPI_PART): the GEMM's value at (n, c) is
+// sum_s part[s * stride + n * ld + c] + bias[c]; with gate non-null it is a gated residual, h += gate * value.
+struct Pend {
+  const float* part = nullptr;  // null: nothing pending
+  int S = 0;
+  size_t stride = 0;
+  int ld = 0;
+  const float* bias = nullptr;
+  const float* gate = nullptr;
 };
 
 // cfg < 0: by shape (split-K through g.ws when a tile grid would be too small to fill the chip)
@@ -52,8 +67,9 @@ hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg = -1);
 bool gemm_splits(const GemmArgs& g);  // whether gemm_bf16 (cfg < 0) takes the split-K path for g
 
 // One-kernel GEMM for calls of at most GEMM_SMALL_MAX_M rows (K split over the waves of a workgroup, reduced in LDS):
-// plain epilogues (EPI_BF16 .. EPI_F32; K % 64 == 0, K <= 3072, ldc % 4 == 0) and EPI_QKV (dense A, K <= 1024,
-// N = 3 qk.H, qk.H % 64 == 0).  gemm_bf16 (cfg < 0) takes it whenever it fits.
+// plain epilogues (EPI_BF16 .. EPI_F32; K % 64 == 0, K <= 3072, ldc % 4 == 0), EPI_PART (the same, K also split over
+// g.splits workgroups) and EPI_QKV (dense A, K <= 1024, N = 3 qk.H, qk.H % 64 == 0).  gemm_bf16 (cfg < 0) takes it
+// whenever it fits (EPI_PART only through gemm_small).
 constexpr int GEMM_SMALL_MAX_M = 128;
 bool gemm_small_fits(const GemmArgs& g, int epi);
 hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st);
@@ -75,8 +91,10 @@ hipError_t quant_mx8(const bf16_t* x, int ldx, int M, int K, uint8_t* q, int ldq
 hipError_t gemm_splitk(const GemmArgs& g, int epi, const SplitPlan& p, float* part, hipStream_t st);
 
 // Per-token row kernels of the DiT block (H = hidden, one wave per token).
-hipError_t ln_mod(const float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H,
-                  hipStream_t st);
+// With pd.part set they first finish a pending gated residual (h updated in place) or, for ln_mish_conv, take the
+// pending GEMM's bf16-rounded value as their input row instead of y.
+hipError_t ln_mod(float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H,
+                  hipStream_t st, const Pend& pd = Pend());
 // ln_mod with MX fp8 output: codes q [N, H], block scales qs [N, H / 32]
 hipError_t ln_mod_mx8(const float* h, const float* shift, const float* scale1, float eps, uint8_t* q, uint8_t* qs, int N,
                       int H, hipStream_t st);
@@ -97,10 +115,10 @@ struct ConvPlace {   // where the normed frames of a causal conv go (the padded 
   uint8_t* P8s = nullptr;    // and its block scales [N + 2 R, H / 32]
 };
 
-hipError_t ln_mod_conv(const float* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H,
-                       hipStream_t st);
+hipError_t ln_mod_conv(float* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H,
+                       hipStream_t st, const Pend& pd = Pend());
 hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float eps, const ConvPlace& cp, int H,
-                        hipStream_t st);
+                        hipStream_t st, const Pend& pd = Pend());
 hipError_t qk_norm_scatter(const bf16_t* qkv, const float* qw, const float* qb, const float* kw, const float* kb,
                            float eps, bf16_t* q_out, bf16_t* k_pool, bf16_t* v_pool, const int* slots, int N, int heads,
                            hipStream_t st);

@@ -196,8 +196,8 @@ def estimator_chunk(W, d: DiTDims, x, mu, temb, spks, cond, cnn_cache, att_cache
 
 @dataclass
 class Cache:
-    """One request's estimator caches: att [steps, depth, 2 (cond, uncond), nh, L, 2 dk] in the reference order
-    (newest window first), cnn [steps, depth, 2, 2H, 2], and the trim length ``keep`` (prompt mel frames)."""
+    """One request's estimator caches: att [steps, 2 (cond, uncond), depth, nh, L, 2 dk] in the reference order
+    (newest window first), cnn [steps, 2, depth, 2H, 2], and the trim length ``keep`` (prompt mel frames)."""
     att: torch.Tensor
     cnn: torch.Tensor
     keep: int = 0
@@ -208,7 +208,9 @@ class Cache:
 
 
 def empty_cache(d: DiTDims, keep: int = 0) -> Cache:
-    return Cache(torch.zeros(d.steps, d.depth, 2, d.heads, 0, 2 * d.head_dim), torch.zeros(d.steps, d.depth, 2, 2 * d.hidden, 2), keep)
+    """Per Euler step, per CFG row (2), per block: keys / values [heads, 0, 2 dk] and conv frames [2 H, 2] (the layout
+    ``solve`` stores)."""
+    return Cache(torch.zeros(d.steps, 2, d.depth, d.heads, 0, 2 * d.head_dim), torch.zeros(d.steps, 2, d.depth, 2 * d.hidden, 2), keep)
 
 
 def trim_order(order: list, keep: int) -> list:

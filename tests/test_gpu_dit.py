@@ -66,14 +66,15 @@ def test_estimator_forward_3000_tokens(dev, full):
     assert e < TOL
 
 
-def _stream_case(W, model, graphs: bool, buckets: bool = False, outs: list | None = None, stats: dict | None = None):
+def _stream_case(W, model, graphs: bool, buckets: bool = False, outs: list | None = None, stats: dict | None = None,
+                 prompts=(70, 40)):
     d = od.dims_of(W, steps=TINY.steps)
     fd = FastDiT(model, n_slots=4096, max_streams=4, use_graphs=graphs, buckets=buckets)
     g = torch.Generator().manual_seed(1)
-    prompts = [70, 40]
+    n = len(prompts)
     caches = [fd.new_cache(keep=p) for p in prompts]
     refc = [od.empty_cache(d, keep=p) for p in prompts]
-    spks = torch.randn(2, 80, generator=g)
+    spks = torch.randn(n, 80, generator=g)
     mus = [torch.randn(80, p, generator=g) for p in prompts]
     conds = [torch.randn(80, p, generator=g) for p in prompts]
     errs = []
@@ -83,8 +84,8 @@ def _stream_case(W, model, graphs: bool, buckets: bool = False, outs: list | Non
     if outs is not None:
         outs += [a.cpu() for a in got]
     for w in range(5):
-        Ts = [50, 16 if w == 0 else 50]
-        keep = [w < 4, True]
+        Ts = [50, 16 if w == 0 else 50][:n] if n > 1 else [16 if w == 0 else 50]
+        keep = [w < 4, True][:n]
         if w == 4:
             Ts[0] = 34
         mus = [torch.randn(80, t, generator=g) for t in Ts]
@@ -108,6 +109,45 @@ def test_solve_streaming_tiny(dev, tiny):
     W, model = tiny
     errs = _stream_case(W, model, graphs=False)
     print("stream rel-L2 per call", errs)
+    assert max(errs) < TOL
+
+
+def test_solve_streaming_one_request(dev, tiny):
+    """One request per call (120-token setup, then 32- to 100-token windows): every call has at most 128 tokens, so the
+    gated-residual and conv GEMMs split K over four workgroups per tile and the row kernels finish their epilogues."""
+    W, model = tiny
+    errs = _stream_case(W, model, graphs=False, prompts=(60,))
+    print("one-request stream rel-L2 per call", errs)
+    assert max(errs) < TOL
+
+
+def test_solve_streaming_one_request_graphs_equal_eager(dev, tiny):
+    """The deferred GEMM epilogues replay bit for bit under graphs."""
+    W, model = tiny
+    assert _stream_case(W, model, graphs=False, prompts=(60,)) == _stream_case(W, model, graphs=True, prompts=(60,))
+
+
+def test_solve_streaming_full_size_window(dev, full):
+    """Full model size, one stream: a 100-frame prompt setup (200 tokens), then windows of 50 and 16 frames (100 and
+    32 tokens: two and four K splits of the deferred GEMMs), each against the oracle."""
+    W, model = full
+    d = od.dims_of(W)
+    fd = FastDiT(model, n_slots=4096, max_streams=2)
+    g = torch.Generator().manual_seed(5)
+    cache, refc = fd.new_cache(keep=100), od.empty_cache(d, keep=100)
+    spk = torch.randn(1, 80, generator=g)
+    mu, cond = torch.randn(80, 100, generator=g), torch.randn(80, 100, generator=g)
+    errs = []
+    ref = od.solve(W, d, W["rand_noise"], [refc], [mu], spk, [cond], [True])
+    got = fd.solve([cache], [mu.cuda()], spk.cuda(), [cond.cuda()], [True])
+    errs.append(rel(got[0].cpu(), ref[0]))
+    for T in (50, 16):
+        mu = torch.randn(80, T, generator=g)
+        ref = od.solve(W, d, W["rand_noise"], [refc], [mu], spk, None, [True])
+        got = fd.solve([cache], [mu.cuda()], spk.cuda(), None, [True])
+        errs.append(rel(got[0].cpu(), ref[0]))
+    fd.release(cache)
+    print("full-size window rel-L2 per call", errs)
     assert max(errs) < TOL
 
 

@@ -95,9 +95,13 @@ def test_attention_mask_and_cache_order_vs_brute_force(W):
     torch.testing.assert_close(out, ref, rtol=1e-4, atol=1e-5)
 
 
-def test_streaming_equals_full_sequence(W):
+@pytest.mark.parametrize("depth", [2, 3])
+def test_streaming_equals_full_sequence(W, depth):
     """A prompt setup followed by two kept windows (each attending the previous ones through per-step caches, reading the
-    flow noise at its cache offset) equals one whole-sequence solve under the block-causal mask [prompt | w1 | w2]."""
+    flow noise at its cache offset) equals one whole-sequence solve under the block-causal mask [prompt | w1 | w2].
+    Depth 3 as well: the caches' CFG-row and block axes must not be interchangeable."""
+    if depth != 2:
+        W = init_dit(DiTConfig(hidden=128, depth=depth, heads=2, ffn=256, steps=4), seed=7)
     d = d_of(W)
     g = torch.Generator().manual_seed(3)
     P, T1, T2 = 12, 6, 9
