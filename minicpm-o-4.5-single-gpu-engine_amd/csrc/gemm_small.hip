@@ -25,56 +25,98 @@ namespace {
 constexpr int GS_WAVES = 16;  // waves per workgroup, sharing K
 constexpr int GS_MAXSTEPS = 3;  // 64-K steps per wave: K <= 16 * 3 * 64 = 3072
 
+// 16-byte fragments as a native vector (an aggregate copy of uint4 into LDS keeps the loaded registers in scratch)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8 frag(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
 template <bool TAPS, int EPI>
 __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
-  __shared__ float4 red[GS_WAVES][4][64];  // per wave: its 32x32 block in register order (quad q, lane)
+  // per wave 8 KB: the W and activation rows of one 64-K step (32 rows x 8 chunks of 16 bytes each), then its 32x32
+  // block in register order (quad q, lane) for the reduction
+  __shared__ u32x4 slab[GS_WAVES][512];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
   const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
   const int KT = g.K / 64, z = blockIdx.z, S = gridDim.z;
   const int kb = z * KT / S, KS = (z + 1) * KT / S - kb;  // this workgroup's K split
   const int nw = blockDim.x >> 6;
   const int s0 = kb + w * KS / nw, s1 = kb + (w + 1) * KS / nw;  // this wave's steps (possibly none)
-  const bf16_t* wrow = g.B + (size_t)min(n0 + c, g.N - 1) * g.ldb + h * 32;
-  const int m = min(m0 + c, g.M - 1);  // rows past M load row M - 1; their results are never stored
-  const bf16_t* arow = g.A + (size_t)(TAPS ? g.a_src[m] : m) * g.lda + h * 32;
-
-  uint4 wf[GS_MAXSTEPS][4], af[GS_MAXSTEPS][4];
+  // Load instruction kk of a step covers rows kk * 8 + lane / 8, eight lanes per row (its 64 K values, one 128-byte
+  // line): whole lines per instruction run at about 1.4x the CU's rate for 32-byte pieces of 32 rows.  The wave's slab
+  // turns them into MFMA fragments (lane (c, h) takes bytes h * 64 + kk * 16 of row c), 16-byte chunks XOR-swizzled by
+  // (row / 2) % 8 so that both the writes and the fragment reads are free of bank conflicts.
+  const int lr = lane >> 3, lc = lane & 7;
+  int arow[4];  // activation row (taps: frame) of each load instruction
 #pragma unroll
-  for (int t = 0; t < GS_MAXSTEPS; ++t) {
-    if (s0 + t < s1) {
-      const int k0 = (s0 + t) * 64;
-      size_t aoff = k0;
-      if (TAPS) {
-        const int tap = k0 / g.tapC;  // a 64-K step never straddles two taps (tapC % 64 == 0)
-        aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);
-      }
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        wf[t][kk] = *(const uint4*)(wrow + k0 + kk * 8);
-        af[t][kk] = *(const uint4*)(arow + aoff + kk * 8);
-      }
-    }
+  for (int kk = 0; kk < 4; ++kk) {
+    const int m = min(m0 + kk * 8 + lr, g.M - 1);  // rows past M load row M - 1; their results are never stored
+    arow[kk] = TAPS ? g.a_src[m] : m;
   }
+
+  // two register sets: steps 0 and 1 in flight from the start, step 2 (K = 3072 unsplit) once step 0 is consumed
+  u32x4 wf[2][4], af[2][4];
+  auto load = [&](int t, u32x4 (&wd)[4], u32x4 (&ad)[4]) {
+    const int k0 = (s0 + t) * 64;
+    size_t aoff = k0;
+    if (TAPS) {
+      const int tap = k0 / g.tapC;  // a 64-K step never straddles two taps (tapC % 64 == 0)
+      aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      wd[kk] = *(const u32x4*)(g.B + (size_t)min(n0 + kk * 8 + lr, g.N - 1) * g.ldb + k0 + lc * 8);
+      ad[kk] = *(const u32x4*)(g.A + (size_t)arow[kk] * g.lda + aoff + lc * 8);
+    }
+  };
   f32x16 acc;
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  u32x4* sl = slab[w];  // this wave's own: LDS accesses of one wave complete in order, no barrier needed
+  auto consume = [&](const u32x4 (&wd)[4], const u32x4 (&ad)[4]) {
 #pragma unroll
-  for (int t = 0; t < GS_MAXSTEPS; ++t)
-    if (s0 + t < s1) {
+    for (int kk = 0; kk < 4; ++kk) {
+      const int r = kk * 8 + lr, x = r * 8 + (lc ^ ((r >> 1) & 7));
+      sl[x] = wd[kk];
+      sl[256 + x] = ad[kk];
+    }
+    u32x4 wv[4], av[4];
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wf[t][kk]), as_bf16x8(af[t][kk]), acc, 0, 0, 0);
+    for (int kk = 0; kk < 4; ++kk) {
+      const int x = c * 8 + ((h * 4 + kk) ^ ((c >> 1) & 7));
+      wv[kk] = sl[x];
+      av[kk] = sl[256 + x];
     }
 #pragma unroll
-  for (int q = 0; q < 4; ++q) red[w][q][lane] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+    for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(wv[kk]), frag(av[kk]), acc, 0, 0, 0);
+  };
+  const int ns = s1 - s0;  // 0 .. GS_MAXSTEPS; one straight path per count (no register sets merged across branches)
+  if (ns == 1) {
+    load(0, wf[0], af[0]);
+    consume(wf[0], af[0]);
+  } else if (ns == 2) {
+    load(0, wf[0], af[0]);
+    load(1, wf[1], af[1]);
+    consume(wf[0], af[0]);
+    consume(wf[1], af[1]);
+  } else if (ns == 3) {
+    load(0, wf[0], af[0]);
+    load(1, wf[1], af[1]);
+    consume(wf[0], af[0]);
+    load(2, wf[0], af[0]);
+    consume(wf[1], af[1]);
+    consume(wf[0], af[0]);
+  }
+  float4* red = (float4*)sl;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) red[q * 64 + lane] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
   __syncthreads();
 
   // one float4 (four columns of one row) per thread of the first four waves, summed over the waves in order
   if (tid >= 256) return;
   const int q = tid >> 6, l = tid & 63;
-  float4 a = red[0][q][l];
+  float4 a = ((const float4*)slab[0])[q * 64 + l];
 #pragma unroll
   for (int x = 1; x < nw; ++x) {
-    const float4 b = red[x][q][l];
+    const float4 b = ((const float4*)slab[x])[q * 64 + l];
     a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
   }
   // lane l of the MFMA holds token m0 + l % 32 and columns n0 + q * 8 + (l / 32) * 4 + 0..3
