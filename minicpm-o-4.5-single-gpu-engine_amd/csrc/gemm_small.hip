@@ -165,46 +165,63 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
 // row's 64 columns: bias, rounding to bf16 (the projection's own precision), LayerNorm + affine for q and k, then q
 // to its token row and k, v to the token's key slot.
 __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_qkv_kernel(GemmArgs g) {
-  __shared__ float4 red[GS_WAVES][2][4][64];  // per wave: two 32x32 blocks (column tiles) in register order
-  __shared__ float rowm[32][68];               // the summed 32 x 64 block, row-major (padded rows)
+  // per wave 8 KB: one 64-K step of the activation rows and of one column tile's W rows (the two tiles in turn), then
+  // its two 32x32 blocks (column tiles) in register order for the reduction
+  __shared__ u32x4 slab[GS_WAVES][512];
+  __shared__ float rowm[32][68];  // the summed 32 x 64 block, row-major (padded rows)
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
   const int n0 = blockIdx.x * 64, m0 = blockIdx.y * 32;
   const int KS = g.K / 64;
   const int s0 = w * KS / GS_WAVES, s1 = (w + 1) * KS / GS_WAVES;  // at most one step
-  const int m = min(m0 + c, g.M - 1);
+  const int lr = lane >> 3, lc = lane & 7;  // whole-line loads and the slab's swizzle, as in gemm_small_kernel
   f32x16 acc[2];
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[ct][r] = 0.0f;
+  u32x4* sl = slab[w];
   if (s0 < s1) {
     const int k0 = s0 * 64;
-    uint4 wf[2][4], af[4];
+    u32x4 wf[2][4], af[4];
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const bf16_t* wrow = g.B + (size_t)min(n0 + ct * 32 + c, g.N - 1) * g.ldb + h * 32 + k0;
+    for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) wf[ct][kk] = *(const uint4*)(wrow + kk * 8);
-    }
-    const bf16_t* arow = g.A + (size_t)m * g.lda + h * 32 + k0;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) af[kk] = *(const uint4*)(arow + kk * 8);
+      for (int kk = 0; kk < 4; ++kk)
+        wf[ct][kk] = *(const u32x4*)(g.B + (size_t)min(n0 + ct * 32 + kk * 8 + lr, g.N - 1) * g.ldb + k0 + lc * 8);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
+      af[kk] = *(const u32x4*)(g.A + (size_t)min(m0 + kk * 8 + lr, g.M - 1) * g.lda + k0 + lc * 8);
+    u32x4 av[4], wv[4];
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wf[ct][kk]), as_bf16x8(af[kk]), acc[ct], 0, 0, 0);
+    for (int ct = 0; ct < 2; ++ct) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int r = kk * 8 + lr, x = r * 8 + (lc ^ ((r >> 1) & 7));
+        sl[x] = wf[ct][kk];
+        if (ct == 0) sl[256 + x] = af[kk];
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int x = c * 8 + ((h * 4 + kk) ^ ((c >> 1) & 7));
+        wv[kk] = sl[x];
+        if (ct == 0) av[kk] = sl[256 + x];
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(wv[kk]), frag(av[kk]), acc[ct], 0, 0, 0);
+    }
   }
+  float4* red = (float4*)sl;  // [ct][q][lane]
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) red[w][ct][q][lane] = make_float4(acc[ct][4 * q], acc[ct][4 * q + 1], acc[ct][4 * q + 2], acc[ct][4 * q + 3]);
+    for (int q = 0; q < 4; ++q) red[(ct * 4 + q) * 64 + lane] = make_float4(acc[ct][4 * q], acc[ct][4 * q + 1], acc[ct][4 * q + 2], acc[ct][4 * q + 3]);
   __syncthreads();
   if (tid < 512) {  // sum over the waves in order; lane l holds token m0 + l % 32, columns ct * 32 + q * 8 + (l / 32) * 4 + 0..3
     const int ct = tid >> 8, q = (tid >> 6) & 3, l = tid & 63;
-    float4 a = red[0][ct][q][l];
+    float4 a = ((const float4*)slab[0])[(ct * 4 + q) * 64 + l];
 #pragma unroll
     for (int x = 1; x < GS_WAVES; ++x) {
-      const float4 b = red[x][ct][q][l];
+      const float4 b = ((const float4*)slab[x])[(ct * 4 + q) * 64 + l];
       a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
     }
     *(float4*)&rowm[l & 31][ct * 32 + q * 8 + (l >> 5) * 4] = a;
