@@ -141,11 +141,12 @@ GemmArgs gemm8(const uint8_t* A, int lda, const int* a_src, const uint8_t* as, c
 
 // K splits of the deferred GEMMs of a call of N tokens (0: no deferral): enough workgroups to occupy the 256 CUs, at
 // most 4 (the row kernels' limit), and the sums must fit the partial area.  Taken only when every deferred GEMM fits the
-// small-row kernel.
+// small-row kernel.  Tiles are 64 rows above 32 tokens (gemm_small_part64).
 int defer_splits(const t2w_dit_dims& d, int N, const Work& w) {
   const int H = d.hidden;
   if (N > GEMM_SMALL_MAX_M || !w.part) return 0;
-  const int tiles = ((N + 31) / 32) * ((H + 31) / 32);
+  const int rows = N > 32 ? 64 : 32;
+  const int tiles = ((N + rows - 1) / rows) * ((H + 31) / 32);
   const int S = std::min(4, 256 / tiles);
   if (S < 2 || (size_t)S * N * H * 4 > w.part_bytes) return 0;
   GemmArgs g{};

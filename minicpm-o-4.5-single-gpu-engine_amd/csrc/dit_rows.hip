@@ -179,7 +179,7 @@ template <int VPL>
 __global__ void __launch_bounds__(256) ln_mod_kernel(float* h, const float* shift, const float* scale1, float eps,
                                                      bf16_t* out, uint8_t* q, uint8_t* qs, int N, int H, Pend pd) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (n >= N) return;
   float v[VPL], sc[VPL], sh[VPL];
   row_load_f32<VPL, 4>(h + (size_t)n * H, lane, v);
@@ -242,7 +242,7 @@ template <int VPL>
 __global__ void __launch_bounds__(256) ln_mod_conv_kernel(float* h, const float* shift, const float* scale1, float eps,
                                                           ConvPlace cp, int H, Pend pd) {
   const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (w < cp.N) {
     float v[VPL], sc[VPL], sh[VPL];
     row_load_f32<VPL, 4>(h + (size_t)w * H, lane, v);
@@ -264,7 +264,7 @@ template <int VPL>
 __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, const float* lw, const float* lb, float eps,
                                                            ConvPlace cp, int H, Pend pd) {
   const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (w < cp.N) {
     constexpr int G = VPL >= 8 ? 8 : 4;  // the row comes in as bf16
     float v[VPL], a[VPL], b[VPL];
@@ -298,7 +298,7 @@ __global__ void __launch_bounds__(256) qk_norm_kernel(const bf16_t* qkv, const f
                                                       bf16_t* v_pool, const int* slots, int N, int H) {
   constexpr int LPH = 64 / VPL;
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (n >= N) return;
   const int c0 = lane * VPL, d0 = c0 & 63;
   const size_t slot = (size_t)slots[n];
@@ -436,6 +436,10 @@ inline unsigned blocks_for(long long n, int per) { return (unsigned)((n + per - 
 
 }  // namespace
 
+// Rows per block of the row kernels: calls of few rows (a streaming chunk) spread one row per CU, since a CU's load
+// throughput bounds them (a LayerNorm row with pending K-split sums reads ~20 KB); large calls take four rows per block.
+inline int row_waves(long long rows) { return rows <= 1024 ? 1 : 4; }
+
 #define T2W_VPL_DISPATCH(H, CALL)          \
   switch ((H) / 64) {                      \
     case 4: { constexpr int V = 4; CALL; } break;   \
@@ -448,7 +452,7 @@ hipError_t ln_mod(float* h, const float* shift, const float* scale1, float eps, 
                   const Pend& pd) {
   if (N <= 0) return hipSuccess;
   if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, 4)), dim3(256), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H, pd));
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H, pd));
   return hipGetLastError();
 }
 
@@ -456,7 +460,7 @@ hipError_t ln_mod_mx8(const float* h, const float* shift, const float* scale1, f
                       int H, hipStream_t st) {
   if (N <= 0) return hipSuccess;
   // nothing pending: h is only read
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, 4)), dim3(256), 0, st, const_cast<float*>(h), shift, scale1, eps, nullptr, q, qs, N, H, Pend()));
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, const_cast<float*>(h), shift, scale1, eps, nullptr, q, qs, N, H, Pend()));
   return hipGetLastError();
 }
 
@@ -464,7 +468,7 @@ hipError_t ln_mod_conv(float* h, const float* shift, const float* scale1, float 
                        const Pend& pd) {
   if (cp.N + cp.R <= 0) return hipSuccess;
   if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_conv_kernel<V>, dim3(blocks_for(cp.N + cp.R, 4)), dim3(256), 0, st, h, shift, scale1, eps, cp, H, pd));
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_conv_kernel<V>, dim3(blocks_for(cp.N + cp.R, row_waves(cp.N + cp.R))), dim3(64 * row_waves(cp.N + cp.R)), 0, st, h, shift, scale1, eps, cp, H, pd));
   return hipGetLastError();
 }
 
@@ -472,7 +476,7 @@ hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float e
                         const Pend& pd) {
   if (cp.N + cp.R <= 0) return hipSuccess;
   if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mish_conv_kernel<V>, dim3(blocks_for(cp.N + cp.R, 4)), dim3(256), 0, st, y, w, b, eps, cp, H, pd));
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mish_conv_kernel<V>, dim3(blocks_for(cp.N + cp.R, row_waves(cp.N + cp.R))), dim3(64 * row_waves(cp.N + cp.R)), 0, st, y, w, b, eps, cp, H, pd));
   return hipGetLastError();
 }
 
@@ -480,7 +484,7 @@ hipError_t qk_norm_scatter(const bf16_t* qkv, const float* qw, const float* qb, 
                            bf16_t* q_out, bf16_t* k_pool, bf16_t* v_pool, const int* slots, int N, int heads, hipStream_t st) {
   if (N <= 0) return hipSuccess;
   const int H = heads * 64;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(qk_norm_kernel<V>, dim3(blocks_for(N, 4)), dim3(256), 0, st, qkv, qw, qb, kw, kb, eps, q_out, k_pool, v_pool, slots, N, H));
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(qk_norm_kernel<V>, dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, qkv, qw, qb, kw, kb, eps, q_out, k_pool, v_pool, slots, N, H));
   return hipGetLastError();
 }
 

@@ -159,6 +159,86 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
   }
 }
 
+// EPI_PART with 64-row tiles for calls of more than 32 rows: every W slice is read by half as many workgroups as with
+// 32-row tiles (at ~100 rows the fourth 32-row tile held 4 rows and still read all of W).  A wave takes at most one
+// 64-K step (K / splits <= 1024): its W rows and the first 32 activation rows go through the slab, then the other 32
+// activation rows, both against the same W fragments.
+template <bool TAPS>
+__global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_part64_kernel(GemmArgs g) {
+  __shared__ u32x4 slab[GS_WAVES][512];  // per wave: W rows + 32 activation rows of its step, then its two blocks
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, c = lane & 31;
+  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 64;
+  const int KT = g.K / 64, z = blockIdx.z, S = gridDim.z;
+  const int kb = z * KT / S, KS = (z + 1) * KT / S - kb;
+  const int nw = blockDim.x >> 6;
+  const int s0 = kb + w * KS / nw, s1 = kb + (w + 1) * KS / nw;  // at most one step
+  const int lr = lane >> 3, lc = lane & 7;
+  f32x16 acc[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[rb][r] = 0.0f;
+  u32x4* sl = slab[w];
+  if (s0 < s1) {
+    const int k0 = s0 * 64;
+    size_t aoff = k0;
+    if (TAPS) {
+      const int tap = k0 / g.tapC;
+      aoff = (size_t)tap * g.lda + (k0 - tap * g.tapC);
+    }
+    u32x4 wf[4], af[8];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      wf[kk] = *(const u32x4*)(g.B + (size_t)min(n0 + kk * 8 + lr, g.N - 1) * g.ldb + k0 + lc * 8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int m = min(m0 + j * 8 + lr, g.M - 1);  // rows past M load row M - 1; their results are never stored
+      af[j] = *(const u32x4*)(g.A + (size_t)(TAPS ? g.a_src[m] : m) * g.lda + aoff + lc * 8);
+    }
+    u32x4 wv[4], av[4];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int r = kk * 8 + lr, x = r * 8 + (lc ^ ((r >> 1) & 7));
+        if (rb == 0) sl[x] = wf[kk];
+        sl[256 + x] = af[rb * 4 + kk];
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int x = c * 8 + ((h * 4 + kk) ^ ((c >> 1) & 7));
+        if (rb == 0) wv[kk] = sl[x];
+        av[kk] = sl[256 + x];
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(wv[kk]), frag(av[kk]), acc[rb], 0, 0, 0);
+    }
+  }
+  float4* red = (float4*)sl;  // [row block][quad][lane]
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[(rb * 4 + q) * 64 + lane] = make_float4(acc[rb][4 * q], acc[rb][4 * q + 1], acc[rb][4 * q + 2], acc[rb][4 * q + 3]);
+  __syncthreads();
+  if (tid >= 512) return;  // one float4 per thread of the first eight waves, summed over the waves in order
+  const int rb = tid >> 8, q = (tid >> 6) & 3, l = tid & 63;
+  float4 a = ((const float4*)slab[0])[(rb * 4 + q) * 64 + l];
+#pragma unroll
+  for (int x = 1; x < nw; ++x) {
+    const float4 b = ((const float4*)slab[x])[(rb * 4 + q) * 64 + l];
+    a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+  }
+  const int mo = m0 + rb * 32 + (l & 31), n = n0 + q * 8 + (l >> 5) * 4;
+  if (mo >= g.M || n >= g.N) return;
+  float* part = (float*)g.C + (size_t)z * g.c_split + (size_t)mo * g.ldc;
+  if (n + 3 < g.N) {
+    *(float4*)(part + n) = a;
+    return;
+  }
+  const float v[4] = {a.x, a.y, a.z, a.w};
+  for (int e = 0; e < 4 && n + e < g.N; ++e) part[n + e] = v[e];
+}
+
 // The qkv projection (N = 3 H) for few rows, with the per-head q / k LayerNorm and the key / value scatter fused:
 // 64 columns (one head of q, k or v) x 32 rows per workgroup, K split over the 16 waves (one 64-K step each, so
 // K <= 1024).  The block summed over the waves goes row-major through LDS, where the 16 lanes of one DPP row hold a
@@ -275,8 +355,17 @@ bool gemm_small_fits(const GemmArgs& g, int epi) {
          (!g.a_src || g.tapC % 64 == 0);
 }
 
+bool gemm_small_part64(const GemmArgs& g) { return g.M > 32 && (g.K / 64 + g.splits - 1) / g.splits <= GS_WAVES; }
+
 hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st) {
   if (!gemm_small_fits(g, epi)) return hipErrorInvalidValue;
+  if (epi == EPI_PART && gemm_small_part64(g)) {
+    const int nwv = max(8, min(GS_WAVES, (g.K / 64 + g.splits - 1) / g.splits));
+    const dim3 grid((g.N + 31) / 32, (g.M + 63) / 64, g.splits);
+    if (g.a_src) hipLaunchKernelGGL(gemm_small_part64_kernel<true>, grid, dim3(64 * nwv), 0, st, g);
+    else hipLaunchKernelGGL(gemm_small_part64_kernel<false>, grid, dim3(64 * nwv), 0, st, g);
+    return hipGetLastError();
+  }
   switch (epi) {
     case EPI_BF16: return launch_small<EPI_BF16>(g, st);
     case EPI_GELU_BF16: return launch_small<EPI_GELU_BF16>(g, st);
