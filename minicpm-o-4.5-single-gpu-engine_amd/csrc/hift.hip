@@ -390,16 +390,21 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
 
 // Small grids (a streaming window: one item of a few thousand samples) leave most CUs idle with whole-slab tiles, and
 // each tile's tap loop is a chain of weight-load latencies.  Here a workgroup of CS_WAVES waves owns 32 output rows x
-// 64 output channels and splits the (tap, 64-channel input chunk) steps over its waves: per step a lane loads 32
-// input channels of its row straight into registers (activation applied, rounded to bf16) and the 32 matching weights
-// of each of its two output-channel rows, the next step's loads issued before this step's MFMAs; the waves' 32 x 64
-// fp32 blocks are summed through LDS in wave order (deterministic) and the epilogue writes four channels per thread.
-// MFMA roles as in the small-row GEMM: the weights are the A operand (32 output channels), the activations the B
-// operand (32 output rows); both sides see the same K permutation (lane half h supplies channels h * 32 + kk * 8 ..).
+// NB * 32 output channels and splits the (tap, 64-channel input chunk) steps over its waves, the next step's loads
+// issued before this step's MFMAs; the waves' fp32 blocks are summed through LDS in wave order (deterministic) and the
+// epilogue writes four channels per thread.  A CU's load throughput bounds these calls, so (as in the small-row GEMM)
+// the loads cover whole lines: a step's weights are NB * 32 rows of 128 bytes, eight lanes per row; its activations 32
+// rows of 64 fp32 channels, sixteen lanes per row (activation applied, rounded to bf16).  Both go through the wave's
+// LDS slab (16-byte chunks XOR-swizzled by (row / 2) % 8) and come back as MFMA fragments.  NB = 1 halves the weight
+// bytes each workgroup reads where the grid stays within the chip.  MFMA roles as in the small-row GEMM: the weights
+// are the A operand (32 output channels), the activations the B operand (32 output rows).
 constexpr int CS_WAVES = 8;
 
+template <int NB>
 __global__ void __launch_bounds__(64 * CS_WAVES) conv_bf16_split_kernel(ConvDesc c, const bf16_t* __restrict__ wbf) {
-  __shared__ float4 red[CS_WAVES][2][4][64];  // per wave: its two 32x32 blocks in register order
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  __shared__ u32x4 slab[CS_WAVES][(NB + 1) * 256];  // per wave: W rows then activation rows of a step; then its blocks
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, cl = lane & 31;
   const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
   const int Tin = c.in_len[b], Tout = c.out_len[b];
@@ -408,77 +413,96 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_bf16_split_kernel(ConvDesc
   const int r_hi = Tout - 1 - oo < 0 ? -1 : (Tout - 1 - oo) / c.s_out;
   const int r0 = r_lo + blockIdx.x * 32;
   if (r0 > r_hi) return;  // the whole workgroup leaves together
-  const int co0 = blockIdx.y * HB_BN;
+  const int co0 = blockIdx.y * (NB * 32);
   const float* xb = c.x + (size_t)c.in_off[b] * c.ldx;
   const int cin_pad = (c.Cin + 63) & ~63, nch = cin_pad / 64;
+  // rows co0 .. co0 + NB * 32 - 1 exist: the weights are padded to 64 output channels
   const bf16_t* wph = wbf + ((size_t)ph * ((c.Cout + 63) & ~63) + co0) * c.taps * cin_pad;
   const int NS = c.taps * nch;
   const int s0 = w * NS / CS_WAVES, s1 = (w + 1) * NS / CS_WAVES;  // this wave's steps (possibly none)
-  const int r = r0 + cl;
+  const int wr = lane >> 3, wc = lane & 7;    // weight loads: row i * 8 + wr, 16-byte chunk wc
+  const int xr = lane >> 4, xc = lane & 15;   // activation loads: row i * 4 + xr, channels xc * 4 .. + 3
 
-  // step s: tap j = s / nch, channels cc .. cc + 63 with cc = (s % nch) * 64; this lane's 32 of them: cc + h * 32 ..
-  auto load = [&](int st, float4 (&xv)[8], uint4 (&wv)[2][4]) {
-    const int j = st / nch, cc = (st - j * nch) * 64 + h * 32;
-    const int in_row = r + j * c.d_in + c.off_in[ph];
-    const bool rok = r <= r_hi && in_row >= 0 && in_row < Tin;
-    const float* xp = xb + (size_t)(rok ? in_row : 0) * c.ldx + cc;
+  // step st: tap j = st / nch, input channels cc .. cc + 63 with cc = (st % nch) * 64
+  auto load = [&](int st, float4 (&xv)[8], u32x4 (&wv)[4 * NB]) {
+    const int j = st / nch, cc = (st - j * nch) * 64;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if (rok && cc + e * 4 + 3 < c.Cin) xv[e] = *(const float4*)(xp + e * 4);
+    for (int i = 0; i < 4 * NB; ++i)
+      wv[i] = *(const u32x4*)(wph + ((size_t)(i * 8 + wr) * c.taps + j) * cin_pad + cc + wc * 8);
+    const int ch = cc + xc * 4;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = r0 + i * 4 + xr, in_row = r + j * c.d_in + c.off_in[ph];
+      const bool rok = r <= r_hi && in_row >= 0 && in_row < Tin;
+      const float* xp = xb + (size_t)(rok ? in_row : 0) * c.ldx + ch;
+      if (rok && ch + 3 < c.Cin) xv[i] = *(const float4*)xp;
       else {
         float t[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) t[u] = (rok && cc + e * 4 + u < c.Cin) ? xp[e * 4 + u] : 0.f;
-        xv[e] = make_float4(t[0], t[1], t[2], t[3]);
+        for (int u = 0; u < 4; ++u) t[u] = (rok && ch + u < c.Cin) ? xp[u] : 0.f;
+        xv[i] = make_float4(t[0], t[1], t[2], t[3]);
       }
     }
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        wv[jj][kk] = *(const uint4*)(wph + ((size_t)(jj * 32 + cl) * c.taps + j) * cin_pad + cc + kk * 8);
   };
-  // activation (zero inputs stay zero: the padding rows and channels of the reference's zero-padded conv) and bf16
-  auto mma = [&](int st, const float4 (&xv)[8], const uint4 (&wv)[2][4], f32x16 (&acc)[2]) {
-    const int j = st / nch, cc = (st - j * nch) * 64 + h * 32;
-    const int in_row = r + j * c.d_in + c.off_in[ph];
-    const bool rok = r <= r_hi && in_row >= 0 && in_row < Tin;
-    const bool snake4 = c.pre == PRE_SNAKE && cc + 31 < c.Cin;  // the lane's 32 Snake parameters as float4s
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      float v[8] = {xv[2 * kk].x, xv[2 * kk].y, xv[2 * kk].z, xv[2 * kk].w, xv[2 * kk + 1].x, xv[2 * kk + 1].y, xv[2 * kk + 1].z, xv[2 * kk + 1].w};
-      float al[8], in[8];
-      if (snake4) {
-        const float4 a0 = *(const float4*)(c.alpha + cc + kk * 8), a1 = *(const float4*)(c.alpha + cc + kk * 8 + 4);
-        const float4 i0 = *(const float4*)(c.inv + cc + kk * 8), i1 = *(const float4*)(c.inv + cc + kk * 8 + 4);
-        al[0] = a0.x; al[1] = a0.y; al[2] = a0.z; al[3] = a0.w; al[4] = a1.x; al[5] = a1.y; al[6] = a1.z; al[7] = a1.w;
-        in[0] = i0.x; in[1] = i0.y; in[2] = i0.z; in[3] = i0.w; in[4] = i1.x; in[5] = i1.y; in[6] = i1.z; in[7] = i1.w;
+  // activation (zero inputs stay zero: the padding rows and channels of the reference's zero-padded conv), bf16, slab,
+  // fragments, MFMAs
+  auto mma = [&](int st, const float4 (&xv)[8], const u32x4 (&wv)[4 * NB], f32x16 (&acc)[NB]) {
+    const int j = st / nch, cc = (st - j * nch) * 64, ch = cc + xc * 4;
+    float al[4] = {0.f, 0.f, 0.f, 0.f}, iv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (c.pre == PRE_SNAKE) {
+      if (ch + 3 < c.Cin) {
+        const float4 a4 = *(const float4*)(c.alpha + ch), i4 = *(const float4*)(c.inv + ch);
+        al[0] = a4.x; al[1] = a4.y; al[2] = a4.z; al[3] = a4.w;
+        iv[0] = i4.x; iv[1] = i4.y; iv[2] = i4.z; iv[3] = i4.w;
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int ci = cc + kk * 8 + e;
-          al[e] = (c.pre == PRE_SNAKE && ci < c.Cin) ? c.alpha[ci] : 0.f;
-          in[e] = (c.pre == PRE_SNAKE && ci < c.Cin) ? c.inv[ci] : 0.f;
+        for (int u = 0; u < 4; ++u) {
+          al[u] = ch + u < c.Cin ? c.alpha[ch + u] : 0.f;
+          iv[u] = ch + u < c.Cin ? c.inv[ch + u] : 0.f;
         }
       }
+    }
+    u32x4* sl = slab[w];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const bool ok = rok && cc + kk * 8 + e < c.Cin;
-        v[e] = ok ? pre_fast(v[e], c.pre, c.slope, al[e], in[e]) : 0.f;
-      }
-      const uint4 xq = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+    for (int i = 0; i < 4 * NB; ++i) {
+      const int r = i * 8 + wr;
+      sl[r * 8 + (wc ^ ((r >> 1) & 7))] = wv[i];
+    }
+    u32x2* sx = (u32x2*)(sl + NB * 256);
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) acc[jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wv[jj][kk]), as_bf16x8(xq), acc[jj], 0, 0, 0);
+    for (int i = 0; i < 8; ++i) {
+      const int rr = i * 4 + xr, r = r0 + rr, in_row = r + j * c.d_in + c.off_in[ph];
+      const bool rok = r <= r_hi && in_row >= 0 && in_row < Tin;
+      const float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+      float o[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) o[u] = (rok && ch + u < c.Cin) ? pre_fast(v[u], c.pre, c.slope, al[u], iv[u]) : 0.f;
+      u32x2 pk;
+      pk.x = pack2(o[0], o[1]);
+      pk.y = pack2(o[2], o[3]);
+      sx[(rr * 8 + ((xc >> 1) ^ ((rr >> 1) & 7))) * 2 + (xc & 1)] = pk;
+    }
+    u32x4 xf[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) xf[kk] = sl[NB * 256 + cl * 8 + ((h * 4 + kk) ^ ((cl >> 1) & 7))];
+#pragma unroll
+    for (int jj = 0; jj < NB; ++jj) {
+      u32x4 wf[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) wf[kk] = sl[(jj * 32 + cl) * 8 + ((h * 4 + kk) ^ ((cl >> 1) & 7))];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        acc[jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[kk]), __builtin_bit_cast(bf16x8, xf[kk]), acc[jj], 0, 0, 0);
     }
   };
 
-  f32x16 acc[2];
+  f32x16 acc[NB];
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj)
+  for (int jj = 0; jj < NB; ++jj)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[jj][i] = 0.f;
   float4 xa[8], xb2[8];
-  uint4 wa[2][4], wb2[2][4];
+  u32x4 wa[4 * NB], wb2[4 * NB];
   // two register sets named at compile time: the loop runs two steps per pass
   if (s0 < s1) load(s0, xa, wa);
   for (int st = s0; st < s1; st += 2) {
@@ -489,23 +513,25 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_bf16_split_kernel(ConvDesc
       mma(st + 1, xb2, wb2, acc);
     }
   }
+  float4* red = (float4*)slab[w];  // [block jj][quad q][lane]; the wave's own slab (its LDS accesses complete in order)
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj)
+  for (int jj = 0; jj < NB; ++jj)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) red[w][jj][q][lane] = make_float4(acc[jj][4 * q], acc[jj][4 * q + 1], acc[jj][4 * q + 2], acc[jj][4 * q + 3]);
+    for (int q = 0; q < 4; ++q) red[(jj * 4 + q) * 64 + lane] = make_float4(acc[jj][4 * q], acc[jj][4 * q + 1], acc[jj][4 * q + 2], acc[jj][4 * q + 3]);
   __syncthreads();
 
   // one float4 (four channels of one row) per thread, summed over the waves in order
+  if (tid >= NB * 256) return;
   const int jj = tid >> 8, q = (tid >> 6) & 3, l = tid & 63;
-  float4 sum = red[0][jj][q][l];
+  float4 sum = ((const float4*)slab[0])[(jj * 4 + q) * 64 + l];
 #pragma unroll
   for (int x = 1; x < CS_WAVES; ++x) {
-    const float4 v = red[x][jj][q][l];
+    const float4 v = ((const float4*)slab[x])[(jj * 4 + q) * 64 + l];
     sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
   }
   // lane l of the MFMA holds output row r0 + l % 32 and channels co0 + jj * 32 + q * 8 + (l / 32) * 4 + 0..3
   const int ro = r0 + (l & 31), cn = jj * 32 + q * 8 + (l >> 5) * 4;
-  const int ncols = min(HB_BN, c.Cout - co0);
+  const int ncols = min(NB * 32, c.Cout - co0);
   if (ro > r_hi || cn >= ncols) return;
   const size_t orow = (size_t)c.out_off[b] + (size_t)(ro * c.s_out + oo);
   if (cn + 3 < ncols) conv_epilogue4(c, orow, co0 + cn, sum);
@@ -808,8 +834,15 @@ hipError_t conv_bf16(const ConvDesc& c, const bf16_t* wbf, int max_rows, hipStre
   const long tiles512 = (long)cdiv(max_rows, 512) * cdiv(c.Cout, HB_BN) * c.n_items * c.n_phase;
   const long tiles128 = (long)cdiv(max_rows, 128) * cdiv(c.Cout, HB_BN) * c.n_items * c.n_phase;
   if (tiles128 < 128) {
-    dim3 grid(cdiv(max_rows, 32), cdiv(c.Cout, HB_BN), c.n_items * c.n_phase);
-    hipLaunchKernelGGL(conv_bf16_split_kernel, grid, dim3(64 * CS_WAVES), 0, st, c, wbf);
+    // 32 output channels per workgroup while that grid fits the chip in one round, else 64
+    const long t32 = (long)cdiv(max_rows, 32) * cdiv(c.Cout, 32) * c.n_items * c.n_phase;
+    if (t32 <= 256) {
+      dim3 grid(cdiv(max_rows, 32), cdiv(c.Cout, 32), c.n_items * c.n_phase);
+      hipLaunchKernelGGL(conv_bf16_split_kernel<1>, grid, dim3(64 * CS_WAVES), 0, st, c, wbf);
+    } else {
+      dim3 grid(cdiv(max_rows, 32), cdiv(c.Cout, 64), c.n_items * c.n_phase);
+      hipLaunchKernelGGL(conv_bf16_split_kernel<2>, grid, dim3(64 * CS_WAVES), 0, st, c, wbf);
+    }
   } else if (tiles512 >= 256) {
     constexpr int BM = 512;
     const size_t lds = conv_bf16_lds(BM);

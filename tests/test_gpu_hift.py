@@ -117,6 +117,22 @@ def test_forward_bf16_end_to_end(dev, case):
     assert e < 1e-2
 
 
+def test_forward_bf16_streaming_window(dev, case):
+    """One 50-frame window with a source cache (the per-chunk call of a stream): every decoder conv runs on the
+    small-grid kernels (32 output channels per workgroup where the grid allows)."""
+    W, h, gm, mels, noise = case
+    gb = HiFTModel(W, HiFTConfig(), decode_bf16=True)
+    g = torch.Generator().manual_seed(12)
+    mel = torch.randn(1, 80, 50, generator=g) * 2 - 5
+    cs = torch.randn(1, 1, 3840, generator=g) * 0.01
+    ri, nz = oh.hift_noise(9, [11], 50 * 480)
+    sp, src = gb.forward_noise(mel.cuda(), cs.cuda(), ri.cuda(), nz.cuda())
+    rsp, rsrc = oh.forward_noise(h, mel, cs, ri, nz)
+    e = rel(sp.cpu(), rsp)
+    print("bf16 50-frame window speech rel-L2", e, "source", rel(src.cpu(), rsrc))
+    assert e < 1e-2
+
+
 def test_hift_graphs_equal_eager():
     """Graph replays (one graph per row lengths and source-cache length) equal eager calls bit for bit, replay after
     replay with new inputs, eager work and synchronisations in between; a second key gets its own graph."""
