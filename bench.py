@@ -53,6 +53,8 @@ def main() -> int:
     ap.add_argument("--hift-fp32", action="store_true", help="HiFT decoder in strict fp32 (default: bf16 MFMA decoder)")
     ap.add_argument("--no-extra", action="store_true", help="skip the ragged-length and HiFT-alone measurements")
     ap.add_argument("--no-fp8", action="store_true", help="skip the fp8 (e4m3 weights, MX fp8 activations) measurement")
+    ap.add_argument("--latency-only", action="store_true",
+                    help="only the per-chunk latency case (one stream, 300 cached + 50 new frames, + HiFT of the window)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the conv1 GEMM launches, after three 256 MiB calibration copies (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -93,6 +95,40 @@ def main() -> int:
         hsrc = torch.zeros(n, 1, 0, device=dev)
         hnoise = hift.noise([1000 + i for i in range(n)], T * hift.cfg.upsample_scale)
 
+    def chunk_latency():
+        # one stream, 300-frame prompt cached, 50 new frames, CFG pair, 10 steps, + HiFT of the window: medians of the
+        # whole call and of its DiT solve and HiFT parts
+        fl = FastDiT(model, n_slots=4096, max_streams=2, use_graphs=True)
+        c = fl.new_cache(keep=300)
+        pm = torch.randn(cfg.mel, 300, generator=g).to(dev)
+        fl.solve([c], [pm], spks[:1], [torch.randn(cfg.mel, 300, generator=g).to(dev)], [True])
+        wm = torch.randn(cfg.mel, 50, generator=g).to(dev)
+        hs = None
+        if hift is not None:
+            hs = (torch.zeros(1, 1, 0, device=dev), *hift.noise([7], 50 * hift.cfg.upsample_scale))
+        ts, td, th = [], [], []
+        for i in range(args.latency_reps + 3):
+            torch.cuda.synchronize()
+            a = time.perf_counter()
+            m = fl.solve([c], [wm], spks[:1], None, [False])
+            torch.cuda.synchronize()
+            b = time.perf_counter()
+            if hift is not None:
+                hift.forward_noise(m[0][None], *hs)
+            torch.cuda.synchronize()
+            e = time.perf_counter()
+            if i >= 3:
+                ts.append(e - a)
+                td.append(b - a)
+                th.append(e - b)
+        return float(np.median(ts) * 1e3), float(np.median(td) * 1e3), float(np.median(th) * 1e3)
+
+    if args.latency_only:
+        lat, lat_dit, lat_hift = chunk_latency()
+        print(json.dumps({"p50_chunk_latency_ms": lat, "p50_chunk_dit_ms": lat_dit, "p50_chunk_hift_ms": lat_hift,
+                          "reps": args.latency_reps}))
+        return 0
+
     def step():
         mels = fd.solve(caches, mus, spks, None, [False] * n, chunk=args.chunk)
         if hift is not None:
@@ -121,28 +157,9 @@ def main() -> int:
 
     k_ms, k_tflops, k_flops = conv1_roofline(cfg, n, T)
 
-    # per-chunk latency: one stream, 300-frame prompt cached, 50 new frames, CFG pair, 10 steps, + HiFT of the window
-    lat = None
+    lat = lat_dit = lat_hift = None
     if args.latency_reps > 0:
-        fl = FastDiT(model, n_slots=4096, max_streams=2, use_graphs=True)
-        c = fl.new_cache(keep=300)
-        pm = torch.randn(cfg.mel, 300, generator=g).to(dev)
-        fl.solve([c], [pm], spks[:1], [torch.randn(cfg.mel, 300, generator=g).to(dev)], [True])
-        wm = torch.randn(cfg.mel, 50, generator=g).to(dev)
-        hs = None
-        if hift is not None:
-            hs = (torch.zeros(1, 1, 0, device=dev), *hift.noise([7], 50 * hift.cfg.upsample_scale))
-        ts = []
-        for i in range(args.latency_reps + 3):
-            torch.cuda.synchronize()
-            a = time.perf_counter()
-            m = fl.solve([c], [wm], spks[:1], None, [False])
-            if hift is not None:
-                hift.forward_noise(m[0][None], *hs)
-            torch.cuda.synchronize()
-            if i >= 3:
-                ts.append(time.perf_counter() - a)
-        lat = float(np.median(ts) * 1e3)
+        lat, lat_dit, lat_hift = chunk_latency()
 
     extra = {}
     if not args.no_fp8:
@@ -173,6 +190,8 @@ def main() -> int:
                    "global_batch": 2 * n, "seq_len": T, "parallelism": "single GPU"},
         "audio_seconds_per_s": frames / 50.0 / dt,
         "p50_chunk_latency_ms": lat,
+        "p50_chunk_dit_ms": lat_dit,
+        "p50_chunk_hift_ms": lat_hift,
         "dit_solve_ms": dit_dt * 1e3,
         "dit_mfma_frac": (gemm_f + attn_f) / dit_dt / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "roofline": {"bound": "mfma", "kernel": "gemm_kernel<256,256,4,2,EPI_BF16,taps> (DiT conv1)", "achieved": k_tflops,
