@@ -114,10 +114,43 @@ hipError_t launch_tile(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
+// g without its first r rows (bf16 operands): activation rows (taps: their frame ids), output rows, qkv rows and slots
+template <int EPI>
+GemmArgs rows_from(const GemmArgs& g, int r) {
+  GemmArgs h = g;
+  h.M = g.M - r;
+  if (g.a_src) h.a_src = g.a_src + r;
+  else h.A = g.A + (size_t)r * g.lda;
+  if (EPI == EPI_RESID_F32 || EPI == EPI_F32) h.C = (float*)g.C + (size_t)r * g.ldc;
+  else h.C = (bf16_t*)g.C + (size_t)r * g.ldc;
+  if (EPI == EPI_QKV) {
+    h.qk.q_out = g.qk.q_out + (size_t)r * g.qk.H;
+    h.qk.slots = g.qk.slots + r;
+  }
+  return h;
+}
+
 // tile configurations: 0 = 128x128 (4 waves of 64x64), 1 = 256x256 (8 waves of 64x128), 2 = 256x128 (8 waves of 64x64)
 template <int EPI, bool TAPS>
 hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
+  const bool by_shape = cfg < 0;
   if (cfg < 0) cfg = pick_cfg(g);
+  // A 256x256 grid whose last round would leave most of the 256 CUs idle (qkv at 12,800 tokens: 600 tiles = two
+  // rounds + 88) runs the rows of its full rounds on 256x256 tiles and the rest on 256x128 tiles, one round of
+  // half-size tiles instead of a third round of mostly idle CUs.  The products are the same per output element.
+  if (by_shape && cfg == 1 && !g.w_scale) {
+    const long gn = (g.N + 255) / 256, tiles = (long)((g.M + 255) / 256) * gn;
+    const long rounds = (tiles + 255) / 256, last = tiles - (rounds - 1) * 256;
+    const int rows1 = (int)((rounds - 1) * 256 / gn) * 256;
+    const long tiles2 = (long)((g.M - rows1 + 255) / 256) * ((g.N + 127) / 128);
+    if (rounds >= 2 && 2 * last < 256 && rows1 > 0 && rows1 < g.M && tiles2 <= 256) {
+      GemmArgs g1 = g;
+      g1.M = rows1;
+      const hipError_t e = launch_tile<256, 256, 4, 2, EPI, TAPS>(g1, st);
+      if (e != hipSuccess) return e;
+      return launch_tile<256, 128, 4, 2, EPI, TAPS>(rows_from<EPI>(g, rows1), st);
+    }
+  }
   switch (cfg) {
     case 0: return launch_tile<128, 128, 2, 2, EPI, TAPS>(g, st);
     case 1: return launch_tile<256, 256, 4, 2, EPI, TAPS>(g, st);

@@ -27,9 +27,12 @@ def _gemm(A, W, bias, C_, epi, gate=None, a_src=None, lda=None, K=None, ws=None)
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 256, 64), (100, 80, 1024), (333, 1024, 320), (1000, 3072, 1024), (257, 2048, 2048)])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 64), (100, 80, 1024), (333, 1024, 320), (1000, 3072, 1024), (257, 2048, 2048),
+                                   (5400, 3072, 1024)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 def test_gemm_dense(dev, M, N, K, epi):
+    """5400 x 3072: 264 tiles of 256 x 256, so the rows of the first full round run on 256 x 256 tiles and the last
+    24 rows on 256 x 128 tiles (a second round of 8 tiles would leave most CUs idle)."""
     g = torch.Generator(device=dev).manual_seed(M * 7 + N + K + epi)
     A = torch.randn(M, K, device=dev, generator=g).bfloat16()
     W = (torch.randn(N, K, device=dev, generator=g) / K ** 0.5).bfloat16()
@@ -51,6 +54,23 @@ def test_gemm_dense(dev, M, N, K, epi):
         out = torch.zeros(M, N, device=dev)
         _gemm(A, W, bias, out, 3)
         assert rel(out, ref) < 1e-5
+
+
+def test_gemm_row_split_taps(dev):
+    """The row split of a mostly idle last round in taps mode: the second launch reads its frames through the frame ids
+    of its own rows."""
+    M, N, H = 5400, 3072, 1024
+    g = torch.Generator(device=dev).manual_seed(77)
+    P = torch.randn(M + 40, H, device=dev, generator=g).bfloat16()
+    a_src = (torch.arange(M, device=dev) + torch.arange(M, device=dev) // 300 * 2).int()
+    W = (torch.randn(N, 3 * H, device=dev, generator=g) / (3 * H) ** 0.5).bfloat16()
+    bias = torch.randn(N, device=dev, generator=g)
+    out = torch.full((M, N), 7.0, device=dev).bfloat16()
+    _gemm(P, W, bias, out, 0, a_src=a_src, lda=H, K=3 * H)
+    rows = a_src.long()
+    X = torch.cat([P[rows], P[rows + 1], P[rows + 2]], 1).float()
+    ref = X @ W.float().t() + bias
+    assert rel(out.float(), ref) < 6e-3
 
 
 @pytest.mark.parametrize("M,N,K", [(1100, 640, 1024), (2048, 3072, 1024), (1300, 1024, 3072), (300, 256, 128)])
