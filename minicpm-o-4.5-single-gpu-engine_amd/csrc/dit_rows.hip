@@ -175,7 +175,9 @@ __device__ __forceinline__ void normalize(float (&v)[VPL], int H, float eps) {
 }
 
 // out: bf16 [N, H]; or, with q non-null, MX fp8 codes q [N, H] and block scales qs [N, H / 32]
-template <int VPL>
+// PEND: a pending GEMM result is finished first (a separate instantiation, so that the large calls, which never defer,
+// keep the registers and occupancy of the plain kernel)
+template <int VPL, bool PEND>
 __global__ void __launch_bounds__(256) ln_mod_kernel(float* h, const float* shift, const float* scale1, float eps,
                                                      bf16_t* out, uint8_t* q, uint8_t* qs, int N, int H, Pend pd) {
   const int lane = threadIdx.x & 63;
@@ -183,7 +185,7 @@ __global__ void __launch_bounds__(256) ln_mod_kernel(float* h, const float* shif
   if (n >= N) return;
   float v[VPL], sc[VPL], sh[VPL];
   row_load_f32<VPL, 4>(h + (size_t)n * H, lane, v);
-  if (pd.part) pend_resid<VPL, 4>(pd, h + (size_t)n * H, n, lane, v);
+  if (PEND) pend_resid<VPL, 4>(pd, h + (size_t)n * H, n, lane, v);
   normalize<VPL>(v, H, eps);
   row_load_f32<VPL, 4>(scale1, lane, sc);
   row_load_f32<VPL, 4>(shift, lane, sh);
@@ -238,7 +240,7 @@ __device__ __forceinline__ void place_row(const ConvPlace& cp, int r, int H, int
   }
 }
 
-template <int VPL>
+template <int VPL, bool PEND>
 __global__ void __launch_bounds__(256) ln_mod_conv_kernel(float* h, const float* shift, const float* scale1, float eps,
                                                           ConvPlace cp, int H, Pend pd) {
   const int lane = threadIdx.x & 63;
@@ -246,7 +248,7 @@ __global__ void __launch_bounds__(256) ln_mod_conv_kernel(float* h, const float*
   if (w < cp.N) {
     float v[VPL], sc[VPL], sh[VPL];
     row_load_f32<VPL, 4>(h + (size_t)w * H, lane, v);
-    if (pd.part) pend_resid<VPL, 4>(pd, h + (size_t)w * H, w, lane, v);
+    if (PEND) pend_resid<VPL, 4>(pd, h + (size_t)w * H, w, lane, v);
     normalize<VPL>(v, H, eps);
     row_load_f32<VPL, 4>(scale1, lane, sc);
     row_load_f32<VPL, 4>(shift, lane, sh);
@@ -260,7 +262,7 @@ __global__ void __launch_bounds__(256) ln_mod_conv_kernel(float* h, const float*
   }
 }
 
-template <int VPL>
+template <int VPL, bool PEND>
 __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, const float* lw, const float* lb, float eps,
                                                            ConvPlace cp, int H, Pend pd) {
   const int lane = threadIdx.x & 63;
@@ -268,7 +270,7 @@ __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, cons
   if (w < cp.N) {
     constexpr int G = VPL >= 8 ? 8 : 4;  // the row comes in as bf16
     float v[VPL], a[VPL], b[VPL];
-    if (pd.part) {  // the pending conv GEMM's value, rounded to bf16 as its own epilogue would
+    if (PEND) {  // the pending conv GEMM's value, rounded to bf16 as its own epilogue would
       pend_value<VPL, G>(pd, w, lane, v);
 #pragma unroll
       for (int i = 0; i < VPL; ++i) v[i] = bf2f(f2bf(v[i]));
@@ -452,7 +454,11 @@ hipError_t ln_mod(float* h, const float* shift, const float* scale1, float eps, 
                   const Pend& pd) {
   if (N <= 0) return hipSuccess;
   if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H, pd));
+  if (pd.part) {
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, true>), dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H, pd));
+  } else {
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, false>), dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H, pd));
+  }
   return hipGetLastError();
 }
 
@@ -460,7 +466,7 @@ hipError_t ln_mod_mx8(const float* h, const float* shift, const float* scale1, f
                       int H, hipStream_t st) {
   if (N <= 0) return hipSuccess;
   // nothing pending: h is only read
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_kernel<V>, dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, const_cast<float*>(h), shift, scale1, eps, nullptr, q, qs, N, H, Pend()));
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, false>), dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, const_cast<float*>(h), shift, scale1, eps, nullptr, q, qs, N, H, Pend()));
   return hipGetLastError();
 }
 
@@ -468,7 +474,11 @@ hipError_t ln_mod_conv(float* h, const float* shift, const float* scale1, float 
                        const Pend& pd) {
   if (cp.N + cp.R <= 0) return hipSuccess;
   if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mod_conv_kernel<V>, dim3(blocks_for(cp.N + cp.R, row_waves(cp.N + cp.R))), dim3(64 * row_waves(cp.N + cp.R)), 0, st, h, shift, scale1, eps, cp, H, pd));
+  if (pd.part) {
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_conv_kernel<V, true>), dim3(blocks_for(cp.N + cp.R, row_waves(cp.N + cp.R))), dim3(64 * row_waves(cp.N + cp.R)), 0, st, h, shift, scale1, eps, cp, H, pd));
+  } else {
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_conv_kernel<V, false>), dim3(blocks_for(cp.N + cp.R, row_waves(cp.N + cp.R))), dim3(64 * row_waves(cp.N + cp.R)), 0, st, h, shift, scale1, eps, cp, H, pd));
+  }
   return hipGetLastError();
 }
 
@@ -476,7 +486,11 @@ hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float e
                         const Pend& pd) {
   if (cp.N + cp.R <= 0) return hipSuccess;
   if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(ln_mish_conv_kernel<V>, dim3(blocks_for(cp.N + cp.R, row_waves(cp.N + cp.R))), dim3(64 * row_waves(cp.N + cp.R)), 0, st, y, w, b, eps, cp, H, pd));
+  if (pd.part) {
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mish_conv_kernel<V, true>), dim3(blocks_for(cp.N + cp.R, row_waves(cp.N + cp.R))), dim3(64 * row_waves(cp.N + cp.R)), 0, st, y, w, b, eps, cp, H, pd));
+  } else {
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mish_conv_kernel<V, false>), dim3(blocks_for(cp.N + cp.R, row_waves(cp.N + cp.R))), dim3(64 * row_waves(cp.N + cp.R)), 0, st, y, w, b, eps, cp, H, pd));
+  }
   return hipGetLastError();
 }
 
