@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <initializer_list>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -140,23 +141,24 @@ GemmArgs gemm8(const uint8_t* A, int lda, const int* a_src, const uint8_t* as, c
 }
 
 // K splits of the deferred GEMMs of a call of N tokens (0: no deferral): enough workgroups to occupy the 256 CUs, at
-// most 4 (the row kernels' limit), and the sums must fit the partial area.  Taken only when every deferred GEMM fits the
-// small-row kernel.  Tiles are 64 rows above 32 tokens (gemm_small_part64).
-int defer_splits(const t2w_dit_dims& d, int N, const Work& w) {
+// most 4 (the row kernels' limit), and the sums must fit the partial area; 0 unless the deferred GEMMs of the kind fit
+// the small-row kernel.  The conv GEMMs (taps) run on 64-row tiles above 32 tokens (gemm_small_part64), proj and fc2
+// on 32-row tiles (measured faster for them: K = 1024 / 2048 leaves 64-row tiles too few steps per workgroup).
+int defer_splits(const t2w_dit_dims& d, int N, const Work& w, bool taps) {
   const int H = d.hidden;
   if (N > GEMM_SMALL_MAX_M || !w.part) return 0;
-  const int rows = N > 32 ? 64 : 32;
+  const int rows = taps && N > 32 ? 64 : 32;
   const int tiles = ((N + rows - 1) / rows) * ((H + 31) / 32);
   const int S = std::min(4, 256 / tiles);
   if (S < 2 || (size_t)S * N * H * 4 > w.part_bytes) return 0;
+  static const int taps_marker = 0;  // gemm_small_fits checks only the presence of a frame id list
   GemmArgs g{};
-  g.M = N; g.N = H; g.lda = H; g.ldb = H; g.ldc = H; g.splits = S;
-  for (int K : {H, 3 * H, d.ffn}) {
+  g.M = N; g.N = H; g.ldc = H; g.splits = S; g.tapC = H;
+  for (int K : taps ? std::initializer_list<int>{3 * H} : std::initializer_list<int>{H, d.ffn}) {
     g.K = K;
     g.ldb = K;
-    g.lda = K == 3 * H ? H : K;
-    g.a_src = K == 3 * H ? (const int*)&w : nullptr;  // taps mode (only the pointer's presence is checked)
-    g.tapC = H;
+    g.lda = taps ? H : K;
+    g.a_src = taps ? &taps_marker : nullptr;
     if (!gemm_small_fits(g, EPI_PART)) return 0;
   }
   return S;
@@ -184,7 +186,8 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
   const bool f8 = a->fp8 != 0;
   // Calls of few tokens: the gated-residual GEMMs and conv1 split K over several workgroups per tile and the row
   // kernel that reads their result next finishes their epilogue (pend: the result it has to finish).
-  const int S = f8 ? 0 : defer_splits(d, N, w);
+  const int Sd = f8 ? 0 : defer_splits(d, N, w, false), St = f8 ? 0 : defer_splits(d, N, w, true);
+  const bool S = Sd > 0 && St > 0;  // deferral on: proj / fc2 split Sd ways, conv1 / conv2 St ways
   Pend pend;
   hipError_t perr = hipSuccess;
   for (int b = 0; b < D; ++b) {
@@ -222,7 +225,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     if (f8)
       T2W_CHECK(gemm_bf16(gemm8(w.o8, H, nullptr, w.o8s, k8->proj_w8, k8->proj_ws, k.proj_b, g_a, w.h, H, N, H, H), EPI_RESID_F32, st), "proj");
     else if (S) {
-      pend = gemm_deferred(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), S, w, st, &perr);
+      pend = gemm_deferred(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), Sd, w, st, &perr);
       T2W_CHECK(perr, "proj");
     } else {
       T2W_CHECK(gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F32, st), "proj");
@@ -239,7 +242,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     if (f8) {
       T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c1_w8, k8->c1_ws, k.c1_b, nullptr, w.ao, H, N, H, 3 * H), EPI_BF16, st), "conv1");
     } else if (S) {
-      pend = gemm_deferred(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), S, w, st, &perr);
+      pend = gemm_deferred(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), St, w, st, &perr);
       T2W_CHECK(perr, "conv1");
     } else {
       T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), EPI_BF16, st), "conv1");
@@ -251,7 +254,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     if (f8) {
       T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c2_w8, k8->c2_ws, k.c2_b, g_c, w.h, H, N, H, 3 * H), EPI_RESID_F32, st), "conv2");
     } else if (S) {
-      pend = gemm_deferred(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), S, w, st, &perr);
+      pend = gemm_deferred(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), St, w, st, &perr);
       T2W_CHECK(perr, "conv2");
     } else {
       T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), EPI_RESID_F32, st), "conv2");
@@ -268,7 +271,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
       pend = Pend();
       T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.fc1_w, k.fc1_b, nullptr, w.big, F, N, F, H, &w), EPI_GELU_BF16, st), "fc1");
       if (S) {
-        pend = gemm_deferred(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), S, w, st, &perr);
+        pend = gemm_deferred(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), Sd, w, st, &perr);
         T2W_CHECK(perr, "fc2");
       } else {
         T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F32, st), "fc2");

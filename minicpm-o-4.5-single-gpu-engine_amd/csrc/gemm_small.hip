@@ -355,7 +355,9 @@ bool gemm_small_fits(const GemmArgs& g, int epi) {
          (!g.a_src || g.tapC % 64 == 0);
 }
 
-bool gemm_small_part64(const GemmArgs& g) { return g.M > 32 && (g.K / 64 + g.splits - 1) / g.splits <= GS_WAVES; }
+bool gemm_small_part64(const GemmArgs& g) {
+  return g.a_src && g.M > 32 && (g.K / 64 + g.splits - 1) / g.splits <= GS_WAVES;
+}
 
 hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st) {
   if (!gemm_small_fits(g, epi)) return hipErrorInvalidValue;

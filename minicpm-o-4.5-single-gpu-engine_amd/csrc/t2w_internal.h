@@ -73,7 +73,7 @@ bool gemm_splits(const GemmArgs& g);  // whether gemm_bf16 (cfg < 0) takes the s
 constexpr int GEMM_SMALL_MAX_M = 128;
 bool gemm_small_fits(const GemmArgs& g, int epi);
 hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st);
-// whether an EPI_PART call runs on 64-row tiles (more than 32 rows, at most 16 64-K steps per split)
+// whether an EPI_PART call runs on 64-row tiles (taps mode, more than 32 rows, at most 16 64-K steps per split)
 bool gemm_small_part64(const GemmArgs& g);
 
 // Four-wave 256 x 256 tile GEMM with a four-stage LDS ring (gemm_ring.hip): bf16 operands, every epilogue but
