@@ -3,10 +3,10 @@
 // At ~100 rows the time of a GEMM is the weight stream plus fixed per-kernel costs, and a split-K pass followed by a
 // separate reduce kernel pays those costs twice and moves fp32 partials through HBM.  Here a workgroup of 16 waves
 // owns 32 output columns x 32 rows and splits K over its waves: each wave loads its (at most three) 64-K steps of the
-// W rows and activation rows straight into registers, all loads in flight before the first MFMA (64 contiguous bytes
-// per lane and step, seen by the MFMA as four 16-K slices of the same K permutation on both sides), then leaves its
-// 32x32 fp32 block in LDS.  After one barrier the block is summed over the waves in wave order (deterministic) and the
-// epilogue (bias, GELU, gated fp32 residual) writes four consecutive columns per lane.
+// W rows and activation rows into registers with whole-line loads (two steps in flight from the start), turns each
+// step into MFMA fragments through its LDS slab (four 16-K slices of the same K permutation on both sides), then
+// leaves its 32x32 fp32 block in LDS.  After one barrier the block is summed over the waves in wave order
+// (deterministic) and the epilogue (bias, GELU, gated fp32 residual) writes four consecutive columns per lane.
 //
 // A workgroup moves its W and activation rows through one CU, and a CU's load throughput (not HBM) is what bounds
 // these calls: ~100 rows x K = 3072 (conv taps) is 384 KB per workgroup on 128 CUs.  EPI_PART therefore also splits K
