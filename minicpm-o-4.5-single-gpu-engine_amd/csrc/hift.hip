@@ -539,12 +539,13 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_bf16_split_kernel(ConvDesc
 }
 
 // The fp32 convolution for small grids (the f0 predictor of a streaming window: ~50 frames x 512 channels), on the
-// same plan as conv_bf16_split_kernel: 32 output rows x 64 output channels per workgroup, the (tap, 32-channel input
+// same plan as conv_bf16_split_kernel: 32 output rows x NB * 32 output channels per workgroup, the (tap, 32-channel input
 // chunk) steps split over the waves, operands straight into registers with the next step's loads in flight, fp32 MFMA
 // (v_mfma_f32_32x32x2f32; lane half h supplies channels h * 16 + u of MFMA u on both sides), blocks summed in LDS in
 // wave order.
+template <int NB>
 __global__ void __launch_bounds__(64 * CS_WAVES) conv_f32_split_kernel(ConvDesc c) {
-  __shared__ float4 red[CS_WAVES][2][4][64];
+  __shared__ float4 red[CS_WAVES][NB][4][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, cl = lane & 31;
   const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
   const int Tin = c.in_len[b], Tout = c.out_len[b];
@@ -553,7 +554,7 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_f32_split_kernel(ConvDesc 
   const int r_hi = Tout - 1 - oo < 0 ? -1 : (Tout - 1 - oo) / c.s_out;
   const int r0 = r_lo + blockIdx.x * 32;
   if (r0 > r_hi) return;
-  const int co0 = blockIdx.y * 64;
+  const int co0 = blockIdx.y * (NB * 32);
   const float* xb = c.x + (size_t)c.in_off[b] * c.ldx;
   const float* wph = c.w + (size_t)ph * c.Cout * c.taps * c.Cin;
   const int nch = (c.Cin + 31) / 32, NS = c.taps * nch;
@@ -562,7 +563,7 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_f32_split_kernel(ConvDesc 
   const bool vec = c.Cin % 4 == 0 && c.ldx % 4 == 0;  // 16-byte loads of whole 4-channel groups
 
   // step s: tap j = s / nch, this lane's channels cc .. cc + 15 with cc = (s % nch) * 32 + h * 16, activation applied
-  auto load = [&](int st, float4 (&xv)[4], float4 (&wv)[2][4]) {
+  auto load = [&](int st, float4 (&xv)[4], float4 (&wv)[NB][4]) {
     const int j = st / nch, cc = (st - j * nch) * 32 + h * 16;
     const int in_row = r * c.s_in + j * c.d_in + c.off_in[ph];
     const bool rok = r <= r_hi && in_row >= 0 && in_row < Tin;
@@ -578,7 +579,7 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_f32_split_kernel(ConvDesc 
       }
     }
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
+    for (int jj = 0; jj < NB; ++jj) {
       const int co = co0 + jj * 32 + cl;
       const float* wp = wph + ((size_t)(co < c.Cout ? co : 0) * c.taps + j) * c.Cin + cc;
 #pragma unroll
@@ -593,7 +594,7 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_f32_split_kernel(ConvDesc 
       }
     }
   };
-  auto mma = [&](int st, const float4 (&xv)[4], const float4 (&wv)[2][4], f32x16 (&acc)[2]) {
+  auto mma = [&](int st, const float4 (&xv)[4], const float4 (&wv)[NB][4], f32x16 (&acc)[NB]) {
     const int j = st / nch, cc = (st - j * nch) * 32 + h * 16;
     const int in_row = r * c.s_in + j * c.d_in + c.off_in[ph];
     const bool rok = r <= r_hi && in_row >= 0 && in_row < Tin;
@@ -606,21 +607,21 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_f32_split_kernel(ConvDesc 
       float v = xs[u];
       if (c.pre && ok) v = pre_act(v, c.pre, c.slope, c.alpha ? c.alpha[ci] : 0.f, c.inv ? c.inv[ci] : 0.f);
       v = ok ? v : 0.f;
-      const float4* w0 = wv[0];
-      const float4* w1 = wv[1];
-      const float a0 = (u & 3) == 0 ? w0[u >> 2].x : (u & 3) == 1 ? w0[u >> 2].y : (u & 3) == 2 ? w0[u >> 2].z : w0[u >> 2].w;
-      const float a1 = (u & 3) == 0 ? w1[u >> 2].x : (u & 3) == 1 ? w1[u >> 2].y : (u & 3) == 2 ? w1[u >> 2].z : w1[u >> 2].w;
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, v, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, v, acc[1], 0, 0, 0);
+#pragma unroll
+      for (int jj = 0; jj < NB; ++jj) {
+        const float4 w4 = wv[jj][u >> 2];
+        const float a = (u & 3) == 0 ? w4.x : (u & 3) == 1 ? w4.y : (u & 3) == 2 ? w4.z : w4.w;
+        acc[jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, v, acc[jj], 0, 0, 0);
+      }
     }
   };
 
-  f32x16 acc[2];
+  f32x16 acc[NB];
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj)
+  for (int jj = 0; jj < NB; ++jj)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[jj][i] = 0.f;
-  float4 xa[4], xb2[4], wa[2][4], wb2[2][4];
+  float4 xa[4], xb2[4], wa[NB][4], wb2[NB][4];
   if (s0 < s1) load(s0, xa, wa);
   for (int st = s0; st < s1; st += 2) {
     if (st + 1 < s1) load(st + 1, xb2, wb2);
@@ -631,10 +632,11 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_f32_split_kernel(ConvDesc 
     }
   }
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj)
+  for (int jj = 0; jj < NB; ++jj)
 #pragma unroll
     for (int q = 0; q < 4; ++q) red[w][jj][q][lane] = make_float4(acc[jj][4 * q], acc[jj][4 * q + 1], acc[jj][4 * q + 2], acc[jj][4 * q + 3]);
   __syncthreads();
+  if (tid >= NB * 256) return;
   const int jj = tid >> 8, q = (tid >> 6) & 3, l = tid & 63;
   float4 sum = red[0][jj][q][l];
 #pragma unroll
@@ -643,7 +645,7 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_f32_split_kernel(ConvDesc 
     sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
   }
   const int ro = r0 + (l & 31), cn = jj * 32 + q * 8 + (l >> 5) * 4;
-  const int ncols = min(64, c.Cout - co0);
+  const int ncols = min(NB * 32, c.Cout - co0);
   if (ro > r_hi || cn >= ncols) return;
   const size_t orow = (size_t)c.out_off[b] + (size_t)(ro * c.s_out + oo);
   if (cn + 3 < ncols) conv_epilogue4(c, orow, co0 + cn, sum);
@@ -809,8 +811,15 @@ hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
   // grids that would keep fewer than half the CUs busy: 32-row tiles with the taps and channels split over the waves
   const long tiles = (long)cdiv(max_rows, CBM) * cdiv(c.Cout, CBN) * c.n_items * c.n_phase;
   if (tiles < 128) {
-    dim3 grid(cdiv(max_rows, 32), cdiv(c.Cout, 64), c.n_items * c.n_phase);
-    hipLaunchKernelGGL(conv_f32_split_kernel, grid, dim3(64 * CS_WAVES), 0, st, c);
+    // 32 output channels per workgroup while that grid fits the chip in one round (half the weight bytes each), else 64
+    const long t32 = (long)cdiv(max_rows, 32) * cdiv(c.Cout, 32) * c.n_items * c.n_phase;
+    if (t32 <= 256) {
+      dim3 grid(cdiv(max_rows, 32), cdiv(c.Cout, 32), c.n_items * c.n_phase);
+      hipLaunchKernelGGL(conv_f32_split_kernel<1>, grid, dim3(64 * CS_WAVES), 0, st, c);
+    } else {
+      dim3 grid(cdiv(max_rows, 32), cdiv(c.Cout, 64), c.n_items * c.n_phase);
+      hipLaunchKernelGGL(conv_f32_split_kernel<2>, grid, dim3(64 * CS_WAVES), 0, st, c);
+    }
     return hipGetLastError();
   }
   dim3 grid(cdiv(max_rows, CBM), cdiv(c.Cout, CBN), c.n_items * c.n_phase);
