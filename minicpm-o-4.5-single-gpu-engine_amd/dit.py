@@ -151,70 +151,140 @@ class DiTModel:
 # --- stream state ---------------------------------------------------------------------------------------------------
 
 class SlotPool:
-    """Host free list of key slots (``engine/runtime/dit_fast.py:58-78``)."""
+    """Slot ids of the key/value pools (a slot holds one cached frame of one CFG row in every (Euler step, block) pool).
 
-    def __init__(self, n: int):
-        self.n = n
-        self.free = list(range(n - 1, -1, -1))
+    Free ids live in one int32 array used as a stack (``_stack[:_top]``, the next id handed out on top).  ``reserved``
+    ids are taken once at construction and never returned: padding tokens of bucketed calls write their keys there.
+    They count as in use, as the reference's reserved padding slots do (callers subtract ``FastDiT.scratch``)."""
 
-    def alloc(self, k: int) -> list[int]:
-        if k > len(self.free):
-            raise RuntimeError(f"Token2Wav cache pool exhausted ({k} slots wanted, {len(self.free)} free of {self.n})")
-        out = self.free[len(self.free) - k:][::-1] if k else []
-        del self.free[len(self.free) - k:]
-        return out
+    def __init__(self, n: int, reserved: int = 0):
+        self.n = int(n)
+        self._stack = np.arange(self.n - 1, -1, -1, dtype=np.int32)
+        self._top = self.n
+        self.reserved = self.alloc(reserved)
 
-    def release(self, ids: list[int]) -> None:
-        self.free.extend(ids)
+    def alloc(self, k: int) -> np.ndarray:
+        k = int(k)
+        if k > self._top:
+            raise RuntimeError(f"Token2Wav key/value slots exhausted: {k} needed, {self._top} of {self.n} free")
+        self._top -= k
+        return self._stack[self._top:self._top + k][::-1].copy()
+
+    def release(self, ids) -> None:
+        ids = np.asarray(ids, dtype=np.int32).ravel()
+        self._stack[self._top:self._top + ids.size] = ids
+        self._top += ids.size
 
     def in_use(self) -> int:
-        return self.n - len(self.free)
+        return self.n - self._top
+
+    @property
+    def n_free(self) -> int:
+        return self._top
+
+
+_NO_SLOTS = np.zeros(0, dtype=np.int32)
 
 
 @dataclass
 class FastRow:
-    """One CFG row: key slots in the reference tensor order (newest window first) and its two conv-cache row slots
-    (the current one is read, the other written)."""
-    order: list[int] = field(default_factory=list)
-    cnn: tuple[int, int] = (-1, -1)
+    """Cached frames of one CFG row of a stream.  ``slots``: key/value slot ids, the newest window's frames first (the
+    order the reference concatenates ``[new, cache]`` in, which the trim relies on).  ``conv``: two row slots of the
+    conv-cache pool; ``conv[cur]`` holds the two cached frames per (step, block, conv), a kept window writes the other
+    one and flips ``cur``."""
+    slots: np.ndarray = field(default_factory=lambda: _NO_SLOTS)
+    conv: tuple = (-1, -1)
     cur: int = 0
+
+    @property
+    def order(self) -> list[int]:
+        return self.slots.tolist()
 
 
 @dataclass
 class FastCache:
-    """A request's estimator caches (conditional and unconditional row) and its trim length (prompt mel frames)."""
-    rows: tuple[FastRow, FastRow]
+    """Estimator state of one stream: its conditional and unconditional rows, and ``keep``, the number of cached frames
+    the trim always keeps from the newest end (the prompt's mel frames)."""
+    rows: tuple
     keep: int = 0
 
     @property
     def length(self) -> int:
-        return len(self.rows[0].order)
+        return int(self.rows[0].slots.size)
 
 
-def plan_call(rows: list[FastRow], Ts: list[int], new: list[list[int]], keep: list[bool], cnn_scratch: int) -> dict:
-    """Host plan of one call (``engine/runtime/dit_fast.py:223-266``): rows ``[cond 0..n-1 | uncond 0..n-1]`` each with
-    its window's ``Ts[i]`` tokens and freshly allocated key slots ``new[r]``.  Returns the device tables (in
-    ``t2w_solve_args`` order; kv_idx last because its length varies) and the bookkeeping the solve needs afterwards."""
+def _tile_list(lens: np.ndarray) -> np.ndarray:
+    """(row, first query) of every 64-query attention tile of rows with ``lens`` tokens, interleaved."""
+    per = (lens + 63) // 64
+    rows = np.repeat(np.arange(lens.size, dtype=np.int64), per)
+    first = np.arange(rows.size, dtype=np.int64) - np.repeat(np.cumsum(per) - per, per)
+    return np.stack([rows, 64 * first], 1).ravel()
+
+
+def _layout(lens, new, kv, rd, wr) -> list[np.ndarray]:
+    """The device tables of a call (``t2w_solve_args`` order, ``kv_idx`` last) from its rows in call order: token counts
+    ``lens``, new key slots ``new[r]``, key lists ``kv[r]`` and conv-cache read / write slots."""
+    lens = np.asarray(lens, dtype=np.int64)
+    starts = np.cumsum(lens) - lens
+    tok_row = np.repeat(np.arange(lens.size, dtype=np.int64), lens)
+    idx = np.arange(tok_row.size, dtype=np.int64)
+    tok_pos = idx - starts[tok_row]
+    kv_len = np.array([x.size for x in kv], dtype=np.int64)
+    cat = lambda xs: np.concatenate(xs) if len(xs) else _NO_SLOTS  # noqa: E731
+    return [tok_row, tok_pos, idx + 2 * tok_row, cat(new), starts, lens, np.cumsum(kv_len) - kv_len, kv_len,
+            np.asarray(rd, dtype=np.int64), np.asarray(wr, dtype=np.int64), _tile_list(lens), cat(kv)]
+
+
+def plan_call(rows: list[FastRow], Ts: list[int], new: list[np.ndarray], keep: list[bool], cnn_scratch: int, cnn_zero: int | None = None,
+              bucket: tuple[int, int] | None = None, kv_scratch: int | None = None) -> dict:
+    """Host plan of one call over ``n`` requests (``engine/runtime/dit_fast.py:223-266``): rows ``[cond 0..n-1 | uncond
+    0..n-1]``, row r with its window's ``Ts[r % n]`` tokens and freshly allocated key slots ``new[r]``; a row's keys are
+    its new frames, then its cache (masking is by position).  A kept window's conv caches go to the row's other conv
+    slot, others to ``cnn_scratch``.
+
+    ``bucket = (rb, nb)`` pads the call to a graph bucket: each CFG half then holds its requests, ``rb / 2 - n`` empty
+    rows and one padding row with the half's ``nb / 2 - sum(Ts)`` padding tokens, which write their keys to slot
+    ``kv_scratch`` and attend to it alone; empty and padding rows read the zero conv slot ``cnn_zero`` and write
+    ``cnn_scratch``; the tile list is filled to ``bucket_tiles`` with tiles past a row's end (skipped by the kernel).
+    No real row reads padding data: every kernel works within a token or a row.
+
+    Returns the tables (``parts``) and what the solve needs afterwards."""
     n = len(Ts)
-    lens = Ts + Ts
-    tok_row, tok_pos, new_slot = [], [], []
-    row_start, row_kv_off, row_kv_len, rd, wr, kv, tiles = [], [], [], [], [], [], []
-    o = 0
-    for r, (row, t, nw) in enumerate(zip(rows, lens, new)):
-        row_start.append(o)
-        tok_row += [r] * t
-        tok_pos += list(range(t))
-        new_slot += nw
-        row_kv_off.append(len(kv))
-        kv += nw + row.order  # the row's new frames first (masking is by position), then its cache
-        row_kv_len.append(t + len(row.order))
-        rd.append(row.cnn[row.cur])
-        wr.append(row.cnn[1 - row.cur] if keep[r % n] else cnn_scratch)
-        tiles += [v for q0 in range(0, t, 64) for v in (r, q0)]
-        o += t
-    a_src = [i + 2 * r for i, r in enumerate(tok_row)]
-    parts = [tok_row, tok_pos, a_src, new_slot, row_start, lens, row_kv_off, row_kv_len, rd, wr, tiles, kv]
-    return {"n_tok": o, "n_rows": 2 * n, "half": o // 2, "n_tiles": len(tiles) // 2, "parts": parts, "new": new, "rows": rows}
+    half = int(sum(Ts))
+    lens, nw, kv, rd, wr = [], [], [], [], []
+    pad = 0 if bucket is None else bucket[1] // 2 - half
+    extra = 0 if bucket is None else bucket[0] // 2 - n  # empty rows per half
+    zero = cnn_scratch if cnn_zero is None else cnn_zero
+    for h in range(2):
+        for i in range(n):
+            r = rows[h * n + i]
+            lens.append(Ts[i])
+            nw.append(new[h * n + i])
+            kv.append(np.concatenate([new[h * n + i], r.slots]))
+            rd.append(r.conv[r.cur])
+            wr.append(r.conv[1 - r.cur] if keep[i] else cnn_scratch)
+        if bucket is not None:
+            for j in range(extra + 1):
+                T = pad if j == extra else 0
+                pads = np.full(T, kv_scratch, dtype=np.int32)
+                lens.append(T)
+                nw.append(pads)
+                kv.append(pads)
+                rd.append(zero)
+                wr.append(cnn_scratch)
+    parts = _layout(lens, nw, kv, rd, wr)
+    R = len(lens)
+    n_tiles = parts[10].size // 2
+    if bucket is not None:
+        rb, nb = bucket
+        want = bucket_tiles(rb, nb)
+        if n_tiles > want:
+            raise AssertionError("attention tiles beyond the bucket's bound")
+        fill = np.tile(np.array([R - 1, 1 << 30], dtype=np.int64), want - n_tiles)
+        parts[10] = np.concatenate([parts[10], fill])
+        n_tiles = want
+    return {"n_tok": int(sum(lens)), "n_rows": R, "half": half + pad, "real_half": half, "n_tiles": n_tiles, "parts": parts,
+            "new": new, "rows": rows}
 
 
 ROW_BUCKETS = (2, 4, 8, 16, 32, 64)  # request rows (both CFG halves) of a graph bucket, padding rows excluded
@@ -223,22 +293,27 @@ SETUP_TOKENS = 4096  # row buckets up to SETUP_ROWS also take whole-prompt setup
 SETUP_ROWS = 8
 
 
+def bucket_top(rb: int) -> int:
+    """The most tokens (both halves) a row bucket takes: ``MAX_GRAPH_T`` frames per row, and whole prompt setups up to
+    ``SETUP_TOKENS`` in the small buckets (``bucket_top``, ``engine/runtime/dit_fast.py:37-45``)."""
+    return max(rb * MAX_GRAPH_T, SETUP_TOKENS if rb <= SETUP_ROWS else 0)
+
+
 def token_buckets(rb: int) -> list[int]:
-    """Token buckets (both halves) of row bucket ``rb`` (``token_buckets``, ``engine/runtime/dit_fast.py:43-55``):
-    multiples of 128 below 512, then of 256, up to the bucket's top (``MAX_GRAPH_T`` frames per row, at least
-    ``SETUP_TOKENS`` for small buckets), which is a bucket itself."""
-    top = max(rb * MAX_GRAPH_T, SETUP_TOKENS if rb <= SETUP_ROWS else 0)
-    return [b for b in list(range(128, 512, 128)) + list(range(512, top, 256)) if b < top] + [top]
+    """Token buckets (both halves) of row bucket ``rb`` (``token_buckets``, ``engine/runtime/dit_fast.py:48-55``): steps of
+    128 below 512, of 256 from there, and the bucket's top."""
+    top = bucket_top(rb)
+    steps = [b for b in range(128, 512, 128)] + [b for b in range(512, top, 256)]
+    return [b for b in steps if b < top] + [top]
 
 
 def bucket_of(n_rows: int, n_tok: int) -> tuple[int, int] | None:
-    """The smallest row bucket holding ``n_rows`` request rows with a token bucket for ``n_tok`` tokens, and that token
-    bucket (``FastDiT._bucket``, ``engine/runtime/dit_fast.py:212-221``); None when no bucket fits."""
-    for rb in ROW_BUCKETS:
-        if rb >= n_rows:
-            nb = next((b for b in token_buckets(rb) if b >= n_tok), None)
-            if nb is not None:
-                return rb, nb
+    """The (row bucket, token bucket) a call of ``n_rows`` request rows and ``n_tok`` tokens pads to: the first row
+    bucket with room for both, and its smallest token bucket that holds the call; None when none does."""
+    for rb in (b for b in ROW_BUCKETS if b >= n_rows):
+        fits = [b for b in token_buckets(rb) if b >= n_tok]
+        if fits:
+            return rb, fits[0]
     return None
 
 
@@ -248,114 +323,81 @@ def bucket_tiles(rb: int, nb: int) -> int:
     return 2 * ((nb // 2 + 63) // 64 + rb // 2 + 1)
 
 
-def pad_plan(p: dict, rb: int, nb: int, kv_scratch: int, cnn_scratch: int) -> dict:
-    """Pads a call's plan to bucket ``(rb, nb)`` (the layout of ``FastDiT._plan``, ``engine/runtime/dit_fast.py:223-263``):
-    each CFG half holds its request rows, ``rb / 2 - n`` empty rows and one padding row carrying the half's
-    ``nb / 2 - half`` padding tokens.  Padding tokens have zero inputs, write their keys and values to one scratch slot
-    and attend to it alone; empty and padding rows read and write the scratch conv-cache slot; their outputs are
-    discarded.  No real row reads padding data, since every kernel works within a token or a row.  The attention tile
-    list is filled up to ``bucket_tiles`` with tiles past a row's end, which the kernel skips."""
-    tok_row, tok_pos, _, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, kv = p["parts"]
-    n = p["n_rows"] // 2
-    hr, half_b = rb // 2 + 1, nb // 2
-    pad = half_b - p["half"]
-    row_tiles: dict[int, list[int]] = {}
-    for i in range(0, len(tiles), 2):
-        row_tiles.setdefault(tiles[i], []).append(tiles[i + 1])
-    out = [[] for _ in range(12)]
-    t_row, t_pos, _, t_slot, t_start, t_len, t_kvo, t_kvl, t_rd, t_wr, t_tiles, t_kv = out
-    o = 0
-    for h in range(2):  # cond half, then uncond half
-        for j in range(hr):
-            r_new = h * hr + j
-            if j < n:  # a request row
-                r = h * n + j
-                s0, T = row_start[r], lens[r]
-                t_pos += tok_pos[s0:s0 + T]
-                t_slot += new_slot[s0:s0 + T]
-                t_kvo.append(len(t_kv))
-                t_kv += kv[kv_off[r]:kv_off[r] + kv_len[r]]
-                t_kvl.append(kv_len[r])
-                t_rd.append(rd[r])
-                t_wr.append(wr[r])
-                q0s = row_tiles.get(r, [])
-            else:  # empty rows, then the padding row
-                T = pad if j == hr - 1 else 0
-                t_pos += list(range(T))
-                t_slot += [kv_scratch] * T
-                t_kvo.append(len(t_kv))
-                t_kv += [kv_scratch] * T
-                t_kvl.append(T)
-                t_rd.append(cnn_scratch)
-                t_wr.append(cnn_scratch)
-                q0s = list(range(0, T, 64))
-            t_row += [r_new] * T
-            t_tiles += [v for q0 in q0s for v in (r_new, q0)]
-            t_start.append(o)
-            t_len.append(T)
-            o += T
-    n_tiles = bucket_tiles(rb, nb)
-    if len(t_tiles) // 2 > n_tiles:
-        raise AssertionError("attention tiles beyond the bucket's bound")
-    t_tiles += [hr - 1, 1 << 30] * (n_tiles - len(t_tiles) // 2)
-    out[2] = [i + 2 * r for i, r in enumerate(t_row)]
-    q = dict(p)
-    q.update({"n_tok": o, "n_rows": 2 * hr, "half": half_b, "n_tiles": n_tiles, "parts": out, "real_half": p["half"]})
-    return q
+def all_buckets() -> list[tuple[int, int]]:
+    return [(rb, nb) for rb in ROW_BUCKETS for nb in token_buckets(rb)]
 
 
-def advance_row(r: FastRow, new: list[int], keep: bool, keep_len: int) -> list[int]:
-    """After a solve: a kept window's slots join the row as ``[new, cache]`` (the reference's concatenation order), then
-    the order is trimmed to its first ``keep_len`` and last 100 entries (``engine/runtime/dit_fast.py:480-490``) and
-    the conv caches swap to the slot just written; a window that is not kept leaves the row as it was.  Returns the
-    slots to release."""
+def advance_row(r: FastRow, new: np.ndarray, keep: bool, keep_len: int) -> np.ndarray:
+    """A row after its window was solved.  A kept window's frames go in front of the cache (``[new, cache]``); a cache
+    longer than ``keep_len + 100`` then drops the entries between its first ``keep_len`` and its last 100
+    (``engine/runtime/dit_fast.py:480-490``), and the conv slots flip.  A window that is not kept leaves the row alone.
+    Returns the slot ids to give back to the pool."""
     if not keep:
-        return list(new)
-    order = new + r.order
-    freed = []
-    if len(order) > keep_len + TRIM_SUFFIX:
-        freed = order[keep_len:len(order) - TRIM_SUFFIX]
-        order = order[:keep_len] + order[len(order) - TRIM_SUFFIX:]
-    r.order = order
-    r.cur = 1 - r.cur
+        return new
+    merged = np.concatenate([new, r.slots])
+    cut = merged.size - TRIM_SUFFIX
+    if cut > keep_len:
+        freed = merged[keep_len:cut].copy()
+        merged = np.concatenate([merged[:keep_len], merged[cut:]])
+    else:
+        freed = _NO_SLOTS
+    r.slots = merged
+    r.cur ^= 1
     return freed
 
 
-def _pad_halves(x: torch.Tensor, real: int, padded: int) -> torch.Tensor:
-    """Conditional-token rows [real, C] padded with zero rows to [padded, C] (the padding rows come last)."""
-    if padded == real:
-        return x
-    return torch.cat([x, x.new_zeros(padded - real, x.shape[1])])
+class _Upload:
+    """Host tables to the device without a wait: a pinned staging copy, then an asynchronous copy on the current
+    stream (the caching host allocator keeps the pinned block until that copy has run)."""
+
+    @staticmethod
+    def into(dst: torch.Tensor, host: np.ndarray) -> None:
+        src = torch.from_numpy(host)
+        if dst.is_cuda:
+            src = src.pin_memory()
+        dst[:host.size].copy_(src, non_blocking=True)
+
+    @staticmethod
+    def new(host: np.ndarray, device) -> torch.Tensor:
+        out = torch.empty(max(host.size, 1), dtype=torch.int32, device=device)
+        _Upload.into(out, host)
+        return out
 
 
 class FastDiT:
-    """The packed ragged CFG Euler solve over per-request caches (``FastDiT`` of ``engine/runtime/dit_fast.py``)."""
+    """The packed ragged CFG Euler solve over per-stream caches (the ``FastDiT`` surface of
+    ``engine/runtime/dit_fast.py``: ``new_cache / release / clone / solve / capture / capture_all``, attributes ``pool``,
+    ``scratch``, ``cnn_free``, ``counts``, ``use_graphs``)."""
 
     def __init__(self, model: DiTModel, n_slots: int = 32768, max_streams: int = 96, use_graphs: bool = False, fp8: bool = False,
-                 buckets: bool = True):
-        """``fp8``: solves run the block GEMMs on fp8 MFMA (the model must have been built with fp8 weights).
-        ``buckets`` (with ``use_graphs``): a call that fits a (rows, tokens) bucket is padded to it, so that one captured
-        graph serves every call of the bucket; other calls (and every call without ``buckets``) take a graph keyed by
-        their exact shape."""
-        self.buckets = buckets
+                 buckets: bool = True, max_exact_graphs: int = 8):
+        """``n_slots`` cached frames per pool (one CFG row's frame each).  ``fp8``: the block GEMMs on fp8 MFMA (the model
+        needs fp8 weights).  ``use_graphs``: every call replays a captured hipGraph of its whole 10-step solve; with
+        ``buckets`` a call that fits a (rows, tokens) bucket is padded to it, so one graph serves all its calls
+        (``capture_all`` makes them all up front); other calls take a graph of their exact shape (the last
+        ``max_exact_graphs`` are kept)."""
         if fp8 and not model.fp8:
             raise ValueError("fp8 solves need a DiTModel built with fp8=True")
-        self.fp8 = fp8
         cfg = model.cfg
-        self.model, self.cfg, self.device = model, cfg, model.device
+        self.model, self.cfg, self.device, self.fp8 = model, cfg, model.device, fp8
+        self.use_graphs, self.buckets, self.max_exact_graphs = use_graphs, buckets, max_exact_graphs
         S, D, H = cfg.steps, cfg.depth, cfg.hidden
-        self.pool = SlotPool(n_slots - 1)
-        self.kv_scratch = n_slots - 1  # key slot written by padding tokens, outside the pool
+        self.pool = SlotPool(n_slots, reserved=1)
+        self.kv_scratch = int(self.pool.reserved[0])
+        self.scratch = self.pool.reserved.size  # reserved slots counted by pool.in_use()
         self.n_slots = n_slots
         self.k_pool = torch.zeros(S * D, n_slots, H, dtype=torch.bfloat16, device=self.device)
         self.v_pool = torch.zeros_like(self.k_pool)
         n_rs = 4 * max_streams + 2
         self.conv_pool = torch.zeros(n_rs, S, D, 2, 2, H, dtype=torch.bfloat16, device=self.device)
-        self.cnn_free = list(range(n_rs - 1, -1, -1))
-        self.cnn_scratch = self.cnn_free.pop()  # write slot of rows whose caches are not kept
-        self.use_graphs = use_graphs
-        self.graphs: dict[tuple, tuple] = {}
+        self.cnn_free = list(range(n_rs))
+        self.cnn_zero = self.cnn_free.pop()     # stays zero: read by rows without a cache of their own
+        self.cnn_scratch = self.cnn_free.pop()  # written by rows whose conv caches are not kept
+        self.graphs: dict[tuple, dict] = {}
+        self.exact: dict[tuple, dict] = {}
+        self._arena = None
         self._ws = None
+        self._cap = None
         self.counts = {"graph": 0, "eager": 0}
 
     # --- caches -----------------------------------------------------------------------------------------------------
@@ -364,37 +406,88 @@ class FastDiT:
             raise RuntimeError("Token2Wav conv-cache row slots exhausted")
         rows = []
         for _ in range(2):
-            a, b = self.cnn_free.pop(), self.cnn_free.pop()
-            self.conv_pool[a].zero_()
-            rows.append(FastRow(cnn=(a, b)))
-        return FastCache((rows[0], rows[1]), keep)
+            conv = (self.cnn_free.pop(), self.cnn_free.pop())
+            self.conv_pool[conv[0]].zero_()
+            rows.append(FastRow(conv=conv))
+        return FastCache(tuple(rows), keep)
 
     def release(self, c: FastCache) -> None:
         for r in c.rows:
-            self.pool.release(r.order)
-            r.order = []
-            if r.cnn[0] >= 0:
-                self.cnn_free.extend(r.cnn)
-                r.cnn = (-1, -1)
+            self.pool.release(r.slots)
+            r.slots = _NO_SLOTS
+            if r.conv[0] >= 0:
+                self.cnn_free += list(r.conv)
+                r.conv = (-1, -1)
 
     def clone(self, c: FastCache) -> FastCache:
-        """An independent copy (new slots holding the same keys, values and conv caches)."""
+        """A copy with its own slots holding the same keys, values and conv frames (one gather per pool)."""
         out = self.new_cache(c.keep)
         for src, dst in zip(c.rows, out.rows):
-            self.conv_pool[dst.cnn[0]] = self.conv_pool[src.cnn[src.cur]]
-            dst.order = self.pool.alloc(len(src.order))
-            if src.order:
-                s = torch.tensor(src.order, device=self.device)
-                d = torch.tensor(dst.order, device=self.device)
-                self.k_pool[:, d] = self.k_pool[:, s]
-                self.v_pool[:, d] = self.v_pool[:, s]
+            self.conv_pool[dst.conv[0]].copy_(self.conv_pool[src.conv[src.cur]])
+            dst.slots = self.pool.alloc(src.slots.size)
+        n = c.length
+        if n:
+            ids = _Upload.new(np.concatenate([r.slots for r in c.rows] + [r.slots for r in out.rows]), self.device).long()
+            s, d = ids[:2 * n], ids[2 * n:]
+            for pool in (self.k_pool, self.v_pool):
+                pool.index_copy_(1, d, pool.index_select(1, s))
         return out
 
-    # --- planning ---------------------------------------------------------------------------------------------------
-    def _plan(self, caches: list[FastCache], Ts: list[int], keep: list[bool]) -> dict:
+    # --- inputs -----------------------------------------------------------------------------------------------------
+    def _inputs(self, caches: list[FastCache], mu: list[torch.Tensor], spks: torch.Tensor, cond: list | None, Ts: list[int]):
+        """x0 (the flow's noise buffer read from each stream's cache length on) and the per-token conditioning
+        ``[mu | spk | cond]`` of the conditional half, token-major fp32 (the unconditional half is zero)."""
+        noise, mel, dev = self.model.rand_noise, self.cfg.mel, self.device
+        n, half = len(Ts), int(sum(Ts))
+        starts = np.array([c.length for c in caches], dtype=np.int64)
+        if int((starts + np.asarray(Ts)).max()) > noise.shape[1]:
+            raise RuntimeError("window beyond the flow's noise buffer")
+        # one upload: the noise column and the stream of every conditional token
+        lens = np.asarray(Ts, dtype=np.int64)
+        req = np.repeat(np.arange(n, dtype=np.int64), lens)
+        col = np.arange(half, dtype=np.int64) - np.repeat(np.cumsum(lens) - lens, lens) + starts[req]
+        idx = _Upload.new(np.concatenate([col, req]).astype(np.int32), dev).long()
+        x0 = noise.index_select(1, idx[:half]).t().contiguous()
+        spk_t = spks.to(dev, torch.float32).reshape(n, mel).index_select(0, idx[half:])
+        mu_t = torch.cat([m.to(dev, torch.float32) for m in mu], dim=1).t()
+        if cond is None or all(c is None for c in cond):
+            cond_t = torch.zeros_like(mu_t)
+        else:
+            cond_t = torch.cat([(c.to(dev, torch.float32) if c is not None else m.new_zeros(mel, m.shape[1], dtype=torch.float32))
+                                for c, m in zip(cond, mu)], dim=1).t()
+        return x0, torch.cat([mu_t, spk_t, cond_t], dim=1)
+
+    # --- solve ------------------------------------------------------------------------------------------------------
+    @torch.inference_mode()
+    def solve(self, caches: list[FastCache], mu: list[torch.Tensor], spks: torch.Tensor, cond: list | None,
+              keep: list[bool], chunk: int = 0) -> list[torch.Tensor]:
+        """The CFG Euler solve of one window per stream (``FastDiT.solve``, ``engine/runtime/dit_fast.py:431-495``).
+
+        ``mu[i]`` [mel, T_i]; ``spks`` [n, mel] (after the speaker affine layer); ``cond[i]`` [mel, T_i] or None;
+        ``keep[i]``: keep the window's keys and conv caches (then trim as the reference does), else leave the caches
+        untouched (final flushes).  ``chunk`` > 0: chunk-causal attention among each row's new frames.  Returns each
+        stream's mel [mel, T_i] in fp32.  Nothing waits for the GPU."""
+        Ts = [int(m.shape[1]) for m in mu]
+        x0, stat = self._inputs(caches, mu, spks, cond, Ts)
         rows = [c.rows[0] for c in caches] + [c.rows[1] for c in caches]
         new = [self.pool.alloc(t) for t in Ts + Ts]
-        return plan_call(rows, Ts, new, keep, self.cnn_scratch)
+        bucket = bucket_of(2 * len(Ts), 2 * sum(Ts)) if (self.use_graphs and self.buckets) else None
+        p = plan_call(rows, Ts, new, keep, self.cnn_scratch, self.cnn_zero, bucket, self.kv_scratch)
+        out = self._run(p, x0, stat, chunk, bucket)
+        n = len(caches)
+        for i, c in enumerate(caches):
+            for h in range(2):
+                self.pool.release(advance_row(c.rows[h], new[h * n + i], keep[i], c.keep))
+        offs = np.cumsum([0] + Ts)
+        return [out[offs[i]:offs[i + 1]].t() for i in range(n)]
+
+    def _args(self, p: dict, tables: torch.Tensor, x0, stat, out, ws, chunk: int, in_rows=None) -> _lib.SolveArgs:
+        offs = np.cumsum([0] + [x.size for x in p["parts"]])
+        tp = lambda i: tables.data_ptr() + 4 * int(offs[i])  # noqa: E731
+        return _lib.SolveArgs(p["n_tok"], p["n_rows"], p["half"], p["n_tiles"], int(chunk), _lib.ptr(x0), _lib.ptr(stat), _lib.ptr(in_rows),
+                              out.data_ptr(), tp(0), tp(1), tp(2), tp(3), tp(4), tp(5), tp(6), tp(7), tp(8), tp(9), tp(11), tp(10),
+                              self.k_pool.data_ptr(), self.v_pool.data_ptr(), self.n_slots * self.cfg.hidden, self.conv_pool.data_ptr(),
+                              ws.data_ptr(), ws.numel(), int(self.fp8))
 
     def _workspace(self, N: int, R: int) -> torch.Tensor:
         need = _lib.lib().t2w_dit_workspace_bytes(self.model.handle, N, R)
@@ -402,135 +495,159 @@ class FastDiT:
             self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         return self._ws
 
-    def _args(self, p: dict, tables: torch.Tensor, x0, stat, out, ws, chunk: int, in_rows=None) -> _lib.SolveArgs:
-        offs = np.cumsum([0] + [len(x) for x in p["parts"]])
-        tp = lambda i: tables.data_ptr() + 4 * int(offs[i])  # noqa: E731
-        H = self.cfg.hidden
-        return _lib.SolveArgs(p["n_tok"], p["n_rows"], p["half"], p["n_tiles"], int(chunk), _lib.ptr(x0), _lib.ptr(stat), _lib.ptr(in_rows),
-                              out.data_ptr(), tp(0), tp(1), tp(2), tp(3), tp(4), tp(5), tp(6), tp(7), tp(8), tp(9), tp(11), tp(10),
-                              self.k_pool.data_ptr(), self.v_pool.data_ptr(), self.n_slots * H, self.conv_pool.data_ptr(),
-                              ws.data_ptr(), ws.numel(), int(self.fp8))
-
     @staticmethod
-    def _tables(p: dict, device) -> torch.Tensor:
-        flat = np.concatenate([np.asarray(x, dtype=np.int32) for x in p["parts"]]) if p["n_tok"] else np.zeros(1, np.int32)
-        return torch.from_numpy(flat).to(device)
+    def _flat(p: dict) -> np.ndarray:
+        return np.concatenate([x.astype(np.int32, copy=False) for x in p["parts"]])
 
-    # --- solve ------------------------------------------------------------------------------------------------------
-    @torch.inference_mode()
-    def solve(self, caches: list[FastCache], mu: list[torch.Tensor], spks: torch.Tensor, cond: list | None,
-              keep: list[bool], chunk: int = 0) -> list[torch.Tensor]:
-        """The CFG Euler solve of one window per request (``FastDiT.solve``, ``engine/runtime/dit_fast.py:431-495``).
-
-        ``mu[i]`` [mel, T_i]; ``spks`` [n, mel] (after the speaker affine layer); ``cond[i]`` [mel, T_i] or None;
-        ``keep[i]``: keep the window's keys and conv caches (then trim as the reference does), else leave the caches
-        untouched (final flushes).  ``chunk`` > 0: chunk-causal attention among each row's new frames.  Returns each
-        request's mel [mel, T_i] in fp32."""
-        n = len(caches)
-        Ts = [int(m.shape[1]) for m in mu]
-        lens = [c.length for c in caches]
-        p = self._plan(caches, Ts, keep)
-        half, dev, mel = p["half"], self.device, self.cfg.mel
-        noise = self.model.rand_noise
-        if max(o + t for o, t in zip(lens, Ts)) > noise.shape[1]:
-            raise RuntimeError("window beyond the flow's noise buffer")
-        x0 = torch.cat([noise[:, o:o + t].t() for o, t in zip(lens, Ts)])
-        mu_t = torch.cat([m.t() for m in mu]).to(dev, torch.float32)
-        spk_t = torch.cat([spks[i:i + 1].to(dev, torch.float32).expand(t, -1) for i, t in enumerate(Ts)])
-        cond_t = torch.cat([(c.t() if c is not None else mu_t.new_zeros(t, mel)) for c, t in zip(cond, Ts)]).to(dev, torch.float32) \
-            if cond is not None else torch.zeros_like(mu_t)
-        stat = torch.cat([mu_t, spk_t, cond_t], dim=1).contiguous()
-        out = self._run(p, x0.contiguous(), stat, chunk)
-        for i, c in enumerate(caches):
-            for r, nw in ((p["rows"][i], p["new"][i]), (p["rows"][n + i], p["new"][n + i])):
-                self.pool.release(advance_row(r, nw, keep[i], c.keep))
-        res, o = [], 0
-        for t in Ts:
-            res.append(out[o:o + t].t())
-            o += t
-        return res
-
-    def _run(self, p: dict, x0: torch.Tensor, stat: torch.Tensor, chunk: int) -> torch.Tensor:
-        L = _lib.lib()
-        N, R = p["n_tok"], p["n_rows"]
-        st = _lib.stream_handle()
+    def _run(self, p: dict, x0: torch.Tensor, stat: torch.Tensor, chunk: int, bucket) -> torch.Tensor:
+        L, st = _lib.lib(), _lib.stream_handle()
         if not self.use_graphs:
-            tables = self._tables(p, self.device)
+            tables = _Upload.new(self._flat(p), self.device)
             out = torch.empty(p["half"], self.cfg.mel, device=self.device)
-            ws = self._workspace(N, R)
-            a = self._args(p, tables, x0, stat, out, ws, chunk)
+            a = self._args(p, tables, x0, stat, out, self._workspace(p["n_tok"], p["n_rows"]), chunk)
             _lib.check(L.t2w_dit_solve(self.model.handle, C.byref(a), st), "dit_solve")
             self.counts["eager"] += 1
             return out
-        real_half = p["half"]
-        bucket = bucket_of(R, N) if self.buckets else None
-        if bucket is not None:
-            p = pad_plan(p, *bucket, self.kv_scratch, self.cnn_scratch)
-            x0 = _pad_halves(x0, real_half, p["half"])
-            stat = _pad_halves(stat, real_half, p["half"])
-            N, R = p["n_tok"], p["n_rows"]
-        key = (N, R, p["n_tiles"], chunk, self.fp8)
-        flat = np.concatenate([np.asarray(x, dtype=np.int32) for x in p["parts"]])
-        g = self.graphs.get(key)
-        if g is not None and g["tables"].numel() < flat.size:  # more cached keys than this graph's table holds
-            L.t2w_graph_destroy(g["graph"])
-            g = None
-        if g is None:
-            g = {"tables": torch.zeros(flat.size + max(8192, flat.size), dtype=torch.int32, device=self.device), "x0": torch.empty_like(x0),
-                 "stat": torch.empty_like(stat), "out": torch.empty(p["half"], self.cfg.mel, device=self.device),
-                 "ws": torch.empty(L.t2w_dit_workspace_bytes(self.model.handle, N, R), dtype=torch.uint8, device=self.device),
-                 "graph": None}
-            self.graphs[key] = g
-        # every table but kv_idx has a size fixed by the key; kv_idx is last, so all offsets the graph reads are stable
-        g["tables"][:flat.size].copy_(torch.from_numpy(flat))
-        g["x0"].copy_(x0)
-        g["stat"].copy_(stat)
+        flat = self._flat(p)
+        g = self._bucket_graph(bucket, chunk, flat.size) if bucket is not None else self._exact_graph(p, chunk, flat.size)
+        _Upload.into(g["tables"], flat)
+        half = p["real_half"]
+        g["x0"][:half].copy_(x0)
+        g["stat"][:half].copy_(stat)
+        if p["half"] > half:  # padding tokens: zero inputs
+            g["x0"][half:p["half"]].zero_()
+            g["stat"][half:p["half"]].zero_()
         if g["graph"] is None:
-            a = self._args(p, g["tables"], g["x0"], g["stat"], g["out"], g["ws"], chunk)
-            cap = self._capture_stream()  # capture needs a non-default stream; replays go on the caller's
-            cst = cap.cuda_stream
-            _lib.check(L.t2w_graph_begin(cst), "graph_begin")
-            rc = L.t2w_dit_solve(self.model.handle, C.byref(a), cst)
-            h = C.c_void_p()
-            rc2 = L.t2w_graph_end(cst, C.byref(h))
-            _lib.check(rc, "dit_solve (capture)")
-            _lib.check(rc2, "graph_end")
-            g["graph"] = h
+            g["graph"] = self._capture(p, g, chunk)
         _lib.check(L.t2w_graph_launch(g["graph"], st), "graph_launch")
         self.counts["graph"] += 1
-        return g["out"][:real_half].clone()
+        return g["out"][:half].clone()
 
-    def _capture_stream(self):
-        if getattr(self, "_cap", None) is None:
+    def _capture(self, p: dict, g: dict, chunk: int):
+        """Capture the solve of plan ``p`` over the graph's buffers on a side stream (capture needs a non-default
+        stream; replays go on the caller's)."""
+        L = _lib.lib()
+        a = self._args(p, g["tables"], g["x0"], g["stat"], g["out"], g["ws"], chunk)
+        if self._cap is None:
             self._cap = torch.cuda.Stream()
-        return self._cap
+        self._cap.wait_stream(torch.cuda.current_stream())
+        cst = self._cap.cuda_stream
+        _lib.check(L.t2w_graph_begin(cst), "graph_begin")
+        rc = L.t2w_dit_solve(self.model.handle, C.byref(a), cst)
+        h = C.c_void_p()
+        rc2 = L.t2w_graph_end(cst, C.byref(h))
+        _lib.check(rc, "dit_solve (capture)")
+        _lib.check(rc2, "graph_end")
+        torch.cuda.current_stream().wait_stream(self._cap)
+        return h
+
+    # --- graphs -----------------------------------------------------------------------------------------------------
+    # Bucket graphs share one arena (tables, inputs, output, workspace) sized for the largest bucket: replays are ordered
+    # on the caller's stream and each output is copied out before the next call writes the arena.
+    KV_ROW_CAP = 2048  # cached keys per row the shared table arena is sized for (a larger call regrows it)
+
+    def _arena_for(self, n_ints: int) -> dict:
+        a = self._arena
+        if a is None or a["tables"].numel() < n_ints:
+            if a is not None:  # every bucket graph points into the old arena
+                self.drop_graphs(exact=False)
+            top = max(nb for _, nb in all_buckets())
+            rows = 2 * (ROW_BUCKETS[-1] // 2 + 1)
+            cap = max(n_ints, 16 * top + 2 * rows * (self.KV_ROW_CAP + 8))
+            ws = max(_lib.lib().t2w_dit_workspace_bytes(self.model.handle, nb, 2 * (rb // 2 + 1)) for rb, nb in all_buckets())
+            dev, mel = self.device, self.cfg.mel
+            a = {"tables": torch.zeros(cap, dtype=torch.int32, device=dev), "x0": torch.zeros(top // 2, mel, device=dev),
+                 "stat": torch.zeros(top // 2, 3 * mel, device=dev), "out": torch.zeros(top // 2, mel, device=dev),
+                 "ws": torch.empty(ws, dtype=torch.uint8, device=dev)}
+            self._arena = a
+        return a
+
+    def _bucket_graph(self, bucket, chunk: int, n_ints: int) -> dict:
+        arena = self._arena_for(n_ints)
+        key = (bucket, chunk, self.fp8)
+        g = self.graphs.get(key)
+        if g is None:
+            g = dict(arena, graph=None)
+            self.graphs[key] = g
+        return g
+
+    def _exact_graph(self, p: dict, chunk: int, n_ints: int) -> dict:
+        key = (p["n_tok"], p["n_rows"], p["n_tiles"], chunk, self.fp8)
+        g = self.exact.pop(key, None)
+        if g is not None and g["tables"].numel() < n_ints:  # more cached keys than this graph's tables hold
+            _lib.lib().t2w_graph_destroy(g["graph"])
+            g = None
+        if g is None:
+            while len(self.exact) >= self.max_exact_graphs:
+                old = self.exact.pop(next(iter(self.exact)))
+                _lib.lib().t2w_graph_destroy(old["graph"])
+            dev, mel, half = self.device, self.cfg.mel, p["half"]
+            g = {"tables": torch.zeros(2 * n_ints + 8192, dtype=torch.int32, device=dev), "x0": torch.empty(half, mel, device=dev),
+                 "stat": torch.empty(half, 3 * mel, device=dev), "out": torch.empty(half, mel, device=dev),
+                 "ws": torch.empty(_lib.lib().t2w_dit_workspace_bytes(self.model.handle, p["n_tok"], p["n_rows"]), dtype=torch.uint8, device=dev),
+                 "graph": None}
+        self.exact[key] = g  # most recently used last
+        return g
+
+    @torch.inference_mode()
+    def capture(self, rb: int, nb: int, chunk: int = 0) -> None:
+        """Capture the graph of bucket (``rb`` request rows, ``nb`` tokens) now (``FastDiT.capture``,
+        ``engine/runtime/dit_fast.py:392-422``), on a plan whose tokens are all padding."""
+        if not self.use_graphs:
+            raise RuntimeError("capture needs use_graphs=True")
+        p = plan_call([], [], [], [], self.cnn_scratch, self.cnn_zero, (rb, nb), self.kv_scratch)
+        flat = self._flat(p)
+        g = self._bucket_graph((rb, nb), chunk, flat.size)
+        if g["graph"] is None:
+            _Upload.into(g["tables"], flat)
+            g["graph"] = self._capture(p, g, chunk)
+
+    def capture_all(self, row_buckets=ROW_BUCKETS) -> int:
+        """Every bucket's graph (``FastDiT.capture_all``, ``engine/runtime/dit_fast.py:424-428``); returns the count."""
+        for rb in row_buckets:
+            for nb in token_buckets(rb):
+                self.capture(rb, nb)
+        return len(self.graphs)
+
+    def drop_graphs(self, exact: bool = True) -> None:
+        L = _lib.lib()
+        for g in self.graphs.values():
+            if g["graph"] is not None:
+                L.t2w_graph_destroy(g["graph"])
+        self.graphs = {}
+        if exact:
+            for g in self.exact.values():
+                if g["graph"] is not None:
+                    L.t2w_graph_destroy(g["graph"])
+            self.exact = {}
+
+    def __del__(self):
+        try:
+            self.drop_graphs()
+        except Exception:
+            pass
 
     # --- single estimator evaluation (no cache, full attention) ------------------------------------------------------
     @torch.inference_mode()
     def estimator_forward(self, x: torch.Tensor, mu: torch.Tensor, t: float, spks: torch.Tensor, cond: torch.Tensor) -> torch.Tensor:
         """One estimator forward (``_estimator_temb``, ``engine/runtime/token2wav_batch.py:787-810``) of B independent
         rows with empty caches and full attention: x, mu, cond [B, mel, T]; spks [B, mel]; t a scalar.  Returns dphi
-        [B, mel, T] fp32."""
+        [B, mel, T] fp32.  Rows read the zero conv slot and write the scratch one, so no row sees another's frames."""
         B, mel, T = x.shape
         dev = self.device
         rows = torch.cat([x, mu, spks[:, :, None].expand(-1, -1, T), cond], dim=1).to(dev, torch.float32)  # [B, 4 mel, T]
         in_rows = rows.permute(0, 2, 1).reshape(B * T, 4 * mel).contiguous()
         slots = self.pool.alloc(B * T)
         try:
-            tok_row = [r for r in range(B) for _ in range(T)]
-            parts = [tok_row, [p for _ in range(B) for p in range(T)], [i + 2 * r for i, r in enumerate(tok_row)], slots,
-                     [r * T for r in range(B)], [T] * B, [r * T for r in range(B)], [T] * B, [self.cnn_scratch] * B, [self.cnn_scratch] * B,
-                     [v for r in range(B) for q0 in range(0, T, 64) for v in (r, q0)], slots]
-            self.conv_pool[self.cnn_scratch].zero_()
-            p = {"n_tok": B * T, "n_rows": B, "half": 0, "n_tiles": len(parts[10]) // 2, "parts": parts}
-            tables = self._tables(p, dev)
+            new = [slots[r * T:(r + 1) * T] for r in range(B)]
+            parts = _layout([T] * B, new, new, [self.cnn_zero] * B, [self.cnn_scratch] * B)
+            p = {"n_tok": B * T, "n_rows": B, "half": 0, "n_tiles": parts[10].size // 2, "parts": parts}
+            tables = _Upload.new(self._flat(p), dev)
             out = torch.empty(B * T, mel, device=dev)
             mods, fin = self.model.tables([float(t)])
-            ws = self._workspace(B * T, B)
-            a = self._args(p, tables, None, None, out, ws, 0, in_rows=in_rows)
+            a = self._args(p, tables, None, None, out, self._workspace(B * T, B), 0, in_rows=in_rows)
             _lib.check(_lib.lib().t2w_dit_forward(self.model.handle, C.byref(a), 0, mods.data_ptr(), fin.data_ptr(), _lib.stream_handle()),
                        "dit_forward")
-            torch.cuda.current_stream().synchronize()
         finally:
             self.pool.release(slots)
         return out.view(B, T, mel).permute(0, 2, 1).contiguous()

@@ -157,12 +157,14 @@ class HiFTModel:
                                       ws.data_ptr(), ws.numel(), int(self.decode_bf16), _lib.stream_handle()), "hift_forward")
         return speech, source, f0
 
-    def _forward_graph(self, frames: list[int], mel_tm: torch.Tensor, noise_tm: torch.Tensor, cache_source, S: int):
+    def _graph(self, frames: list[int], S: int) -> dict:
+        """The graph of a (row lengths, source-cache length) shape, captured on first use over its own static buffers;
+        the least recently used one is dropped beyond ``max_graphs``."""
         L = _lib.lib()
         key = (tuple(frames), S)
         g = self.graphs.pop(key, None)
         if g is None:
-            if len(self.graphs) >= self.max_graphs:
+            while len(self.graphs) >= self.max_graphs:
                 old = self.graphs.pop(next(iter(self.graphs)))
                 L.t2w_graph_destroy(old["graph"])
             n = len(frames)
@@ -172,29 +174,33 @@ class HiFTModel:
             ns = sum(frames) * self.cfg.upsample_scale
             dev = self.device
             g = {"fr": fr, "plan": torch.from_numpy(np.ctypeslib.as_array(plan).copy()).to(dev),
-                 "mel": torch.empty(sum(frames), self.cfg.mel, device=dev), "noise": torch.empty(ns, self.dim, device=dev),
-                 "cs": torch.empty(n, S, device=dev) if S > 0 else None,
+                 "mel": torch.zeros(sum(frames), self.cfg.mel, device=dev), "noise": torch.zeros(ns, self.dim, device=dev),
+                 "cs": torch.zeros(n, S, device=dev) if S > 0 else None,
                  "speech": torch.empty(ns, device=dev), "source": torch.empty(ns, device=dev),
-                 "ws": torch.empty(L.t2w_hift_workspace_bytes(self.handle, n, fr), dtype=torch.uint8, device=dev), "graph": None}
-        g["mel"].copy_(mel_tm)
-        g["noise"].copy_(noise_tm)
-        if S > 0:
-            g["cs"].copy_(cache_source.reshape(len(frames), S))
-        if g["graph"] is None:
+                 "ws": torch.empty(L.t2w_hift_workspace_bytes(self.handle, n, fr), dtype=torch.uint8, device=dev)}
             cap = self._capture_stream()  # capture needs a non-default stream; replays go on the caller's
             cap.wait_stream(torch.cuda.current_stream())
             cst = cap.cuda_stream
             _lib.check(L.t2w_graph_begin(cst), "graph_begin")
-            rc = L.t2w_hift_forward(self.handle, len(frames), g["fr"], g["plan"].data_ptr(), g["mel"].data_ptr(), g["noise"].data_ptr(),
+            rc = L.t2w_hift_forward(self.handle, n, g["fr"], g["plan"].data_ptr(), g["mel"].data_ptr(), g["noise"].data_ptr(),
                                     _lib.ptr(g["cs"]), S, None, None, g["speech"].data_ptr(), g["source"].data_ptr(), None,
                                     g["ws"].data_ptr(), g["ws"].numel(), int(self.decode_bf16), cst)
             h = C.c_void_p()
             rc2 = L.t2w_graph_end(cst, C.byref(h))
             _lib.check(rc, "hift_forward (capture)")
             _lib.check(rc2, "graph_end")
+            torch.cuda.current_stream().wait_stream(cap)
             g["graph"] = h
         self.graphs[key] = g  # most recently used last
-        _lib.check(L.t2w_graph_launch(g["graph"], _lib.stream_handle()), "graph_launch")
+        return g
+
+    def _forward_graph(self, frames: list[int], mel_tm: torch.Tensor, noise_tm: torch.Tensor, cache_source, S: int):
+        g = self._graph(frames, S)
+        g["mel"].copy_(mel_tm)
+        g["noise"].copy_(noise_tm)
+        if S > 0:
+            g["cs"].copy_(cache_source.reshape(len(frames), S))
+        _lib.check(_lib.lib().t2w_graph_launch(g["graph"], _lib.stream_handle()), "graph_launch")
         self.counts["graph"] += 1
         return g["speech"].clone(), g["source"].clone(), None
 
@@ -202,6 +208,20 @@ class HiFTModel:
         if getattr(self, "_cap", None) is None:
             self._cap = torch.cuda.Stream()
         return self._cap
+
+    def capture(self, frames: list[int], S: int) -> None:
+        """Capture the graph of calls with rows of ``frames`` mel frames and ``S`` cached source samples now."""
+        self._graph(list(frames), S)
+
+    def capture_all(self, rows: int = 16, steady: int = MEL_CACHE + 50, first: int = 50) -> int:
+        """The graphs of the streaming shapes (``HiFTGraphs.capture_all``, ``engine/runtime/hift_graph.py:52-57``): 1 to
+        ``rows`` rows of steady windows (8 cached + 50 new frames, a 3840-sample source cache) and of first windows
+        (no cache).  Returns the number of graphs held."""
+        self.max_graphs = max(self.max_graphs, 2 * rows + 8)
+        for n in range(1, rows + 1):
+            self.capture([first] * n, 0)
+            self.capture([steady] * n, SOURCE_CACHE)
+        return len(self.graphs)
 
     @torch.inference_mode()
     def forward_noise(self, mel: torch.Tensor, cache_source: torch.Tensor, rand_ini: torch.Tensor, noise: torch.Tensor):

@@ -1,16 +1,22 @@
 """The Token2Wav module surface the reference's worker calls, over the MI355X DiT solve and HiFT.
 
-Mirrors ``BatchedToken2Wav`` (``engine/runtime/token2wav_batch.py:151-309, 480-554``) as its worker uses it
-(``FakeBT`` in ``tests/engine_api/test_t2w_worker_loop.py:52-82`` pins that contract): ``setup_many``, ``new_stream``
-(with ``adopt``), ``decode``, ``release_stream``, ``release_prompt``.  The flow encoder (codec tokens -> ``mu``) is the
-next stage to be built, so windows and prompts enter as encoder outputs: a window is ``(stream, mu [mel, T], last)`` and
-a prompt setup is ``(mu [mel, P], spk [mel] (after the speaker affine layer), prompt mel [mel, P])``.
+Mirrors ``BatchedToken2Wav`` (``engine/runtime/token2wav_batch.py:151-309, 480-554``) as its worker drives it
+(``engine/runtime/t2w_worker.py:448-560, 642-665, 826-838``; ``FakeBT`` in ``tests/engine_api/test_t2w_worker_loop.py:52-82``
+pins the minimal contract): ``setup_many``, ``setup_encode`` / ``release_presetup``, ``new_stream`` (with ``adopt``),
+``decode(items, async_result=False, setups=None)``, ``release_stream``, ``release_prompt``, ``capture_graphs``, and the
+attributes the loop reads (``max_flow_streams``, ``fuse_setup_frames``, ``fast``, ``profile``, ``trace``).
 
-Per call: one packed ragged CFG Euler solve over every window (``keep`` = not last, as the reference's
-``_flow_finish``/``dit_fast.solve``), then HiFT over all windows in one ragged call per source-cache length (first
-windows have no cache), then the per-stream glue of ``engine/models/token2wav.py:319-332`` (8 cached mel frames, 3840
-cached source / speech samples, Hamming cross-fade, first non-final chunk shifted by 3840 zeros, non-final chunks hold
-back their last 3840 samples), and one device-to-host copy (``token2wav_batch.py:847``).
+Prompt features keep the reference's tuple layout ``(tokens, tokens_len, spk, mels, mels_len)`` (``Token2Wav.features``,
+``engine/models/token2wav.py:266-276``; ``mels`` [1, P, mel] is the prompt mel and sets the trim length).  The flow
+encoder (codec tokens -> ``mu``) is not part of this module yet, so the first entry carries the encoder's output
+``mu`` [1, P, mel] in place of the tokens and ``spk`` is the speaker embedding after the flow's affine layer [1, mel]
+(``prompt_features`` builds such a tuple); a window is ``(stream, mu [mel, T], last)``.
+
+Per call: one packed ragged CFG Euler solve over every window (and fused prompt setups), then HiFT over all windows in
+one ragged call per source-cache length, then the per-stream glue of ``engine/models/token2wav.py:319-332`` (8 cached
+mel frames, 3840 cached source / speech samples, Hamming cross-fade, first non-final chunk shifted by 3840 zeros,
+non-final chunks hold back their last 3840 samples), and one device-to-host copy — synchronous, or through a pinned
+buffer and an event (``PendingAudio``) so the caller does not wait for the GPU.
 """
 
 from __future__ import annotations
@@ -25,11 +31,39 @@ from .dit import FastCache, FastDiT
 from .hift import HiFTModel, HiftState, chunk_noise_seed, fade_in_out
 
 
+def prompt_features(mu: torch.Tensor, spk: torch.Tensor, mels: torch.Tensor) -> tuple:
+    """A prompt-feature tuple in the reference layout for this module: ``mu`` [mel, P] (flow-encoder output of the
+    prompt), ``spk`` [mel] (after the speaker affine layer), ``mels`` [mel, P] (the prompt mel)."""
+    P = int(mels.shape[-1])
+    n = torch.tensor([P], dtype=torch.int32)
+    return (mu.t().reshape(1, P, -1), n, spk.reshape(1, -1), mels.t().reshape(1, P, -1), n)
+
+
 @dataclass
 class Prompt:
-    spk: torch.Tensor            # [mel] after the speaker affine layer
-    frames: int                  # prompt mel frames (the trim length)
-    cache: FastCache | None      # estimator caches after the setup solve
+    """A set-up prompt: its features, speaker embedding (after the affine layer) and estimator caches."""
+    feats: tuple
+    spk: torch.Tensor       # [1, mel]
+    cache: FastCache | None
+
+    @property
+    def mels(self) -> torch.Tensor:
+        return self.feats[3]
+
+    @property
+    def frames(self) -> int:
+        return int(self.feats[3].shape[1])
+
+
+@dataclass
+class PreSetup:
+    """A prompt setup whose inputs are staged and caches allocated, not solved yet (``setup_encode``): ``decode(setups=)``
+    and ``setup_many`` take it in place of the features; an unused one goes back with ``release_presetup``."""
+    feats: tuple
+    cache: FastCache | None
+    mu: torch.Tensor        # [mel, P]
+    spk: torch.Tensor       # [1, mel]
+    cond: torch.Tensor      # [mel, P]
 
 
 @dataclass
@@ -47,30 +81,102 @@ class StreamState:
         return self.hift.noise_seed
 
 
+class PendingAudio:
+    """One decode call's samples on their way to the host (``async_result``): a non-blocking copy of the packed samples
+    into a pinned host buffer on the current stream, and an event after it.  The streams' host-side state is already
+    advanced; ``ready()`` polls the event, ``result()`` waits for it and splits the samples per item."""
+
+    def __init__(self, flat: torch.Tensor | None, lengths: list[int]):
+        self.lengths = lengths
+        self.host = None
+        if flat is not None and flat.numel():
+            self.host = torch.empty(flat.numel(), dtype=torch.float32, pin_memory=True)
+            self.host.copy_(flat, non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record()
+
+    def ready(self) -> bool:
+        return self.event.query()
+
+    def result(self) -> list[np.ndarray]:
+        self.event.synchronize()
+        flat = self.host.numpy() if self.host is not None else np.zeros(0, np.float32)
+        ends = np.cumsum(self.lengths)
+        out = [flat[e - n:e].copy() for n, e in zip(self.lengths, ends)]
+        self.host = None  # the pinned block goes back to torch's host allocator
+        return out
+
+
 class BatchedToken2Wav:
-    def __init__(self, dit: FastDiT, hift: HiFTModel, noise_device: str = "cuda"):
+    def __init__(self, dit: FastDiT, hift: HiFTModel, noise_device: str = "cuda", fuse_setup_frames: int = 0, max_flow_streams: int = 32):
         """``noise_device``: where the per-chunk HiFT source noise is drawn ("cuda" as the reference's ``hift_noise``;
-        "cpu" reproduces a host-generator draw bit for bit, used by the parity tests)."""
+        "cpu" reproduces a host-generator draw bit for bit, used by the parity tests).  ``fuse_setup_frames``: prompt
+        setups of up to this many mel frames in all may ride a decode call's solve (``decode(setups=...)``).
+        ``max_flow_streams``: requests per packed solve (larger calls run in slices)."""
         self.fast, self.hift = dit, hift
         self.device = dit.device
         self.noise_device = noise_device
         self.window = torch.from_numpy(np.hamming(2 * SOURCE_CACHE)).to(self.device)  # float64, as the reference's
-        self.max_flow_streams = 32
-        self.fuse_setup_frames = 0
+        self.max_flow_streams = int(max_flow_streams)
+        self.fuse_setup_frames = int(fuse_setup_frames)
         self.profile = None
         self.trace = None
 
-    # --- prompts and streams ------------------------------------------------------------------------------------------
-    @torch.inference_mode()
-    def setup_many(self, feats: list[tuple]) -> list[Prompt]:
-        """Prompt setups: one solve over every prompt's frames with its prompt mel as condition and empty caches
-        (``token2wav_batch.py:507-554``, the fast-DiT branch)."""
-        caches = [self.fast.new_cache(keep=int(mu.shape[1])) for mu, _, _ in feats]
-        spks = torch.stack([s.to(self.device, torch.float32).reshape(-1) for _, s, _ in feats])
-        self.fast.solve(caches, [mu.to(self.device) for mu, _, _ in feats], spks, [c.to(self.device) for _, _, c in feats],
-                        [True] * len(feats))
-        return [Prompt(spks[i], int(mu.shape[1]), c) for i, ((mu, _, _), c) in enumerate(zip(feats, caches))]
+    # --- prompts ------------------------------------------------------------------------------------------------------
+    def _stage(self, feats: tuple) -> PreSetup:
+        mu, _, spk, mels, _ = feats
+        if not torch.is_floating_point(mu):
+            raise NotImplementedError("codec-token prompts need the flow encoder; pass its output mu (prompt_features)")
+        P = int(mels.shape[1])
+        if mu.shape[1] != P:
+            raise ValueError(f"prompt mu has {mu.shape[1]} frames, its mel {P}")
+        dev = self.device
+        return PreSetup(feats, self.fast.new_cache(keep=P), mu[0].to(dev, torch.float32).t(), spk.to(dev, torch.float32).reshape(1, -1),
+                        mels[0].to(dev, torch.float32).t())
 
+    @torch.inference_mode()
+    def setup_encode(self, feats_list: list[tuple]) -> list[PreSetup]:
+        """Prompt setups staged ahead of their solve (``setup_encode``, ``token2wav_batch.py:480-485``): inputs on the
+        device and empty estimator caches allocated."""
+        out = []
+        try:
+            for f in feats_list:
+                out.append(self._stage(f))
+        except Exception:
+            for p in out:
+                self.release_presetup(p)
+            raise
+        return out
+
+    def release_presetup(self, p: PreSetup) -> None:
+        if p is not None and p.cache is not None:
+            self.fast.release(p.cache)
+            p.cache = None
+
+    def _presetups(self, setups: list) -> list[PreSetup]:
+        return [s if isinstance(s, PreSetup) else self.setup_encode([s])[0] for s in setups]
+
+    @staticmethod
+    def _prompt(p: PreSetup) -> Prompt:
+        pr = Prompt(p.feats, p.spk, p.cache)
+        p.cache = None  # the prompt owns the caches now
+        return pr
+
+    @torch.inference_mode()
+    def setup_many(self, feats_list: list) -> list[Prompt]:
+        """Prompt setups: one solve over every prompt's frames with its prompt mel as condition and empty caches
+        (``token2wav_batch.py:507-554``, the fast-DiT branch).  Entries may be ``PreSetup``."""
+        pre = self._presetups(feats_list)
+        for a in range(0, len(pre), self.max_flow_streams):
+            part = pre[a:a + self.max_flow_streams]
+            self.fast.solve([p.cache for p in part], [p.mu for p in part], torch.cat([p.spk for p in part]), [p.cond for p in part],
+                            [True] * len(part))
+        return [self._prompt(p) for p in pre]
+
+    def setup(self, feats) -> Prompt:
+        return self.setup_many([feats])[0]
+
+    # --- streams ------------------------------------------------------------------------------------------------------
     def new_stream(self, prompt: Prompt, noise_seed: int = 0, adopt: bool = False) -> StreamState:
         """A stream with its own copy of the prompt's caches, or taking them over (``adopt``: the prompt is used once)."""
         if adopt:
@@ -89,18 +195,41 @@ class BatchedToken2Wav:
             self.fast.release(p.cache)
             p.cache = None
 
+    @torch.inference_mode()
+    def capture_graphs(self, prompt: Prompt | None = None) -> dict:
+        """Capture every graph up front (``capture_graphs``, ``token2wav_batch.py:292-309``): the DiT's (rows, tokens)
+        buckets and HiFT's steady shapes.  ``prompt`` is accepted for the reference's signature and not needed."""
+        n = {}
+        if self.fast.use_graphs:
+            n["dit"] = self.fast.capture_all()
+        if self.hift.use_graphs:
+            n["hift"] = self.hift.capture_all()
+        return n
+
     # --- decode -------------------------------------------------------------------------------------------------------
     @torch.inference_mode()
-    def decode(self, items: list[tuple[StreamState, torch.Tensor, bool]]) -> list[np.ndarray]:
-        """``items[i] = (stream, mu [mel, T_i], last)`` -> float32 24 kHz samples per item."""
-        if not items:
-            return []
+    def decode(self, items: list[tuple], async_result: bool = False, setups: list | None = None):
+        """``items[i] = (stream, mu [mel, T_i], last)`` -> float32 24 kHz samples per item (``decode``,
+        ``token2wav_batch.py:220-255``).  ``async_result``: a ``PendingAudio`` instead, without waiting for the GPU.
+        ``setups`` (``fuse_setup_frames``): prompt features (or ``PreSetup``) set up in the same packed solve; then the
+        result is ``(samples, prompts)``."""
+        if setups:
+            frames = sum(int((s.feats if isinstance(s, PreSetup) else s)[3].shape[1]) for s in setups)
+            if not self.fuse_setup_frames or frames > self.fuse_setup_frames or len(items) + len(setups) > self.max_flow_streams:
+                raise ValueError(f"fused setups: {len(setups)} prompts of {frames} frames with {len(items)} windows exceed "
+                                 f"fuse_setup_frames={self.fuse_setup_frames} / max_flow_streams={self.max_flow_streams}")
+        pre = self._presetups(setups) if setups else []
+        rows = [(p.cache, p.mu, p.spk, p.cond, True) for p in pre]
+        rows += [(st.cache, mu.to(self.device), st.prompt.spk, None, not last) for st, mu, last in items]
         mels = []
-        for a in range(0, len(items), self.max_flow_streams):
-            part = items[a:a + self.max_flow_streams]
-            mels += self.fast.solve([st.cache for st, _, _ in part], [mu.to(self.device) for _, mu, _ in part],
-                                    torch.stack([st.prompt.spk for st, _, _ in part]), None, [not last for _, _, last in part])
-        return self._vocode(items, mels)
+        for a in range(0, len(rows), self.max_flow_streams):
+            part = rows[a:a + self.max_flow_streams]
+            conds = [r[3] for r in part] if any(r[3] is not None for r in part) else None
+            mels += self.fast.solve([r[0] for r in part], [r[1] for r in part], torch.cat([r[2] for r in part]), conds,
+                                    [r[4] for r in part])
+        prompts = [self._prompt(p) for p in pre]
+        out = self._vocode(items, mels[len(pre):], async_result)
+        return (out, prompts) if setups else out
 
     def _noise(self, seeds: list[int], n: int):
         dim = self.hift.dim
@@ -109,7 +238,7 @@ class BatchedToken2Wav:
         noise = torch.cat([torch.randn(1, dim, n, generator=g, device=self.noise_device) for g in gens]).transpose(1, 2)
         return rand_ini.to(self.device), noise.to(self.device)
 
-    def _vocode(self, items, mels) -> list[np.ndarray]:
+    def _vocode(self, items, mels, async_result: bool = False):
         """HiFT per source-cache length (first windows have none), rows of different lengths in one call, then the
         reference's cross-fade, cache update and hold-back per stream (``token2wav_batch.py:813-848``)."""
         up = self.hift.cfg.upsample_scale
@@ -146,9 +275,10 @@ class BatchedToken2Wav:
             if not last:
                 sp = torch.cat([torch.zeros(SOURCE_CACHE, device=sp.device, dtype=sp.dtype), sp[:-SOURCE_CACHE]]) if first else sp[:-SOURCE_CACHE]
             pieces.append(sp)
-        flat = torch.cat(pieces).float().cpu().numpy()
-        out, o = [], 0
-        for p in pieces:
-            out.append(flat[o:o + p.numel()])
-            o += p.numel()
-        return out
+        lengths = [int(p.numel()) for p in pieces]
+        flat = torch.cat(pieces).float() if pieces else None
+        if async_result:
+            return PendingAudio(flat, lengths)
+        host = flat.cpu().numpy() if flat is not None else np.zeros(0, np.float32)
+        ends = np.cumsum(lengths)
+        return [host[e - n:e] for n, e in zip(lengths, ends)]

@@ -81,11 +81,19 @@ def freq_table(freq: int, max_period: float = 10000.0) -> torch.Tensor:
     return torch.exp(-math.log(max_period) * torch.arange(0, half, dtype=torch.float32) / half)
 
 
+T_SCALE = 1000.0  # the embedder sees 1000 t (t in [0, 1])
+
+
+def timestep_sinusoid(t: torch.Tensor, dim: int) -> torch.Tensor:
+    """The DiT timestep frequency embedding of ``1000 t``: ``[cos(1000 t f_k) | sin(1000 t f_k)]`` with
+    ``f_k = 10000^(-k / (dim / 2))``, k = 0 .. dim/2 - 1.  t [B] -> [B, dim]."""
+    args = (t.float() * T_SCALE)[:, None] * freq_table(dim)[None]
+    return torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
+
+
 def t_embed(W: dict, t: torch.Tensor) -> torch.Tensor:
-    """Timestep embedder: ``[cos(1000 t f) | sin(1000 t f)]`` -> Linear -> SiLU -> Linear.  t [B] -> [B, H]."""
-    f = freq_table(W["t_embedder.mlp.0.weight"].shape[1])
-    args = (t.float() * 1000.0)[:, None] * f[None]
-    emb = torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
+    """Timestep embedder: sinusoid -> Linear -> SiLU -> Linear.  t [B] -> [B, H]."""
+    emb = timestep_sinusoid(t, W["t_embedder.mlp.0.weight"].shape[1])
     h = F.silu(F.linear(emb, W["t_embedder.mlp.0.weight"], W["t_embedder.mlp.0.bias"]))
     return F.linear(h, W["t_embedder.mlp.2.weight"], W["t_embedder.mlp.2.bias"])
 
@@ -173,15 +181,20 @@ def block_chunk(W, d: DiTDims, b: int, h, temb, cnn_cache, att_cache, mask, tr):
     return h, new_cnn, new_att
 
 
+def pack_inputs(x, mu, spks, cond) -> torch.Tensor:
+    """The estimator input ``[x | mu | spk | cond]`` per frame (``token2wav_batch.py:801-803``: x and mu packed, then the
+    speaker embedding repeated over frames, then cond): x, mu, cond [B, mel, T]; spks [B, mel] -> [B, T, 4 mel]."""
+    T = x.shape[2]
+    return torch.cat([x, mu, spks[:, :, None].expand(-1, -1, T), cond], dim=1).transpose(1, 2)
+
+
 def estimator_chunk(W, d: DiTDims, x, mu, temb, spks, cond, cnn_cache, att_cache, mask, tr):
     """``_estimator_temb`` (``token2wav_batch.py:787-810``).
 
     x, mu, cond [B, mel, T]; temb [B, H]; spks [B, mel]; cnn_cache [depth, B, 2H, 2]; att_cache [depth, B, nh, L, 2dk];
     mask [B, T, T + L] bool over keys ``[new, cache]``; tr [B] real frames per row.
     Returns (dphi [B, mel, T], new cnn [depth, B, 2H, 2], new att [depth, B, nh, T + L, 2dk])."""
-    T = x.shape[2]
-    inp = torch.cat([x, mu, spks[:, :, None].expand(-1, -1, T), cond], dim=1).transpose(1, 2)
-    h = F.linear(inp, W["in_proj.weight"], W["in_proj.bias"])
+    h = F.linear(pack_inputs(x, mu, spks, cond), W["in_proj.weight"], W["in_proj.bias"])
     new_cnn, new_att = [], []
     for b in range(d.depth):
         h, c, a = block_chunk(W, d, b, h, temb, cnn_cache[b], att_cache[b], mask, tr)

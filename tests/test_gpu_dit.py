@@ -51,8 +51,9 @@ def test_estimator_forward_config1(dev, full):
 
 
 def test_estimator_forward_3000_tokens(dev, full):
-    """One estimator forward with 3000 tokens (B=2 rows, T=1500, t=0.3): the qkv projection (with the fused q/k
-    LayerNorm and key/value scatter) runs on the four-wave ring GEMM, the other projections on split-K."""
+    """One estimator forward with 3000 tokens (B=2 rows, T=1500, t=0.3): every block GEMM runs on the 256 x 256 tile
+    GEMM over a partly filled grid (12 row tiles: 48 tiles at N = 1024, 144 for the qkv projection with its fused q/k
+    LayerNorm and key/value scatter)."""
     W, model = full
     fd = FastDiT(model, n_slots=4096, max_streams=2)
     g = torch.Generator().manual_seed(3)
@@ -97,7 +98,7 @@ def _stream_case(W, model, graphs: bool, buckets: bool = False, outs: list | Non
         assert [c.length for c in caches] == [c.length for c in refc], w
     for c in caches:
         fd.release(c)
-    assert fd.pool.in_use() == 0
+    assert fd.pool.in_use() == fd.scratch
     if stats is not None:
         stats.update(fd.counts, n_graphs=len(fd.graphs))
     return errs
@@ -156,7 +157,8 @@ def test_solve_streaming_graphs_equal_eager(dev, tiny):
     W, model = tiny
     a = _stream_case(W, model, graphs=False)
     b = _stream_case(W, model, graphs=True)
-    assert a == b
+    print("exact-shape graphs vs oracle rel-L2 per call", b)
+    assert a == b and max(b) < TOL
 
 
 def test_solve_streaming_bucketed_graphs(dev, tiny):

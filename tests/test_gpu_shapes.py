@@ -1,0 +1,114 @@
+"""Parity at the benchmarked shapes, full model size (hidden 1024, 22 blocks, 16 heads, FFN 2048).
+
+* 16 streams x 400 frames, chunk-causal attention (chunk 50), one packed 10-step CFG solve (B = 32 rows, 12,800 tokens
+  per step: the 256 x 256 tile GEMMs with their fused epilogues, the qkv row split, the tiled attention): three sampled
+  streams against the fp32 oracle solving each alone (rows are independent), the other streams against the GPU solving
+  each alone (batched == per-stream, the reference's invariant ``tests/engine/test_token2wav_stream.py:93-134``).
+* The same over 16 ragged streams of U[150, 450] frames (numpy ``default_rng(2)``, as the benchmark's ragged case).
+* fp8 block GEMMs (e4m3 weights with per-output-channel scales, MX fp8 activations) at 16 x 400 against bf16.
+* HiFT over 16 rows of U[50, 400] mel frames (``default_rng(3)``), strict fp32 and the bf16 decoder, against the oracle.
+
+Bounds: DiT mel rel-L2 <= 2e-2 against the oracle and <= 1e-2 batched against per-stream (different row counts take
+different GEMM paths, so the bf16 roundings differ); fp8 <= 5e-2 against bf16; HiFT as in ``test_gpu_hift.py``.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import t2w_amd  # noqa: F401
+from t2w_amd.config import DiTConfig, HiFTConfig
+from t2w_amd.dit import DiTModel, FastDiT
+from t2w_amd.hift import HiFTModel
+from t2w_amd.weights import init_dit, init_hift
+from oracle import dit as od
+from oracle import hift as oh
+from conftest import rel
+
+pytestmark = pytest.mark.gpu
+
+TOL, SAME, FP8_TOL = 2e-2, 1e-2, 5e-2
+
+
+@pytest.fixture(scope="module")
+def full():
+    W = init_dit(DiTConfig(), seed=2)
+    return W, DiTModel(W, DiTConfig(), fp8=True)
+
+
+def _packed_vs_oracle(W, model, Ts, sample, seed, chunk=50):
+    d = od.dims_of(W)
+    n = len(Ts)
+    fd = FastDiT(model, n_slots=2 * sum(Ts) + 4096, max_streams=n)
+    g = torch.Generator().manual_seed(seed)
+    mus = [torch.randn(80, t, generator=g) for t in Ts]
+    spks = torch.randn(n, 80, generator=g)
+    print(f"packed solve: {n} streams, {2 * sum(Ts)} tokens per step, chunk {chunk}", flush=True)
+    caches = [fd.new_cache() for _ in Ts]
+    got = [o.cpu() for o in fd.solve(caches, [m.cuda() for m in mus], spks.cuda(), None, [False] * n, chunk=chunk)]
+    for c in caches:
+        fd.release(c)
+    worst = 0.0
+    for i in sample:
+        ref = od.solve(W, d, W["rand_noise"], [od.empty_cache(d)], [mus[i]], spks[i:i + 1], None, [False], chunk=chunk)[0]
+        e = rel(got[i], ref)
+        print(f"  stream {i} ({Ts[i]} frames) vs oracle rel-L2 {e:.3e} max-abs {float((got[i] - ref).abs().max()):.3e}", flush=True)
+        worst = max(worst, e)
+    same = 0.0
+    for i in range(n):
+        c = fd.new_cache()
+        one = fd.solve([c], [mus[i].cuda()], spks[i:i + 1].cuda(), None, [False], chunk=chunk)[0].cpu()
+        fd.release(c)
+        same = max(same, rel(got[i], one))
+    print(f"  batched vs per-stream worst rel-L2 {same:.3e}", flush=True)
+    assert fd.pool.in_use() == fd.scratch
+    return worst, same, got
+
+
+def test_north_star_16x400_chunk50(dev, full):
+    W, model = full
+    worst, same, _ = _packed_vs_oracle(W, model, [400] * 16, sample=(0, 7, 15), seed=2)
+    assert worst < TOL and same < SAME
+
+
+def test_ragged_16_streams_150_450(dev, full):
+    W, model = full
+    Ts = [int(t) for t in np.random.default_rng(2).integers(150, 451, size=16)]
+    order = np.argsort(Ts)
+    worst, same, _ = _packed_vs_oracle(W, model, Ts, sample=(int(order[0]), int(order[8]), int(order[-1])), seed=3)
+    assert worst < TOL and same < SAME
+
+
+def test_fp8_16x400_vs_bf16(dev, full):
+    W, model = full
+    g = torch.Generator().manual_seed(4)
+    mus = [torch.randn(80, 400, generator=g).cuda() for _ in range(16)]
+    spks = torch.randn(16, 80, generator=g).cuda()
+    outs = []
+    for fp8 in (False, True):
+        fd = FastDiT(model, n_slots=16 * 800 + 4096, max_streams=16, fp8=fp8)
+        caches = [fd.new_cache() for _ in range(16)]
+        outs.append([o.cpu() for o in fd.solve(caches, mus, spks, None, [False] * 16, chunk=50)])
+        for c in caches:
+            fd.release(c)
+    e = max(rel(a, b) for a, b in zip(outs[1], outs[0]))
+    print("fp8 vs bf16 mel rel-L2 (16 x 400)", e)
+    assert e < FP8_TOL
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_hift_16_rows_50_400(dev, bf16):
+    W = init_hift(HiFTConfig(), seed=3)
+    lens = [int(t) for t in np.random.default_rng(3).integers(50, 401, size=16)]
+    g = torch.Generator().manual_seed(3)
+    mels = [torch.randn(1, 80, t, generator=g) * 2 - 5 for t in lens]
+    noise = [oh.hift_noise(9, [300 + i], t * 480) for i, t in enumerate(lens)]
+    gm = HiFTModel(W, HiFTConfig(), decode_bf16=bf16)
+    mel_tm = torch.cat([m[0].t() for m in mels]).cuda()
+    noise_tm = torch.cat([nz[0] for _, nz in noise]).cuda()
+    sp, _, _ = gm.forward_packed(lens, mel_tm, noise_tm, None, 0)
+    h = oh.HiFT(W)
+    ref = torch.cat([oh.forward_noise(h, m, torch.zeros(1, 1, 0), ri, nz)[0][0] for m, (ri, nz) in zip(mels, noise)])
+    e = rel(sp.cpu(), ref)
+    print(f"HiFT 16 rows x U[50,400] ({sum(lens)} frames) {'bf16' if bf16 else 'fp32'} speech rel-L2 {e:.3e}")
+    assert e < (1e-2 if bf16 else 1e-3)

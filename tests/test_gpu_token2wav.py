@@ -20,10 +20,11 @@ import t2w_amd  # noqa: F401
 from t2w_amd.config import DiTConfig, HiFTConfig
 from t2w_amd.dit import DiTModel, FastDiT
 from t2w_amd.hift import HiFTModel
-from t2w_amd.token2wav import BatchedToken2Wav
+from t2w_amd.token2wav import BatchedToken2Wav, PendingAudio, prompt_features
 from t2w_amd.weights import init_dit, init_hift
 from oracle import dit as od
 from oracle import hift as oh
+from conftest import rel
 
 pytestmark = pytest.mark.gpu
 
@@ -39,7 +40,7 @@ def test_batched_decode_matches_oracle_per_stream(dev):
     g = torch.Generator().manual_seed(4)
     P = [60, 30, 45]
     feats = [(torch.randn(80, p, generator=g), torch.randn(80, generator=g), torch.randn(80, p, generator=g)) for p in P]
-    prompts = bt.setup_many([(m.cuda(), s.cuda(), c.cuda()) for m, s, c in feats])
+    prompts = bt.setup_many([prompt_features(m.cuda(), s.cuda(), c.cuda()) for m, s, c in feats])
     sts = [bt.new_stream(p, noise_seed=j, adopt=True) for j, p in enumerate(prompts)]
     # oracle streams
     rc = [od.empty_cache(d, keep=p) for p in P]
@@ -90,4 +91,116 @@ def test_batched_decode_matches_oracle_per_stream(dev):
         assert sts[j].cache.length == rc[j].length
     for st in sts:
         bt.release_stream(st)
-    assert fd.pool.in_use() == 0
+    assert fd.pool.in_use() == fd.scratch
+
+
+def _stream_pair(W, Wh, cfg, P, windows, seed, graphs=False):
+    """One stream through the module: a P-frame prompt setup, then the windows (the last one final); returns the module's
+    audio per window, its GPU mels, and the oracle's mels and vocode glue on those GPU mels."""
+    fd = FastDiT(DiTModel(W, cfg), n_slots=4096, max_streams=2, use_graphs=graphs)
+    bt = BatchedToken2Wav(fd, HiFTModel(Wh, use_graphs=graphs), noise_device="cpu")
+    d = od.dims_of(W)
+    h = oh.HiFT(Wh)
+    g = torch.Generator().manual_seed(seed)
+    mu, spk, pm = torch.randn(80, P, generator=g), torch.randn(80, generator=g), torch.randn(80, P, generator=g)
+    st = bt.new_stream(bt.setup(prompt_features(mu.cuda(), spk.cuda(), pm.cuda())), noise_seed=seed, adopt=True)
+    rc = od.empty_cache(d, keep=P)
+    od.solve(W, d, W["rand_noise"], [rc], [mu], spk[None], [pm], [True])
+    rh = oh.new_hift_state(noise_seed=seed)
+    seen, solve = [], fd.solve
+
+    def recording_solve(*a, **k):
+        out = solve(*a, **k)
+        seen.extend(out)
+        return out
+
+    fd.solve = recording_solve
+    mel_err, got, ref = [], [], []
+    for k, T in enumerate(windows):
+        last = k == len(windows) - 1
+        w = torch.randn(80, T, generator=g)
+        seen.clear()
+        got.append(bt.decode([(st, w.cuda(), last)])[0])
+        gm = seen[0].float().cpu()
+        mel = od.solve(W, d, W["rand_noise"], [rc], [w], spk[None], None, [not last])[0]
+        mel_err.append(rel(gm, mel))
+        ref.append(oh.vocode_chunk(h, rh, gm[None], last))
+    bt.release_stream(st)
+    assert fd.pool.in_use() == fd.scratch
+    return mel_err, got, ref
+
+
+def test_config2_chunk_full_size(dev):
+    """The streaming chunk of the latency workload at full model size: a 300-frame prompt setup (600 tokens with the CFG
+    pair), then a 50-frame first window and a 50-frame final window through ``decode`` (DiT + HiFT + glue)."""
+    W, Wh = init_dit(DiTConfig(), seed=1), init_hift(HiFTConfig(), seed=1)
+    mel_err, got, ref = _stream_pair(W, Wh, DiTConfig(), 300, [50, 50], seed=1)
+    a, b = np.concatenate(got), np.concatenate(ref)
+    e = float(np.linalg.norm(a - b) / np.linalg.norm(b))
+    print("config-2 window mel rel-L2", mel_err, "audio vs oracle glue on the same mels", e)
+    assert max(mel_err) < 2e-2 and e < 1e-4
+
+
+def test_worker_call_sequence(dev):
+    """The worker's sequence of calls (``engine/runtime/t2w_worker.py:448-560, 642-665, 826-838``) with graphs on:
+    startup prompt set up, ``capture_graphs``, that prompt released; stats reads; ``setup_many`` + ``new_stream(adopt)``;
+    asynchronous decodes polled with ``ready()`` and collected with ``result()``; a prefetched setup (``setup_encode``)
+    fused into a decode (``decode(setups=...)``) and adopted; an unused prefetched setup released; streams released.
+    Asynchronous audio equals a second module's synchronous audio bit for bit (same graphs, same inputs), and every
+    slot comes back."""
+    W, Wh = init_dit(TINY, seed=31), init_hift(HiFTConfig(), seed=32)
+
+    def module():
+        fd = FastDiT(DiTModel(W, TINY), n_slots=8192, max_streams=8, use_graphs=True)
+        return BatchedToken2Wav(fd, HiFTModel(Wh, decode_bf16=True, use_graphs=True), fuse_setup_frames=200, max_flow_streams=8)
+
+    bt, ref = module(), module()
+    g = torch.Generator().manual_seed(5)
+    feat = lambda P: prompt_features(torch.randn(80, P, generator=g).cuda(), torch.randn(80, generator=g).cuda(),  # noqa: E731
+                                     torch.randn(80, P, generator=g).cuda())
+    stats = lambda b: (b.fast.pool.in_use() - b.fast.scratch, len(b.fast.cnn_free), b.fast.counts["graph"], b.fast.counts["eager"])  # noqa: E731
+    free0 = len(bt.fast.cnn_free)
+    p0 = bt.setup(feat(40))
+    n = bt.capture_graphs(p0)
+    bt.release_prompt(p0)
+    print("captured", n, "stats", stats(bt))
+    assert n["dit"] > 0 and n["hift"] > 0 and stats(bt)[:2] == (0, free0)
+    feats = [feat(60), feat(35), feat(50)]
+    streams = {}
+    for b in (bt, ref):
+        ps = b.setup_many(feats[:2])
+        streams[id(b)] = [b.new_stream(p, noise_seed=10 + j, adopt=True) for j, p in enumerate(ps)]
+    windows = [[torch.randn(80, T, generator=g).cuda() for T in (16, 50, 50, 30)] for _ in range(3)]
+    out_async, out_sync = [[], [], []], [[], [], []]
+    for k in range(4):
+        last = k == 3
+        if k == 1:  # prefetch the third prompt's setup while a call runs, then fuse it into this decode
+            pre = bt.setup_encode([feats[2]])
+            spare = bt.setup_encode([feat(20)])
+            pend, prompts = bt.decode([(st, windows[j][k], last) for j, st in enumerate(streams[id(bt)])], async_result=True, setups=pre)
+            streams[id(bt)].append(bt.new_stream(prompts[0], noise_seed=12, adopt=True))
+            bt.release_presetup(spare[0])
+            wavs, rp = ref.decode([(st, windows[j][k], last) for j, st in enumerate(streams[id(ref)])], setups=ref.setup_encode([feats[2]]))
+            streams[id(ref)].append(ref.new_stream(rp[0], noise_seed=12, adopt=True))
+        else:
+            items = [(st, windows[j][k], last) for j, st in enumerate(streams[id(bt)])]
+            pend = bt.decode(items, async_result=True)
+            wavs = ref.decode([(st, windows[j][k], last) for j, st in enumerate(streams[id(ref)])])
+        assert isinstance(pend, PendingAudio)
+        while not pend.ready():
+            pass
+        res = pend.result()
+        for j, (a, b) in enumerate(zip(res, wavs)):
+            out_async[j].append(a)
+            out_sync[j].append(b)
+        print("decode", k, "stats", stats(bt))
+    for j in range(3):
+        a, b = np.concatenate(out_async[j]), np.concatenate(out_sync[j])
+        print("stream", j, "samples", a.size, "async vs sync max-abs", float(np.abs(a - b).max()) if a.size else 0.0)
+        assert a.shape == b.shape and np.array_equal(a, b)
+    assert sum(x.size for x in out_async[2]) > 0
+    for b in (bt, ref):
+        for st in streams[id(b)]:
+            b.release_stream(st)
+    assert stats(bt)[:2] == (0, free0)
+    assert bt.fast.counts["graph"] > 0

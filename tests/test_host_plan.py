@@ -1,25 +1,34 @@
 """Host logic of the solve (CPU): call planning tables and the per-row cache bookkeeping against the oracle's trim."""
 
+import numpy as np
 import pytest
 
 import t2w_amd  # noqa: F401
-from t2w_amd.dit import FastRow, SlotPool, advance_row, bucket_of, bucket_tiles, pad_plan, plan_call, token_buckets
+from t2w_amd.dit import FastRow, SlotPool, advance_row, all_buckets, bucket_of, bucket_tiles, plan_call, token_buckets
 from oracle import dit as od
 
 
+def _rows(specs):
+    return [FastRow(slots=np.asarray(s, dtype=np.int32), conv=c, cur=cur) for s, c, cur in specs]
+
+
+def _L(x):
+    return np.asarray(x).tolist()
+
+
 def test_plan_tables_are_consistent():
-    rows = [FastRow(order=[100, 101, 102], cnn=(0, 1)), FastRow(order=[], cnn=(2, 3), cur=1),
-            FastRow(order=[200, 201, 202], cnn=(4, 5)), FastRow(order=[], cnn=(6, 7), cur=1)]
+    rows = _rows([([100, 101, 102], (0, 1), 0), ([], (2, 3), 1), ([200, 201, 202], (4, 5), 0), ([], (6, 7), 1)])
     Ts = [70, 1]
-    new = [list(range(10, 80)), [90], list(range(300, 370)), [390]]
+    new = [np.arange(10, 80), np.array([90]), np.arange(300, 370), np.array([390])]
     p = plan_call(rows, Ts, new, [True, False], cnn_scratch=99)
-    tok_row, tok_pos, a_src, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, kv = p["parts"]
+    tok_row, tok_pos, a_src, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, kv = map(_L, p["parts"])
     assert p["n_tok"] == 142 and p["half"] == 71 and p["n_rows"] == 4
     assert a_src == [i + 2 * r for i, r in enumerate(tok_row)]
+    assert tok_pos == [t for T in lens for t in range(T)]
     assert lens == [70, 1, 70, 1] and row_start == [0, 70, 71, 141]
     for r in range(4):
         lst = kv[kv_off[r]:kv_off[r] + kv_len[r]]
-        assert lst[:lens[r]] == new[r] and lst[lens[r]:] == rows[r].order
+        assert lst[:lens[r]] == _L(new[r]) and lst[lens[r]:] == rows[r].order
     assert rd == [0, 3, 4, 7] and wr == [1, 99, 5, 99]
     covered = sorted((r, q) for r, q0 in zip(tiles[::2], tiles[1::2]) for q in range(q0, min(q0 + 64, lens[r])))
     assert covered == sorted((r, q) for r in range(4) for q in range(lens[r]))
@@ -34,20 +43,21 @@ def test_bucket_table():
     assert bucket_of(4, 220) == (4, 256) and bucket_of(4, 256) == (4, 256) and bucket_of(3, 257) == (4, 384)
     assert bucket_of(2, 5000) is None and bucket_of(6, 4000) == (8, 4096) and bucket_of(10, 4000) is None
     assert bucket_of(10, 900) == (32, 1024) and bucket_of(64, 3584) == (64, 3584) and bucket_of(66, 10) is None
+    assert len(all_buckets()) == sum(len(token_buckets(rb)) for rb in (2, 4, 8, 16, 32, 64))
 
 
 @pytest.mark.parametrize("Ts,keep", [([70, 1], [True, False]), ([64, 128, 5], [True, True, False]), ([50], [True])])
 def test_padded_plan_keeps_every_real_row(Ts, keep):
     n = len(Ts)
-    rows = [FastRow(order=list(range(1000 * r, 1000 * r + 7 * r)), cnn=(2 * r, 2 * r + 1), cur=r % 2) for r in range(2 * n)]
-    new = [list(range(100000 + 1000 * r, 100000 + 1000 * r + Ts[r % n])) for r in range(2 * n)]
-    p = plan_call(rows, Ts, new, keep, cnn_scratch=99)
-    rb, nb = bucket_of(2 * n, p["n_tok"])
-    q = pad_plan(p, rb, nb, kv_scratch=77, cnn_scratch=99)
+    rows = _rows([(range(1000 * r, 1000 * r + 7 * r), (2 * r, 2 * r + 1), r % 2) for r in range(2 * n)])
+    new = [np.arange(100000 + 1000 * r, 100000 + 1000 * r + Ts[r % n]) for r in range(2 * n)]
+    P = [_L(x) for x in plan_call(rows, Ts, new, keep, cnn_scratch=99)["parts"]]
+    rb, nb = bucket_of(2 * n, 2 * sum(Ts))
+    q = plan_call(rows, Ts, new, keep, cnn_scratch=99, cnn_zero=98, bucket=(rb, nb), kv_scratch=77)
     hr = rb // 2 + 1
-    tok_row, tok_pos, a_src, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, kv = q["parts"]
-    P = p["parts"]
+    tok_row, tok_pos, a_src, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, kv = map(_L, q["parts"])
     assert q["n_rows"] == 2 * hr and q["n_tok"] == nb and q["half"] == nb // 2 and len(tok_row) == nb
+    assert q["real_half"] == sum(Ts)
     assert sum(lens[:hr]) == sum(lens[hr:]) == nb // 2
     assert a_src == [i + 2 * r for i, r in enumerate(tok_row)]
     for h in range(2):
@@ -60,27 +70,48 @@ def test_padded_plan_keeps_every_real_row(Ts, keep):
                 assert T == P[5][o] and new_slot[s:s + T] == P[3][P[4][o]:P[4][o] + T]
                 assert kv[kv_off[r]:kv_off[r] + kv_len[r]] == P[11][P[6][o]:P[6][o] + P[7][o]]
                 assert (rd[r], wr[r]) == (P[8][o], P[9][o])
-            else:  # empty rows, then the padding row: scratch slots only
-                assert T == (0 if j < hr - 1 else nb // 2 - p["half"])
+            else:  # empty rows, then the padding row: scratch key slot, zero conv cache in, scratch conv cache out
+                assert T == (0 if j < hr - 1 else nb // 2 - sum(Ts))
                 assert new_slot[s:s + T] == [77] * T and kv[kv_off[r]:kv_off[r] + kv_len[r]] == [77] * T
-                assert rd[r] == wr[r] == 99
+                assert rd[r] == 98 and wr[r] == 99
     assert q["n_tiles"] == len(tiles) // 2 == bucket_tiles(rb, nb)
     live = [(r, q0) for r, q0 in zip(tiles[::2], tiles[1::2]) if q0 < lens[r]]
     covered = sorted((r, t) for r, q0 in live for t in range(q0, min(q0 + 64, lens[r])))
     assert covered == sorted((r, t) for r in range(2 * hr) for t in range(lens[r]))
+    # no row reads a conv slot that any row of the call writes
+    assert set(rd).isdisjoint(set(wr))
+
+
+def test_every_bucket_plans_within_its_tile_bound():
+    for rb, nb in all_buckets():
+        q = plan_call([], [], [], [], cnn_scratch=1, cnn_zero=0, bucket=(rb, nb), kv_scratch=5)
+        assert q["n_tok"] == nb and q["n_tiles"] == bucket_tiles(rb, nb)
 
 
 @pytest.mark.parametrize("keep_len", [0, 40, 300])
 def test_row_bookkeeping_follows_the_oracle_trim(keep_len):
-    pool = SlotPool(10000)
-    row = FastRow(order=pool.alloc(keep_len), cnn=(0, 1))
-    ref = list(row.order)
+    pool = SlotPool(10000, reserved=1)
+    row = FastRow(slots=pool.alloc(keep_len), conv=(0, 1))
+    ref = row.order
     for w in range(7):
         nw = pool.alloc(50)
         freed = advance_row(row, nw, keep=w != 3, keep_len=keep_len)
         pool.release(freed)
         if w != 3:
-            ref = od.trim_order(nw + ref, keep_len)
+            ref = od.trim_order(_L(nw) + ref, keep_len)
         assert row.order == ref
-        assert pool.in_use() == len(row.order)
+        assert pool.in_use() - 1 == len(row.order)
     assert row.cur == 0  # six kept windows swapped the conv slots six times
+
+
+def test_slot_pool_reserved_and_exhaustion():
+    pool = SlotPool(8, reserved=1)
+    assert pool.in_use() == 1 and pool.n_free == 7
+    a = pool.alloc(5)
+    assert len(set(_L(a)) | set(_L(pool.reserved))) == 6
+    with pytest.raises(RuntimeError, match="exhausted"):
+        pool.alloc(3)
+    pool.release(a)
+    assert pool.in_use() == 1
+    b = pool.alloc(7)
+    assert sorted(_L(b) + _L(pool.reserved)) == list(range(8))
