@@ -128,6 +128,13 @@ typedef struct {
 /* includes the fp8 activation buffers once the model has fp8 weights */
 size_t t2w_dit_workspace_bytes(const t2w_dit* m, int n_tok, int n_rows);
 int t2w_dit_solve(const t2w_dit* m, const t2w_solve_args* a, void* stream);
+/* t2w_dit_solve without a workspace, allocating nothing: for callers that cannot allocate device memory (code under
+ * hipGraph capture, tight serving loops).  No counterpart in the reference.  The workspace is a static device array of
+ * 32 MiB that the library holds on each device it runs on until the process ends; a->workspace and
+ * a->workspace_bytes are ignored.  Calls needing more (t2w_dit_workspace_bytes() > 32 MiB: at hidden 1024 about 800
+ * tokens) fail with a message.  Every call on a device shares that device's array, so calls that overlap on one
+ * device (concurrent streams or threads) race; serialise them.  Nothing in it needs clearing between calls. */
+int t2w_dit_solve_noalloc(const t2w_dit* m, const t2w_solve_args* a, void* stream);
 /* One estimator evaluation at Euler step `step`'s key/value and conv-cache layers with the given tables
  * (mods [depth, 9, H], final_mods [2, H]) on in_rows; writes dphi [n_tok, mel] to a->out. */
 int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const float* mods, const float* final_mods,

@@ -80,6 +80,7 @@ _SIGS = {
     "t2w_dit_workspace_bytes": (C.c_size_t, [P, I, I]),
     "t2w_dit_solve": (I, [P, C.POINTER(SolveArgs), P]),
     "t2w_dit_forward": (I, [P, C.POINTER(SolveArgs), I, P, P, P]),
+    "t2w_dit_solve_noalloc": (I, [P, C.POINTER(SolveArgs), P]),
     "t2w_gemm_bf16": (I, [P, I, P, P, P, P, P, I, I, I, I, I, P]),
     "t2w_gemm_bf16_tile": (I, [P, I, P, P, P, P, P, I, I, I, I, I, I, P]),
     "t2w_gemm_bf16_ws": (I, [P, I, P, P, P, P, P, I, I, I, I, I, P, C.c_size_t, P]),

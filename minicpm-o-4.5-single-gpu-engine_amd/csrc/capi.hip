@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <mutex>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -41,6 +42,35 @@ size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 namespace t2w {
 int set_error(const char* what, hipError_t e) { return fail(what, e); }
 }  // namespace t2w
+
+// Scratch of t2w_dit_solve_noalloc: the solve's whole workspace (activations, split-K partials) for calls that fit,
+// in device memory the library owns.  Each device holds its own copy from module load until the process ends; host
+// code only ever uses the per-device address hipGetSymbolAddress returns (the symbol itself names a host stand-in).
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_dev;  // device ordinal -> address of that device's scratch (null until looked up)
+
+// The current device's scratch address, looked up once per device (the current device must be the one asked about).
+int scratch_address(void** out) {
+  int dev = 0;
+  T2W_CHECK(hipGetDevice(&dev), "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((size_t)dev >= g_scratch_dev.size()) g_scratch_dev.resize(dev + 1, nullptr);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    T2W_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!p) return fail("hipGetSymbolAddress(scratch) returned null");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
+}
+
+}  // namespace
 
 struct t2w_dit {
   t2w_dit_dims d;
@@ -310,6 +340,8 @@ int t2w_dit_create(const t2w_dit_dims* dims, t2w_dit** out) {
   if (d.hidden != 256 && d.hidden != 512 && d.hidden != 1024) return fail("hidden must be 256, 512 or 1024");
   if ((4 * d.mel) % 64 || d.ffn % 64) return fail("4 * mel and ffn must be multiples of 64");
   if (d.depth <= 0 || d.steps <= 0 || d.steps > 16) return fail("bad depth / steps");
+  void* scr = nullptr;
+  if (scratch_address(&scr)) return 1;  // the no-allocation solve's scratch on the current device, looked up at set-up
   t2w_dit* m = new t2w_dit();
   m->d = d;
   m->blocks.resize(d.depth);
@@ -394,6 +426,24 @@ int t2w_dit_solve(const t2w_dit* m, const t2w_solve_args* a, void* stream) {
               "euler");
   }
   return 0;
+}
+
+int t2w_dit_solve_noalloc(const t2w_dit* m, const t2w_solve_args* a, void* stream) {
+  if (check_model(m)) return 1;
+  if (!a) return fail("null args");
+  const size_t need = carve(m->d, a->n_tok, a->n_rows, m->fp8_ready(), nullptr, nullptr);
+  if (need > NOALLOC_SCRATCH_BYTES) {
+    char buf[256];
+    snprintf(buf, sizeof buf, "t2w_dit_solve_noalloc: a call of %d tokens and %d rows needs %zu bytes of scratch, the static "
+             "scratch holds %zu (use t2w_dit_solve with a workspace)", a->n_tok, a->n_rows, need, NOALLOC_SCRATCH_BYTES);
+    return fail(buf);
+  }
+  void* scr = nullptr;
+  if (scratch_address(&scr)) return 1;
+  t2w_solve_args b = *a;
+  b.workspace = scr;
+  b.workspace_bytes = NOALLOC_SCRATCH_BYTES;
+  return t2w_dit_solve(m, &b, stream);
 }
 
 int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const float* mods, const float* final_mods, void* stream) {
