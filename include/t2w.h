@@ -142,14 +142,15 @@ int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const f
 
 /* ---------------------------------------------------------------- kernel-level entry points (tests, benchmarks) */
 
-/* C = A . W^T + bias; epi 0: bf16 out, 1: GELU-tanh bf16 out, 2: C(fp32) += gate * (.), 3: fp32 out.
+/* C = A . W^T + bias; epi 0: bf16 out, 1: GELU-tanh bf16 out, 2: C(fp16) = fp16(C + gate * (.)) (the gated residual
+ * stream, fp16 as the reference's activations, fp32 arithmetic), 3: fp32 out, 7: fp16 out.
  * a_src non-null: conv taps mode, A row m = frames a_src[m] .. a_src[m] + K / lda - 1 of A (rows lda wide).
  * Calls of at most 128 rows (K <= 3072, ldc % 4 == 0) run as one kernel that splits K over the waves of a workgroup;
- * larger ones on the tile GEMM (bf16 outputs: ldc % 8 == 0 and C 16-byte aligned there). */
+ * larger ones on the tile GEMM (16-bit outputs: ldc % 8 == 0 and C 16-byte aligned there). */
 int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                   void* C, int ldc, int M, int N, int K, int epi, void* stream);
 /* t2w_gemm_bf16 with an explicit tile configuration (-1: chosen by shape; 0: 128x128 of 4 waves, 1: 256x256 of
- * 8 waves, 2: 256x128 of 8 waves, 3: 256x256 of 4 waves on a four-stage LDS ring, K % 128 == 0) for tile sweeps.
+ * 8 waves, 2: 256x128 of 8 waves) for tile sweeps.
  * K % 64 == 0, lda % 8 == 0 (taps mode: lda % 64 == 0). */
 int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                        void* C, int ldc, int M, int N, int K, int epi, int tile, void* stream);
@@ -166,7 +167,8 @@ int t2w_quant_mx8(const void* x, int ldx, int M, int K, void* q, int ldq, void* 
  * (taps mode as t2w_gemm_bf16, rows = frames), W [N, K] e4m3 scaled per output channel by w_scale[N].  K % 128 == 0. */
 int t2w_gemm_fp8(const void* A, int lda, const int* a_src, const void* a_scale, int a_sld, const void* W, const float* w_scale,
                  const float* bias, const float* gate, void* C, int ldc, int M, int N, int K, int epi, void* stream);
-int t2w_ln_mod(const float* h, const float* shift, const float* scale1, float eps, void* out, int N, int H,
+/* LayerNorm (no affine) of the fp16 residual rows h [N, H], then * scale1 + shift (fp32), out bf16 [N, H] */
+int t2w_ln_mod(const void* h, const float* shift, const float* scale1, float eps, void* out, int N, int H,
                void* stream);
 int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const float* kw, const float* kb, float eps,
                         void* q_out, void* k_pool, void* v_pool, const int* slots, int N, int heads, void* stream);

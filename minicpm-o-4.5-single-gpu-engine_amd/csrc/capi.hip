@@ -91,7 +91,7 @@ struct t2w_dit {
 namespace {
 
 struct Work {  // carve of the caller's workspace for n tokens, R rows
-  bf16_t* a_in; float* x; float* h; bf16_t* abuf; bf16_t* big; bf16_t* q; bf16_t* ao; bf16_t* P; float* dphi;
+  bf16_t* a_in; float* x; f16_t* h; bf16_t* abuf; bf16_t* big; bf16_t* q; bf16_t* ao; bf16_t* P; float* dphi;
   float* part; size_t part_bytes;  // split-K partials of the GEMMs of calls with few tokens
   // fp8 mode: MX fp8 activations (codes, block scales) of the qkv / fc1 inputs, the attention output, the conv frame
   // buffer and the fc1 output
@@ -110,7 +110,7 @@ size_t carve(const t2w_dit_dims& d, int N, int R, bool fp8, char* base, Work* w)
   Work t;
   t.a_in = (bf16_t*)take((size_t)N * 4 * M * 2);
   t.x = (float*)take((size_t)N * M * 4);
-  t.h = (float*)take((size_t)N * H * 4);
+  t.h = (f16_t*)take((size_t)N * H * 2);  // the residual stream, fp16
   t.abuf = (bf16_t*)take((size_t)N * H * 2);
   t.big = (bf16_t*)take(bigc * 2);
   t.q = (bf16_t*)take((size_t)N * H * 2);
@@ -211,7 +211,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
                   const float* fmods, float* dphi, hipStream_t st) {
   const t2w_dit_dims& d = m->d;
   const int N = a->n_tok, R = a->n_rows, H = d.hidden, F = d.ffn, M = d.mel, D = d.depth;
-  T2W_CHECK(gemm_bf16(gemm_args(w.a_in, 4 * M, nullptr, m->g.in_w, m->g.in_b, nullptr, w.h, H, N, H, 4 * M, &w), EPI_F32, st), "in_proj");
+  T2W_CHECK(gemm_bf16(gemm_args(w.a_in, 4 * M, nullptr, m->g.in_w, m->g.in_b, nullptr, w.h, H, N, H, 4 * M, &w), EPI_F16, st), "in_proj");
   const long long cstride = (long long)d.steps * D * 4 * H;
   const bool f8 = a->fp8 != 0;
   // Calls of few tokens: the gated-residual GEMMs and conv1 split K over several workgroups per tile and the row
@@ -253,12 +253,12 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     if (f8) { at.out8 = w.o8; at.out8s = w.o8s; }
     T2W_CHECK(attention(at, st), "attention");
     if (f8)
-      T2W_CHECK(gemm_bf16(gemm8(w.o8, H, nullptr, w.o8s, k8->proj_w8, k8->proj_ws, k.proj_b, g_a, w.h, H, N, H, H), EPI_RESID_F32, st), "proj");
+      T2W_CHECK(gemm_bf16(gemm8(w.o8, H, nullptr, w.o8s, k8->proj_w8, k8->proj_ws, k.proj_b, g_a, w.h, H, N, H, H), EPI_RESID_F16, st), "proj");
     else if (S) {
       pend = gemm_deferred(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), Sd, w, st, &perr);
       T2W_CHECK(perr, "proj");
     } else {
-      T2W_CHECK(gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F32, st), "proj");
+      T2W_CHECK(gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F16, st), "proj");
     }
     ConvPlace cp;
     cp.P = w.P; cp.tok_row = a->tok_row; cp.tok_pos = a->tok_pos; cp.row_start = a->row_start; cp.row_len = a->row_len;
@@ -282,12 +282,12 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     T2W_CHECK(ln_mish_conv(w.ao, k.cln_w, k.cln_b, d.eps_conv, cp, H, st, pend), "ln_mish_conv");
     pend = Pend();
     if (f8) {
-      T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c2_w8, k8->c2_ws, k.c2_b, g_c, w.h, H, N, H, 3 * H), EPI_RESID_F32, st), "conv2");
+      T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c2_w8, k8->c2_ws, k.c2_b, g_c, w.h, H, N, H, 3 * H), EPI_RESID_F16, st), "conv2");
     } else if (S) {
       pend = gemm_deferred(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), St, w, st, &perr);
       T2W_CHECK(perr, "conv2");
     } else {
-      T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), EPI_RESID_F32, st), "conv2");
+      T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), EPI_RESID_F16, st), "conv2");
     }
     if (f8) {
       T2W_CHECK(ln_mod_mx8(w.h, sh_m, sc_m, d.eps_block, w.a8, w.a8s, N, H, st), "ln_mod mlp");
@@ -295,7 +295,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
       g1.c_scale = w.b8s;
       g1.c_sld = F / 32;
       T2W_CHECK(gemm_bf16(g1, EPI_GELU_MX8, st), "fc1");
-      T2W_CHECK(gemm_bf16(gemm8(w.b8, F, nullptr, w.b8s, k8->fc2_w8, k8->fc2_ws, k.fc2_b, g_m, w.h, H, N, H, F), EPI_RESID_F32, st), "fc2");
+      T2W_CHECK(gemm_bf16(gemm8(w.b8, F, nullptr, w.b8s, k8->fc2_w8, k8->fc2_ws, k.fc2_b, g_m, w.h, H, N, H, F), EPI_RESID_F16, st), "fc2");
     } else {
       T2W_CHECK(ln_mod(w.h, sh_m, sc_m, d.eps_block, w.abuf, N, H, st, pend), "ln_mod mlp");
       pend = Pend();
@@ -304,7 +304,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
         pend = gemm_deferred(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), Sd, w, st, &perr);
         T2W_CHECK(perr, "fc2");
       } else {
-        T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F32, st), "fc2");
+        T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F16, st), "fc2");
       }
     }
   }
@@ -467,10 +467,9 @@ int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, 
                        int M, int N, int K, int epi, int tile, void* stream) {
   if (K % 64) return fail("K must be a multiple of 64");
   if (lda % 8) return fail("lda must be a multiple of 8 (16-byte rows)");
-  if (epi < 0 || epi > 3) return fail("bad epilogue");
+  if (epi < 0 || (epi > 3 && epi != EPI_F16)) return fail("bad epilogue");
   if (a_src && (K % lda || lda % 64)) return fail("taps mode: K must be a multiple of lda, lda of 64");
-  if (tile > 3) return fail("bad tile configuration");
-  if (tile == 3 && K % 128) return fail("tile 3 (LDS ring): K must be a multiple of 128");
+  if (tile > 2) return fail("bad tile configuration");
   T2W_CHECK(gemm_bf16(gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K), epi, (hipStream_t)stream, tile), "gemm");
   return 0;
 }
@@ -479,7 +478,7 @@ int t2w_gemm_bf16_ws(const void* A, int lda, const int* a_src, const void* W, co
                      int ldc, int M, int N, int K, int epi, void* workspace, size_t workspace_bytes, void* stream) {
   if (K % 64) return fail("K must be a multiple of 64");
   if (lda % 8) return fail("lda must be a multiple of 8 (16-byte rows)");
-  if (epi < 0 || epi > 3) return fail("bad epilogue");
+  if (epi < 0 || (epi > 3 && epi != EPI_F16)) return fail("bad epilogue");
   if (a_src && (K % lda || lda % 64)) return fail("taps mode: K must be a multiple of lda, lda of 64");
   if (((uintptr_t)workspace & 255) != 0) return fail("workspace must be 256-byte aligned");
   GemmArgs g = gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K);
@@ -510,8 +509,8 @@ int t2w_gemm_fp8(const void* A, int lda, const int* a_src, const void* a_scale, 
   return 0;
 }
 
-int t2w_ln_mod(const float* h, const float* shift, const float* scale1, float eps, void* out, int N, int H, void* stream) {
-  T2W_CHECK(ln_mod(const_cast<float*>(h), shift, scale1, eps, (bf16_t*)out, N, H, (hipStream_t)stream), "ln_mod");  // h only read
+int t2w_ln_mod(const void* h, const float* shift, const float* scale1, float eps, void* out, int N, int H, void* stream) {
+  T2W_CHECK(ln_mod((f16_t*)const_cast<void*>(h), shift, scale1, eps, (bf16_t*)out, N, H, (hipStream_t)stream), "ln_mod");  // h only read
   return 0;
 }
 

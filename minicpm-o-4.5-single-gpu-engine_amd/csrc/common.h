@@ -24,6 +24,15 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   const f32x2_t v = {a, b};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+// fp16 storage of the residual stream (the reference's activation dtype): round to nearest even, one value at a time
+typedef uint16_t f16_t;
+
+__device__ __forceinline__ f16_t f2h(float f) { return __builtin_bit_cast(f16_t, (_Float16)f); }
+__device__ __forceinline__ float h2f(f16_t x) { return (float)__builtin_bit_cast(_Float16, x); }
+__device__ __forceinline__ uint32_t pack2h(float a, float b) { return (uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16); }
+__device__ __forceinline__ float lo2h(uint32_t w) { return h2f((f16_t)(w & 0xffffu)); }
+__device__ __forceinline__ float hi2h(uint32_t w) { return h2f((f16_t)(w >> 16)); }
+
 __device__ __forceinline__ float lo2f(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi2f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 

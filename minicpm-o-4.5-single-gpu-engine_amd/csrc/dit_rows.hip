@@ -71,6 +71,36 @@ __device__ __forceinline__ void row_store_f32(float* row, int lane, const float 
     }
 }
 
+// fp16 rows (the residual stream), G-grouped like row_load_f32: 2 G bytes per lane and group
+template <int VPL, int G>
+__device__ __forceinline__ void row_load_f16(const f16_t* row, int lane, float (&v)[VPL]) {
+#pragma unroll
+  for (int k = 0; k < VPL / G; ++k) {
+    const f16_t* p = row + row_col<G>(k, lane);
+    float* d = v + k * G;
+    if (G == 8) {
+      const uint4 x = *(const uint4*)p;
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { d[2 * j] = lo2h(w[j]); d[2 * j + 1] = hi2h(w[j]); }
+    } else {
+      const uint2 x = *(const uint2*)p;
+      d[0] = lo2h(x.x); d[1] = hi2h(x.x); d[2] = lo2h(x.y); d[3] = hi2h(x.y);
+    }
+  }
+}
+
+template <int VPL, int G>
+__device__ __forceinline__ void row_store_f16(f16_t* row, int lane, const float (&v)[VPL]) {
+#pragma unroll
+  for (int k = 0; k < VPL / G; ++k) {
+    f16_t* p = row + row_col<G>(k, lane);
+    const float* x = v + k * G;
+    if (G == 8) *(uint4*)p = make_uint4(pack2h(x[0], x[1]), pack2h(x[2], x[3]), pack2h(x[4], x[5]), pack2h(x[6], x[7]));
+    else *(uint2*)p = make_uint2(pack2h(x[0], x[1]), pack2h(x[2], x[3]));
+  }
+}
+
 // The pending GEMM's value of row n (sum of its K splits in split order, then + bias), G-grouped like row_load_f32;
 // all splits' loads are issued before the first add (at most 4 splits).
 template <int VPL, int G>
@@ -92,15 +122,16 @@ __device__ __forceinline__ void pend_value(const Pend& pd, int n, int lane, floa
   for (int i = 0; i < VPL; ++i) p[i] += b[i];
 }
 
-// h row n (in v) += gate * pending value, stored back to h (the gated residual epilogue of the GEMM, in its order)
+// h row n (in v) += gate * pending value, rounded to fp16 and stored back to h (the gated residual epilogue of the
+// GEMM, in its order); v keeps the rounded values the next norm reads
 template <int VPL, int G>
-__device__ __forceinline__ void pend_resid(const Pend& pd, float* hrow, int n, int lane, float (&v)[VPL]) {
+__device__ __forceinline__ void pend_resid(const Pend& pd, f16_t* hrow, int n, int lane, float (&v)[VPL]) {
   float p[VPL], gt[VPL];
   pend_value<VPL, G>(pd, n, lane, p);
   row_load_f32<VPL, G>(pd.gate, lane, gt);
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) v[i] += gt[i] * p[i];
-  row_store_f32<VPL, G>(hrow, lane, v);
+  for (int i = 0; i < VPL; ++i) v[i] = h2f(f2h(v[i] + gt[i] * p[i]));
+  row_store_f16<VPL, G>(hrow, lane, v);
 }
 
 // raw bf16 words of a row (G / 2 per group)
@@ -178,26 +209,27 @@ __device__ __forceinline__ void normalize(float (&v)[VPL], int H, float eps) {
 // PEND: a pending GEMM result is finished first (a separate instantiation, so that the large calls, which never defer,
 // keep the registers and occupancy of the plain kernel)
 template <int VPL, bool PEND>
-__global__ void __launch_bounds__(256) ln_mod_kernel(float* h, const float* shift, const float* scale1, float eps,
+__global__ void __launch_bounds__(256) ln_mod_kernel(f16_t* h, const float* shift, const float* scale1, float eps,
                                                      bf16_t* out, uint8_t* q, uint8_t* qs, int N, int H, Pend pd) {
+  constexpr int G = VPL >= 8 ? 8 : 4;  // fp16 rows: 16 bytes per lane and instruction
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (n >= N) return;
   float v[VPL], sc[VPL], sh[VPL];
-  row_load_f32<VPL, 4>(h + (size_t)n * H, lane, v);
-  if (PEND) pend_resid<VPL, 4>(pd, h + (size_t)n * H, n, lane, v);
+  row_load_f16<VPL, G>(h + (size_t)n * H, lane, v);
+  if (PEND) pend_resid<VPL, G>(pd, h + (size_t)n * H, n, lane, v);
   normalize<VPL>(v, H, eps);
-  row_load_f32<VPL, 4>(scale1, lane, sc);
-  row_load_f32<VPL, 4>(shift, lane, sh);
+  row_load_f32<VPL, G>(scale1, lane, sc);
+  row_load_f32<VPL, G>(shift, lane, sh);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) v[i] = v[i] * sc[i] + sh[i];
   if (q) {
-    row_store_mx8<VPL, 4>(v, q + (size_t)n * H, qs + (size_t)n * (H / 32), lane);
+    row_store_mx8<VPL, G>(v, q + (size_t)n * H, qs + (size_t)n * (H / 32), lane);
     return;
   }
   uint32_t o[VPL / 2];
   pack_bf<VPL>(v, o);
-  row_store_bf<VPL, 4>(out + (size_t)n * H, lane, o);
+  row_store_bf<VPL, G>(out + (size_t)n * H, lane, o);
 }
 
 // Frame f of token n (position t of row r, T frames) in the padded buffer is n + 2 r + 2; it is also the row's new
@@ -241,24 +273,25 @@ __device__ __forceinline__ void place_row(const ConvPlace& cp, int r, int H, int
 }
 
 template <int VPL, bool PEND>
-__global__ void __launch_bounds__(256) ln_mod_conv_kernel(float* h, const float* shift, const float* scale1, float eps,
+__global__ void __launch_bounds__(256) ln_mod_conv_kernel(f16_t* h, const float* shift, const float* scale1, float eps,
                                                           ConvPlace cp, int H, Pend pd) {
+  constexpr int G = VPL >= 8 ? 8 : 4;
   const int lane = threadIdx.x & 63;
   const int w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (w < cp.N) {
     float v[VPL], sc[VPL], sh[VPL];
-    row_load_f32<VPL, 4>(h + (size_t)w * H, lane, v);
-    if (PEND) pend_resid<VPL, 4>(pd, h + (size_t)w * H, w, lane, v);
+    row_load_f16<VPL, G>(h + (size_t)w * H, lane, v);
+    if (PEND) pend_resid<VPL, G>(pd, h + (size_t)w * H, w, lane, v);
     normalize<VPL>(v, H, eps);
-    row_load_f32<VPL, 4>(scale1, lane, sc);
-    row_load_f32<VPL, 4>(shift, lane, sh);
+    row_load_f32<VPL, G>(scale1, lane, sc);
+    row_load_f32<VPL, G>(shift, lane, sh);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) v[i] = v[i] * sc[i] + sh[i];
     uint32_t o[VPL / 2];
     pack_bf<VPL>(v, o);
-    place_token<VPL, 4>(cp, w, H, lane, v, o);
+    place_token<VPL, G>(cp, w, H, lane, v, o);
   } else if (w < cp.N + cp.R) {
-    place_row<VPL, 4>(cp, w - cp.N, H, lane);
+    place_row<VPL, G>(cp, w - cp.N, H, lane);
   }
 }
 
@@ -450,7 +483,7 @@ inline int row_waves(long long rows) { return rows <= 1024 ? 1 : 4; }
     default: return hipErrorInvalidValue;  \
   }
 
-hipError_t ln_mod(float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H, hipStream_t st,
+hipError_t ln_mod(f16_t* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H, hipStream_t st,
                   const Pend& pd) {
   if (N <= 0) return hipSuccess;
   if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;
@@ -462,15 +495,15 @@ hipError_t ln_mod(float* h, const float* shift, const float* scale1, float eps, 
   return hipGetLastError();
 }
 
-hipError_t ln_mod_mx8(const float* h, const float* shift, const float* scale1, float eps, uint8_t* q, uint8_t* qs, int N,
+hipError_t ln_mod_mx8(const f16_t* h, const float* shift, const float* scale1, float eps, uint8_t* q, uint8_t* qs, int N,
                       int H, hipStream_t st) {
   if (N <= 0) return hipSuccess;
   // nothing pending: h is only read
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, false>), dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, const_cast<float*>(h), shift, scale1, eps, nullptr, q, qs, N, H, Pend()));
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, false>), dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, const_cast<f16_t*>(h), shift, scale1, eps, nullptr, q, qs, N, H, Pend()));
   return hipGetLastError();
 }
 
-hipError_t ln_mod_conv(float* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H, hipStream_t st,
+hipError_t ln_mod_conv(f16_t* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H, hipStream_t st,
                        const Pend& pd) {
   if (cp.N + cp.R <= 0) return hipSuccess;
   if (pd.part && (pd.S < 1 || pd.S > 4)) return hipErrorInvalidValue;

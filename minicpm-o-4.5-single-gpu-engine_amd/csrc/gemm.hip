@@ -121,8 +121,8 @@ GemmArgs rows_from(const GemmArgs& g, int r) {
   h.M = g.M - r;
   if (g.a_src) h.a_src = g.a_src + r;
   else h.A = g.A + (size_t)r * g.lda;
-  if (EPI == EPI_RESID_F32 || EPI == EPI_F32) h.C = (float*)g.C + (size_t)r * g.ldc;
-  else h.C = (bf16_t*)g.C + (size_t)r * g.ldc;
+  if (EPI == EPI_F32) h.C = (float*)g.C + (size_t)r * g.ldc;
+  else h.C = (uint16_t*)g.C + (size_t)r * g.ldc;  // bf16 or fp16 rows
   if (EPI == EPI_QKV) {
     h.qk.q_out = g.qk.q_out + (size_t)r * g.qk.H;
     h.qk.slots = g.qk.slots + r;
@@ -183,23 +183,21 @@ hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
   if (cfg < 0 && gemm_small_fits(g, epi)) return gemm_small(g, epi, st);
   // the tile epilogues store bf16 rows 16 bytes per lane
-  const bool bf16_out = epi == EPI_BF16 || epi == EPI_GELU_BF16;
+  const bool bf16_out = epi == EPI_BF16 || epi == EPI_GELU_BF16 || epi == EPI_RESID_F16 || epi == EPI_F16;  // 16-bit rows
   if (bf16_out && (g.ldc % 8 || ((size_t)g.C & 15)) && !(cfg < 0 && gemm_splits(g))) return hipErrorInvalidValue;
   if (cfg < 0 && gemm_splits(g)) {
     if (epi == EPI_QKV || epi == EPI_GELU_MX8) return hipErrorInvalidValue;  // tile-path epilogues
     return gemm_splitk(g, epi, splitk_plan(g.M, g.N, g.K, g.ws_bytes), g.ws, st);
   }
-  // the four-wave ring on request only: on its own its main loop is the faster one, but with the DiT's epilogues
-  // (gated fp32 residual, q/k LayerNorm scatter) four waves hide less of the epilogue's memory traffic than eight
-  if (cfg == 3) return gemm_ring(g, epi, st);
   const bool taps = g.a_src != nullptr;
   switch (epi * 2 + (taps ? 1 : 0)) {
     case EPI_BF16 * 2: return launch_epi<EPI_BF16, false>(g, cfg, st);
     case EPI_BF16 * 2 + 1: return launch_epi<EPI_BF16, true>(g, cfg, st);
     case EPI_GELU_BF16 * 2: return launch_epi<EPI_GELU_BF16, false>(g, cfg, st);
     case EPI_GELU_BF16 * 2 + 1: return launch_epi<EPI_GELU_BF16, true>(g, cfg, st);
-    case EPI_RESID_F32 * 2: return launch_epi<EPI_RESID_F32, false>(g, cfg, st);
-    case EPI_RESID_F32 * 2 + 1: return launch_epi<EPI_RESID_F32, true>(g, cfg, st);
+    case EPI_RESID_F16 * 2: return launch_epi<EPI_RESID_F16, false>(g, cfg, st);
+    case EPI_RESID_F16 * 2 + 1: return launch_epi<EPI_RESID_F16, true>(g, cfg, st);
+    case EPI_F16 * 2: return launch_epi<EPI_F16, false>(g, cfg, st);
     case EPI_F32 * 2: return launch_epi<EPI_F32, false>(g, cfg, st);
     case EPI_F32 * 2 + 1: return launch_epi<EPI_F32, true>(g, cfg, st);
     case EPI_GELU_MX8 * 2:

@@ -138,11 +138,13 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
     }
     if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) {
       *(uint2*)((bf16_t*)g.C + off) = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
-    } else if (EPI == EPI_RESID_F32) {
+    } else if (EPI == EPI_RESID_F16) {
       const float4 gt = *(const float4*)(g.gate + n);
-      float4* hp = (float4*)((float*)g.C + off);
-      const float4 hv = *hp;
-      *hp = make_float4(hv.x + gt.x * o[0], hv.y + gt.y * o[1], hv.z + gt.z * o[2], hv.w + gt.w * o[3]);
+      uint2* hp = (uint2*)((f16_t*)g.C + off);
+      const uint2 hv = *hp;
+      *hp = make_uint2(pack2h(lo2h(hv.x) + gt.x * o[0], hi2h(hv.x) + gt.y * o[1]), pack2h(lo2h(hv.y) + gt.z * o[2], hi2h(hv.y) + gt.w * o[3]));
+    } else if (EPI == EPI_F16) {
+      *(uint2*)((f16_t*)g.C + off) = make_uint2(pack2h(o[0], o[1]), pack2h(o[2], o[3]));
     } else {
       *(float4*)((float*)g.C + off) = make_float4(o[0], o[1], o[2], o[3]);
     }
@@ -154,7 +156,8 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
     if (EPI == EPI_PART) { part[off] = v[e]; continue; }
     if (EPI == EPI_GELU_BF16) x = gelu_tanh(x);
     if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[off] = f2bf(x);
-    else if (EPI == EPI_RESID_F32) ((float*)g.C)[off] += g.gate[n + e] * x;
+    else if (EPI == EPI_RESID_F16) ((f16_t*)g.C)[off] = f2h(h2f(((const f16_t*)g.C)[off]) + g.gate[n + e] * x);
+    else if (EPI == EPI_F16) ((f16_t*)g.C)[off] = f2h(x);
     else ((float*)g.C)[off] = x;
   }
 }
@@ -350,7 +353,7 @@ bool gemm_small_fits(const GemmArgs& g, int epi) {
     return g.M > 0 && g.M <= GEMM_SMALL_MAX_M && !g.w_scale && !g.a_src && g.K % 64 == 0 && g.K <= GS_WAVES * 64 &&
            g.qk.H % 64 == 0 && g.N == 3 * g.qk.H && g.lda % 8 == 0 && g.ldb % 8 == 0;
   if (epi == EPI_PART && (g.splits < 1 || g.splits > 4 || g.splits > g.K / 64)) return false;
-  return g.M > 0 && g.M <= GEMM_SMALL_MAX_M && !g.w_scale && (epi <= EPI_F32 || epi == EPI_PART) && g.K % 64 == 0 &&
+  return g.M > 0 && g.M <= GEMM_SMALL_MAX_M && !g.w_scale && (epi <= EPI_F32 || epi == EPI_PART || epi == EPI_F16) && g.K % 64 == 0 &&
          g.K <= GS_WAVES * GS_MAXSTEPS * 64 && g.lda % 8 == 0 && g.ldb % 8 == 0 && g.ldc % 4 == 0 &&
          (!g.a_src || g.tapC % 64 == 0);
 }
@@ -371,7 +374,8 @@ hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st) {
   switch (epi) {
     case EPI_BF16: return launch_small<EPI_BF16>(g, st);
     case EPI_GELU_BF16: return launch_small<EPI_GELU_BF16>(g, st);
-    case EPI_RESID_F32: return launch_small<EPI_RESID_F32>(g, st);
+    case EPI_RESID_F16: return launch_small<EPI_RESID_F16>(g, st);
+    case EPI_F16: return launch_small<EPI_F16>(g, st);
     case EPI_F32: return launch_small<EPI_F32>(g, st);
     case EPI_PART: return launch_small<EPI_PART>(g, st);
     case EPI_QKV:

@@ -137,7 +137,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, const fl
       if (s0 + x < S) { a.x += b[x].x; a.y += b[x].y; a.z += b[x].z; a.w += b[x].w; }
   }
   const float bias = g.bias[n];
-  const float gate = EPI == EPI_RESID_F32 ? g.gate[n] : 0.f;
+  const float gate = EPI == EPI_RESID_F16 ? g.gate[n] : 0.f;
   const float v[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -147,7 +147,8 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, const fl
     const size_t o = (size_t)m * g.ldc + n;
     if (EPI == EPI_GELU_BF16) x = gelu_tanh(x);
     if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[o] = f2bf(x);
-    else if (EPI == EPI_RESID_F32) ((float*)g.C)[o] += gate * x;
+    else if (EPI == EPI_RESID_F16) ((f16_t*)g.C)[o] = f2h(h2f(((const f16_t*)g.C)[o]) + gate * x);
+    else if (EPI == EPI_F16) ((f16_t*)g.C)[o] = f2h(x);
     else ((float*)g.C)[o] = x;
   }
 }
@@ -192,7 +193,8 @@ hipError_t gemm_splitk(const GemmArgs& g, int epi, const SplitPlan& p, float* pa
   switch (epi) {
     case EPI_BF16: hipLaunchKernelGGL(splitk_reduce_kernel<EPI_BF16>, dim3(blocks), dim3(256), 0, st, g, part, p.splits, ntile, items); break;
     case EPI_GELU_BF16: hipLaunchKernelGGL(splitk_reduce_kernel<EPI_GELU_BF16>, dim3(blocks), dim3(256), 0, st, g, part, p.splits, ntile, items); break;
-    case EPI_RESID_F32: hipLaunchKernelGGL(splitk_reduce_kernel<EPI_RESID_F32>, dim3(blocks), dim3(256), 0, st, g, part, p.splits, ntile, items); break;
+    case EPI_RESID_F16: hipLaunchKernelGGL(splitk_reduce_kernel<EPI_RESID_F16>, dim3(blocks), dim3(256), 0, st, g, part, p.splits, ntile, items); break;
+    case EPI_F16: hipLaunchKernelGGL(splitk_reduce_kernel<EPI_F16>, dim3(blocks), dim3(256), 0, st, g, part, p.splits, ntile, items); break;
     case EPI_F32: hipLaunchKernelGGL(splitk_reduce_kernel<EPI_F32>, dim3(blocks), dim3(256), 0, st, g, part, p.splits, ntile, items); break;
     default: return hipErrorInvalidValue;
   }

@@ -1,6 +1,5 @@
 // The eight-wave tile machinery of the bf16 / fp8 MFMA GEMM (gemm.hip): LDS swizzle, epilogue columns and the Tile
-// (loads, fragments, MFMAs, K stage), and the row-coalesced epilogue tile_store shared with the four-wave ring kernel
-// (gemm_ring.hip).
+// (loads, fragments, MFMAs, K stage), and the row-coalesced epilogue tile_store.
 #pragma once
 
 #include "common.h"
@@ -29,7 +28,7 @@ struct Cols {
     wsc = make_float4(1.f, 1.f, 1.f, 1.f);
     if (full) {
       bias = *(const float4*)(g.bias + n);
-      if (EPI == EPI_RESID_F32) gate = *(const float4*)(g.gate + n);
+      if (EPI == EPI_RESID_F16) gate = *(const float4*)(g.gate + n);
       if (g.w_scale) wsc = *(const float4*)(g.w_scale + n);
     }
   }
@@ -40,12 +39,14 @@ struct Cols {
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
     }
-    if (EPI == EPI_RESID_F32) return make_float4(h.x + gate.x * v[0], h.y + gate.y * v[1], h.z + gate.z * v[2], h.w + gate.w * v[3]);
+    if (EPI == EPI_RESID_F16) return make_float4(h.x + gate.x * v[0], h.y + gate.y * v[1], h.z + gate.z * v[2], h.w + gate.w * v[3]);
     return make_float4(v[0], v[1], v[2], v[3]);
   }
   __device__ __forceinline__ void put(const GemmArgs& g, int m, float4 o) const {
     if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16)
       *(uint2*)((bf16_t*)g.C + (size_t)m * g.ldc + n) = make_uint2(pack2(o.x, o.y), pack2(o.z, o.w));
+    else if (EPI == EPI_RESID_F16 || EPI == EPI_F16)
+      *(uint2*)((f16_t*)g.C + (size_t)m * g.ldc + n) = make_uint2(pack2h(o.x, o.y), pack2h(o.z, o.w));
     else
       *(float4*)((float*)g.C + (size_t)m * g.ldc + n) = o;
   }
@@ -57,7 +58,8 @@ struct Cols {
       const size_t o = (size_t)m * g.ldc + n + e;
       if (EPI == EPI_BF16) ((bf16_t*)g.C)[o] = f2bf(x);
       else if (EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[o] = f2bf(gelu_tanh(x));
-      else if (EPI == EPI_RESID_F32) ((float*)g.C)[o] += g.gate[n + e] * x;
+      else if (EPI == EPI_RESID_F16) ((f16_t*)g.C)[o] = f2h(h2f(((const f16_t*)g.C)[o]) + g.gate[n + e] * x);
+      else if (EPI == EPI_F16) ((f16_t*)g.C)[o] = f2h(x);
       else ((float*)g.C)[o] = x;
     }
   }
@@ -81,16 +83,17 @@ struct FragT<true> { typedef i32x8 type; };
 // Writes one wave's accumulators (a WTM x WTN block at rows mw.., columns nw..; acc[i][j] = MFMA block (i, j), lane l
 // holding column nw + j * 32 + q * 8 + (l / 32) * 4 + (0..3) of row mw + i * 32 + l % 32 in registers q * 4 ..) through
 // its LDS slab st (32 x WTN fp32, 16-byte chunks XOR-swizzled by row) so that each global access of the epilogue covers
-// whole rows.  bf16 outputs go out 16 bytes per lane (8 columns); the others 4 columns per lane, in batches of RB
-// read-back instructions whose residual loads are all in flight before the first store.  bf16 outputs need
-// ldc % 8 == 0 and a 16-byte aligned C (gemm_bf16 checks).
+// whole rows.  bf16 and fp16 outputs go out 16 bytes per lane (8 columns; the fp16 residual's rows of a batch are all
+// loaded before its first store); fp32 outputs 4 columns per lane.  16-byte outputs need ldc % 8 == 0 and a 16-byte
+// aligned C (gemm_bf16 checks).
 template <int EPI, int TM, int TN, int WTM, int WTN>
 __device__ __forceinline__ void tile_store(const GemmArgs& g, const f32x16 (&acc)[TM][TN], float4* st, int mw, int nw, int lane) {
   constexpr int CPR = WTN / 4;   // 16-byte chunks per slab row
   constexpr int RPI = 64 / CPR;  // slab rows per read-back instruction
   constexpr int NRB = 32 / RPI;  // read-back instructions per slab
   constexpr int RB = NRB < 8 ? NRB : 8;
-  constexpr bool WIDE = (EPI == EPI_BF16 || EPI == EPI_GELU_BF16 || EPI == EPI_QKV) && WTN % 8 == 0;
+  constexpr bool WIDE = (EPI == EPI_BF16 || EPI == EPI_GELU_BF16 || EPI == EPI_QKV || EPI == EPI_RESID_F16 || EPI == EPI_F16) &&
+                        WTN % 8 == 0;
   constexpr int CW = WTN / 8, RW = 64 / CW;  // wide: lanes per slab row, slab rows per instruction
   const int cc = WIDE ? (lane % CW) * 2 : lane % CPR;
   const Cols<EPI> cols(g, nw + cc * 4);
@@ -175,17 +178,38 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const f32x16 (&acc
         }
       }
     } else if constexpr (WIDE) {
+      constexpr int NB = 32 / RW;
+      uint4 hv[NB];  // EPI_RESID_F16: the residual's current 8 values of each row of the batch, loaded up front
+      if constexpr (EPI == EPI_RESID_F16) {
 #pragma unroll
-      for (int b = 0; b < 32 / RW; ++b) {
+        for (int b = 0; b < NB; ++b) {
+          const int m = mw + i * 32 + b * RW + lane / CW;
+          hv[b] = make_uint4(0u, 0u, 0u, 0u);
+          if (m < g.M && cols2.full) hv[b] = *(const uint4*)((const f16_t*)g.C + (size_t)m * g.ldc + cols.n);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
         const int row = b * RW + lane / CW;
         const int m = mw + i * 32 + row;
         const float4 v0 = st[row * CPR + (cc ^ (row & (CPR - 1)))];
         const float4 v1 = st[row * CPR + ((cc + 1) ^ (row & (CPR - 1)))];
         if (m >= g.M) continue;
         if (cols2.full) {
-          const float4 o0 = cols.apply(v0, v0), o1 = cols2.apply(v1, v1);
-          *(uint4*)((bf16_t*)g.C + (size_t)m * g.ldc + cols.n) =
-              make_uint4(pack2(o0.x, o0.y), pack2(o0.z, o0.w), pack2(o1.x, o1.y), pack2(o1.z, o1.w));
+          if constexpr (EPI == EPI_RESID_F16 || EPI == EPI_F16) {
+            float4 h0 = v0, h1 = v1;
+            if constexpr (EPI == EPI_RESID_F16) {
+              h0 = make_float4(lo2h(hv[b].x), hi2h(hv[b].x), lo2h(hv[b].y), hi2h(hv[b].y));
+              h1 = make_float4(lo2h(hv[b].z), hi2h(hv[b].z), lo2h(hv[b].w), hi2h(hv[b].w));
+            }
+            const float4 o0 = cols.apply(v0, h0), o1 = cols2.apply(v1, h1);
+            *(uint4*)((f16_t*)g.C + (size_t)m * g.ldc + cols.n) =
+                make_uint4(pack2h(o0.x, o0.y), pack2h(o0.z, o0.w), pack2h(o1.x, o1.y), pack2h(o1.z, o1.w));
+          } else {
+            const float4 o0 = cols.apply(v0, v0), o1 = cols2.apply(v1, v1);
+            *(uint4*)((bf16_t*)g.C + (size_t)m * g.ldc + cols.n) =
+                make_uint4(pack2(o0.x, o0.y), pack2(o0.z, o0.w), pack2(o1.x, o1.y), pack2(o1.z, o1.w));
+          }
         } else {
           cols.put_partial(g, m, v0);
           cols2.put_partial(g, m, v1);
@@ -202,7 +226,10 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const f32x16 (&acc
           m[x] = mw + i * 32 + row;
           v[x] = st[row * CPR + (cc ^ (row & (CPR - 1)))];
           h[x] = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (EPI == EPI_RESID_F32 && cols.full && m[x] < g.M) h[x] = *(const float4*)((const float*)g.C + (size_t)m[x] * g.ldc + cols.n);
+          if (EPI == EPI_RESID_F16 && cols.full && m[x] < g.M) {
+            const uint2 hw = *(const uint2*)((const f16_t*)g.C + (size_t)m[x] * g.ldc + cols.n);
+            h[x] = make_float4(lo2h(hw.x), hi2h(hw.x), lo2h(hw.y), hi2h(hw.y));
+          }
           slot[x] = 0;
           if (EPI == EPI_QKV && qpart > 0 && m[x] < g.M) slot[x] = g.qk.slots[m[x]];
         }

@@ -7,13 +7,16 @@
 namespace t2w {
 
 typedef uint16_t bf16_t;
+typedef uint16_t f16_t;  // storage type of the fp16 residual stream
 
 // EPI_GELU_MX8: GELU, then MX fp8 codes to C (bytes, ldc) and block scales to c_scale (N % 32 == 0)
 // EPI_QKV: the attention projection (N = 3 H): q and k rounded to bf16, per-head LayerNorm + affine, q to its token
 // row of q_out, k and v to the token's key slot of the pools (fields qk.*); tile path only
 // EPI_PART (small-row GEMM only): K split over `splits` workgroups per tile, split z writes its fp32 sum without bias
 // to C + z * c_split (rows ldc apart); a row kernel that takes the sums as a Pend finishes the GEMM's epilogue
-enum Epi { EPI_BF16 = 0, EPI_GELU_BF16 = 1, EPI_RESID_F32 = 2, EPI_F32 = 3, EPI_GELU_MX8 = 4, EPI_QKV = 5, EPI_PART = 6 };
+// Epilogues.  EPI_RESID_F16: the gated residual C(fp16) = fp16(C + gate * (acc + bias)), the residual stream kept in the
+// reference's fp16 with fp32 arithmetic; EPI_F16: fp16 out.
+enum Epi { EPI_BF16 = 0, EPI_GELU_BF16 = 1, EPI_RESID_F16 = 2, EPI_F32 = 3, EPI_GELU_MX8 = 4, EPI_QKV = 5, EPI_PART = 6, EPI_F16 = 7 };
 
 struct QkvOut {
   bf16_t* q_out;        // [M, H]
@@ -33,7 +36,7 @@ struct GemmArgs {
   const bf16_t* B;     // weights [N, K] row-major
   int ldb;
   const float* bias;   // [N]
-  const float* gate;   // [N], EPI_RESID_F32: C += gate * (acc + bias)
+  const float* gate;   // [N], EPI_RESID_F16: C += gate * (acc + bias)
   void* C;
   int ldc;
   int M, N, K;         // K % 64 == 0
@@ -76,12 +79,6 @@ hipError_t gemm_small(const GemmArgs& g, int epi, hipStream_t st);
 // whether an EPI_PART call runs on 64-row tiles (taps mode, more than 32 rows, at most 16 64-K steps per split)
 bool gemm_small_part64(const GemmArgs& g);
 
-// Four-wave 256 x 256 tile GEMM with a four-stage LDS ring (gemm_ring.hip): bf16 operands, every epilogue but
-// EPI_GELU_MX8, K % 128 == 0, lda % 8 == 0, ldb % 8 == 0 (taps: tapC % 32 == 0, frames within 4 GB of A).
-// gemm_bf16 runs it when cfg 3 asks for it.
-bool gemm_ring_fits(const GemmArgs& g, int epi);
-hipError_t gemm_ring(const GemmArgs& g, int epi, hipStream_t st);
-
 struct SplitPlan {
   int splits;  // 0: split-K not possible for this shape / workspace
   int steps;   // 64-K steps per split
@@ -92,13 +89,13 @@ SplitPlan splitk_plan(int M, int N, int K, size_t ws_bytes);
 hipError_t quant_mx8(const bf16_t* x, int ldx, int M, int K, uint8_t* q, int ldq, uint8_t* s, hipStream_t st);
 hipError_t gemm_splitk(const GemmArgs& g, int epi, const SplitPlan& p, float* part, hipStream_t st);
 
-// Per-token row kernels of the DiT block (H = hidden, one wave per token).
+// Per-token row kernels of the DiT block (H = hidden, one wave per token); h is the fp16 residual stream [N, H].
 // With pd.part set they first finish a pending gated residual (h updated in place) or, for ln_mish_conv, take the
 // pending GEMM's bf16-rounded value as their input row instead of y.
-hipError_t ln_mod(float* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H,
+hipError_t ln_mod(f16_t* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H,
                   hipStream_t st, const Pend& pd = Pend());
 // ln_mod with MX fp8 output: codes q [N, H], block scales qs [N, H / 32]
-hipError_t ln_mod_mx8(const float* h, const float* shift, const float* scale1, float eps, uint8_t* q, uint8_t* qs, int N,
+hipError_t ln_mod_mx8(const f16_t* h, const float* shift, const float* scale1, float eps, uint8_t* q, uint8_t* qs, int N,
                       int H, hipStream_t st);
 
 struct ConvPlace {   // where the normed frames of a causal conv go (the padded frame buffer and the conv caches)
@@ -117,7 +114,7 @@ struct ConvPlace {   // where the normed frames of a causal conv go (the padded 
   uint8_t* P8s = nullptr;    // and its block scales [N + 2 R, H / 32]
 };
 
-hipError_t ln_mod_conv(float* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H,
+hipError_t ln_mod_conv(f16_t* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H,
                        hipStream_t st, const Pend& pd = Pend());
 hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float eps, const ConvPlace& cp, int H,
                         hipStream_t st, const Pend& pd = Pend());

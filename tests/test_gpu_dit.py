@@ -1,6 +1,6 @@
 """DiT estimator and CFG Euler solve on the GPU against the fp32 CPU oracle (same seeded random-init weights/inputs).
 
-Tolerance: bf16 GEMM operands with fp32 accumulation, fp32 residual stream and Euler state: mel rel-L2 <= 2e-2 against
+Tolerance: bf16 GEMM operands with fp32 accumulation, fp16 residual stream (the reference's), fp32 Euler state: mel rel-L2 <= 2e-2 against
 the fp32 oracle (the reference's own fast-vs-reference FP16 bounds are 2e-2 for setups and 3e-2 for windows,
 ``tests/engine/test_dit_fast.py:86,103`` of the reference); measured values are printed.
 """

@@ -29,7 +29,7 @@ def _gemm(A, W, bias, C_, epi, gate=None, a_src=None, lda=None, K=None, ws=None)
 
 @pytest.mark.parametrize("M,N,K", [(1, 256, 64), (100, 80, 1024), (333, 1024, 320), (1000, 3072, 1024), (257, 2048, 2048),
                                    (5400, 3072, 1024)])
-@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 7])
 def test_gemm_dense(dev, M, N, K, epi):
     """5400 x 3072: 264 tiles of 256 x 256, so the rows of the first full round run on 256 x 256 tiles and the last
     24 rows on 256 x 128 tiles (a second round of 8 tiles would leave most CUs idle)."""
@@ -44,12 +44,16 @@ def test_gemm_dense(dev, M, N, K, epi):
         if epi == 1:
             ref = torch.nn.functional.gelu(ref, approximate="tanh")
         assert rel(out.float(), ref) < 6e-3
-    elif epi == 2:
-        h = torch.randn(M, N, device=dev, generator=g)
+    elif epi == 2:  # the fp16 residual stream: h = fp16(h + gate * (.))
+        h = torch.randn(M, N, device=dev, generator=g).half()
         gate = torch.randn(N, device=dev, generator=g)
-        expect = h + gate * ref
+        expect = h.float() + gate * ref
         _gemm(A, W, bias, h, 2, gate=gate)
-        assert rel(h, expect) < 1e-5
+        assert rel(h.float(), expect) < 1e-3
+    elif epi == 7:
+        out = torch.zeros(M, N, device=dev).half()
+        _gemm(A, W, bias, out, 7)
+        assert rel(out.float(), ref) < 1e-3
     else:
         out = torch.zeros(M, N, device=dev)
         _gemm(A, W, bias, out, 3)
@@ -74,11 +78,11 @@ def test_gemm_row_split_taps(dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(1100, 640, 1024), (2048, 3072, 1024), (1300, 1024, 3072), (300, 256, 128)])
-@pytest.mark.parametrize("tile", [1, 3])
+@pytest.mark.parametrize("tile", [0, 1, 2])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 def test_gemm_tiles(dev, M, N, K, tile, epi):
-    """Explicit tile configurations (1: eight waves of 64 x 128; 3: four waves of 128 x 128 on the LDS ring) with
-    ragged rows and columns against fp32."""
+    """Explicit tile configurations (0: four waves of 64 x 64; 1: eight waves of 64 x 128; 2: eight waves of 64 x 64)
+    with ragged rows and columns against fp32."""
     L = _lib.lib()
     g = torch.Generator(device=dev).manual_seed(M + N * 3 + K * 5 + epi)
     A = torch.randn(M, K, device=dev, generator=g).bfloat16()
@@ -91,14 +95,14 @@ def test_gemm_tiles(dev, M, N, K, tile, epi):
         if epi == 1:
             ref = torch.nn.functional.gelu(ref, approximate="tanh")
     elif epi == 2:
-        out = torch.randn(M, N, device=dev, generator=g)
-        ref = out + gate * ref
+        out = torch.randn(M, N, device=dev, generator=g).half()
+        ref = out.float() + gate * ref
     else:
         out = torch.zeros(M, N, device=dev)
     _lib.check(L.t2w_gemm_bf16_tile(A.data_ptr(), K, None, W.data_ptr(), bias.data_ptr(), gate.data_ptr() if epi == 2 else None,
                                     out.data_ptr(), N, M, N, K, epi, tile, _lib.stream_handle()), "gemm tile")
     torch.cuda.synchronize()
-    assert rel(out.float(), ref) < (6e-3 if epi in (0, 1) else 1e-5)
+    assert rel(out.float(), ref) < {0: 6e-3, 1: 6e-3, 2: 1e-3, 3: 1e-5}[epi]
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (37, 3072, 1024), (100, 1024, 2048), (100, 80, 1024), (300, 2048, 1024), (600, 1024, 320)])
@@ -120,8 +124,8 @@ def test_gemm_splitk(dev, M, N, K, epi):
         if epi in (0, 1):
             out = torch.full((M, N), 7.0, device=dev).bfloat16()
         elif epi == 2:
-            out = torch.randn(M, N, device=dev, generator=torch.Generator(device=dev).manual_seed(9))
-            h0 = out.clone()
+            out = torch.randn(M, N, device=dev, generator=torch.Generator(device=dev).manual_seed(9)).half()
+            h0 = out.float()
         else:
             out = torch.zeros(M, N, device=dev)
         _gemm(A, W, bias, out, epi, gate=gate if epi == 2 else None, ws=ws)
@@ -129,7 +133,7 @@ def test_gemm_splitk(dev, M, N, K, epi):
     if epi in (0, 1):
         assert rel(outs[0].float(), ref) < 6e-3
     elif epi == 2:
-        assert rel(outs[0], h0 + gate * ref) < 1e-5
+        assert rel(outs[0].float(), h0 + gate * ref) < 1e-3
     else:
         assert rel(outs[0], ref) < 1e-5
     assert torch.equal(outs[0], outs[1])
@@ -152,8 +156,8 @@ def test_gemm_splitk_taps(dev):
     assert rel(out, ref) < 1e-5
 
 
-@pytest.mark.parametrize("lens,tile", [([5, 0, 1, 2, 3, 40, 0, 17, 1, 56], -1), ([400] * 3, -1), ([400] * 3, 1), ([400] * 3, 3),
-                                       ([5, 0, 300, 2, 3, 400, 0, 17, 1, 560], 3)])
+@pytest.mark.parametrize("lens,tile", [([5, 0, 1, 2, 3, 40, 0, 17, 1, 56], -1), ([400] * 3, -1), ([400] * 3, 1), ([400] * 3, 2),
+                                       ([5, 0, 300, 2, 3, 400, 0, 17, 1, 560], 0)])
 def test_gemm_conv_taps(dev, lens, tile):
     """Taps mode: row m reads three consecutive frames starting at a_src[m] of the padded frame buffer; equals a
     kernel-3 conv over [2 cached frames | row frames] (F.conv1d, fp32).  tile: as chosen by shape (-1) or explicit."""
@@ -187,12 +191,12 @@ def test_ln_mod(dev):
     g = torch.Generator(device=dev).manual_seed(2)
     for H in (256, 512, 1024):
         N = 77
-        h = torch.randn(N, H, device=dev, generator=g) * 3 + 1
+        h = (torch.randn(N, H, device=dev, generator=g) * 3 + 1).half()  # the fp16 residual stream
         sh, sc = torch.randn(H, device=dev, generator=g), 1 + torch.randn(H, device=dev, generator=g)
         out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
         _lib.check(L.t2w_ln_mod(h.data_ptr(), sh.data_ptr(), sc.data_ptr(), 1e-6, out.data_ptr(), N, H, _lib.stream_handle()))
         torch.cuda.synchronize()
-        ref = torch.nn.functional.layer_norm(h, (H,), eps=1e-6) * sc + sh
+        ref = torch.nn.functional.layer_norm(h.float(), (H,), eps=1e-6) * sc + sh
         assert rel(out.float(), ref) < 4e-3
 
 
@@ -309,9 +313,9 @@ def test_gemm_fp8(dev, M, N, K, epi):
         ref = torch.nn.functional.gelu(ref, approximate="tanh")
     if epi in (0, 1):
         out = torch.full((M, N), 7.0, device=dev).bfloat16()
-    elif epi == 2:
-        out = torch.randn(M, N, device=dev)
-        h0 = out.clone()
+    elif epi == 2:  # the fp16 residual stream
+        out = torch.randn(M, N, device=dev).half()
+        h0 = out.float()
     else:
         out = torch.zeros(M, N, device=dev)
     _lib.check(L.t2w_gemm_fp8(qa.data_ptr(), K, None, sa.data_ptr(), K // 32, qw.data_ptr(), sw.data_ptr(), bias.data_ptr(),
@@ -320,7 +324,7 @@ def test_gemm_fp8(dev, M, N, K, epi):
     if epi in (0, 1):
         assert rel(out.float(), ref) < 6e-3
     elif epi == 2:
-        assert rel(out, h0 + gate * ref) < 1e-4
+        assert rel(out.float(), h0 + gate * ref) < 1e-3
     else:
         assert rel(out, ref) < 1e-4
         # and against the unquantized bf16 product: the fp8 rounding error itself
