@@ -172,6 +172,10 @@ int t2w_ln_mod(const void* h, const float* shift, const float* scale1, float eps
                void* stream);
 int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const float* kw, const float* kb, float eps,
                         void* q_out, void* k_pool, void* v_pool, const int* slots, int N, int heads, void* stream);
+/* Block-causal attention of packed rows over paged key slots: q [N, heads * 64]; row r's queries are tokens
+ * row_start[r] .. + row_len[r], its keys the slots kv_idx[row_kv_off[r] ..][0 .. row_kv_len[r]) (its new tokens first,
+ * then cached keys); tiles [n_tiles, 2] lists (row, first query) of every 64-query tile.  chunk > 0: a new token sees
+ * the new tokens of its own and earlier chunks only; cached keys are always visible. */
 int t2w_attention(const void* q, const void* k_pool, const void* v_pool, void* out, const int* kv_idx,
                   const int* row_start, const int* row_len, const int* row_kv_off, const int* row_kv_len,
                   const int* tiles, int n_tiles, int heads, int chunk, float scale, void* stream);
