@@ -2,10 +2,11 @@
 mel frames, chunk-causal attention with chunk 50), random-init weights, synthetic inputs resident in HBM.
 
 Prints one JSON line: mel frames/s of the 16 streams' output (value), audio-seconds/s, per-chunk p50 latency of a
-streaming chunk (300-frame cached prompt + 50 new frames, one stream, CFG pair, 10 steps, + HiFT), the ragged variant
-of the 16-stream workload (lengths uniform 150-450), HiFT alone (16 rows, 50-400 frames, fp32 and bf16 decoder), the
-roofline of the dominant kernel (the DiT's conv1 GEMM, timed with HIP events on its own stream) and the fp32 CPU
-oracle baseline timed on a bounded sample on this host.
+streaming chunk through ``BatchedToken2Wav.decode`` (300-frame cached prompt, steady 50-frame windows, one stream, CFG
+pair, 10 steps, HiFT with its 8 cached mel frames and source cache, cross-fade, device-to-host copy), the roofline of
+the dominant kernel (the gated-residual GEMM instantiation that runs proj and fc2, timed with HIP events on its own
+stream), every DiT GEMM of the workload next to hipBLASLt on the same shape, the ragged variant (lengths uniform
+150-450), fp8 block GEMMs, HiFT alone, and the fp32 CPU oracle baseline timed on a bounded sample on this host.
 """
 
 from __future__ import annotations
@@ -23,6 +24,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (AMD public spec)
+HBM_PEAK_GBS = 8000.0
 
 
 def dit_flops_per_solve(cfg, rows_T: list[int], chunk: int) -> tuple[float, float]:
@@ -39,6 +41,21 @@ def dit_flops_per_solve(cfg, rows_T: list[int], chunk: int) -> tuple[float, floa
     return float(per_tok * toks * cfg.steps), float(4 * H * pairs * D * cfg.steps)
 
 
+def hift_model(Wh, mode: str, use_graphs: bool = True):
+    """HiFT in one of three precisions: "reference" (the reference's split: f0 predictor, source, conv_pre, stage 0's
+    transposed conv and conv_post fp32, the other decoder convs on bf16 MFMA where the reference allows TF32), "bf16"
+    (every decoder conv on bf16 MFMA), "fp32" (strict fp32)."""
+    from t2w_amd.config import HiFTConfig
+    from t2w_amd.hift import REFERENCE_FP32_CONVS, HiFTModel
+
+    return HiFTModel(Wh, HiFTConfig(), decode_bf16=mode != "fp32", use_graphs=use_graphs,
+                     fp32_convs=REFERENCE_FP32_CONVS if mode == "reference" else ())
+
+
+HIFT_DESC = {"reference": "HiFT in the reference's precision split (fp32 f0/source/conv_pre/ups.0/conv_post, bf16-MFMA elsewhere)",
+             "bf16": "HiFT with every decoder conv on bf16 MFMA (fp32 f0/source)", "fp32": "HiFT strict fp32"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -47,35 +64,33 @@ def main() -> int:
     ap.add_argument("--streams", type=int, default=16)
     ap.add_argument("--frames", type=int, default=400)
     ap.add_argument("--chunk", type=int, default=50)
+    ap.add_argument("--hift-mode", choices=("reference", "bf16", "fp32"), default="reference")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-hift", action="store_true")
     ap.add_argument("--latency-reps", type=int, default=20)
-    ap.add_argument("--hift-fp32", action="store_true", help="HiFT decoder in strict fp32 (default: bf16 MFMA decoder)")
     ap.add_argument("--no-extra", action="store_true", help="skip the ragged-length and HiFT-alone measurements")
     ap.add_argument("--no-fp8", action="store_true", help="skip the fp8 (e4m3 weights, MX fp8 activations) measurement")
-    ap.add_argument("--latency-only", action="store_true",
-                    help="only the per-chunk latency case (one stream, 300 cached + 50 new frames, + HiFT of the window)")
+    ap.add_argument("--no-gemms", action="store_true", help="skip the per-GEMM timings and their hipBLASLt comparison")
+    ap.add_argument("--latency-only", action="store_true", help="only the per-chunk latency case")
     ap.add_argument("--roofline-only", action="store_true",
-                    help="only the conv1 GEMM launches, after three 256 MiB calibration copies (for rocprofv3 --pmc runs)")
+                    help="only the dominant kernel's launches, after three 256 MiB calibration copies (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no sharding or collectives); use --gpus 1", file=sys.stderr)
         return 2
 
     import t2w_amd  # noqa: F401
-    from t2w_amd import _lib
     from t2w_amd.config import DiTConfig, HiFTConfig
 
+    cfg = DiTConfig()
     if args.roofline_only:
-        k_ms, k_tf, k_fl = conv1_roofline(DiTConfig(), args.streams, args.frames, calibrate=True)
-        print(json.dumps({"kernel": "gemm_kernel<256,256,4,2,EPI_BF16,taps> (DiT conv1)", "launch_ms": k_ms, "tflops": k_tf,
-                          "calibration_copy_bytes": 2 * (256 << 20)}))
+        r = resid_gemm_roofline(cfg, args.streams, args.frames, calibrate=True)
+        print(json.dumps({"kernel": r["kernel"], "launch_ms": r["launch_ms"], "tflops": r["achieved"], "calibration_copy_bytes": 2 * (256 << 20)}))
         return 0
     from t2w_amd.dit import DiTModel, FastDiT
     from t2w_amd.weights import init_dit, init_hift
 
     dev = "cuda"
-    cfg = DiTConfig()
     W = init_dit(cfg, seed=2)
     model = DiTModel(W, cfg, fp8=not args.no_fp8)
     model.drop_table_weights()
@@ -86,54 +101,21 @@ def main() -> int:
     spks = torch.randn(n, cfg.mel, generator=g).to(dev)
     caches = [fd.new_cache() for _ in range(n)]
 
-    hift = None
+    hift = Wh = None
     if not args.no_hift:
-        from t2w_amd.hift import HiFTModel
-
         Wh = init_hift(HiFTConfig(), seed=3)
-        hift = HiFTModel(Wh, HiFTConfig(), decode_bf16=not args.hift_fp32, use_graphs=True)
+        hift = hift_model(Wh, args.hift_mode)
         hsrc = torch.zeros(n, 1, 0, device=dev)
         hnoise = hift.noise([1000 + i for i in range(n)], T * hift.cfg.upsample_scale)
 
-    def chunk_latency():
-        # one stream, 300-frame prompt cached, 50 new frames, CFG pair, 10 steps, + HiFT of the window: medians of the
-        # whole call and of its DiT solve and HiFT parts
-        fl = FastDiT(model, n_slots=4096, max_streams=2, use_graphs=True)
-        c = fl.new_cache(keep=300)
-        pm = torch.randn(cfg.mel, 300, generator=g).to(dev)
-        fl.solve([c], [pm], spks[:1], [torch.randn(cfg.mel, 300, generator=g).to(dev)], [True])
-        wm = torch.randn(cfg.mel, 50, generator=g).to(dev)
-        hs = None
-        if hift is not None:
-            hs = (torch.zeros(1, 1, 0, device=dev), *hift.noise([7], 50 * hift.cfg.upsample_scale))
-        ts, td, th = [], [], []
-        for i in range(args.latency_reps + 3):
-            torch.cuda.synchronize()
-            a = time.perf_counter()
-            m = fl.solve([c], [wm], spks[:1], None, [False])
-            torch.cuda.synchronize()
-            b = time.perf_counter()
-            if hift is not None:
-                hift.forward_noise(m[0][None], *hs)
-            torch.cuda.synchronize()
-            e = time.perf_counter()
-            if i >= 3:
-                ts.append(e - a)
-                td.append(b - a)
-                th.append(e - b)
-        return float(np.median(ts) * 1e3), float(np.median(td) * 1e3), float(np.median(th) * 1e3)
-
     if args.latency_only:
-        lat, lat_dit, lat_hift = chunk_latency()
-        print(json.dumps({"p50_chunk_latency_ms": lat, "p50_chunk_dit_ms": lat_dit, "p50_chunk_hift_ms": lat_hift,
-                          "reps": args.latency_reps}))
+        print(json.dumps(chunk_latency(model, Wh, args)))
         return 0
 
     def step():
         mels = fd.solve(caches, mus, spks, None, [False] * n, chunk=args.chunk)
         if hift is not None:
-            mel = torch.stack(mels)
-            hift.forward_noise(mel, hsrc, *hnoise)
+            hift.forward_noise(torch.stack(mels), hsrc, *hnoise)
         return mels
 
     for _ in range(args.warmup):
@@ -155,22 +137,22 @@ def main() -> int:
     torch.cuda.synchronize()
     dit_dt = (time.perf_counter() - t1) / max(1, args.steps // 2)
 
-    k_ms, k_tflops, k_flops = conv1_roofline(cfg, n, T)
+    roof = resid_gemm_roofline(cfg, n, T)
+    roof["traffic"] = pmc_traffic()
+    gemms = None if args.no_gemms else dit_gemm_table(cfg, n, T)
 
-    lat = lat_dit = lat_hift = None
-    if args.latency_reps > 0:
-        lat, lat_dit, lat_hift = chunk_latency()
+    lat = chunk_latency(model, Wh, args) if args.latency_reps > 0 else {}
 
     extra = {}
     if not args.no_fp8:
         extra["fp8"] = fp8_workload(args, cfg, model, mus, spks, hift, hsrc if hift is not None else None,
                                     hnoise if hift is not None else None, step)
     if not args.no_extra:
-        extra.update(extra_workloads(args, cfg, fd, spks, hift, Wh if hift is not None else None))
+        extra.update(extra_workloads(args, cfg, fd, spks, hift, Wh))
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(W, T, args.chunk, hift_weights=Wh if hift is not None else None)
+        cpu = cpu_baseline(W, T, args.chunk, hift_weights=Wh)
 
     res = {
         "metric": "Token2Wav mel frames/s (10-step CFG DiT+HiFT, B=32) + per-chunk p50 latency",
@@ -186,17 +168,14 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (random-init weights, seeded N(0,1) inputs)",
         "config": {"workload": f"{n} streams x {T} mel frames, CFG B={2 * n}, chunk-causal {args.chunk}, 10-step Euler DiT"
-                               + ("" if hift is None else (" + HiFT fp32" if args.hift_fp32 else " + HiFT (bf16-MFMA decoder, fp32 f0/source)")),
+                               + ("" if hift is None else " + " + HIFT_DESC[args.hift_mode]),
                    "global_batch": 2 * n, "seq_len": T, "parallelism": "single GPU"},
         "audio_seconds_per_s": frames / 50.0 / dt,
-        "p50_chunk_latency_ms": lat,
-        "p50_chunk_dit_ms": lat_dit,
-        "p50_chunk_hift_ms": lat_hift,
+        **lat,
         "dit_solve_ms": dit_dt * 1e3,
         "dit_mfma_frac": (gemm_f + attn_f) / dit_dt / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<256,256,4,2,EPI_BF16,taps> (DiT conv1)", "achieved": k_tflops,
-                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": k_tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": pmc_traffic(),
-                     "launch_ms": k_ms, "flops_per_launch": k_flops},
+        "roofline": roof,
+        "dit_gemms": gemms,
         "cpu_baseline": cpu,
         **extra,
     }
@@ -204,10 +183,29 @@ def main() -> int:
     return 0
 
 
-def conv1_roofline(cfg, n: int, T: int, calibrate: bool = False) -> tuple[float, float, float]:
-    """The dominant kernel alone: the DiT's conv1 GEMM (taps mode, bf16 out) at the workload's shape, 20 launches timed
-    with HIP events on its own stream.  calibrate: first three plain 256 MiB device copies (torch copy_), the known-size
-    reference for the HBM byte counters of a rocprofv3 --pmc run of this same command."""
+def _timed(launch, reps: int = 20, warm: int = 3) -> float:
+    """Mean duration (ms) of ``launch(stream)`` over ``reps`` launches on a side stream, HIP events on that stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())  # operands were written on the current stream
+    with torch.cuda.stream(s):
+        for _ in range(warm):
+            launch(s.cuda_stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            launch(s.cuda_stream)
+        e1.record(s)
+    s.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def resid_gemm_roofline(cfg, n: int, T: int, calibrate: bool = False) -> dict:
+    """The dominant kernel of the DiT solve by total time: the gated fp16-residual GEMM instantiation (256 x 256
+    tiles, dense A) that runs the attention output projection (K = H) and fc2 (K = F) of every block.  Its launches
+    are timed as the solve issues them, proj and fc2 alternating at the workload's 2 n T tokens, 20 launches with HIP
+    events on their own stream; achieved = the mean algorithmic FLOPs per launch / the mean launch time.  calibrate:
+    first three plain 256 MiB device copies, the known-size reference for the HBM byte counters of a rocprofv3 --pmc
+    run of this same command."""
     from t2w_amd import _lib
 
     dev = "cuda"
@@ -218,43 +216,124 @@ def conv1_roofline(cfg, n: int, T: int, calibrate: bool = False) -> tuple[float,
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    H, N = cfg.hidden, 2 * n * T
-    R = 2 * n
-    P = torch.randn(N + 2 * R, H, device=dev).bfloat16()
-    Wc = (torch.randn(H, 3 * H, device=dev) * 0.02).bfloat16()
-    bc = torch.zeros(H, device=dev)
-    tok_row = np.repeat(np.arange(R), T)
-    a_src = torch.from_numpy((np.arange(N) + 2 * tok_row).astype(np.int32)).to(dev)
-    out = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())  # operands were written on the default stream
+    H, F, N = cfg.hidden, cfg.ffn, 2 * n * T
+    g = torch.Generator(device=dev).manual_seed(7)
+    ao = torch.randn(N, H, device=dev, generator=g).bfloat16()
+    big = torch.randn(N, F, device=dev, generator=g).bfloat16()
+    Wp = (torch.randn(H, H, device=dev, generator=g) / H ** 0.5).bfloat16()
+    W2 = (torch.randn(H, F, device=dev, generator=g) / F ** 0.5).bfloat16()
+    b, gate = torch.zeros(H, device=dev), torch.full((H,), 1e-3, device=dev)
+    h = torch.randn(N, H, device=dev, generator=g).half()
     L = _lib.lib()
-    with torch.cuda.stream(s):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 20
-        for _ in range(3):
-            _lib.check(L.t2w_gemm_bf16(P.data_ptr(), H, a_src.data_ptr(), Wc.data_ptr(), bc.data_ptr(), None, out.data_ptr(), H, N, H, 3 * H, 0, s.cuda_stream))
-        e0.record(s)
-        for _ in range(reps):
-            _lib.check(L.t2w_gemm_bf16(P.data_ptr(), H, a_src.data_ptr(), Wc.data_ptr(), bc.data_ptr(), None, out.data_ptr(), H, N, H, 3 * H, 0, s.cuda_stream))
-        e1.record(s)
-    s.synchronize()
-    k_ms = e0.elapsed_time(e1) / reps
-    flops = 2.0 * N * H * 3 * H
-    return k_ms, flops / (k_ms * 1e-3) / 1e12, flops
+    state = {"i": 0}
+
+    def launch(st):
+        A, Wt, K = (ao, Wp, H) if state["i"] % 2 == 0 else (big, W2, F)
+        state["i"] += 1
+        _lib.check(L.t2w_gemm_bf16(A.data_ptr(), K, None, Wt.data_ptr(), b.data_ptr(), gate.data_ptr(), h.data_ptr(), H, N, H, K, 2, st))
+
+    ms = _timed(launch, reps=20, warm=4)
+    flops = 2.0 * N * H * (H + F) / 2
+    ach = flops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "kernel": "gemm_kernel<256,256,4,2,EPI_RESID_F16,dense> (DiT proj and fc2, alternating)",
+            "achieved": ach, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": ach / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
+            "launch_ms": ms, "flops_per_launch": flops}
+
+
+def dit_gemm_table(cfg, n: int, T: int) -> dict:
+    """Every block GEMM of the workload (2 n T tokens) alone, with the solve's epilogue where the kernel-level entry
+    point has it (qkv without its fused q/k LayerNorm and key scatter), next to hipBLASLt (torch.matmul, bf16 out) on
+    the same shape: TFLOP/s and the fraction of bf16 peak of each, 20 launches each with HIP events."""
+    from t2w_amd import _lib
+
+    dev, L = "cuda", _lib.lib()
+    H, F, N = cfg.hidden, cfg.ffn, 2 * n * T
+    R = 2 * n
+    g = torch.Generator(device=dev).manual_seed(9)
+    a_src = torch.from_numpy((np.arange(N) + 2 * np.repeat(np.arange(R), T)).astype(np.int32)).to(dev)
+    P = torch.randn(N + 2 * R, H, device=dev, generator=g).bfloat16()
+    X = {H: torch.randn(N, H, device=dev, generator=g).bfloat16(), F: torch.randn(N, F, device=dev, generator=g).bfloat16()}
+    h = torch.randn(N, H, device=dev, generator=g).half()
+    gate = torch.full((max(3 * H, F),), 1e-3, device=dev)
+    bias = torch.zeros(max(3 * H, F), device=dev)
+    out = torch.empty(N, max(3 * H, F), dtype=torch.bfloat16, device=dev)
+    # name: (N_out, K, epilogue, taps)
+    shapes = {"qkv": (3 * H, H, 0, False), "proj": (H, H, 2, False), "conv1": (H, 3 * H, 0, True), "conv2": (H, 3 * H, 2, True),
+              "fc1": (F, H, 1, False), "fc2": (H, F, 2, False)}
+    res = {}
+    for name, (No, K, epi, taps) in shapes.items():
+        Wt = (torch.randn(No, K, device=dev, generator=g) / K ** 0.5).bfloat16()
+        A = P if taps else X[K]
+        C, ldc = (h, H) if epi == 2 else (out, No)
+
+        def launch(st, A=A, Wt=Wt, C=C, ldc=ldc, No=No, K=K, epi=epi, taps=taps):
+            _lib.check(L.t2w_gemm_bf16(A.data_ptr(), H if taps else K, a_src.data_ptr() if taps else None, Wt.data_ptr(), bias.data_ptr(),
+                                       gate.data_ptr() if epi == 2 else None, C.data_ptr(), ldc, N, No, K, epi, st))
+
+        ms = _timed(launch)
+        Al = torch.cat([P[a_src.long() + j] for j in range(3)], 1) if taps else A
+        Wc = Wt.t()
+        lib_ms = _timed(lambda st, Al=Al, Wc=Wc: torch.matmul(Al, Wc))
+        fl = 2.0 * N * No * K
+        res[name] = {"us": ms * 1e3, "tflops": fl / ms / 1e9, "frac": fl / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS,
+                     "hipblaslt_us": lib_ms * 1e3, "hipblaslt_frac": fl / lib_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS}
+        del Al
+    tot = sum(2.0 * N * No * K for No, K, _, _ in shapes.values())
+    ours = sum(v["us"] for v in res.values()) * 1e-6
+    lib = sum(v["hipblaslt_us"] for v in res.values()) * 1e-6
+    return {"tokens": N, "per_gemm": res, "block_frac": tot / ours / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "block_frac_hipblaslt": tot / lib / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "note": "isolated launches; hipBLASLt without fused epilogues (taps as an explicit im2col)"}
 
 
 def pmc_traffic() -> float | None:
-    """HBM bytes per launch of the conv1 GEMM as measured by the committed rocprofv3 --pmc summary (FETCH_SIZE +
-    WRITE_SIZE of the GEMM dispatches, each scaled by the same counter's reading on a plain copy of known size), or
-    None when the summary is absent."""
-    path = os.path.join(ROOT, "profiles", "gemm_conv1_b32x400_pmc.md")
+    """HBM bytes per launch of the dominant kernel as measured by the committed rocprofv3 --pmc summary (FETCH_SIZE +
+    WRITE_SIZE of its dispatches, each scaled by the same counter's reading on a plain copy of known size), or None
+    when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gemm_resid_f16_b32x400_pmc.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
         if line.startswith("traffic_bytes_per_launch:"):
             return float(line.split(":", 1)[1])
     return None
+
+
+def chunk_latency(model, Wh, args) -> dict:
+    """One stream through ``BatchedToken2Wav.decode`` as the worker calls it: a 300-frame prompt set up, then steady
+    50-frame windows (kept, so the caches grow and trim), each with HiFT over 8 cached + 50 new mel frames and a
+    3840-sample source cache, the cross-fade and the device-to-host copy; graphs on.  p50 of the whole call over
+    ``latency_reps`` windows after three, then the mean of its solve and vocode stages (the module's profile hook)."""
+    from t2w_amd.dit import FastDiT
+    from t2w_amd.token2wav import BatchedToken2Wav, prompt_features
+
+    dev, mel = "cuda", model.cfg.mel
+    fl = FastDiT(model, n_slots=8192, max_streams=4, use_graphs=True)
+    if Wh is None:
+        return {}
+    bt = BatchedToken2Wav(fl, hift_model(Wh, args.hift_mode))
+    g = torch.Generator().manual_seed(11)
+    mk = lambda *s: torch.randn(*s, generator=g).to(dev)  # noqa: E731
+    st = bt.new_stream(bt.setup(prompt_features(mk(mel, 300), mk(mel), mk(mel, 300))), noise_seed=7, adopt=True)
+    reps = args.latency_reps
+    wins = [mk(mel, 50) for _ in range(2 * reps + 6)]
+    ts = []
+    for i in range(reps + 3):
+        torch.cuda.synchronize()
+        a = time.perf_counter()
+        bt.decode([(st, wins[i], False)])
+        b = time.perf_counter()
+        if i >= 3:
+            ts.append(b - a)
+    bt.profile = {}
+    for i in range(reps):
+        bt.decode([(st, wins[reps + 3 + i], False)])
+    prof = {k: v[1] / v[0] * 1e3 for k, v in bt.profile.items()}
+    bt.release_stream(st)
+    return {"p50_chunk_latency_ms": float(np.median(ts) * 1e3), "p50_chunk_dit_ms": prof.get("solve"),
+            "p50_chunk_hift_ms": prof.get("vocode"),
+            "chunk_case": "BatchedToken2Wav.decode of one stream: 300-frame prompt cached, steady 50-frame windows, "
+                          "HiFT on 58 frames + glue + device-to-host copy; stage times are means of profiled calls"}
 
 
 def fp8_workload(args, cfg, model, mus, spks, hift, hsrc, hnoise, bf16_step) -> dict:
@@ -299,11 +378,8 @@ def fp8_workload(args, cfg, model, mus, spks, hift, hsrc, hnoise, bf16_step) -> 
 
 def extra_workloads(args, cfg, fd, spks, hift, Wh) -> dict:
     """The ragged 16-stream workload (lengths uniform 150-450, seed 2; DiT solve + HiFT of the ragged mels) and HiFT
-    alone (16 rows of mel ~ N(-5, 2), lengths uniform 50-400, seed 3), each timed over args.steps calls after a
-    warm-up call."""
-    from t2w_amd.config import HiFTConfig
-    from t2w_amd.hift import HiFTModel
-
+    alone (16 rows of mel ~ N(-5, 2), lengths uniform 50-400, seed 3) in each precision, timed over args.steps calls
+    after a warm-up call."""
     dev = "cuda"
     n = args.streams
     rng = np.random.default_rng(2)
@@ -339,8 +415,8 @@ def extra_workloads(args, cfg, fd, spks, hift, Wh) -> dict:
     g = torch.Generator().manual_seed(3)
     mel_tm = torch.cat([torch.randn(t, cfg.mel, generator=g) * 2 - 5 for t in hl]).to(dev)
     res = {"rows": 16, "lengths": "uniform 50-400 (numpy default_rng(3))", "frames": sum(hl)}
-    for tag, bf in (("fp32", False), ("bf16", True)):
-        hm = HiFTModel(Wh, HiFTConfig(), decode_bf16=bf, use_graphs=True)
+    for tag in ("fp32", "reference", "bf16"):
+        hm = hift_model(Wh, tag)
         ri, nz = hm.noise([3000 + i for i in range(16)], max(hl) * 480)
         ntm = torch.cat([nz[i, : t * 480] for i, t in enumerate(hl)])
         hm.forward_packed(hl, mel_tm, ntm, None, 0)

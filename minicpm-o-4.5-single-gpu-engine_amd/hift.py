@@ -23,10 +23,16 @@ def chunk_noise_seed(noise_seed: int, chunk: int) -> int:
     return (noise_seed * 1_000_003 + chunk) & ((1 << 63) - 1)
 
 
+# The convs the reference keeps in strict FP32 when it lets the upsampling stages run in TF32 (``decoder_tf32`` /
+# ``tf32_stages``, engine/models/token2wav.py:42-55, 195-211): the input and output convs and stage 0's transposed conv.
+REFERENCE_FP32_CONVS = ("conv_pre", "ups.0", "conv_post")
+
+
 class HiFTModel:
     def __init__(self, W: dict, cfg: HiFTConfig = HiFTConfig(), device: str = "cuda", decode_bf16: bool = False,
-                 use_graphs: bool = False, max_graphs: int = 32):
+                 use_graphs: bool = False, max_graphs: int = 32, fp32_convs: tuple = ()):
         """``decode_bf16``: the decoder convs on bf16 MFMA (fp32 activations); f0 predictor and source stay fp32.
+        ``fp32_convs``: decoder convs that stay fp32 even then (``REFERENCE_FP32_CONVS``: the reference's split).
         ``use_graphs``: calls without overrides replay one captured graph per (row lengths, source-cache length), the
         role of ``HiFTGraphs`` (``engine/runtime/hift_graph.py:22-88``): inputs are copied into the graph's static
         buffers, outputs are returned as copies; at most ``max_graphs`` graphs are kept (least recently used dropped)."""
@@ -53,7 +59,7 @@ class HiFTModel:
 
         def conv(name, bf=True):
             w = W[name + ".weight"].permute(0, 2, 1).contiguous()  # [Cout, taps, Cin]
-            return _lib.Conv(keep(w), keep(W[name + ".bias"]), keep_bf(w[None]) if bf else None)
+            return _lib.Conv(keep(w), keep(W[name + ".bias"]), keep_bf(w[None]) if bf and name not in fp32_convs else None)
 
         def conv_t(name, u):
             w = W[name + ".weight"]  # [Cin, Cout, k]
@@ -65,7 +71,7 @@ class HiFTModel:
                     j = ph + m * u
                     if j < k:
                         wp[ph, :, m, :] = w[:, :, j].t()
-            return _lib.Conv(keep(wp), keep(W[name + ".bias"]), keep_bf(wp))
+            return _lib.Conv(keep(wp), keep(W[name + ".bias"]), keep_bf(wp) if name not in fp32_convs else None)
 
         def resblock(p):
             rb = _lib.ResBlock()

@@ -119,8 +119,25 @@ class BatchedToken2Wav:
         self.window = torch.from_numpy(np.hamming(2 * SOURCE_CACHE)).to(self.device)  # float64, as the reference's
         self.max_flow_streams = int(max_flow_streams)
         self.fuse_setup_frames = int(fuse_setup_frames)
-        self.profile = None
+        self.profile: dict | None = None  # stage -> [calls, seconds, items] when set (each stage then synchronises)
         self.trace = None
+
+    def _prof(self, name: str, n: int, fn, *a):
+        """Run one stage; with ``profile`` set, time it between stream synchronisations (``_prof``,
+        ``token2wav_batch.py:311-327``)."""
+        if self.profile is None:
+            return fn(*a)
+        import time
+
+        torch.cuda.current_stream().synchronize()
+        t = time.perf_counter()
+        r = fn(*a)
+        torch.cuda.current_stream().synchronize()
+        acc = self.profile.setdefault(name, [0, 0.0, 0])
+        acc[0] += 1
+        acc[1] += time.perf_counter() - t
+        acc[2] += n
+        return r
 
     # --- prompts ------------------------------------------------------------------------------------------------------
     def _stage(self, feats: tuple) -> PreSetup:
@@ -225,10 +242,10 @@ class BatchedToken2Wav:
         for a in range(0, len(rows), self.max_flow_streams):
             part = rows[a:a + self.max_flow_streams]
             conds = [r[3] for r in part] if any(r[3] is not None for r in part) else None
-            mels += self.fast.solve([r[0] for r in part], [r[1] for r in part], torch.cat([r[2] for r in part]), conds,
-                                    [r[4] for r in part])
+            mels += self._prof("solve", len(part), self.fast.solve, [r[0] for r in part], [r[1] for r in part],
+                               torch.cat([r[2] for r in part]), conds, [r[4] for r in part])
         prompts = [self._prompt(p) for p in pre]
-        out = self._vocode(items, mels[len(pre):], async_result)
+        out = self._prof("vocode", len(items), self._vocode, items, mels[len(pre):], async_result)
         return (out, prompts) if setups else out
 
     def _noise(self, seeds: list[int], n: int):
