@@ -1,9 +1,10 @@
-"""Model dimensions of the Token2Wav hot path (DiT estimator + HiFT vocoder).
+"""Model dimensions of the Token2Wav hot path (flow encoder, DiT estimator, HiFT vocoder).
 
 The reference reads every shape from ``stepaudio2`` modules at runtime (``engine/runtime/dit_fast.py:107-145``,
 ``engine/models/token2wav.py:250-261``); those modules are not part of the reference repository, so the shapes of the
 synthetic workloads are fixed here: DiT 22 blocks, hidden 1024, 16 heads of 64, FFN 2x, mel 80, ``in_proj`` 4 x 80 ->
-hidden; HiFT CosyVoice2-style at 24 kHz (base 512 channels, upsampling 8 x 5 x 3, ISTFT 16 / 4).
+hidden; HiFT CosyVoice2-style at 24 kHz (base 512 channels, upsampling 8 x 5 x 3, ISTFT 16 / 4); the flow encoder
+CosyVoice2's ``UpsampleConformerEncoder`` (width 512, 8 heads, FFN 2048, 6 + 4 layers, 2x upsampling, vocabulary 6561).
 """
 
 from __future__ import annotations
@@ -70,6 +71,33 @@ class HiFTConfig:
         return [int(v) for v in np.cumprod(r)[::-1]]
 
 
+@dataclass(frozen=True)
+class FlowConfig:
+    vocab: int = 6561
+    dim: int = 512
+    heads: int = 8
+    ffn: int = 2048
+    depth1: int = 6          # conformer layers before the upsampling
+    depth2: int = 4          # after it
+    look: int = 3            # pre-lookahead tokens
+    stride: int = 2          # token frames -> mel frames
+    mel: int = 80
+    spk: int = 192           # speaker embedding size (before the affine layer)
+    eps_layer: float = 1e-12  # norm_mha / norm_ff
+    eps_embed: float = 1e-5   # the input layers' LayerNorm
+    eps_after: float = 1e-5   # after_norm
+    rmax: int = 4096         # relative positions +-(rmax - 1) are tabulated: keys per stream and stack at most rmax
+
+    @property
+    def head_dim(self) -> int:
+        return self.dim // self.heads
+
+    @property
+    def cnn_frames(self) -> int:
+        return 2 + 2 * self.stride
+
+
+SILENCE_TOKEN = 4218
 SAMPLE_RATE = 24000
 MEL_CACHE = 8
 SOURCE_CACHE = MEL_CACHE * 480

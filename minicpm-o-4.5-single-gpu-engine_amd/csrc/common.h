@@ -87,6 +87,19 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
+// Activation of the plain bf16 GEMM epilogue (GemmArgs::act), applied after the bias.
+enum Act { ACT_NONE = 0, ACT_SILU = 1, ACT_LRELU = 2 };
+
+// x sigmoid(x) = x / (1 + 2^(-x log2 e)): one v_exp_f32 and one v_rcp_f32
+__device__ __forceinline__ float silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
+// ACT_LRELU is torch's leaky_relu at its default slope 0.01
+__device__ __forceinline__ float act_apply(float x, int act) {
+  return act == ACT_SILU ? silu(x) : (act == ACT_LRELU ? (x > 0.0f ? x : 0.01f * x) : x);
+}
+
 __device__ __forceinline__ float mish(float y) {
   // y tanh(softplus(y)) = y n (n + 2) / (n (n + 2) + 2) with n = e^y; above torch's softplus threshold 20 it is y
   if (y > 20.0f) return y;

@@ -136,6 +136,10 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = gelu_tanh(o[e]);
     }
+    if (EPI == EPI_BF16 && g.act) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = act_apply(o[e], g.act);
+    }
     if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) {
       *(uint2*)((bf16_t*)g.C + off) = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
     } else if (EPI == EPI_RESID_F16) {
@@ -155,6 +159,7 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
     const size_t off = (size_t)mo * g.ldc + n + e;
     if (EPI == EPI_PART) { part[off] = v[e]; continue; }
     if (EPI == EPI_GELU_BF16) x = gelu_tanh(x);
+    if (EPI == EPI_BF16) x = act_apply(x, g.act);
     if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[off] = f2bf(x);
     else if (EPI == EPI_RESID_F16) ((f16_t*)g.C)[off] = f2h(h2f(((const f16_t*)g.C)[off]) + g.gate[n + e] * x);
     else if (EPI == EPI_F16) ((f16_t*)g.C)[off] = f2h(x);

@@ -146,6 +146,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, const fl
     float x = v[e] + bias;
     const size_t o = (size_t)m * g.ldc + n;
     if (EPI == EPI_GELU_BF16) x = gelu_tanh(x);
+    if (EPI == EPI_BF16) x = act_apply(x, g.act);
     if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[o] = f2bf(x);
     else if (EPI == EPI_RESID_F16) ((f16_t*)g.C)[o] = f2h(h2f(((const f16_t*)g.C)[o]) + gate * x);
     else if (EPI == EPI_F16) ((f16_t*)g.C)[o] = f2h(x);

@@ -23,7 +23,8 @@ struct Cols {
   float4 bias, gate, wsc;
   int n;
   bool full;  // all four columns inside N
-  __device__ __forceinline__ Cols(const GemmArgs& g, int n_) : n(n_), full(n_ + 3 < g.N) {
+  int act;
+  __device__ __forceinline__ Cols(const GemmArgs& g, int n_) : n(n_), full(n_ + 3 < g.N), act(EPI == EPI_BF16 ? g.act : 0) {
     bias = gate = make_float4(0.f, 0.f, 0.f, 0.f);
     wsc = make_float4(1.f, 1.f, 1.f, 1.f);
     if (full) {
@@ -38,6 +39,10 @@ struct Cols {
     if (EPI == EPI_GELU_BF16 || EPI == EPI_GELU_MX8) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+    }
+    if (EPI == EPI_BF16 && act) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = act_apply(v[e], act);
     }
     if (EPI == EPI_RESID_F16) return make_float4(h.x + gate.x * v[0], h.y + gate.y * v[1], h.z + gate.z * v[2], h.w + gate.w * v[3]);
     return make_float4(v[0], v[1], v[2], v[3]);
@@ -56,7 +61,7 @@ struct Cols {
     for (int e = 0; e < 4 && n + e < g.N; ++e) {
       const float x = v[e] * (g.w_scale ? g.w_scale[n + e] : 1.0f) + g.bias[n + e];
       const size_t o = (size_t)m * g.ldc + n + e;
-      if (EPI == EPI_BF16) ((bf16_t*)g.C)[o] = f2bf(x);
+      if (EPI == EPI_BF16) ((bf16_t*)g.C)[o] = f2bf(act_apply(x, act));
       else if (EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[o] = f2bf(gelu_tanh(x));
       else if (EPI == EPI_RESID_F16) ((f16_t*)g.C)[o] = f2h(h2f(((const f16_t*)g.C)[o]) + g.gate[n + e] * x);
       else if (EPI == EPI_F16) ((f16_t*)g.C)[o] = f2h(x);

@@ -52,6 +52,7 @@ struct GemmArgs {
   QkvOut qk;           // EPI_QKV
   int splits;          // EPI_PART: K splits (1..4)
   size_t c_split;      // EPI_PART: elements between the splits' sums
+  int act;             // EPI_BF16: activation after the bias (Act: none, SiLU, leaky ReLU 0.01)
 };
 
 // K-split sums of a GEMM whose epilogue is left to the next row kernel (EPI_PART): the GEMM's value at (n, c) is

@@ -1,8 +1,9 @@
-"""Seeded random-init weights of the DiT estimator and HiFT (fp32 master copies on the host).
+"""Seeded random-init weights of the flow encoder, the DiT estimator and HiFT (fp32 master copies on the host).
 
 No checkpoint is available offline, so every workload runs on random-init weights of the real architecture.  Names
 follow the stepaudio2 module attributes the reference reads (``engine/runtime/dit_fast.py:131-145``,
-``engine/models/token2wav.py:160-236``).  Linear and conv weights and biases are uniform in ``+-1/sqrt(fan_in)`` (torch's
+``engine/models/token2wav.py:160-236``; the flow encoder's CosyVoice2 ``UpsampleConformerEncoder`` names,
+``engine/runtime/token2wav_batch.py:42-79``).  Linear and conv weights and biases are uniform in ``+-1/sqrt(fan_in)`` (torch's
 default init); LayerNorm affines are ``1 + 0.1 N`` / ``0.1 N``; Snake alphas uniform in [0.5, 1.5]; the f0 classifier is
 scaled so that a mel of the workloads' statistics gives both voiced (> 10 Hz) and unvoiced frames.
 """
@@ -13,7 +14,7 @@ import math
 
 import torch
 
-from .config import DiTConfig, HiFTConfig
+from .config import DiTConfig, FlowConfig, HiFTConfig
 
 
 class _Init:
@@ -98,3 +99,34 @@ def _resblock(ini: _Init, W, p, ch, k, dils):
         ini.conv(W, f"{p}.convs2.{j}", ch, ch, k)
         W[f"{p}.activations1.{j}.alpha"] = 0.5 + torch.rand(ch, generator=ini.g)
         W[f"{p}.activations2.{j}.alpha"] = 0.5 + torch.rand(ch, generator=ini.g)
+
+
+def init_flow(cfg: FlowConfig = FlowConfig(), seed: int = 0) -> dict[str, torch.Tensor]:
+    """The flow's token embedding, encoder, ``encoder_proj`` and speaker affine layer.  Embedding rows are N(0, 1) (torch's
+    default); ``pos_bias_u`` / ``pos_bias_v`` uniform in ``+-1/sqrt(head_dim)``."""
+    ini = _Init(seed)
+    C, W = cfg.dim, {}
+    W["input_embedding.weight"] = torch.randn(cfg.vocab, C, generator=ini.g)
+    ini.linear(W, "encoder.embed.out.0", C, C)
+    ini.norm(W, "encoder.embed.out.1", C)
+    ini.conv(W, "encoder.pre_lookahead_layer.conv1", C, C, cfg.look + 1)
+    ini.conv(W, "encoder.pre_lookahead_layer.conv2", C, C, 3)
+    for name, depth in (("encoders", cfg.depth1), ("up_encoders", cfg.depth2)):
+        for i in range(depth):
+            p = f"encoder.{name}.{i}."
+            for n in ("linear_q", "linear_k", "linear_v", "linear_out"):
+                ini.linear(W, p + "self_attn." + n, C, C)
+            W[p + "self_attn.linear_pos.weight"] = ini.uniform((C, C), 1.0 / math.sqrt(C))
+            W[p + "self_attn.pos_bias_u"] = ini.uniform((cfg.heads, cfg.head_dim), 1.0 / math.sqrt(cfg.head_dim))
+            W[p + "self_attn.pos_bias_v"] = ini.uniform((cfg.heads, cfg.head_dim), 1.0 / math.sqrt(cfg.head_dim))
+            ini.linear(W, p + "feed_forward.w_1", cfg.ffn, C)
+            ini.linear(W, p + "feed_forward.w_2", C, cfg.ffn)
+            ini.norm(W, p + "norm_mha", C)
+            ini.norm(W, p + "norm_ff", C)
+    ini.conv(W, "encoder.up_layer.conv", C, C, 2 * cfg.stride + 1)
+    ini.linear(W, "encoder.up_embed.out.0", C, C)
+    ini.norm(W, "encoder.up_embed.out.1", C)
+    ini.norm(W, "encoder.after_norm", C)
+    ini.linear(W, "encoder_proj", cfg.mel, C)
+    ini.linear(W, "spk_embed_affine_layer", cfg.mel, cfg.spk)
+    return W
