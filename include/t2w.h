@@ -18,6 +18,10 @@
  *                        with the hift_lean Snake / folded weight norm (engine/runtime/hift_lean.py:27-30, 107-134)
  *   t2w_graph_*          torch.cuda.CUDAGraph capture / replay of the solve and HiFT (dit_fast.py:392-422,
  *                        hift_graph.py:35-47)
+ *   t2w_flow_encode      BatchedToken2Wav._encoder + _encoder_core + the encoder_proj of _flow_encode
+ *                        (engine/runtime/token2wav_batch.py:42-79, 365-386, 402-444) and _setup_encoder_one /
+ *                        _setup_encoder_batched (:556-616): UpsampleConformerEncoderV2.forward_chunk over many streams
+ *   t2w_flow_speaker     spk_embed_affine_layer(F.normalize(spk)) (engine/runtime/token2wav_batch.py:375)
  */
 #ifndef T2W_H
 #define T2W_H
@@ -139,6 +143,81 @@ int t2w_dit_solve_noalloc(const t2w_dit* m, const t2w_solve_args* a, void* strea
  * (mods [depth, 9, H], final_mods [2, H]) on in_rows; writes dphi [n_tok, mel] to a->out. */
 int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const float* mods, const float* final_mods,
                     void* stream);
+
+/* ---------------------------------------------------------------- flow encoder (codec tokens -> mu) */
+
+typedef struct t2w_flow t2w_flow;
+
+/* dim % 512 == 0 with heads of 64; stride 2; relative positions |r| <= rmax - 1 are tabulated, so a stream may hold
+ * at most rmax keys per stack in a call */
+typedef struct {
+  int vocab, dim, heads, ffn, depth1, depth2, look, stride, mel, spk, rmax;
+  float eps_layer, eps_embed, eps_after;
+} t2w_flow_dims;
+
+/* one conformer layer: layers 0 .. depth1 - 1 before the upsampling, depth1 .. depth1 + depth2 - 1 after it */
+typedef struct {
+  const void* qkv_w; const float* qkv_b;      /* [3C, C]: linear_q | linear_k | linear_v */
+  const float* pos_u; const float* pos_v;      /* pos_bias_u / pos_bias_v [C] (head h at h * 64) */
+  const void* ptab;                            /* fp16 [2 rmax - 1, C]: linear_pos(sinusoid(r)) at row r + rmax - 1 */
+  const void* out_w; const float* out_b;       /* linear_out [C, C] */
+  const float* ln1_w; const float* ln1_b;      /* norm_mha */
+  const float* ln2_w; const float* ln2_b;      /* norm_ff */
+  const void* w1; const float* b1;             /* feed_forward.w_1 [ffn, C] (SiLU) */
+  const void* w2; const float* b2;             /* feed_forward.w_2 [C, ffn] */
+} t2w_flow_layer;
+
+typedef struct {
+  const float* embed_table;                    /* fp32 [vocab, C]: input_embedding rows through the embed Linear */
+  const float* embed_ln_w; const float* embed_ln_b;
+  const void* conv1_w; const float* conv1_b;   /* pre-lookahead conv1 [C, (look + 1) C] frame-major */
+  const void* conv2_w; const float* conv2_b;   /* pre-lookahead conv2 [C, 3C] frame-major (tap 0: frame t - 2) */
+  const void* up_w; const float* up_b;         /* [C, (2 stride + 1) C]: the up_layer conv followed by up_embed's Linear */
+  const float* up_ln_w; const float* up_ln_b;  /* up_embed LayerNorm */
+  const float* after_w; const float* after_b;  /* after_norm */
+  const void* proj_w; const float* proj_b;     /* encoder_proj [mel, C] */
+  const float* spk_w; const float* spk_b;      /* fp32 spk_embed_affine_layer [mel, spk] */
+  const float* ones;                           /* [C] of 1.0 (the residual adds use the gated-residual epilogue) */
+} t2w_flow_globals;
+
+/* One packed ragged call over R streams (see flow_capi.hip for the row layout).  Stream s: T1 = t1[s] frames (its
+ * window's tokens less the lookahead, or all of a final window's), T2 = stride T1. */
+typedef struct {
+  int n_rows, n_in, n_gap, n1, n_up, n2, n_tiles1, n_tiles2;  /* n_in = n1 + look R, n_gap = n1 + 2R, n2 = 2 n1, n_up = n2 + 4R */
+  const int* tok;        /* [n_in] token of each conv1 input row, -1: zero row (a final window's lookahead) */
+  const int* res;        /* [n_in] h1 row that the embedded row also starts, -1: none (lookahead rows) */
+  const int* c1_src;     /* [n_gap] conv1 taps: first input row (any valid row for the two cache rows of a stream) */
+  const int* gofs;       /* [R] first row of the stream in the conv1 output (its two cached frames) */
+  const int* t1;         /* [R] */
+  const int* c2_src;     /* [n1] conv2 taps: first row in the conv1 output (gofs + t) */
+  const int* up_dst;     /* [n1] row of the first upsampled copy of stack-1 row m (uofs + 4 + 2t) */
+  const int* uofs;       /* [R] first row of the stream in the upsampling input (its four cached frames) */
+  const int* o1;         /* [R] first stack-1 row */
+  const int* up_src;     /* [n2] upsampling conv taps: uofs + f */
+  const int* o2;         /* [R] first stack-2 row */
+  const int* t2;         /* [R] */
+  const int* cnn_rd;     /* [R] conv-cache slot read (a zero slot for an empty cache) */
+  const int* cnn_wr;     /* [R] conv-cache slot written (never one any stream of the call reads) */
+  const int* new1;       /* [n1] pool slot receiving each stack-1 row's keys / values */
+  const int* new2;       /* [n2] */
+  const int* kv1_idx; const int* kv1_off; const int* kv1_len; const int* tiles1;  /* stack-1 key lists, [n_tiles1, 2] */
+  const int* kv2_idx; const int* kv2_off; const int* kv2_len; const int* tiles2;
+  void* pool1; long long pool1_layer_stride;  /* fp16 [depth1][slots][2C] (k | v), stride in elements */
+  void* pool2; long long pool2_layer_stride;  /* fp16 [depth2][slots][2C] */
+  void* cnn_pool;        /* bf16 [slots][(2 + 2 stride) C]: two pre-lookahead frames, then 2 stride upsampled frames */
+  float* mu_out;         /* [n2, mel] */
+  void* workspace;
+  size_t workspace_bytes;
+} t2w_flow_args;
+
+int t2w_flow_create(const t2w_flow_dims* dims, t2w_flow** out);
+int t2w_flow_set_layer(t2w_flow* m, int layer, const t2w_flow_layer* w);
+int t2w_flow_set_globals(t2w_flow* m, const t2w_flow_globals* g);
+void t2w_flow_destroy(t2w_flow* m);
+size_t t2w_flow_workspace_bytes(const t2w_flow* m, int n_in, int n_gap, int n1, int n_up, int n2);
+int t2w_flow_encode(const t2w_flow* m, const t2w_flow_args* a, void* stream);
+/* out [R, mel] = spk_w F.normalize(spk [R, spk]) + spk_b */
+int t2w_flow_speaker(const t2w_flow* m, const float* spk, float* out, int R, void* stream);
 
 /* ---------------------------------------------------------------- kernel-level entry points (tests, benchmarks) */
 

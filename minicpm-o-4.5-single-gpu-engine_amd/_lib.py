@@ -68,6 +68,30 @@ class HiftWeights(C.Structure):
                 ("src_down", Conv * 3), ("conv_post", Conv), ("src_res", ResBlock * 3), ("res", ResBlock * 9), ("window", P)]
 
 
+class FlowDims(C.Structure):
+    _fields_ = [(n, I) for n in ("vocab", "dim", "heads", "ffn", "depth1", "depth2", "look", "stride", "mel", "spk", "rmax")] + \
+               [(n, F) for n in ("eps_layer", "eps_embed", "eps_after")]
+
+
+class FlowLayer(C.Structure):
+    _fields_ = [(n, P) for n in ("qkv_w", "qkv_b", "pos_u", "pos_v", "ptab", "out_w", "out_b", "ln1_w", "ln1_b", "ln2_w", "ln2_b",
+                                 "w1", "b1", "w2", "b2")]
+
+
+class FlowGlobals(C.Structure):
+    _fields_ = [(n, P) for n in ("embed_table", "embed_ln_w", "embed_ln_b", "conv1_w", "conv1_b", "conv2_w", "conv2_b", "up_w", "up_b",
+                                 "up_ln_w", "up_ln_b", "after_w", "after_b", "proj_w", "proj_b", "spk_w", "spk_b", "ones")]
+
+
+class FlowArgs(C.Structure):
+    _fields_ = [(n, I) for n in ("n_rows", "n_in", "n_gap", "n1", "n_up", "n2", "n_tiles1", "n_tiles2")] + \
+               [(n, P) for n in ("tok", "res", "c1_src", "gofs", "t1", "c2_src", "up_dst", "uofs", "o1", "up_src", "o2", "t2", "cnn_rd",
+                                 "cnn_wr", "new1", "new2", "kv1_idx", "kv1_off", "kv1_len", "tiles1", "kv2_idx", "kv2_off", "kv2_len",
+                                 "tiles2")] + \
+               [("pool1", P), ("pool1_layer_stride", C.c_longlong), ("pool2", P), ("pool2_layer_stride", C.c_longlong), ("cnn_pool", P),
+                ("mu_out", P), ("workspace", P), ("workspace_bytes", C.c_size_t)]
+
+
 _SIGS = {
     "t2w_abi_version": (I, []),
     "t2w_last_error": (C.c_char_p, []),
@@ -96,6 +120,13 @@ _SIGS = {
     "t2w_hift_plan": (I, [P, I, P, P]),
     "t2w_hift_workspace_bytes": (C.c_size_t, [P, I, P]),
     "t2w_hift_forward": (I, [P, I, P, P, P, P, P, I, P, P, P, P, P, P, C.c_size_t, I, P]),
+    "t2w_flow_create": (I, [C.POINTER(FlowDims), C.POINTER(P)]),
+    "t2w_flow_set_layer": (I, [P, I, C.POINTER(FlowLayer)]),
+    "t2w_flow_set_globals": (I, [P, C.POINTER(FlowGlobals)]),
+    "t2w_flow_destroy": (None, [P]),
+    "t2w_flow_workspace_bytes": (C.c_size_t, [P, I, I, I, I, I]),
+    "t2w_flow_encode": (I, [P, C.POINTER(FlowArgs), P]),
+    "t2w_flow_speaker": (I, [P, P, P, I, P]),
     "t2w_graph_begin": (I, [P]),
     "t2w_graph_end": (I, [P, C.POINTER(P)]),
     "t2w_graph_launch": (I, [P, P]),
