@@ -7,12 +7,17 @@ pins the minimal contract): ``setup_many``, ``setup_encode`` / ``release_presetu
 attributes the loop reads (``max_flow_streams``, ``fuse_setup_frames``, ``fast``, ``profile``, ``trace``).
 
 Prompt features keep the reference's tuple layout ``(tokens, tokens_len, spk, mels, mels_len)`` (``Token2Wav.features``,
-``engine/models/token2wav.py:266-276``; ``mels`` [1, P, mel] is the prompt mel and sets the trim length).  The flow
-encoder (codec tokens -> ``mu``) is not part of this module yet, so the first entry carries the encoder's output
-``mu`` [1, P, mel] in place of the tokens and ``spk`` is the speaker embedding after the flow's affine layer [1, mel]
-(``prompt_features`` builds such a tuple); a window is ``(stream, mu [mel, T], last)``.
+``engine/models/token2wav.py:266-276``): ``tokens`` [1, n] codec tokens, ``spk`` [1, 192] the speaker embedding,
+``mels`` [1, 2n, mel] the prompt mel (it sets the trim length).  A window is ``(stream, tokens, last)`` with the
+chunker's tokens (a non-final window ends with 3 lookahead tokens).  Every call runs the flow encoder once over all its
+token windows and token prompts (``FlowEncoder``), as ``_flow_encode`` does per group.
 
-Per call: one packed ragged CFG Euler solve over every window (and fused prompt setups), then HiFT over all windows in
+The encoder can be bypassed: a feature tuple whose first entry is the encoder's output ``mu`` [1, P, mel] (floating
+point) and whose ``spk`` is already through the affine layer [1, mel] (``prompt_features`` builds one), and a window
+``(stream, mu [mel, T], last)``, go straight to the solve (DiT + HiFT measurements and tests use this).
+
+Per call: the flow encoder over the token windows, one packed ragged CFG Euler solve over every window (and fused prompt
+setups), then HiFT over all windows in
 one ragged call per source-cache length, then the per-stream glue of ``engine/models/token2wav.py:319-332`` (8 cached
 mel frames, 3840 cached source / speech samples, Hamming cross-fade, first non-final chunk shifted by 3840 zeros,
 non-final chunks hold back their last 3840 samples), and one device-to-host copy — synchronous, or through a pinned
@@ -28,7 +33,23 @@ import torch
 
 from .config import MEL_CACHE, SOURCE_CACHE
 from .dit import FastCache, FastDiT
+from .flow import FlowEncoder, FlowState
 from .hift import HiFTModel, HiftState, chunk_noise_seed, fade_in_out
+
+
+def _is_tokens(x) -> bool:
+    """Codec tokens (a list, an integer array or tensor) rather than an encoder output (a floating-point tensor)."""
+    if isinstance(x, torch.Tensor):
+        return not torch.is_floating_point(x)
+    if isinstance(x, np.ndarray):
+        return np.issubdtype(x.dtype, np.integer)
+    return isinstance(x, (list, tuple))
+
+
+def _token_list(x) -> list[int]:
+    if isinstance(x, torch.Tensor):
+        return x.reshape(-1).tolist()
+    return np.asarray(x, dtype=np.int64).reshape(-1).tolist()
 
 
 def prompt_features(mu: torch.Tensor, spk: torch.Tensor, mels: torch.Tensor) -> tuple:
@@ -41,10 +62,12 @@ def prompt_features(mu: torch.Tensor, spk: torch.Tensor, mels: torch.Tensor) -> 
 
 @dataclass
 class Prompt:
-    """A set-up prompt: its features, speaker embedding (after the affine layer) and estimator caches."""
+    """A set-up prompt: its features, speaker embedding (after the affine layer), estimator caches and flow-encoder
+    caches (None for an encoder-output prompt)."""
     feats: tuple
     spk: torch.Tensor       # [1, mel]
     cache: FastCache | None
+    flow: FlowState | None = None
 
     @property
     def mels(self) -> torch.Tensor:
@@ -64,6 +87,7 @@ class PreSetup:
     mu: torch.Tensor        # [mel, P]
     spk: torch.Tensor       # [1, mel]
     cond: torch.Tensor      # [mel, P]
+    flow: FlowState | None = None
 
 
 @dataclass
@@ -71,6 +95,7 @@ class StreamState:
     prompt: Prompt
     cache: FastCache | None
     hift: HiftState = field(default_factory=HiftState)
+    flow: FlowState | None = None
 
     @property
     def chunks(self) -> int:
@@ -108,12 +133,14 @@ class PendingAudio:
 
 
 class BatchedToken2Wav:
-    def __init__(self, dit: FastDiT, hift: HiFTModel, noise_device: str = "cuda", fuse_setup_frames: int = 0, max_flow_streams: int = 32):
-        """``noise_device``: where the per-chunk HiFT source noise is drawn ("cuda" as the reference's ``hift_noise``;
-        "cpu" reproduces a host-generator draw bit for bit, used by the parity tests).  ``fuse_setup_frames``: prompt
-        setups of up to this many mel frames in all may ride a decode call's solve (``decode(setups=...)``).
-        ``max_flow_streams``: requests per packed solve (larger calls run in slices)."""
-        self.fast, self.hift = dit, hift
+    def __init__(self, dit: FastDiT, hift: HiFTModel, flow: FlowEncoder | None = None, noise_device: str = "cuda", fuse_setup_frames: int = 0,
+                 max_flow_streams: int = 32):
+        """``flow``: the flow encoder (needed for codec-token prompts and windows).  ``noise_device``: where the
+        per-chunk HiFT source noise is drawn ("cuda" as the reference's ``hift_noise``; "cpu" reproduces a host-generator
+        draw bit for bit, used by the parity tests).  ``fuse_setup_frames``: prompt setups of up to this many mel frames
+        in all may ride a decode call's solve (``decode(setups=...)``).  ``max_flow_streams``: requests per packed solve
+        (larger calls run in slices)."""
+        self.fast, self.hift, self.flow = dit, hift, flow
         self.device = dit.device
         self.noise_device = noise_device
         self.window = torch.from_numpy(np.hamming(2 * SOURCE_CACHE)).to(self.device)  # float64, as the reference's
@@ -140,10 +167,8 @@ class BatchedToken2Wav:
         return r
 
     # --- prompts ------------------------------------------------------------------------------------------------------
-    def _stage(self, feats: tuple) -> PreSetup:
+    def _stage_mu(self, feats: tuple) -> PreSetup:
         mu, _, spk, mels, _ = feats
-        if not torch.is_floating_point(mu):
-            raise NotImplementedError("codec-token prompts need the flow encoder; pass its output mu (prompt_features)")
         P = int(mels.shape[1])
         if mu.shape[1] != P:
             raise ValueError(f"prompt mu has {mu.shape[1]} frames, its mel {P}")
@@ -151,14 +176,36 @@ class BatchedToken2Wav:
         return PreSetup(feats, self.fast.new_cache(keep=P), mu[0].to(dev, torch.float32).t(), spk.to(dev, torch.float32).reshape(1, -1),
                         mels[0].to(dev, torch.float32).t())
 
+    def _stage_tokens(self, feats_list: list[tuple]) -> list[PreSetup]:
+        """Token prompts: the flow encoder over every prompt (plus 3 silence tokens) in one call and the speaker affine
+        layer over their embeddings (``_setup_encoder_batched``, ``token2wav_batch.py:567-616``)."""
+        if self.flow is None:
+            raise ValueError("codec-token prompts need the flow encoder (BatchedToken2Wav(flow=...))")
+        toks = [_token_list(f[0]) for f in feats_list]
+        for t, f in zip(toks, feats_list):
+            if 2 * len(t) != int(f[3].shape[1]):
+                raise ValueError(f"prompt of {len(t)} tokens needs a mel of {2 * len(t)} frames, got {int(f[3].shape[1])}")
+        states, mu, rows, frames = self.flow.setup(toks)
+        spk = self.flow.model.speaker(torch.cat([f[2].reshape(1, -1).to(self.device, torch.float32) for f in feats_list]))
+        dev = self.device
+        out = []
+        for i, (f, st) in enumerate(zip(feats_list, states)):
+            P = frames[i]
+            out.append(PreSetup(f, self.fast.new_cache(keep=P), mu[rows[i]:rows[i] + P].t(), spk[i:i + 1], f[3][0].to(dev, torch.float32).t(), st))
+        return out
+
     @torch.inference_mode()
     def setup_encode(self, feats_list: list[tuple]) -> list[PreSetup]:
-        """Prompt setups staged ahead of their solve (``setup_encode``, ``token2wav_batch.py:480-485``): inputs on the
-        device and empty estimator caches allocated."""
-        out = []
+        """Prompt setups staged ahead of their solve (``setup_encode``, ``token2wav_batch.py:480-485``): the flow encoder
+        of token prompts run (one call for all), inputs on the device and empty estimator caches allocated."""
+        out: list = [None] * len(feats_list)
         try:
-            for f in feats_list:
-                out.append(self._stage(f))
+            tok_idx = [i for i, f in enumerate(feats_list) if _is_tokens(f[0])]
+            for i, p in zip(tok_idx, self._stage_tokens([feats_list[i] for i in tok_idx]) if tok_idx else []):
+                out[i] = p
+            for i, f in enumerate(feats_list):
+                if out[i] is None:
+                    out[i] = self._stage_mu(f)
         except Exception:
             for p in out:
                 self.release_presetup(p)
@@ -166,17 +213,24 @@ class BatchedToken2Wav:
         return out
 
     def release_presetup(self, p: PreSetup) -> None:
-        if p is not None and p.cache is not None:
+        if p is None:
+            return
+        if p.cache is not None:
             self.fast.release(p.cache)
             p.cache = None
+        if p.flow is not None:
+            self.flow.release(p.flow)
+            p.flow = None
 
     def _presetups(self, setups: list) -> list[PreSetup]:
-        return [s if isinstance(s, PreSetup) else self.setup_encode([s])[0] for s in setups]
+        raw = [s for s in setups if not isinstance(s, PreSetup)]
+        staged = iter(self.setup_encode(raw) if raw else ())
+        return [s if isinstance(s, PreSetup) else next(staged) for s in setups]
 
     @staticmethod
     def _prompt(p: PreSetup) -> Prompt:
-        pr = Prompt(p.feats, p.spk, p.cache)
-        p.cache = None  # the prompt owns the caches now
+        pr = Prompt(p.feats, p.spk, p.cache, p.flow)
+        p.cache = p.flow = None  # the prompt owns the caches now
         return pr
 
     @torch.inference_mode()
@@ -195,22 +249,35 @@ class BatchedToken2Wav:
 
     # --- streams ------------------------------------------------------------------------------------------------------
     def new_stream(self, prompt: Prompt, noise_seed: int = 0, adopt: bool = False) -> StreamState:
-        """A stream with its own copy of the prompt's caches, or taking them over (``adopt``: the prompt is used once)."""
+        """A stream with its own copy of the prompt's caches, or taking them over (``adopt``: the prompt is used once).
+        Flow-encoder caches are shared slot lists, so a copy costs no device work."""
         if adopt:
             cache, prompt.cache = prompt.cache, None
+            flow, prompt.flow = prompt.flow, None
         else:
             cache = self.fast.clone(prompt.cache)
-        return StreamState(prompt, cache, HiftState(noise_seed=noise_seed, device=self.device))
+            flow = self.flow.clone(prompt.flow) if prompt.flow is not None else None
+        return StreamState(prompt, cache, HiftState(noise_seed=noise_seed, device=self.device), flow)
 
     def release_stream(self, st: StreamState | None) -> None:
-        if st is not None and st.cache is not None:
+        if st is None:
+            return
+        if st.cache is not None:
             self.fast.release(st.cache)
             st.cache = None
+        if st.flow is not None:
+            self.flow.release(st.flow)
+            st.flow = None
 
     def release_prompt(self, p: Prompt | None) -> None:
-        if p is not None and p.cache is not None:
+        if p is None:
+            return
+        if p.cache is not None:
             self.fast.release(p.cache)
             p.cache = None
+        if p.flow is not None:
+            self.flow.release(p.flow)
+            p.flow = None
 
     @torch.inference_mode()
     def capture_graphs(self, prompt: Prompt | None = None) -> dict:
@@ -224,18 +291,39 @@ class BatchedToken2Wav:
         return n
 
     # --- decode -------------------------------------------------------------------------------------------------------
+    def _encode_windows(self, items: list[tuple]) -> list[tuple]:
+        """Items with codec tokens through the flow encoder (one call): ``(stream, mu [mel, T], last)`` for every item
+        (``_flow_encode``, ``token2wav_batch.py:365-386``)."""
+        idx = [i for i, (_, w, _) in enumerate(items) if _is_tokens(w)]
+        if not idx:
+            return items
+        if self.flow is None:
+            raise ValueError("codec-token windows need the flow encoder (BatchedToken2Wav(flow=...))")
+        for i in idx:
+            if items[i][0].flow is None:
+                raise ValueError("a codec-token window needs a stream set up from a codec-token prompt")
+        mu, rows, frames = self._prof("encoder", len(idx), self.flow.encode, [items[i][0].flow for i in idx],
+                                      [_token_list(items[i][1]) for i in idx], [bool(items[i][2]) for i in idx])
+        out = list(items)
+        for k, i in enumerate(idx):
+            st, _, last = items[i]
+            out[i] = (st, mu[rows[k]:rows[k] + frames[k]].t(), last)
+        return out
+
     @torch.inference_mode()
     def decode(self, items: list[tuple], async_result: bool = False, setups: list | None = None):
-        """``items[i] = (stream, mu [mel, T_i], last)`` -> float32 24 kHz samples per item (``decode``,
-        ``token2wav_batch.py:220-255``).  ``async_result``: a ``PendingAudio`` instead, without waiting for the GPU.
-        ``setups`` (``fuse_setup_frames``): prompt features (or ``PreSetup``) set up in the same packed solve; then the
-        result is ``(samples, prompts)``."""
+        """``items[i] = (stream, tokens, last)`` -> float32 24 kHz samples per item (``decode``,
+        ``token2wav_batch.py:220-255``); ``tokens`` are the window's codec tokens (or the encoder's output ``mu``
+        [mel, T]).  ``async_result``: a ``PendingAudio`` instead, without waiting for the GPU.  ``setups``
+        (``fuse_setup_frames``): prompt features (or ``PreSetup``) set up in the same packed solve; then the result is
+        ``(samples, prompts)``."""
         if setups:
             frames = sum(int((s.feats if isinstance(s, PreSetup) else s)[3].shape[1]) for s in setups)
             if not self.fuse_setup_frames or frames > self.fuse_setup_frames or len(items) + len(setups) > self.max_flow_streams:
                 raise ValueError(f"fused setups: {len(setups)} prompts of {frames} frames with {len(items)} windows exceed "
                                  f"fuse_setup_frames={self.fuse_setup_frames} / max_flow_streams={self.max_flow_streams}")
         pre = self._presetups(setups) if setups else []
+        items = self._encode_windows(items)
         rows = [(p.cache, p.mu, p.spk, p.cond, True) for p in pre]
         rows += [(st.cache, mu.to(self.device), st.prompt.spk, None, not last) for st, mu, last in items]
         mels = []

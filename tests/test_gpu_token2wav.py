@@ -204,3 +204,60 @@ def test_worker_call_sequence(dev):
             b.release_stream(st)
     assert stats(bt)[:2] == (0, free0)
     assert bt.fast.counts["graph"] > 0
+
+
+def test_codec_tokens_end_to_end_mels(dev):
+    """Codec-token prompts and windows (the reference's ``decode(items)`` surface): the flow encoder, speaker affine
+    layer, prompt-mel conditioning and the solve against the oracle pipeline (oracle encoder -> oracle solve) per
+    stream; DiT at hidden 256, encoder at full width.  Mel rel-L2 < 2e-2."""
+    from oracle import flow as of
+    from t2w_amd.config import FlowConfig
+    from t2w_amd.flow import FlowEncoder, FlowModel
+    from t2w_amd.weights import init_flow
+
+    W, Wh, Wf = init_dit(TINY, seed=31), init_hift(HiFTConfig(), seed=32), init_flow(FlowConfig(), seed=33)
+    fd = FastDiT(DiTModel(W, TINY), n_slots=8192, max_streams=8)
+    enc = FlowEncoder(FlowModel(Wf, FlowConfig()), n_slots1=4096, n_slots2=8192, n_cnn=64)
+    bt = BatchedToken2Wav(fd, HiFTModel(Wh), flow=enc, noise_device="cpu")
+    d, fdims = od.dims_of(W), of.enc_dims_of(Wf)
+    g = torch.Generator().manual_seed(6)
+    toks = [torch.randint(0, 6561, (1, n), generator=g) for n in (40, 25)]
+    spks = [torch.randn(1, 192, generator=g) for _ in toks]
+    mels = [torch.randn(1, 2 * t.shape[1], 80, generator=g) for t in toks]
+    feats = [(t, torch.tensor([t.shape[1]]), s, m, torch.tensor([m.shape[1]])) for t, s, m in zip(toks, spks, mels)]
+    seen = []
+    solve = fd.solve
+
+    def recording_solve(*a, **k):
+        out = solve(*a, **k)
+        seen.extend(out)
+        return out
+
+    fd.solve = recording_solve
+    prompts = bt.setup_many(feats)
+    sts = [bt.new_stream(p, noise_seed=j) for j, p in enumerate(prompts)]
+    # oracle: encoder setup, speaker affine, prompt solve with the prompt mel as condition
+    rf, rc, rspk = [], [], []
+    for t, s, m in zip(toks, spks, mels):
+        mu0, fst = of.setup(Wf, fdims, t[0].tolist())
+        rf.append(fst)
+        rspk.append(of.speaker(Wf, s))
+        rc.append(od.empty_cache(d, keep=m.shape[1]))
+        od.solve(W, d, W["rand_noise"], [rc[-1]], [mu0], rspk[-1], [m[0].t()], [True])
+    errs = []
+    plan = [(28, False), (28, False), (28, False), (28, False), (17, True)]
+    for k, (n, last) in enumerate(plan):
+        wins = [torch.randint(0, 6561, (n,), generator=g).tolist() for _ in sts]
+        seen.clear()
+        bt.decode([(st, w, last) for st, w in zip(sts, wins)])
+        for j in range(2):
+            mu = of.encode_window(Wf, fdims, rf[j], wins[j], last)
+            mel = od.solve(W, d, W["rand_noise"], [rc[j]], [mu], rspk[j], None, [not last])[0]
+            errs.append(rel(seen[j].float().cpu(), mel))
+    print("token windows: mel rel-L2 max", max(errs))
+    assert max(errs) < 2e-2
+    for p in prompts:
+        bt.release_prompt(p)
+    for st in sts:
+        bt.release_stream(st)
+    assert fd.pool.in_use() == fd.scratch and enc.in_use() == (0, 0, 0)
