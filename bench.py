@@ -72,6 +72,8 @@ def main() -> int:
     ap.add_argument("--no-fp8", action="store_true", help="skip the fp8 (e4m3 weights, MX fp8 activations) measurement")
     ap.add_argument("--no-gemms", action="store_true", help="skip the per-GEMM timings and their hipBLASLt comparison")
     ap.add_argument("--latency-only", action="store_true", help="only the per-chunk latency case")
+    ap.add_argument("--no-flow", action="store_true", help="skip the flow encoder (codec-token chunk latency, encoder workload)")
+    ap.add_argument("--flow-only", action="store_true", help="only the flow encoder workload (16 streams, 28-token windows)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant kernel's launches, after three 256 MiB calibration copies (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -86,6 +88,9 @@ def main() -> int:
     if args.roofline_only:
         r = resid_gemm_roofline(cfg, args.streams, args.frames, calibrate=True)
         print(json.dumps({"kernel": r["kernel"], "launch_ms": r["launch_ms"], "tflops": r["achieved"], "calibration_copy_bytes": 2 * (256 << 20)}))
+        return 0
+    if args.flow_only:
+        print(json.dumps(flow_workload(args, flow_encoder())))
         return 0
     from t2w_amd.dit import DiTModel, FastDiT
     from t2w_amd.weights import init_dit, init_hift
@@ -109,7 +114,7 @@ def main() -> int:
         hnoise = hift.noise([1000 + i for i in range(n)], T * hift.cfg.upsample_scale)
 
     if args.latency_only:
-        print(json.dumps(chunk_latency(model, Wh, args)))
+        print(json.dumps(chunk_latency(model, Wh, args, None if args.no_flow else flow_encoder())))
         return 0
 
     def step():
@@ -141,7 +146,8 @@ def main() -> int:
     roof["traffic"] = pmc_traffic()
     gemms = None if args.no_gemms else dit_gemm_table(cfg, n, T)
 
-    lat = chunk_latency(model, Wh, args) if args.latency_reps > 0 else {}
+    enc = flow_encoder() if not args.no_flow else None
+    lat = chunk_latency(model, Wh, args, enc) if args.latency_reps > 0 else {}
 
     extra = {}
     if not args.no_fp8:
@@ -149,6 +155,8 @@ def main() -> int:
                                     hnoise if hift is not None else None, step)
     if not args.no_extra:
         extra.update(extra_workloads(args, cfg, fd, spks, hift, Wh))
+    if enc is not None:
+        extra["flow_encoder"] = flow_workload(args, enc)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -299,24 +307,16 @@ def pmc_traffic() -> float | None:
     return None
 
 
-def chunk_latency(model, Wh, args) -> dict:
-    """One stream through ``BatchedToken2Wav.decode`` as the worker calls it: a 300-frame prompt set up, then steady
-    50-frame windows (kept, so the caches grow and trim), each with HiFT over 8 cached + 50 new mel frames and a
-    3840-sample source cache, the cross-fade and the device-to-host copy; graphs on.  p50 of the whole call over
-    ``latency_reps`` windows after three, then the mean of its solve and vocode stages (the module's profile hook)."""
-    from t2w_amd.dit import FastDiT
-    from t2w_amd.token2wav import BatchedToken2Wav, prompt_features
+def flow_encoder(seed: int = 5):
+    """The flow encoder (CosyVoice2-style conformer, width 512) with random-init weights and pools for the workloads."""
+    from t2w_amd.config import FlowConfig
+    from t2w_amd.flow import FlowEncoder, FlowModel
+    from t2w_amd.weights import init_flow
 
-    dev, mel = "cuda", model.cfg.mel
-    fl = FastDiT(model, n_slots=8192, max_streams=4, use_graphs=True)
-    if Wh is None:
-        return {}
-    bt = BatchedToken2Wav(fl, hift_model(Wh, args.hift_mode))
-    g = torch.Generator().manual_seed(11)
-    mk = lambda *s: torch.randn(*s, generator=g).to(dev)  # noqa: E731
-    st = bt.new_stream(bt.setup(prompt_features(mk(mel, 300), mk(mel), mk(mel, 300))), noise_seed=7, adopt=True)
-    reps = args.latency_reps
-    wins = [mk(mel, 50) for _ in range(2 * reps + 6)]
+    return FlowEncoder(FlowModel(init_flow(FlowConfig(), seed), FlowConfig()), n_slots1=16384, n_slots2=32768, n_cnn=1024)
+
+
+def _latency(bt, st, wins, reps: int) -> tuple[float, dict]:
     ts = []
     for i in range(reps + 3):
         torch.cuda.synchronize()
@@ -329,11 +329,92 @@ def chunk_latency(model, Wh, args) -> dict:
     for i in range(reps):
         bt.decode([(st, wins[reps + 3 + i], False)])
     prof = {k: v[1] / v[0] * 1e3 for k, v in bt.profile.items()}
+    bt.profile = None
+    return float(np.median(ts) * 1e3), prof
+
+
+def chunk_latency(model, Wh, args, enc=None) -> dict:
+    """One stream through ``BatchedToken2Wav.decode`` as the worker calls it: a 150-token prompt (300 mel frames) set
+    up, then steady windows of 28 codec tokens (25 + 3 lookahead: 50 mel frames; kept, so the caches grow and trim),
+    each through the flow encoder, the solve and HiFT over 8 cached + 50 new mel frames with a 3840-sample source
+    cache, the cross-fade and the device-to-host copy; graphs on.  p50 of the whole call over ``latency_reps`` windows
+    after three, then the mean of its encoder, solve and vocode stages (the module's profile hook).  The same with the
+    encoder bypassed (50-frame ``mu`` windows) for the DiT + HiFT part alone."""
+    from t2w_amd.dit import FastDiT
+    from t2w_amd.token2wav import BatchedToken2Wav, prompt_features
+
+    dev, mel = "cuda", model.cfg.mel
+    if Wh is None:
+        return {}
+    fl = FastDiT(model, n_slots=8192, max_streams=4, use_graphs=True)
+    hm = hift_model(Wh, args.hift_mode)
+    g = torch.Generator().manual_seed(11)
+    mk = lambda *s: torch.randn(*s, generator=g).to(dev)  # noqa: E731
+    reps = args.latency_reps
+    out = {}
+    if enc is not None:
+        bt = BatchedToken2Wav(fl, hm, flow=enc)
+        tok = lambda n: torch.randint(0, 6561, (n,), generator=g)  # noqa: E731
+        feats = (tok(150)[None], torch.tensor([150]), torch.randn(1, 192, generator=g), torch.randn(1, 300, mel, generator=g), torch.tensor([300]))
+        st = bt.new_stream(bt.setup(feats), noise_seed=7, adopt=True)
+        p50, prof = _latency(bt, st, [tok(28).tolist() for _ in range(2 * reps + 6)], reps)
+        bt.release_stream(st)
+        out.update({"p50_chunk_latency_ms": p50, "p50_chunk_encoder_ms": prof.get("encoder"), "p50_chunk_dit_ms": prof.get("solve"),
+                    "p50_chunk_hift_ms": prof.get("vocode")})
+    bt = BatchedToken2Wav(fl, hm)
+    st = bt.new_stream(bt.setup(prompt_features(mk(mel, 300), mk(mel), mk(mel, 300))), noise_seed=7, adopt=True)
+    p50, prof = _latency(bt, st, [mk(mel, 50) for _ in range(2 * reps + 6)], reps)
     bt.release_stream(st)
-    return {"p50_chunk_latency_ms": float(np.median(ts) * 1e3), "p50_chunk_dit_ms": prof.get("solve"),
-            "p50_chunk_hift_ms": prof.get("vocode"),
-            "chunk_case": "BatchedToken2Wav.decode of one stream: 300-frame prompt cached, steady 50-frame windows, "
-                          "HiFT on 58 frames + glue + device-to-host copy; stage times are means of profiled calls"}
+    out.update({"p50_chunk_latency_no_encoder_ms": p50, "p50_chunk_dit_no_encoder_ms": prof.get("solve"),
+                "p50_chunk_hift_no_encoder_ms": prof.get("vocode")})
+    out["chunk_case"] = ("BatchedToken2Wav.decode of one stream: 150-token / 300-frame prompt cached, steady windows of 28 codec "
+                         "tokens (50 mel frames) through the flow encoder, the solve, HiFT on 58 frames, glue and the "
+                         "device-to-host copy; the no_encoder figures pass 50-frame mu windows; stage times are means of "
+                         "profiled calls")
+    return out
+
+
+def flow_workload(args, enc) -> dict:
+    """The flow encoder alone on the B=32 workload's streams: 16 prompts of uniform 75-225 tokens (150-450 mel frames,
+    numpy default_rng(2)) set up in one call, advanced through four steady windows (so the caches are trimmed), then
+    one call of 16 windows of 28 tokens (25 + 3 lookahead -> 50 mel frames each) timed on clones of that state (HIP
+    events around the call, host planning included in the wall time)."""
+    n = args.streams
+    rng = np.random.default_rng(2)
+    plen = [int(x) for x in rng.integers(75, 226, size=n)]
+    prompts = [rng.integers(0, 6561, p).tolist() for p in plen]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    states, _, _, _ = enc.setup(prompts)
+    torch.cuda.synchronize()
+    setup_ms = (time.perf_counter() - t0) * 1e3
+    for _ in range(4):
+        enc.encode(states, [rng.integers(0, 6561, 28).tolist() for _ in range(n)], [False] * n)
+    wins = [rng.integers(0, 6561, 28).tolist() for _ in range(n)]
+    walls, gpu = [], []
+    for i in range(args.latency_reps + 3):
+        cl = [enc.clone(s) for s in states]
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a = time.perf_counter()
+        e0.record()
+        enc.encode(cl, wins, [False] * n)
+        e1.record()
+        torch.cuda.synchronize()
+        b = time.perf_counter()
+        for c in cl:
+            enc.release(c)
+        if i >= 3:
+            walls.append(b - a)
+            gpu.append(e0.elapsed_time(e1))
+    keys1 = [s.k1.size + 25 for s in states]
+    keys2 = [s.k2.size + 50 for s in states]
+    for s in states:
+        enc.release(s)
+    return {"streams": n, "prompt_tokens": "uniform 75-225", "setup_ms": setup_ms, "p50_call_ms": float(np.median(walls) * 1e3),
+            "p50_call_gpu_ms": float(np.median(gpu)), "mel_frames_per_s": n * 50 / float(np.median(walls)),
+            "keys_per_stream_stack1": f"{min(keys1)}-{max(keys1)}", "keys_per_stream_stack2": f"{min(keys2)}-{max(keys2)}",
+            "case": "16 windows of 28 codec tokens in one encoder call, caches after 4 windows (trimmed)"}
 
 
 def fp8_workload(args, cfg, model, mus, spks, hift, hsrc, hnoise, bf16_step) -> dict:
