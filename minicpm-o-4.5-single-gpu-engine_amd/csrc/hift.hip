@@ -665,22 +665,36 @@ __global__ void __launch_bounds__(256) f0_head_kernel(const float* x, int C, con
 
 // Frame-rate phase of harmonic h of item i: rad_f = (f0_f (h + 1) / sr) mod 1; phase_f = (sum_{g <= f} rad_g) 2 pi;
 // stored already multiplied by the upsampling scale (the reference's F.interpolate(phase * 480, scale 480) input).
-// One thread per (item, harmonic): the running sum is a sequential fp64 accumulation rounded to fp32 per frame, as
-// torch's CPU cumsum does for fp32.
-__global__ void phase_kernel(const float* f0, const int* fr_off, const int* fr_len, int n_items, int harm, float sr, float scale,
-                             float* phase) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n_items * harm) return;
-  const int it = i / harm, h = i % harm;
+// The running sum is an fp64 accumulation rounded to fp32 per frame, as torch's CPU cumsum does for fp32.  One wave per
+// (item, harmonic) scans 64 frames at a time (shuffle scan, then the carry of the earlier frames): rad values of f0
+// above ~1e-4 Hz are multiples of 2^-38 and the sums stay below the frame count, so fp64 holds every partial sum
+// exactly and the scan equals the sequential sum.
+__global__ void __launch_bounds__(256) phase_kernel(const float* f0, const int* fr_off, const int* fr_len, int n_items, int harm, float sr,
+                                                    float scale, float* phase) {
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (w >= n_items * harm) return;
+  const int it = w / harm, h = w % harm;
   const int o = fr_off[it], T = fr_len[it];
   const float mult = (float)(h + 1);
-  double cum = 0.0;
-  for (int f = 0; f < T; ++f) {
-    const float fn = __fmul_rn(f0[o + f], mult);
-    const float rad = fmodf(__fdiv_rn(fn, sr), 1.0f);
-    cum += (double)rad;
-    const float ph = __fmul_rn(__fmul_rn((float)cum, 2.0f), 3.14159265358979323846f);
-    phase[(size_t)(o + f) * harm + h] = __fmul_rn(ph, scale);
+  double carry = 0.0;
+  for (int b = 0; b < T; b += 64) {
+    const int f = b + lane;
+    double r = 0.0;
+    if (f < T) {
+      const float fn = __fmul_rn(f0[o + f], mult);
+      r = (double)fmodf(__fdiv_rn(fn, sr), 1.0f);
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const double t = __shfl_up(r, d, 64);
+      if (lane >= d) r += t;
+    }
+    const double cum = carry + r;
+    if (f < T) {
+      const float ph = __fmul_rn(__fmul_rn((float)cum, 2.0f), 3.14159265358979323846f);
+      phase[(size_t)(o + f) * harm + h] = __fmul_rn(ph, scale);
+    }
+    carry = __shfl(cum, 63, 64);
   }
 }
 
@@ -753,43 +767,64 @@ __global__ void stft_kernel(const float* s, const int* smp_off, const int* smp_l
   }
 }
 
-// ISTFT (``istft_overlap_add``): per output sample, the inverse real FFT values of the <= 4 overlapping frames (mag =
-// min(exp(x_re), 100), phase = sin(x_im), spectrum mag (cos phase, sin phase)), windowed, summed, divided by the summed
-// squared window; n_fft / 2 trimmed at both ends; clamped to +-limit.
-__global__ void istft_kernel(const float* x, const int* fr_off, const int* fr_len, const int* smp_off, const float* win, float limit,
-                             float* out) {
+// ISTFT (``istft_overlap_add``): mag = min(exp(x_re), 100), phase = sin(x_im), spectrum mag (cos phase, sin phase);
+// inverse real FFT of each frame, windowed, overlap-added, divided by the summed squared window; n_fft / 2 trimmed at
+// both ends; clamped to +-limit.  A block takes IST_F consecutive frames: each thread computes one frame's 16 inverse-FFT
+// values once (into LDS), then the block writes the 4 (IST_F - 3) samples those frames cover completely, each the sum
+// over its <= 4 frames in frame order.
+constexpr int IST_F = 256;
+__global__ void __launch_bounds__(256) istft_kernel(const float* x, const int* fr_off, const int* fr_len, const int* smp_off, const float* win,
+                                                    float limit, float* out) {
+  __shared__ float ys[IST_F * 17];  // frame t of the block, value i at t * 17 + i (already times 1 / 16)
   const int it = blockIdx.y;
   const int F = fr_len[it];
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  const int ns = (F - 1) * 4;
-  if (n >= ns) return;
-  const int p = n + 8;
-  int fa = (p - 15 + 3) / 4;
-  if (p - 15 < 0) fa = 0;
-  int fb = p / 4;
-  if (fb > F - 1) fb = F - 1;
-  float y = 0.f, env = 0.f;
-  for (int f = fa; f <= fb; ++f) {
-    const int i = p - 4 * f;
-    const float* xf = x + (size_t)(fr_off[it] + f) * 18;
-    // irfft at index i: (1/16) [X0 + (-1)^i X8 + 2 sum_{k=1..7} (Re X_k cos(2 pi k i / 16) - Im X_k sin(2 pi k i / 16))]
-    float acc = 0.f;
+  const int B0 = blockIdx.x * (IST_F - 3);
+  if (B0 >= F) return;
+  const int t = threadIdx.x;
+  if (B0 + t < F) {
+    const float* xf = x + (size_t)(fr_off[it] + B0 + t) * 18;
+    float re[9], im[9];
 #pragma unroll
     for (int k = 0; k < 9; ++k) {
       const float mag = fminf(expf(xf[k]), 100.0f);
       const float ph = sinf(xf[9 + k]);
-      const float re = __fmul_rn(mag, cosf(ph)), im = __fmul_rn(mag, sinf(ph));
-      const float c = kCos16[(k * i) & 15], s = kSin16[(k * i) & 15];
-      // the imaginary parts of DC and Nyquist are ignored
-      acc += (k == 0 || k == 8) ? re * c : 2.0f * (re * c - im * s);
+      re[k] = __fmul_rn(mag, cosf(ph));
+      im[k] = __fmul_rn(mag, sinf(ph));
     }
-    const float w = win[i];
-    y = fmaf(acc * (1.0f / 16.0f), w, y);
-    env = fmaf(w, w, env);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      // irfft at index i: (1/16) [X0 + (-1)^i X8 + 2 sum_{k=1..7} (Re X_k cos(2 pi k i / 16) - Im X_k sin(2 pi k i / 16))]
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < 9; ++k) {
+        const float c = kCos16[(k * i) & 15], s = kSin16[(k * i) & 15];
+        // the imaginary parts of DC and Nyquist are ignored
+        acc += (k == 0 || k == 8) ? re[k] * c : 2.0f * (re[k] * c - im[k] * s);
+      }
+      ys[t * 17 + i] = acc * (1.0f / 16.0f);
+    }
   }
-  float v = y / env;
-  v = fminf(fmaxf(v, -limit), limit);
-  out[smp_off[it] + n] = v;
+  __syncthreads();
+  // padded sample p (output n = p - 8) sees frames ceil((p - 15) / 4) .. p / 4; this block's frames cover
+  // p in [4 B0 + 12, 4 (B0 + IST_F - 3) + 12) (block 0 from p = 8), and outputs end at p = 4 F + 4
+  const int p_lo = B0 == 0 ? 8 : 4 * B0 + 12;
+  const int p_hi = min(4 * (B0 + IST_F - 3) + 12, 4 * F + 4);
+  for (int p = p_lo + t; p < p_hi; p += blockDim.x) {
+    int fa = (p - 15 + 3) / 4;
+    if (p - 15 < 0) fa = 0;
+    int fb = p / 4;
+    if (fb > F - 1) fb = F - 1;
+    float y = 0.f, env = 0.f;
+    for (int f = fa; f <= fb; ++f) {
+      const int i = p - 4 * f;
+      const float w = win[i];
+      y = fmaf(ys[(f - B0) * 17 + i], w, y);
+      env = fmaf(w, w, env);
+    }
+    float v = y / env;
+    v = fminf(fmaxf(v, -limit), limit);
+    out[smp_off[it] + p - 8] = v;
+  }
 }
 
 // rows 1.. of each item's ups output were written one row down; row 0 = input row 1 (ReflectionPad1d((1, 0)))
@@ -880,7 +915,7 @@ hipError_t f0_head(const float* x, int C, const float* w, const float* b, float*
 
 hipError_t nsf_phase(const float* f0, const int* fr_off, const int* fr_len, int n_items, int harm, float sr, float scale, float* phase,
                      hipStream_t st) {
-  hipLaunchKernelGGL(phase_kernel, dim3(cdiv(n_items * harm, 64)), dim3(64), 0, st, f0, fr_off, fr_len, n_items, harm, sr, scale, phase);
+  hipLaunchKernelGGL(phase_kernel, dim3(cdiv(n_items * harm, 4)), dim3(256), 0, st, f0, fr_off, fr_len, n_items, harm, sr, scale, phase);
   return hipGetLastError();
 }
 
@@ -901,7 +936,8 @@ hipError_t stft16(const float* s, const int* smp_off, const int* smp_len, const 
 
 hipError_t istft16(const float* x, const int* fr_off, const int* fr_len, const int* smp_off, int n_items, int max_smp, const float* win,
                    float limit, float* out, hipStream_t st) {
-  hipLaunchKernelGGL(istft_kernel, dim3(cdiv(max_smp, 256), n_items), dim3(256), 0, st, x, fr_off, fr_len, smp_off, win, limit, out);
+  const int max_fr = max_smp / 4 + 1;  // an item of F frames has (F - 1) 4 samples
+  hipLaunchKernelGGL(istft_kernel, dim3(cdiv(max_fr, IST_F - 3), n_items), dim3(256), 0, st, x, fr_off, fr_len, smp_off, win, limit, out);
   return hipGetLastError();
 }
 
