@@ -12,7 +12,6 @@ namespace t2w {
 
 namespace {
 
-constexpr int CBM = 64, CBN = 64, CBK = 16, CLD = CBK + 1;  // LDS rows padded to 17 floats
 
 // exact twiddles of the 16-point DFT: cos / sin(2 pi m / 16)
 __constant__ float kCos16[16] = {1.0f, 0.923879533f, 0.707106781f, 0.382683432f, 0.0f, -0.382683432f, -0.707106781f, -0.923879533f,
@@ -57,61 +56,245 @@ __device__ __forceinline__ void conv_epilogue(const ConvDesc& c, int b, int out_
   }
 }
 
+// fp32 implicit-GEMM convolution (v_mfma_f32_32x32x2f32) for the convs the reference keeps in strict fp32 (f0
+// predictor, conv_pre, the first upsampling stage, conv_post, the source downsampling convs).  A workgroup of 4 waves
+// owns 128 output rows x 32 WN output channels (waves WM x WN, WM = 4 / WN: 32 WN channels and 128 / WM rows each).
+// K runs in stages of 32 values: the activation rows of the stage (activation applied) and its weights are
+// loaded into registers one stage ahead (16-byte loads where rows and channels allow: eight lanes per 128-byte row
+// segment), stored k-major to one of two LDS buffers, one barrier per stage.  MFMA roles as in the bf16 kernels: the
+// weights are the A operand (32 output channels), the activations the B operand (32 output rows).
+constexpr int F_BM = 128, F_BK = 32, F_AS = F_BM + 4;  // LDS row strides padded by 4 floats (2-way bank conflicts at most)
+
+template <int WN, bool FLAT>
 __global__ void __launch_bounds__(256) conv_f32_kernel(ConvDesc c) {
-  __shared__ float xs[CBM * CLD];
-  __shared__ float ws[CBN * CLD];
+  constexpr int BN = 32 * WN, WM = 4 / WN, WTM = F_BM / WM, TM = WTM / 32, BS = BN + 4;
+  constexpr int AV = F_BM * F_BK / 4 / 256, BV = BN * F_BK / 4 / 256;  // float4 loads per thread and stage
+  static_assert(AV >= 1 && BV >= 1, "load layout");
+  __shared__ float As[2][F_BK * F_AS];  // [k][row]
+  __shared__ float Bs[2][F_BK * BS];    // [k][co]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
   const int Tin = c.in_len[b], Tout = c.out_len[b];
   const int oo = c.off_out[ph];
   // output rows r with 0 <= r * s_out + oo < Tout
   const int r_lo = oo >= 0 ? 0 : (-oo + c.s_out - 1) / c.s_out;
   const int r_hi = Tout - 1 - oo < 0 ? -1 : (Tout - 1 - oo) / c.s_out;
-  const int r0 = r_lo + blockIdx.x * CBM;
+  const int r0 = r_lo + blockIdx.x * F_BM;
   if (r0 > r_hi) return;
-  const int co0 = blockIdx.y * CBN;
-  const float* xb = c.x + (size_t)c.in_off[b] * c.ldx;
-  const float* wph = c.w + (size_t)ph * c.Cout * c.taps * c.Cin;
-
-  f32x16 acc;
+  const int co0 = blockIdx.y * BN;
+  // the fields the loaders use, as locals (indexing the argument struct inside the lambdas put it in scratch memory)
+  const int Cin = c.Cin, Cout = c.Cout, taps = c.taps, s_in = c.s_in, d_in = c.d_in, ldx = c.ldx, off = c.off_in[ph], pre = c.pre;
+  const float slope = c.slope;
+  const float* alpha = c.alpha;
+  const float* inv = c.inv;
+  const float* xb = c.x + (size_t)c.in_off[b] * ldx;
+  const float* wph = c.w + (size_t)ph * Cout * taps * Cin;
+  // K index k = j Cin + ci.  Undilated convs whose Cin is not a multiple of 32 run it flat in chunks of 32 across tap
+  // boundaries (tap j + 1's rows follow tap j's, so a chunk is contiguous per output row and a narrow Cin wastes no K);
+  // the others by (tap, 32-channel chunk).
+  constexpr bool flat = FLAT;
+  const int nck = (Cin + F_BK - 1) / F_BK, KT = taps * Cin;
+  const int S = flat ? (KT + F_BK - 1) / F_BK : taps * nck;
+  const bool vec_x = ldx % 4 == 0, vec_w = Cin % 4 == 0;
+  // loader role: row / channel lr + 32 i, K values 4 lf .. 4 lf + 3 of the stage
+  const int lr = tid >> 3, lf = tid & 7;
+  // flat mode: (tap, channel) of this thread's four K values of stage s (one division per stage); ci = Cin marks a value
+  // past K
+  auto kdec = [&](int s, int (&jj)[4], int (&cc)[4]) {
+    const int k0 = s * F_BK, j0 = k0 / Cin, ci0 = k0 - j0 * Cin + 4 * lf;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    for (int e = 0; e < 4; ++e) {
+      int j = j0, ci = ci0 + e;
+      while (ci >= Cin) { ci -= Cin; ++j; }  // at most 32 / Cin + 1 steps
+      if (j >= taps) { j = 0; ci = Cin; }
+      jj[e] = j;
+      cc[e] = ci;
+    }
+  };
 
-  // staging assignment: 4 consecutive K values of one row per thread
-  const int lrow = tid >> 2, lk = (tid & 3) * 4;
-  for (int j = 0; j < c.taps; ++j) {
-    const int rr = r0 + lrow;
-    const int in_row = rr * c.s_in + j * c.d_in + c.off_in[ph];
-    const bool rok = rr <= r_hi && in_row >= 0 && in_row < Tin;
-    const int co = co0 + lrow;
-    for (int k0 = 0; k0 < c.Cin; k0 += CBK) {
+  float4 ra[AV], rb[BV];
+  // regular K order (tap, 32-channel chunk): one tap and a run of channels per thread and stage
+  auto load_chunk = [&](int s) __attribute__((always_inline)) {
+    const int j = s / nck, ci = (s - j * nck) * F_BK + 4 * lf;
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      const int row = r0 + lr + 32 * i;
+      const int in_row = row * s_in + j * d_in + off;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (row <= r_hi && in_row >= 0 && in_row < Tin) {
+        const float* p = xb + (size_t)in_row * ldx + ci;
+        if (vec_x && ci + 4 <= Cin) {
+          v = *(const float4*)p;
+        } else {
+          if (ci < Cin) v.x = p[0];
+          if (ci + 1 < Cin) v.y = p[1];
+          if (ci + 2 < Cin) v.z = p[2];
+          if (ci + 3 < Cin) v.w = p[3];
+        }
+      }
+      ra[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      const int co = co0 + lr + 32 * i;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (co < Cout) {
+        const float* p = wph + ((size_t)co * taps + j) * Cin + ci;
+        if (vec_w && ci + 4 <= Cin) {
+          v = *(const float4*)p;
+        } else {
+          if (ci < Cin) v.x = p[0];
+          if (ci + 1 < Cin) v.y = p[1];
+          if (ci + 2 < Cin) v.z = p[2];
+          if (ci + 3 < Cin) v.w = p[3];
+        }
+      }
+      rb[i] = v;
+    }
+  };
+  auto store_chunk = [&](int s, int buf) __attribute__((always_inline)) {
+    const int j = s / nck, ci = (s - j * nck) * F_BK + 4 * lf;
+    float al[4] = {0.f, 0.f, 0.f, 0.f}, iv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (pre == PRE_SNAKE) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (ci + e < Cin) { al[e] = alpha[ci + e]; iv[e] = inv[ci + e]; }
+    }
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      const int rl = lr + 32 * i;
+      const int row = r0 + rl, in_row = row * s_in + j * d_in + off;
+      const bool ok = row <= r_hi && in_row >= 0 && in_row < Tin;
+      const float v[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int ci = k0 + lk + e;
-        float v = 0.f;
-        if (rok && ci < c.Cin) {
-          v = xb[(size_t)in_row * c.ldx + ci];
-          if (c.pre) v = pre_act(v, c.pre, c.slope, c.alpha ? c.alpha[ci] : 0.f, c.inv ? c.inv[ci] : 0.f);
-        }
-        xs[lrow * CLD + lk + e] = v;
-        ws[lrow * CLD + lk + e] = (co < c.Cout && ci < c.Cin) ? wph[((size_t)co * c.taps + j) * c.Cin + ci] : 0.f;
+        const float x = (pre && ok && ci + e < Cin) ? pre_act(v[e], pre, slope, al[e], iv[e]) : v[e];
+        As[buf][(4 * lf + e) * F_AS + rl] = x;
       }
-      __syncthreads();
-#pragma unroll
-      for (int kk = 0; kk < CBK / 2; ++kk) {
-        const float a = ws[(wn * 32 + (lane & 31)) * CLD + 2 * kk + (lane >> 5)];
-        const float bb = xs[(wm * 32 + (lane & 31)) * CLD + 2 * kk + (lane >> 5)];
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, acc, 0, 0, 0);
-      }
-      __syncthreads();
     }
-  }
-  const int r = r0 + wm * 32 + (lane & 31);
-  if (r > r_hi) return;
-  conv_epilogue(c, b, r * c.s_out + oo, co0 + wn * 32, lane, acc);
-}
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      const int cl = lr + 32 * i;
+      Bs[buf][(4 * lf + 0) * BS + cl] = rb[i].x;
+      Bs[buf][(4 * lf + 1) * BS + cl] = rb[i].y;
+      Bs[buf][(4 * lf + 2) * BS + cl] = rb[i].z;
+      Bs[buf][(4 * lf + 3) * BS + cl] = rb[i].w;
+    }
+  };
+  // flat K order: each of a thread's four K values has its own (tap, channel)
+  auto load_flat = [&](int s) __attribute__((always_inline)) {
+    int jj[4], cc[4];
+    kdec(s, jj, cc);
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      const int row = r0 + lr + 32 * i;
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      if (row <= r_hi) {
+        const int base = row * s_in + off;
+        if (vec_x && vec_w && cc[0] + 4 <= Cin) {  // Cin % 4 == 0: the four values share a tap
+          const int in_row = base + jj[0];
+          if (in_row >= 0 && in_row < Tin) {
+            const float4 q = *(const float4*)(xb + (size_t)in_row * ldx + cc[0]);
+            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int in_row = base + jj[e];
+            if (cc[e] < Cin && in_row >= 0 && in_row < Tin) v[e] = xb[(size_t)in_row * ldx + cc[e]];
+          }
+        }
+      }
+      ra[i] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      const int co = co0 + lr + 32 * i;
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      if (co < Cout) {
+        const float* p = wph + (size_t)co * KT;
+        if (vec_w && cc[0] + 4 <= Cin) {
+          const float4 q = *(const float4*)(p + jj[0] * Cin + cc[0]);
+          v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (cc[e] < Cin) v[e] = p[jj[e] * Cin + cc[e]];
+        }
+      }
+      rb[i] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  };
+  auto store_flat = [&](int s, int buf) __attribute__((always_inline)) {
+    int jj[4], cc[4];
+    kdec(s, jj, cc);
+    float al[4] = {0.f, 0.f, 0.f, 0.f}, iv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (pre == PRE_SNAKE) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (cc[e] < Cin) { al[e] = alpha[cc[e]]; iv[e] = inv[cc[e]]; }
+    }
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      const int rl = lr + 32 * i;
+      const int row = r0 + rl, base = row * s_in + off;
+      const float v[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int in_row = base + jj[e];
+        const bool ok = row <= r_hi && in_row >= 0 && in_row < Tin && cc[e] < Cin;
+        As[buf][(4 * lf + e) * F_AS + rl] = (pre && ok) ? pre_act(v[e], pre, slope, al[e], iv[e]) : v[e];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      const int cl = lr + 32 * i;
+      Bs[buf][(4 * lf + 0) * BS + cl] = rb[i].x;
+      Bs[buf][(4 * lf + 1) * BS + cl] = rb[i].y;
+      Bs[buf][(4 * lf + 2) * BS + cl] = rb[i].z;
+      Bs[buf][(4 * lf + 3) * BS + cl] = rb[i].w;
+    }
+  };
+  auto load = [&](int s) __attribute__((always_inline)) {
+    if constexpr (FLAT) load_flat(s);
+    else load_chunk(s);
+  };
+  auto store = [&](int s, int buf) __attribute__((always_inline)) {
+    if constexpr (FLAT) store_flat(s, buf);
+    else store_chunk(s, buf);
+  };
 
+  f32x16 acc[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  load(0);
+  store(0, 0);
+  __syncthreads();
+  for (int s = 0; s < S; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < S) load(s + 1);
+    const float* A = As[buf];
+    const float* B = Bs[buf];
+#pragma unroll
+    for (int kk = 0; kk < F_BK / 2; ++kk) {
+      const int k = 2 * kk + (lane >> 5);
+      const float w = B[k * BS + wn * 32 + (lane & 31)];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(w, A[k * F_AS + wm * WTM + i * 32 + (lane & 31)], acc[i], 0, 0, 0);
+    }
+    if (s + 1 < S) store(s + 1, buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int r = r0 + wm * WTM + i * 32 + (lane & 31);
+    if (r <= r_hi) conv_epilogue(c, b, r * c.s_out + oo, co0 + wn * 32, lane, acc[i]);
+  }
+}
 
 // bf16-MFMA convolution (fp32 activations in HBM, bf16 operands, fp32 accumulation) for stride-1 convs and the
 // polyphase transposed convs.  A workgroup owns BM output rows x 64 output channels; its four waves own BM / 4 rows
@@ -844,7 +1027,7 @@ hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
   if (c.n_items <= 0 || max_rows <= 0) return hipSuccess;
   if (c.n_phase < 1 || c.n_phase > 8) return hipErrorInvalidValue;
   // grids that would keep fewer than half the CUs busy: 32-row tiles with the taps and channels split over the waves
-  const long tiles = (long)cdiv(max_rows, CBM) * cdiv(c.Cout, CBN) * c.n_items * c.n_phase;
+  const long tiles = (long)cdiv(max_rows, 64) * cdiv(c.Cout, 64) * c.n_items * c.n_phase;
   if (tiles < 128) {
     // 32 output channels per workgroup while that grid fits the chip in one round (half the weight bytes each), else 64
     const long t32 = (long)cdiv(max_rows, 32) * cdiv(c.Cout, 32) * c.n_items * c.n_phase;
@@ -857,8 +1040,18 @@ hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
     }
     return hipGetLastError();
   }
-  dim3 grid(cdiv(max_rows, CBM), cdiv(c.Cout, CBN), c.n_items * c.n_phase);
-  hipLaunchKernelGGL(conv_f32_kernel, grid, dim3(256), 0, st, c);
+  // 64 output channels per workgroup, 32 where the output has no more (conv_post's 18)
+  // undilated convs whose Cin is not a multiple of 32 take their K flat
+  const bool flat = c.d_in == 1 && c.Cin % F_BK != 0;
+  if (c.Cout <= 32) {
+    dim3 grid(cdiv(max_rows, F_BM), 1, c.n_items * c.n_phase);
+    if (flat) hipLaunchKernelGGL((conv_f32_kernel<1, true>), grid, dim3(256), 0, st, c);
+    else hipLaunchKernelGGL((conv_f32_kernel<1, false>), grid, dim3(256), 0, st, c);
+  } else {
+    dim3 grid(cdiv(max_rows, F_BM), cdiv(c.Cout, 64), c.n_items * c.n_phase);
+    if (flat) hipLaunchKernelGGL((conv_f32_kernel<2, true>), grid, dim3(256), 0, st, c);
+    else hipLaunchKernelGGL((conv_f32_kernel<2, false>), grid, dim3(256), 0, st, c);
+  }
   return hipGetLastError();
 }
 
