@@ -303,9 +303,11 @@ int t2w_hift_forward(const t2w_hift* h, int n_items, const int* frames, const in
                      const float* noise, const float* cache_source, int S, const float* f0_override,
                      const float* source_override, float* speech, float* source, float* f0_out, void* workspace,
                      size_t workspace_bytes, int decode_bf16, void* stream);
-/* decode_bf16: the decoder's stride-1 and transposed convs (conv_pre, upsampling, ResBlocks, conv_post) on bf16 MFMA
- * with fp32 activations and accumulation; the f0 predictor, the NSF source, the source downsampling convs, STFT and ISTFT
- * stay fp32. */
+/* decode_bf16: nonzero puts the decoder's stride-1 and transposed convs (conv_pre, upsampling, ResBlocks, conv_post) on
+ * bf16 MFMA with fp32 activations and accumulation; the f0 predictor, the NSF source, the source downsampling convs, STFT
+ * and ISTFT stay fp32.  Its value picks how a ResBlock dilation's two convs run: 1 as one kernel that keeps the first
+ * conv's output on chip where the call's grid fills the chip (else as two convs), 2 always as two convs, 3 as one kernel
+ * wherever the channel count allows (64, 128 or 256).  The modes give the same result up to the order of fp32 sums. */
 
 /* ---------------------------------------------------------------- graphs (hipGraph capture of a stream) */
 

@@ -571,6 +571,234 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
   }
 }
 
+// One ResBlock dilation in one pass on bf16 MFMA: y = conv2(snake2(conv1(snake1(x)))) + x, both convs C -> C channels
+// with kernel k and zero padding at each item's ends, conv1 dilated by dil (padding dil (k - 1) / 2), conv2 undilated
+// (padding (k - 1) / 2).  A workgroup owns BO = BM1 - (k - 1) output rows and all C channels.  conv1 runs over the BM1
+// rows conv2 reads (its halo included) in 64-channel input chunks staged in LDS as in conv_bf16_kernel; its result,
+// bias and Snake applied, rounded to bf16 and zero outside the item, is written to LDS over the dead input slab (all C
+// channels) and is conv2's input, read with no barrier in conv2's tap loop.  So conv1's output never goes through HBM
+// and the residual is the block's own input rows (L2 hits).  Four waves split the BM1 x C tile into blocks of 128 rows x
+// 64 channels; BM1 = 32768 / C keeps the conv2 slab at 64 KB.  Each output sums its products in the order
+// conv_bf16_kernel does (64-channel chunks, taps, 16-channel steps), and the roundings are the same (conv1 + bias in fp32,
+// Snake, bf16), so the result equals the two-kernel path's.
+constexpr int RP_SPAN = 64;  // conv1's largest tap span (k - 1) dil
+
+template <int C>
+__global__ void __launch_bounds__(256, 2) resblock_pair_kernel(ConvDesc c1, ConvDesc c2) {
+  constexpr int BM1 = 32768 / C, WN = C / 64, WM = 4 / WN, WTM = BM1 / WM, TM = WTM / 32;
+  constexpr int CH = C / 8, MSK = (CH < 16 ? CH : 16) - 1;  // conv2 slab: 16-byte chunks per row; XOR swizzle mask
+  static_assert(WTM == 128 && TM == 4, "waves own 128 rows x 64 channels");
+  constexpr int SU = 4;      // slab rows per thread in flight while staging
+  extern __shared__ uint4 hl[];  // conv1's input slab [BM1 + span][8 chunks]; then conv2's [BM1 + 16][CH]; then the epilogue's
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int b = blockIdx.y;
+  const int T = c1.in_len[b];
+  const int k = c1.taps, dil = c1.d_in;
+  const int h2 = (k - 1) >> 1, BO = BM1 - 2 * h2;
+  const int r0 = blockIdx.x * BO;
+  if (r0 >= T) return;
+  const int t0 = r0 - h2;        // item time of conv2 slab row 0 (conv1 output row)
+  const int u0 = t0 - h2 * dil;  // item time of conv1 slab row 0
+  const int srows = BM1 + (k - 1) * dil;
+  const float* xb = c1.x + (size_t)c1.in_off[b] * C;
+  const bf16_t* w1 = (const bf16_t*)c1.wbf + (size_t)wn * 64 * k * C;
+  const bf16_t* w2 = (const bf16_t*)c2.wbf + (size_t)wn * 64 * k * C;
+  const float* a1 = c1.alpha;
+  const float* iv1 = c1.inv;
+  const int ws = wm * WTM;  // this wave's first tile row
+  // wave-uniform counts of this wave's live 32-row blocks: conv1 rows that conv2 reads for an output row inside the
+  // item, conv2 rows inside the item and the workgroup's BO
+  const int n1 = T - r0 + 2 * h2 - ws, n2 = min(BO, T - r0) - ws;
+  const int live1 = n1 <= 0 ? 0 : min(TM, (n1 + 31) >> 5);
+  const int live2 = n2 <= 0 ? 0 : min(TM, (n2 + 31) >> 5);
+
+  f32x16 acc[TM][2];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // this lane's fragments of tap j, input channels c0 .. c0 + 63: channel rows jj * 32 + lane % 32 of the wave's 64
+  auto load_w = [&](const bf16_t* w, int j, int c0, bf16x8 (&f)[4][2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+        f[kk][jj] = as_bf16x8(*(const uint4*)(w + ((size_t)(jj * 32 + (lane & 31)) * k + j) * C + c0 + kk * 16 + (lane >> 5) * 8));
+  };
+
+  // conv1 over the BM1 rows, one 64-channel input chunk at a time
+  const int sch = tid & 7;
+  for (int c0 = 0; c0 < C; c0 += 64) {
+    __syncthreads();  // the previous chunk's slab is no longer read
+    const int ci = c0 + sch * 8;
+    float al[8], iv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { al[e] = a1[ci + e]; iv[e] = iv1[ci + e]; }
+    for (int sr0 = tid >> 3; sr0 < srows; sr0 += 32 * SU) {
+      float4 u[SU][2];
+      bool in[SU];
+#pragma unroll
+      for (int x = 0; x < SU; ++x) {
+        const int sr = sr0 + 32 * x, t = u0 + sr;
+        in[x] = sr < srows && t >= 0 && t < T;
+        if (in[x]) {
+          u[x][0] = *(const float4*)(xb + (size_t)t * C + ci);
+          u[x][1] = *(const float4*)(xb + (size_t)t * C + ci + 4);
+        }
+      }
+#pragma unroll
+      for (int x = 0; x < SU; ++x) {
+        const int sr = sr0 + 32 * x;
+        if (sr >= srows) break;
+        uint4 o = make_uint4(0u, 0u, 0u, 0u);
+        if (in[x]) {
+          float v[8] = {u[x][0].x, u[x][0].y, u[x][0].z, u[x][0].w, u[x][1].x, u[x][1].y, u[x][1].z, u[x][1].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = pre_fast(v[e], PRE_SNAKE, 0.f, al[e], iv[e]);
+          o = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+        }
+        hl[hswz(sr, sch)] = o;
+      }
+    }
+    bf16x8 wa[4][2], wb[4][2];
+    load_w(w1, 0, c0, wa);
+    __syncthreads();
+    for (int j = 0; j < k; ++j) {
+      if (j + 1 < k) load_w(w1, j + 1, c0, wb);
+      const int shift = j * dil;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int chunk = kk * 2 + (lane >> 5);
+        bf16x8 af[TM];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(hl[hswz(ws + i * 32 + (lane & 31) + shift, chunk)]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          if (i >= live1) break;
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[kk][jj], af[i], acc[i][jj], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) wa[kk][jj] = wb[kk][jj];
+    }
+  }
+
+  // conv1's output to the conv2 slab: row s, 16-byte chunk c at s * CH + (c ^ (s & MSK)); this lane holds row
+  // ws + i * 32 + lane % 32 and, per (jj, q), the four channels wn * 64 + jj * 32 + q * 8 + (lane / 32) * 4 ..
+  __syncthreads();  // every wave is done with conv1's slab
+  {
+    uint2* s2 = (uint2*)hl;
+    const float* b1 = c1.bias;
+    const float* a2 = c2.alpha;
+    const float* iv2 = c2.inv;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int ch = wn * 64 + jj * 32 + q * 8 + (lane >> 5) * 4;
+        const float4 bb = *(const float4*)(b1 + ch), aa = *(const float4*)(a2 + ch), ii = *(const float4*)(iv2 + ch);
+        const int chunk = wn * 8 + jj * 4 + q;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          if (i >= live1) break;
+          const int s = ws + i * 32 + (lane & 31), t = t0 + s;
+          float v[4] = {__fadd_rn(acc[i][jj][q * 4], bb.x), __fadd_rn(acc[i][jj][q * 4 + 1], bb.y),
+                        __fadd_rn(acc[i][jj][q * 4 + 2], bb.z), __fadd_rn(acc[i][jj][q * 4 + 3], bb.w)};
+          v[0] = pre_fast(v[0], PRE_SNAKE, 0.f, aa.x, ii.x);
+          v[1] = pre_fast(v[1], PRE_SNAKE, 0.f, aa.y, ii.y);
+          v[2] = pre_fast(v[2], PRE_SNAKE, 0.f, aa.z, ii.z);
+          v[3] = pre_fast(v[3], PRE_SNAKE, 0.f, aa.w, ii.w);
+          const bool inside = t >= 0 && t < T;
+          s2[(s * CH + (chunk ^ (s & MSK))) * 2 + (lane >> 5)] = inside ? make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3])) : make_uint2(0u, 0u);
+        }
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  __syncthreads();
+
+  // conv2: output row o reads conv2 slab rows o .. o + k - 1; the (chunk, tap) steps in conv_bf16_kernel's order, the
+  // next step's weights loaded while this step's MFMAs run
+  {
+    bf16x8 wa[4][2], wb[4][2];
+    load_w(w2, 0, 0, wa);
+    const int steps = (C / 64) * k;
+    for (int sidx = 0, c0 = 0, j = 0; sidx < steps; ++sidx) {
+      const int nj = j + 1 == k ? 0 : j + 1, nc0 = j + 1 == k ? c0 + 64 : c0;
+      if (sidx + 1 < steps) load_w(w2, nj, nc0, wb);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int chunk = (c0 >> 3) + kk * 2 + (lane >> 5);
+        bf16x8 af[TM];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int s = ws + i * 32 + (lane & 31) + j;
+          af[i] = as_bf16x8(hl[s * CH + (chunk ^ (s & MSK))]);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          if (i >= live2) break;
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[kk][jj], af[i], acc[i][jj], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) wa[kk][jj] = wb[kk][jj];
+      j = nj;
+      c0 = nc0;
+    }
+  }
+
+  // epilogue as in conv_bf16_kernel: bias, residual (the input rows), and the output / running-mean update
+  __syncthreads();  // every wave is done with the conv2 slab
+  float4* st = (float4*)hl + wave * (32 * 16);
+  const int co0 = wn * 64;
+  const int r_end = min(r0 + BO, T);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    if (i >= live2) break;
+    const int t = lane & 31;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c4 = jj * 8 + q * 2 + (lane >> 5);
+        st[t * 16 + (c4 ^ (t & 15))] = make_float4(acc[i][jj][q * 4], acc[i][jj][q * 4 + 1], acc[i][jj][q * 4 + 2], acc[i][jj][q * 4 + 3]);
+      }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int c4 = lane & 15;
+    float4 vv4[8], rr4[8], tt4[8];
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int row = rr * 4 + (lane >> 4);
+      const int r = r0 + ws + i * 32 + row;
+      vv4[rr] = st[row * 16 + (c4 ^ (row & 15))];
+      rr4[rr] = tt4[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (r < r_end) conv_epilogue4_loads(c2, (size_t)c2.out_off[b] + (size_t)r, co0 + c4 * 4, rr4[rr], tt4[rr]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int row = rr * 4 + (lane >> 4);
+      const int r = r0 + ws + i * 32 + row;
+      if (r < r_end) conv_epilogue4_pre(c2, (size_t)c2.out_off[b] + (size_t)r, co0 + c4 * 4, vv4[rr], rr4[rr], tt4[rr]);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+}
+
 // Small grids (a streaming window: one item of a few thousand samples) leave most CUs idle with whole-slab tiles, and
 // each tile's tap loop is a chain of weight-load latencies.  Here a workgroup of CS_WAVES waves owns 32 output rows x
 // NB * 32 output channels and splits the (tap, 64-channel input chunk) steps over its waves, the next step's loads
@@ -1098,6 +1326,52 @@ hipError_t conv_bf16(const ConvDesc& c, const bf16_t* wbf, int max_rows, hipStre
     hipLaunchKernelGGL(conv_bf16_kernel<BM>, grid, dim3(256), lds, st, c, wbf);
   }
   return hipGetLastError();
+}
+
+namespace {
+size_t resblock_pair_lds(int C) {
+  const int BM1 = 32768 / C;
+  const size_t s1 = (size_t)(BM1 + RP_SPAN) * 8 * sizeof(uint4), s2 = (size_t)(BM1 + 16) * C * sizeof(bf16_t);
+  const size_t epi = 4 * 32 * 16 * sizeof(float4);
+  return std::max(std::max(s1, s2), epi);
+}
+
+template <int C>
+hipError_t launch_pair(const ConvDesc& c1, const ConvDesc& c2, int max_rows, hipStream_t st) {
+  const size_t lds = resblock_pair_lds(C);
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)resblock_pair_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  dim3 grid(cdiv(max_rows, resblock_pair_rows(C, c1.taps)), c1.n_items);
+  hipLaunchKernelGGL(resblock_pair_kernel<C>, grid, dim3(256), lds, st, c1, c2);
+  return hipGetLastError();
+}
+}  // namespace
+
+int resblock_pair_rows(int C, int k) { return 32768 / C - (k - 1); }
+
+bool resblock_pair_fits(int C, int k, int dil) {
+  return (C == 64 || C == 128 || C == 256) && k >= 1 && (k & 1) && dil >= 1 && (k - 1) * dil <= RP_SPAN;
+}
+
+hipError_t resblock_pair_bf16(const ConvDesc& c1, const ConvDesc& c2, int max_rows, hipStream_t st) {
+  if (c1.n_items <= 0 || max_rows <= 0) return hipSuccess;
+  const int C = c1.Cin, k = c1.taps;
+  const bool same = c1.Cout == C && c2.Cin == C && c2.Cout == C && c2.taps == k && c1.ldx == C && c1.ldy == C && c2.ldx == C &&
+                    c2.ldy == C && c1.n_items == c2.n_items && c1.in_off == c2.out_off && c1.in_len == c2.out_len;
+  const bool geom = c1.s_in == 1 && c2.s_in == 1 && c1.s_out == 1 && c2.s_out == 1 && c1.n_phase == 1 && c2.n_phase == 1 &&
+                    c2.d_in == 1 && c1.off_in[0] == -c1.d_in * ((k - 1) / 2) && c2.off_in[0] == -((k - 1) / 2) &&
+                    c1.off_out[0] == 0 && c2.off_out[0] == 0;
+  const bool acts = c1.pre == PRE_SNAKE && c2.pre == PRE_SNAKE && c1.epi == EPI_STORE && c2.res == c1.x &&
+                    (c2.epi == EPI_RES || c2.epi == EPI_ADD_RES || c2.epi == EPI_RES_MEAN);
+  if (!same || !geom || !acts || !resblock_pair_fits(C, k, c1.d_in) || !c1.wbf || !c2.wbf) return hipErrorInvalidValue;
+  if (c2.y == c1.x || (c2.epi == EPI_RES_MEAN && c2.sum == c1.x)) return hipErrorInvalidValue;  // halo rows of x are read by other workgroups
+  if (C == 64) return launch_pair<64>(c1, c2, max_rows, st);
+  if (C == 128) return launch_pair<128>(c1, c2, max_rows, st);
+  return launch_pair<256>(c1, c2, max_rows, st);
 }
 
 hipError_t f0_head(const float* x, int C, const float* w, const float* b, float* f0, int rows, hipStream_t st) {

@@ -99,7 +99,8 @@ size_t carve(const t2w_hift* h, const Lens& L, char* base, Bufs* b) {
 
 struct Ctx {
   const t2w_hift* h;
-  bool bf16;
+  bool bf16;       // bf16 MFMA decoder convs
+  int fuse;        // ResBlock dilations as one kernel each: 0 never, 1 where the grid fills the chip, 2 always
   const int* plan;  // device: [class][off | len][n]
   int n;
   Lens L;
@@ -120,6 +121,9 @@ ConvDesc conv_desc(const Ctx& x, const t2w_conv& w, const float* in, int Cin, in
   return c;
 }
 
+// fused ResBlock dilations below this many workgroups leave the chip half idle: two convs with smaller tiles instead
+constexpr long kPairMinBlocks = 128;
+
 int run(const Ctx& x, const ConvDesc& c, int out_cls, const char* what) {
   const int mr = x.L.mx[out_cls] / c.s_out + 2;
   const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
@@ -131,21 +135,29 @@ int run(const Ctx& x, const ConvDesc& c, int out_cls, const char* what) {
 }
 
 // ResBlock on `in` (class cls, C channels): per dilation z = c2(snake(c1(snake(z)))) + z.  The last dilation's output
-// goes to `sum` (mean of the stage's ResBlocks, sum_mode 0 / 1 / 2) or, with add_into, is added into add_into.
+// goes to `sum` (mean of the stage's ResBlocks, sum_mode 0 / 1 / 2) or, with add_into, is added into add_into.  z and tmp
+// are scratch (z may be `in`, which is then overwritten).  A dilation runs as one fused kernel (conv1's output kept in
+// LDS, written to a scratch buffer other than its input) when the bf16 path fuses and the grid fills the chip, else as
+// two convs through a scratch buffer (the second in place when its input is scratch).
 int resblock(const Ctx& x, const t2w_resblock& rb, int k, const float* in, float* z, float* tmp, int C, int cls, float* sum, int sum_mode,
              float* add_into) {
   const t2w_hift_dims& d = x.h->d;
+  const int mr = x.L.mx[cls] + 2;
+  auto other = [&](const float* p) { return p == z ? tmp : z; };  // a scratch buffer that is not p
   const float* cur = in;
   for (int j = 0; j < 3; ++j) {
     const int dil = d.res_dilations[j];
-    ConvDesc c1 = conv_desc(x, rb.c1[j], cur, C, cls, tmp, C, cls, k, dil, 1, dil * (k - 1) / 2);
+    const bool fused = x.bf16 && x.fuse && rb.c1[j].wbf && rb.c2[j].wbf && resblock_pair_fits(C, k, dil) &&
+                       (x.fuse == 2 || (long)((mr + resblock_pair_rows(C, k) - 1) / resblock_pair_rows(C, k)) * x.n >= kPairMinBlocks);
+    float* mid = other(cur);  // conv1's output (two-kernel path)
+    float* out = fused ? other(cur) : (cur == z || cur == tmp ? (float*)cur : other(mid));
+    ConvDesc c1 = conv_desc(x, rb.c1[j], cur, C, cls, mid, C, cls, k, dil, 1, dil * (k - 1) / 2);
     c1.pre = PRE_SNAKE; c1.alpha = rb.a1[j]; c1.inv = rb.inv1[j];
-    if (run(x, c1, cls, "resblock conv1")) return 1;
-    ConvDesc c2 = conv_desc(x, rb.c2[j], tmp, C, cls, z, C, cls, k, 1, 1, (k - 1) / 2);
+    ConvDesc c2 = conv_desc(x, rb.c2[j], fused ? cur : mid, C, cls, out, C, cls, k, 1, 1, (k - 1) / 2);
     c2.pre = PRE_SNAKE; c2.alpha = rb.a2[j]; c2.inv = rb.inv2[j];
     c2.res = cur;
     if (j < 2) {
-      c2.epi = EPI_RES;  // z = conv + res (in place when cur == z: each element is read and written by one thread)
+      c2.epi = EPI_RES;  // out = conv + res (in place when out == cur: each element is read and written by one thread)
     } else if (add_into) {
       c2.epi = EPI_ADD_RES;
       c2.y = add_into;
@@ -155,8 +167,13 @@ int resblock(const Ctx& x, const t2w_resblock& rb, int k, const float* in, float
       c2.sum_mode = sum_mode;
       c2.sum_div = 3;
     }
-    if (run(x, c2, cls, "resblock conv2")) return 1;
-    cur = z;
+    if (fused) {
+      H_CHECK(resblock_pair_bf16(c1, c2, mr, x.st), "resblock pair");
+    } else {
+      if (run(x, c1, cls, "resblock conv1")) return 1;
+      if (run(x, c2, cls, "resblock conv2")) return 1;
+    }
+    cur = out;
   }
   return 0;
 }
@@ -212,7 +229,7 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
                      float* source, float* f0_out, void* workspace, size_t workspace_bytes, int decode_bf16, void* stream) {
   if (!h || n <= 0 || !frames || !plan_dev || !mel || !speech || !source) return t2w::set_error("bad hift arguments", hipSuccess);
   const t2w_hift_dims& d = h->d;
-  Ctx x{h, decode_bf16 != 0, plan_dev, n, lens_of(d, n, frames), (hipStream_t)stream};
+  Ctx x{h, decode_bf16 != 0, decode_bf16 == 1 ? 1 : (decode_bf16 == 3 ? 2 : 0), plan_dev, n, lens_of(d, n, frames), (hipStream_t)stream};
   for (int i = 0; i < n; ++i)
     if (S > class_len(d, C_SMP, frames[i])) return t2w::set_error("source cache longer than a row", hipSuccess);
   if (S > 0 && !cache_source) return t2w::set_error("missing source cache", hipSuccess);

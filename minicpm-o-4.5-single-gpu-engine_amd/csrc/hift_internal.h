@@ -29,6 +29,11 @@ struct ConvDesc {
 hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st);
 // stride-1 / polyphase convs on bf16 MFMA; wbf: bf16 weights [n_phase, Cout padded to 64, taps, Cin padded to 64]
 hipError_t conv_bf16(const ConvDesc& c, const uint16_t* wbf, int max_rows, hipStream_t st);
+// One ResBlock dilation (conv c1 with Snake, conv c2 with Snake and the residual c1.x) in one kernel on bf16 MFMA,
+// conv1's output kept in LDS.  c2 writes y (EPI_RES / EPI_ADD_RES) or the running mean (EPI_RES_MEAN); y must not be x.
+bool resblock_pair_fits(int C, int k, int dil);
+int resblock_pair_rows(int C, int k);  // output rows per workgroup
+hipError_t resblock_pair_bf16(const ConvDesc& c1, const ConvDesc& c2, int max_rows, hipStream_t st);
 hipError_t f0_head(const float* x, int C, const float* w, const float* b, float* f0, int rows, hipStream_t st);
 hipError_t nsf_phase(const float* f0, const int* fr_off, const int* fr_len, int n_items, int harm, float sr, float scale, float* phase,
                      hipStream_t st);

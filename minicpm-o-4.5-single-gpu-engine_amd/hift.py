@@ -30,14 +30,20 @@ REFERENCE_FP32_CONVS = ("conv_pre", "ups.0", "conv_post")
 
 class HiFTModel:
     def __init__(self, W: dict, cfg: HiFTConfig = HiFTConfig(), device: str = "cuda", decode_bf16: bool = False,
-                 use_graphs: bool = False, max_graphs: int = 32, fp32_convs: tuple = ()):
+                 use_graphs: bool = False, max_graphs: int = 32, fp32_convs: tuple = (), resblock_fusion: str = "auto"):
         """``decode_bf16``: the decoder convs on bf16 MFMA (fp32 activations); f0 predictor and source stay fp32.
+        ``resblock_fusion`` (bf16 only): each ResBlock dilation's two convs as one kernel that keeps the first conv's
+        output on chip -- "auto" where the call's grid fills the chip, "on" wherever the channel count allows, "off"
+        never (two convs through a scratch buffer).
         ``fp32_convs``: decoder convs that stay fp32 even then (``REFERENCE_FP32_CONVS``: the reference's split).
         ``use_graphs``: calls without overrides replay one captured graph per (row lengths, source-cache length), the
         role of ``HiFTGraphs`` (``engine/runtime/hift_graph.py:22-88``): inputs are copied into the graph's static
         buffers, outputs are returned as copies; at most ``max_graphs`` graphs are kept (least recently used dropped)."""
         self.cfg, self.device = cfg, device
         self.decode_bf16 = decode_bf16
+        if resblock_fusion not in ("auto", "off", "on"):
+            raise ValueError(f"resblock_fusion must be auto / off / on, not {resblock_fusion!r}")
+        self._mode = {"auto": 1, "off": 2, "on": 3}[resblock_fusion] if decode_bf16 else 0
         self.use_graphs, self.max_graphs = use_graphs, max_graphs
         self.graphs: dict[tuple, dict] = {}
         self.counts = {"graph": 0, "eager": 0}
@@ -160,7 +166,7 @@ class HiFTModel:
         cs = cache_source.contiguous().float() if (cache_source is not None and S > 0) else None
         _lib.check(L.t2w_hift_forward(self.handle, n, fr, plan_dev.data_ptr(), mel_tm.data_ptr(), noise_tm.data_ptr(), _lib.ptr(cs), S,
                                       _lib.ptr(f0_override), _lib.ptr(source_override), speech.data_ptr(), source.data_ptr(), _lib.ptr(f0),
-                                      ws.data_ptr(), ws.numel(), int(self.decode_bf16), _lib.stream_handle()), "hift_forward")
+                                      ws.data_ptr(), ws.numel(), self._mode, _lib.stream_handle()), "hift_forward")
         return speech, source, f0
 
     def _graph(self, frames: list[int], S: int) -> dict:
@@ -190,7 +196,7 @@ class HiFTModel:
             _lib.check(L.t2w_graph_begin(cst), "graph_begin")
             rc = L.t2w_hift_forward(self.handle, n, g["fr"], g["plan"].data_ptr(), g["mel"].data_ptr(), g["noise"].data_ptr(),
                                     _lib.ptr(g["cs"]), S, None, None, g["speech"].data_ptr(), g["source"].data_ptr(), None,
-                                    g["ws"].data_ptr(), g["ws"].numel(), int(self.decode_bf16), cst)
+                                    g["ws"].data_ptr(), g["ws"].numel(), self._mode, cst)
             h = C.c_void_p()
             rc2 = L.t2w_graph_end(cst, C.byref(h))
             _lib.check(rc, "hift_forward (capture)")

@@ -88,11 +88,13 @@ def test_forward_noise_end_to_end_with_cache(dev, case):
     assert e_sp < 1e-2 and e_src < 1e-2
 
 
-def test_decoder_bf16_given_source(dev, case):
+@pytest.mark.parametrize("fusion", ["auto", "on"])
+def test_decoder_bf16_given_source(dev, case, fusion):
     """The bf16-MFMA decoder (fp32 activations and accumulation) against the strict-fp32 oracle on the oracle's source:
-    the reference's reduced-precision HiFT bound, waveform rel-L2 <= 1e-2 (``tests/engine/test_hift_tf32.py:227``)."""
+    the reference's reduced-precision HiFT bound, waveform rel-L2 <= 1e-2 (``tests/engine/test_hift_tf32.py:227``).
+    "on" runs every ResBlock dilation as one kernel (rows of 17 to 123 frames: one to thirty workgroups per row)."""
     W, h, gm, mels, noise = case
-    gb = HiFTModel(W, HiFTConfig(), decode_bf16=True)
+    gb = HiFTModel(W, HiFTConfig(), decode_bf16=True, resblock_fusion=fusion)
     mel_tm, noise_tm = _packed(mels, noise)
     srcs = [oh.source(h, m, torch.zeros(1, 1, 0), ri, nz) for m, (ri, nz) in zip(mels, noise)]
     s_tm = torch.cat([s[0, 0] for s in srcs]).cuda()
@@ -117,11 +119,12 @@ def test_forward_bf16_end_to_end(dev, case):
     assert e < 1e-2
 
 
-def test_forward_bf16_streaming_window(dev, case):
-    """One 50-frame window with a source cache (the per-chunk call of a stream): every decoder conv runs on the
-    small-grid kernels (32 output channels per workgroup where the grid allows)."""
+@pytest.mark.parametrize("fusion", ["auto", "on"])
+def test_forward_bf16_streaming_window(dev, case, fusion):
+    """One 50-frame window with a source cache (the per-chunk call of a stream): with "auto" every decoder conv runs on
+    the small-grid kernels (32 output channels per workgroup where the grid allows); "on" fuses the ResBlock dilations."""
     W, h, gm, mels, noise = case
-    gb = HiFTModel(W, HiFTConfig(), decode_bf16=True)
+    gb = HiFTModel(W, HiFTConfig(), decode_bf16=True, resblock_fusion=fusion)
     g = torch.Generator().manual_seed(12)
     mel = torch.randn(1, 80, 50, generator=g) * 2 - 5
     cs = torch.randn(1, 1, 3840, generator=g) * 0.01
@@ -131,6 +134,32 @@ def test_forward_bf16_streaming_window(dev, case):
     e = rel(sp.cpu(), rsp)
     print("bf16 50-frame window speech rel-L2", e, "source", rel(src.cpu(), rsrc))
     assert e < 1e-2
+
+
+def test_resblock_fusion_equals_two_kernels():
+    """Fused ResBlock dilations (conv1's output kept on chip) against the same dilations as two conv kernels.  On a call
+    large enough for the two-kernel path's whole-slab tiles (eight rows of 150 to 220 frames; "auto" fuses stages 1 and
+    2 and keeps stage 0 as two convs) both sum each output's products in the same order and round at the same points:
+    equal bit for bit.  On rows of 1 to 7 frames (one partial workgroup per row) the two-kernel path's small-grid
+    kernels split the sums over waves, which moves a bf16 rounding now and then (measured rel-L2 1.5e-3)."""
+    W = init_hift(HiFTConfig(), seed=4)
+    g = torch.Generator().manual_seed(4)
+    for lens in ([150, 220, 171, 200, 163, 209, 188, 195], [1, 7, 3, 2]):
+        mel_tm = torch.cat([torch.randn(t, 80, generator=g) * 2 - 5 for t in lens]).cuda()
+        outs = {}
+        for fusion in ("off", "auto", "on"):
+            hm = HiFTModel(W, HiFTConfig(), decode_bf16=True, resblock_fusion=fusion)
+            ri, nz = hm.noise([50 + i for i in range(len(lens))], max(lens) * 480)
+            noise_tm = torch.cat([nz[i, : t * 480] for i, t in enumerate(lens)])
+            sp, src, _ = hm.forward_packed(lens, mel_tm, noise_tm, None, 0)
+            outs[fusion] = sp.cpu()
+            assert torch.isfinite(outs[fusion]).all()
+        e_auto, e_on = rel(outs["auto"], outs["off"]), rel(outs["on"], outs["off"])
+        print("rows", lens, "fused vs two-kernel rel-L2: auto", e_auto, "on", e_on)
+        if max(lens) >= 150:
+            assert torch.equal(outs["auto"], outs["off"]) and torch.equal(outs["on"], outs["off"])
+        else:
+            assert torch.equal(outs["auto"], outs["off"]) and e_on < 5e-3
 
 
 def test_hift_graphs_equal_eager():
