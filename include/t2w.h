@@ -63,6 +63,10 @@ typedef struct {
   const float* mods;                          /* [steps, depth, 9, H]: shift, 1 + scale, gate of msa, mlp, conv */
   const float* final_mods;                    /* [steps, 2, H]: shift, 1 + scale */
   const float* dts;                           /* HOST pointer [steps]: Euler step sizes */
+  const float* rope_freq;                     /* [head_dim / 2] or null.  No counterpart in the reference (its DiT has no
+                                               * positional encoding): rotary embedding of q and k after their
+                                               * LayerNorm, channel pair (2i, 2i + 1) of a head turned by the angle
+                                               * tok_abs * rope_freq[i] (RoFormer); null = none, the reference's DiT */
 } t2w_dit_globals;
 
 /* fp8 copies of a block's six GEMM weights (no counterpart in the reference; its fp8 convention of
@@ -127,6 +131,8 @@ typedef struct {
   void* workspace;
   size_t workspace_bytes;
   int fp8;                  /* 1: the block GEMMs on fp8 MFMA (e4m3 weights, MX fp8 activations; needs fp8 weights) */
+  const int* tok_abs;       /* [n_tok] position of the token in its stream (frames of kept windows before it); read
+                             * only with globals.rope_freq */
 } t2w_solve_args;
 
 /* includes the fp8 activation buffers once the model has fp8 weights */

@@ -30,7 +30,7 @@ class DitBlock(C.Structure):
 
 
 class DitGlobals(C.Structure):
-    _fields_ = [(n, P) for n in ("in_w", "in_b", "out_w", "out_b", "mods", "final_mods")] + [("dts", FP)]
+    _fields_ = [(n, P) for n in ("in_w", "in_b", "out_w", "out_b", "mods", "final_mods")] + [("dts", FP), ("rope_freq", P)]
 
 
 class ModWeights(C.Structure):
@@ -41,7 +41,8 @@ class SolveArgs(C.Structure):
     _fields_ = [(n, I) for n in ("n_tok", "n_rows", "half", "n_tiles", "chunk")] + \
                [(n, P) for n in ("x0", "stat", "in_rows", "out", "tok_row", "tok_pos", "a_src", "new_slot", "row_start", "row_len",
                                  "row_kv_off", "row_kv_len", "conv_rd", "conv_wr", "kv_idx", "tiles", "k_pool", "v_pool")] + \
-               [("pool_layer_stride", C.c_longlong), ("conv_pool", P), ("workspace", P), ("workspace_bytes", C.c_size_t), ("fp8", I)]
+               [("pool_layer_stride", C.c_longlong), ("conv_pool", P), ("workspace", P), ("workspace_bytes", C.c_size_t), ("fp8", I),
+                ("tok_abs", P)]
 
 
 class DitBlockFp8(C.Structure):

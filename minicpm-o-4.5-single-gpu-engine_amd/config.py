@@ -30,6 +30,7 @@ class DiTConfig:
     cfg_rate: float = 0.7    # CausalConditionalCFM.inference_cfg_rate
     steps: int = 10
     noise_frames: int = 50 * 300  # the flow's fixed noise buffer ``rand_noise`` [1, mel, frames]
+    rope_theta: float = 0.0  # > 0: rotary embedding of q and k at stream positions (not in the reference; 0 = off)
 
     @property
     def in_dim(self) -> int:

@@ -238,13 +238,19 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
       pend = Pend();
       gq = gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H, &w);
     }
-    gq.qk = QkvOut{w.q, kp, vp, a->new_slot, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, H};
-    if (gemm_small_fits(gq, EPI_QKV) || (!gemm_splits(gq) && H % 256 == 0)) {
-      // per-head q / k LayerNorm and the key / value scatter in the projection's epilogue
+    gq.qk = QkvOut{w.q, kp, vp, a->new_slot, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, H, m->g.rope_freq, a->tok_abs};
+    const bool small_qkv = gemm_small_fits(gq, EPI_QKV);
+    if (small_qkv || (!gemm_splits(gq) && H % 256 == 0)) {
+      // per-head q / k LayerNorm and the key / value scatter in the projection's epilogue; the small-row kernel also
+      // rotates q and k, the tile kernel leaves that to rope_qk (the sine and cosine would spill its registers)
+      if (!small_qkv) gq.qk.rfreq = nullptr;
       T2W_CHECK(gemm_bf16(gq, EPI_QKV, st), "qkv");
+      if (!small_qkv && m->g.rope_freq) T2W_CHECK(rope_qk(w.q, kp, a->new_slot, a->tok_abs, m->g.rope_freq, N, H, st), "rope");
     } else {
       T2W_CHECK(gemm_bf16(gq, EPI_BF16, st), "qkv");
-      T2W_CHECK(qk_norm_scatter(w.big, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, w.q, kp, vp, a->new_slot, N, d.heads, st), "qk_norm");
+      T2W_CHECK(qk_norm_scatter(w.big, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, w.q, kp, vp, a->new_slot, N, d.heads, st,
+                                m->g.rope_freq, a->tok_abs),
+                "qk_norm");
     }
     AttnArgs at;
     at.q = w.q; at.k_pool = kp; at.v_pool = vp; at.out = w.ao; at.kv_idx = a->kv_idx; at.row_start = a->row_start;
@@ -321,6 +327,7 @@ int check_args(const t2w_dit* m, const t2w_solve_args* a) {
   if (a->fp8 && (m->d.hidden % 128 || m->d.ffn % 128)) return fail("fp8 solve needs hidden and ffn multiples of 128");
   if (a->workspace_bytes < carve(m->d, a->n_tok, a->n_rows, m->fp8_ready(), nullptr, nullptr)) return fail("workspace too small");
   if (a->chunk < 0) return fail("negative chunk");
+  if (m->g.rope_freq && !a->tok_abs) return fail("rotary embedding needs tok_abs (stream positions)");
   return 0;
 }
 

@@ -59,6 +59,21 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// Rotary position embedding (RoFormer, consecutive channel pairs): y[0..NV) holds whole pairs of one head, pair e / 2
+// turning by the angle pos * freq[e / 2] (the fp32 product, then an accurate sine and cosine of it)
+template <int NV>
+__device__ __forceinline__ void rope_rotate(float (&y)[NV], int pos, const float* freq) {
+  static_assert(NV % 2 == 0, "whole channel pairs");
+#pragma unroll
+  for (int e = 0; e < NV; e += 2) {
+    float sn, cs;
+    sincosf((float)pos * freq[e >> 1], &sn, &cs);
+    const float y0 = y[e], y1 = y[e + 1];
+    y[e] = y0 * cs - y1 * sn;
+    y[e + 1] = y0 * sn + y1 * cs;
+  }
+}
+
 // MX fp8: OCP e4m3 values with one power-of-two (E8M0) scale per 32 consecutive K values.  The scale is the smallest
 // power of two that keeps the block's largest magnitude within e4m3's 448, so nothing clips: with amax = 1.m * 2^E and
 // 448 = 1.75 * 2^8, that exponent is E - 8, plus one when 1.m > 1.75.  Returns the unbiased exponent in [-126, 126].

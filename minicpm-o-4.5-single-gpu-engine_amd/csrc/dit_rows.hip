@@ -326,17 +326,20 @@ __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, cons
 }
 
 // Per-head affine LayerNorm of q and k (64 values per head, LPH = 64 / VPL lanes per head), q to its token row, k and
-// v to the token's key slot (the reference's _qk_norm_scatter_kernel, engine/runtime/dit_kernels.py:103-142).
+// v to the token's key slot (the reference's _qk_norm_scatter_kernel, engine/runtime/dit_kernels.py:103-142).  With
+// rfreq, q and k are then rotated at the token's stream position pos[n] (rotary embedding, no reference counterpart).
 template <int VPL>
 __global__ void __launch_bounds__(256) qk_norm_kernel(const bf16_t* qkv, const float* qw, const float* qb, const float* kw,
                                                       const float* kb, float eps, bf16_t* q_out, bf16_t* k_pool,
-                                                      bf16_t* v_pool, const int* slots, int N, int H) {
+                                                      bf16_t* v_pool, const int* slots, int N, int H, const float* rfreq,
+                                                      const int* pos) {
   constexpr int LPH = 64 / VPL;
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (n >= N) return;
   const int c0 = lane * VPL, d0 = c0 & 63;
   const size_t slot = (size_t)slots[n];
+  const int tpos = rfreq ? pos[n] : 0;
   const bf16_t* src = qkv + (size_t)n * 3 * H + c0;
 #pragma unroll
   for (int which = 0; which < 2; ++which) {
@@ -361,6 +364,7 @@ __global__ void __launch_bounds__(256) qk_norm_kernel(const bf16_t* qkv, const f
     const float* b = which ? kb : qb;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) v[i] = v[i] * rstd * w[d0 + i] + b[d0 + i];
+    if (rfreq) rope_rotate<VPL>(v, tpos, rfreq + (d0 >> 1));
     uint32_t o[VPL / 2];
     pack_bf<VPL>(v, o);
     store_packed<VPL>(which ? k_pool + slot * H + c0 : q_out + (size_t)n * H + c0, o);
@@ -371,6 +375,22 @@ __global__ void __launch_bounds__(256) qk_norm_kernel(const bf16_t* qkv, const f
   } else {
     *(uint2*)(v_pool + slot * H + c0) = *(const uint2*)(src + 2 * H);
   }
+}
+
+// Rotary embedding after the tile GEMM's q / k epilogue: 8 values (4 channel pairs) of one q row or one key slot per
+// thread, q rows first; the token's stream position pos[n]
+__global__ void __launch_bounds__(256) rope_qk_kernel(bf16_t* q, bf16_t* k_pool, const int* slots, const int* pos,
+                                                      const float* rfreq, int N, int H) {
+  const long long per = H / 8, t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= 2 * (long long)N * per) return;
+  const int which = t >= (long long)N * per ? 1 : 0;
+  const long long r = t - (long long)which * N * per;
+  const int n = (int)(r / per), c = (int)(r - (long long)n * per) * 8;
+  bf16_t* p = which ? k_pool + (size_t)slots[n] * H + c : q + (size_t)n * H + c;
+  const uint4 u = *(const uint4*)p;
+  float y[8] = {lo2f(u.x), hi2f(u.x), lo2f(u.y), hi2f(u.y), lo2f(u.z), hi2f(u.z), lo2f(u.w), hi2f(u.w)};
+  rope_rotate<8>(y, pos[n], rfreq + ((c & 63) >> 1));
+  *(uint4*)p = make_uint4(pack2(y[0], y[1]), pack2(y[2], y[3]), pack2(y[4], y[5]), pack2(y[6], y[7]));
 }
 
 __global__ void pack_inputs_kernel(const float* x0, const float* stat, bf16_t* a_in, float* x, int half, int mel) {
@@ -528,10 +548,19 @@ hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float e
 }
 
 hipError_t qk_norm_scatter(const bf16_t* qkv, const float* qw, const float* qb, const float* kw, const float* kb, float eps,
-                           bf16_t* q_out, bf16_t* k_pool, bf16_t* v_pool, const int* slots, int N, int heads, hipStream_t st) {
+                           bf16_t* q_out, bf16_t* k_pool, bf16_t* v_pool, const int* slots, int N, int heads, hipStream_t st,
+                           const float* rfreq, const int* pos) {
   if (N <= 0) return hipSuccess;
   const int H = heads * 64;
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(qk_norm_kernel<V>, dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, qkv, qw, qb, kw, kb, eps, q_out, k_pool, v_pool, slots, N, H));
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL(qk_norm_kernel<V>, dim3(blocks_for(N, row_waves(N))), dim3(64 * row_waves(N)), 0, st, qkv, qw, qb, kw, kb, eps, q_out, k_pool, v_pool, slots, N, H, rfreq, pos));
+  return hipGetLastError();
+}
+
+hipError_t rope_qk(bf16_t* q, bf16_t* k_pool, const int* slots, const int* pos, const float* rfreq, int N, int H, hipStream_t st) {
+  if (N <= 0) return hipSuccess;
+  if (H % 64 || !pos || !rfreq) return hipErrorInvalidValue;
+  const long long threads = 2LL * N * (H / 8);
+  hipLaunchKernelGGL(rope_qk_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, q, k_pool, slots, pos, rfreq, N, H);
   return hipGetLastError();
 }
 

@@ -126,6 +126,7 @@ GemmArgs rows_from(const GemmArgs& g, int r) {
   if (EPI == EPI_QKV) {
     h.qk.q_out = g.qk.q_out + (size_t)r * g.qk.H;
     h.qk.slots = g.qk.slots + r;
+    if (g.qk.pos) h.qk.pos = g.qk.pos + r;
   }
   return h;
 }
@@ -204,7 +205,8 @@ hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
       if (!g.w_scale || !g.c_scale || g.N % 32) return hipErrorInvalidValue;
       return launch_epi<EPI_GELU_MX8, false>(g, cfg, st);
     case EPI_QKV * 2:
-      if (g.N != 3 * g.qk.H || g.qk.H % 256) return hipErrorInvalidValue;
+      // the tile epilogue does not rotate q and k (rope_qk after it does): a rotary table here is a caller error
+      if (g.N != 3 * g.qk.H || g.qk.H % 256 || g.qk.rfreq) return hipErrorInvalidValue;
       return launch_epi<EPI_QKV, false>(g, cfg, st);
   }
   return hipErrorInvalidValue;

@@ -333,6 +333,7 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_qkv_kernel(GemmArgs 
     y[1] = y[1] * rstd * lw.y + lb.y;
     y[2] = y[2] * rstd * lw.z + lb.z;
     y[3] = y[3] * rstd * lw.w + lb.w;
+    if (o.rfreq) rope_rotate<4>(y, m0 + r < g.M ? o.pos[m0 + r] : 0, o.rfreq + (c4 >> 1));
   }
   const int mo = m0 + r;
   if (mo >= g.M) return;

@@ -588,7 +588,7 @@ __global__ void __launch_bounds__(256, 2) resblock_pair_kernel(ConvDesc c1, Conv
   constexpr int BM1 = 32768 / C, WN = C / 64, WM = 4 / WN, WTM = BM1 / WM, TM = WTM / 32;
   constexpr int CH = C / 8, MSK = (CH < 16 ? CH : 16) - 1;  // conv2 slab: 16-byte chunks per row; XOR swizzle mask
   static_assert(WTM == 128 && TM == 4, "waves own 128 rows x 64 channels");
-  constexpr int SU = 4;      // slab rows per thread in flight while staging
+  constexpr int SU = C == 64 ? 4 : 2;  // slab rows per thread in flight while staging (registers: acc is live in later chunks)
   extern __shared__ uint4 hl[];  // conv1's input slab [BM1 + span][8 chunks]; then conv2's [BM1 + 16][CH]; then the epilogue's
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;

@@ -26,6 +26,8 @@ struct QkvOut {
   const float *qw, *qb, *kw, *kb;  // [64] each
   float eps;
   int H;
+  const float* rfreq = nullptr;  // rotary embedding of q and k after their LayerNorm: [32] pair frequencies (null: none)
+  const int* pos = nullptr;      // [M] stream position of each token (with rfreq)
 };
 
 struct GemmArgs {
@@ -119,9 +121,12 @@ hipError_t ln_mod_conv(f16_t* h, const float* shift, const float* scale1, float 
                        hipStream_t st, const Pend& pd = Pend());
 hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float eps, const ConvPlace& cp, int H,
                         hipStream_t st, const Pend& pd = Pend());
+// rotary embedding of the q rows [N, H] and of the keys at slots[n] after the tile GEMM's q / k epilogue: channel pair
+// (2i, 2i + 1) of each head turned by pos[n] * rfreq[i] (bf16 in and out)
+hipError_t rope_qk(bf16_t* q, bf16_t* k_pool, const int* slots, const int* pos, const float* rfreq, int N, int H, hipStream_t st);
 hipError_t qk_norm_scatter(const bf16_t* qkv, const float* qw, const float* qb, const float* kw, const float* kb,
                            float eps, bf16_t* q_out, bf16_t* k_pool, bf16_t* v_pool, const int* slots, int N, int heads,
-                           hipStream_t st);
+                           hipStream_t st, const float* rfreq = nullptr, const int* pos = nullptr);
 
 struct AttnArgs {
   const bf16_t* q;        // [N, heads, 64]

@@ -117,8 +117,14 @@ class DiTModel:
                        "fin_w": f32(W["final_layer.adaLN_modulation.1.weight"]), "fin_b": f32(W["final_layer.adaLN_modulation.1.bias"])}
         self.mods, self.final_mods = self.tables(self.ts)
         self._dts = (C.c_float * cfg.steps)(*self.dts)
+        # optional rotary embedding of q and k (none in the reference): pair i turns at theta^(-2i / head_dim) rad per frame
+        self.rope_freq = None
+        if cfg.rope_theta > 0:
+            i = torch.arange(0, cfg.head_dim, 2, dtype=torch.float64)
+            self.rope_freq = f32((cfg.rope_theta ** (-i / cfg.head_dim)).float())
         g = _lib.DitGlobals(self.t["in_w"].data_ptr(), self.t["in_b"].data_ptr(), self.t["out_w"].data_ptr(), self.t["out_b"].data_ptr(),
-                            self.mods.data_ptr(), self.final_mods.data_ptr(), C.cast(self._dts, _lib.FP))
+                            self.mods.data_ptr(), self.final_mods.data_ptr(), C.cast(self._dts, _lib.FP),
+                            _lib.ptr(self.rope_freq))
         _lib.check(L.t2w_dit_set_globals(h, C.byref(g)), "set_globals")
 
     def tables(self, ts: list[float]) -> tuple[torch.Tensor, torch.Tensor]:
@@ -191,10 +197,12 @@ class FastRow:
     """Cached frames of one CFG row of a stream.  ``slots``: key/value slot ids, the newest window's frames first (the
     order the reference concatenates ``[new, cache]`` in, which the trim relies on).  ``conv``: two row slots of the
     conv-cache pool; ``conv[cur]`` holds the two cached frames per (step, block, conv), a kept window writes the other
-    one and flips ``cur``."""
+    one and flips ``cur``.  ``pos``: the stream position of the next window's first frame (frames of kept windows so
+    far), the angle origin of the optional rotary embedding."""
     slots: np.ndarray = field(default_factory=lambda: _NO_SLOTS)
     conv: tuple = (-1, -1)
     cur: int = 0
+    pos: int = 0
 
     @property
     def order(self) -> list[int]:
@@ -221,18 +229,21 @@ def _tile_list(lens: np.ndarray) -> np.ndarray:
     return np.stack([rows, 64 * first], 1).ravel()
 
 
-def _layout(lens, new, kv, rd, wr) -> list[np.ndarray]:
-    """The device tables of a call (``t2w_solve_args`` order, ``kv_idx`` last) from its rows in call order: token counts
-    ``lens``, new key slots ``new[r]``, key lists ``kv[r]`` and conv-cache read / write slots."""
+def _layout(lens, new, kv, rd, wr, pos0=None) -> list[np.ndarray]:
+    """The device tables of a call (``t2w_solve_args`` order, then the stream positions, ``kv_idx`` last: every table but
+    the key lists has a size fixed by the call's token and row counts) from its rows in call order: token counts
+    ``lens``, new key slots ``new[r]``, key lists ``kv[r]``, conv-cache read / write slots and the stream position of
+    each row's first new frame (``pos0``, default 0)."""
     lens = np.asarray(lens, dtype=np.int64)
     starts = np.cumsum(lens) - lens
     tok_row = np.repeat(np.arange(lens.size, dtype=np.int64), lens)
     idx = np.arange(tok_row.size, dtype=np.int64)
     tok_pos = idx - starts[tok_row]
+    pos0 = np.zeros(lens.size, dtype=np.int64) if pos0 is None else np.asarray(pos0, dtype=np.int64)
     kv_len = np.array([x.size for x in kv], dtype=np.int64)
     cat = lambda xs: np.concatenate(xs) if len(xs) else _NO_SLOTS  # noqa: E731
     return [tok_row, tok_pos, idx + 2 * tok_row, cat(new), starts, lens, np.cumsum(kv_len) - kv_len, kv_len,
-            np.asarray(rd, dtype=np.int64), np.asarray(wr, dtype=np.int64), _tile_list(lens), cat(kv)]
+            np.asarray(rd, dtype=np.int64), np.asarray(wr, dtype=np.int64), _tile_list(lens), pos0[tok_row] + tok_pos, cat(kv)]
 
 
 def plan_call(rows: list[FastRow], Ts: list[int], new: list[np.ndarray], keep: list[bool], cnn_scratch: int, cnn_zero: int | None = None,
@@ -251,7 +262,7 @@ def plan_call(rows: list[FastRow], Ts: list[int], new: list[np.ndarray], keep: l
     Returns the tables (``parts``) and what the solve needs afterwards."""
     n = len(Ts)
     half = int(sum(Ts))
-    lens, nw, kv, rd, wr = [], [], [], [], []
+    lens, nw, kv, rd, wr, p0 = [], [], [], [], [], []
     pad = 0 if bucket is None else bucket[1] // 2 - half
     extra = 0 if bucket is None else bucket[0] // 2 - n  # empty rows per half
     zero = cnn_scratch if cnn_zero is None else cnn_zero
@@ -263,6 +274,7 @@ def plan_call(rows: list[FastRow], Ts: list[int], new: list[np.ndarray], keep: l
             kv.append(np.concatenate([new[h * n + i], r.slots]))
             rd.append(r.conv[r.cur])
             wr.append(r.conv[1 - r.cur] if keep[i] else cnn_scratch)
+            p0.append(r.pos)
         if bucket is not None:
             for j in range(extra + 1):
                 T = pad if j == extra else 0
@@ -272,7 +284,8 @@ def plan_call(rows: list[FastRow], Ts: list[int], new: list[np.ndarray], keep: l
                 kv.append(pads)
                 rd.append(zero)
                 wr.append(cnn_scratch)
-    parts = _layout(lens, nw, kv, rd, wr)
+                p0.append(0)
+    parts = _layout(lens, nw, kv, rd, wr, p0)
     R = len(lens)
     n_tiles = parts[10].size // 2
     if bucket is not None:
@@ -343,6 +356,7 @@ def advance_row(r: FastRow, new: np.ndarray, keep: bool, keep_len: int) -> np.nd
         freed = _NO_SLOTS
     r.slots = merged
     r.cur ^= 1
+    r.pos += int(new.size)
     return freed
 
 
@@ -425,6 +439,7 @@ class FastDiT:
         for src, dst in zip(c.rows, out.rows):
             self.conv_pool[dst.conv[0]].copy_(self.conv_pool[src.conv[src.cur]])
             dst.slots = self.pool.alloc(src.slots.size)
+            dst.pos = src.pos
         n = c.length
         if n:
             ids = _Upload.new(np.concatenate([r.slots for r in c.rows] + [r.slots for r in out.rows]), self.device).long()
@@ -485,9 +500,9 @@ class FastDiT:
         offs = np.cumsum([0] + [x.size for x in p["parts"]])
         tp = lambda i: tables.data_ptr() + 4 * int(offs[i])  # noqa: E731
         return _lib.SolveArgs(p["n_tok"], p["n_rows"], p["half"], p["n_tiles"], int(chunk), _lib.ptr(x0), _lib.ptr(stat), _lib.ptr(in_rows),
-                              out.data_ptr(), tp(0), tp(1), tp(2), tp(3), tp(4), tp(5), tp(6), tp(7), tp(8), tp(9), tp(11), tp(10),
+                              out.data_ptr(), tp(0), tp(1), tp(2), tp(3), tp(4), tp(5), tp(6), tp(7), tp(8), tp(9), tp(12), tp(10),
                               self.k_pool.data_ptr(), self.v_pool.data_ptr(), self.n_slots * self.cfg.hidden, self.conv_pool.data_ptr(),
-                              ws.data_ptr(), ws.numel(), int(self.fp8))
+                              ws.data_ptr(), ws.numel(), int(self.fp8), tp(11))
 
     def _workspace(self, N: int, R: int) -> torch.Tensor:
         need = _lib.lib().t2w_dit_workspace_bytes(self.model.handle, N, R)

@@ -19,6 +19,12 @@ Not visible in the reference (inside ``stepaudio2``) and defined here, CosyVoice
 (1e-6 for the block/final norms and q/k norms, 1e-5 for the conv block's affine norm), attention scale ``1/sqrt(64)``,
 no positional encoding.  Against the real stepaudio2 modules these are parity unpinned; the tests pin this oracle's
 composition (block order, masks, cache order, conv state, CFG/Euler, trim) with invariants and closed forms.
+
+Rotary position embedding (``rope_theta`` > 0; off by default): an option of this build with no counterpart in the
+reference, whose DiT has no positional encoding (``engine/runtime/dit_fast.py:6``).  q and k are rotated after their
+LayerNorm, pairs of consecutive head channels (2i, 2i + 1) by the angle ``pos * theta^(-2i / head_dim)`` (RoFormer,
+Su et al. 2021, eq. 34), at each frame's position in its stream: frames of kept windows count, so cached keys keep the
+angle they were written with and a trim leaves every relative distance as it was.
 """
 
 from __future__ import annotations
@@ -47,15 +53,33 @@ class DiTDims:
     eps_final: float = 1e-6
     cfg_rate: float = 0.7
     steps: int = 10
+    rope_theta: float = 0.0  # 0: no positional encoding (the reference's DiT)
 
 
-def dims_of(W: dict, steps: int = 10, cfg_rate: float = 0.7) -> DiTDims:
+def dims_of(W: dict, steps: int = 10, cfg_rate: float = 0.7, rope_theta: float = 0.0) -> DiTDims:
     H = W["in_proj.weight"].shape[0]
     depth = sum(1 for k in W if k.endswith(".attn.proj.weight"))
     hd = W["blocks.0.attn.q_norm.weight"].shape[0]
     return DiTDims(mel=W["final_layer.linear.weight"].shape[0], hidden=H, depth=depth, heads=H // hd, head_dim=hd,
                    ffn=W["blocks.0.mlp.fc1.weight"].shape[0], freq=W["t_embedder.mlp.0.weight"].shape[1],
-                   cfg_rate=cfg_rate, steps=steps)
+                   cfg_rate=cfg_rate, steps=steps, rope_theta=rope_theta)
+
+
+def rope_freqs(head_dim: int, theta: float) -> torch.Tensor:
+    """Angular frequency of channel pair i: theta^(-2i / head_dim), computed in fp64 and rounded to fp32 (the table the
+    GPU path takes)."""
+    return (theta ** (-torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim)).float()
+
+
+def rope(x: torch.Tensor, pos: torch.Tensor, theta: float) -> torch.Tensor:
+    """Rotate consecutive channel pairs of x [B, T, nh, dk] at positions pos [B, T]: (x0, x1) -> (x0 cos a - x1 sin a,
+    x0 sin a + x1 cos a), a = pos * freq_i rounded to fp32."""
+    B, T, nh, dk = x.shape
+    ang = pos.float()[:, :, None] * rope_freqs(dk, theta)[None, None, :]  # fp32 product, as on the GPU
+    c, s = torch.cos(ang.double()).float()[:, :, None, :], torch.sin(ang.double()).float()[:, :, None, :]
+    xp = x.float().reshape(B, T, nh, dk // 2, 2)
+    x0, x1 = xp[..., 0], xp[..., 1]
+    return torch.stack([x0 * c - x1 * s, x0 * s + x1 * c], dim=-1).reshape(B, T, nh, dk)
 
 
 # --- schedule and timestep conditioning -----------------------------------------------------------------------------
@@ -123,17 +147,21 @@ def mish(x):
     return x * torch.tanh(F.softplus(x, beta=1.0, threshold=20.0))
 
 
-def attention_chunk(W, d: DiTDims, b: int, a: torch.Tensor, att_cache: torch.Tensor, mask: torch.Tensor):
+def attention_chunk(W, d: DiTDims, b: int, a: torch.Tensor, att_cache: torch.Tensor, mask: torch.Tensor, pos=None):
     """Attention of one block on a window: a [B, T, H]; att_cache [B, nh, L, 2 dk] (k | v); mask [B, T, T + L] over keys
-    ``[new, cache]``.  Returns (out [B, T, H], new cache [B, nh, T + L, 2 dk])."""
+    ``[new, cache]``; pos [B, T] stream positions of the window's frames (used with ``d.rope_theta`` > 0).  Returns (out
+    [B, T, H], new cache [B, nh, T + L, 2 dk])."""
     B, T, H = a.shape
     nh, dk = d.heads, d.head_dim
     p = f"blocks.{b}.attn."
     q = F.linear(a, W[p + "to_q.weight"], W[p + "to_q.bias"]).view(B, T, nh, dk)
     k = F.linear(a, W[p + "to_k.weight"], W[p + "to_k.bias"]).view(B, T, nh, dk)
     v = F.linear(a, W[p + "to_v.weight"], W[p + "to_v.bias"]).view(B, T, nh, dk)
-    q = layer_norm(q, d.eps_qk, W[p + "q_norm.weight"], W[p + "q_norm.bias"]).transpose(1, 2)
-    k = layer_norm(k, d.eps_qk, W[p + "k_norm.weight"], W[p + "k_norm.bias"]).transpose(1, 2)
+    q = layer_norm(q, d.eps_qk, W[p + "q_norm.weight"], W[p + "q_norm.bias"])
+    k = layer_norm(k, d.eps_qk, W[p + "k_norm.weight"], W[p + "k_norm.bias"])
+    if d.rope_theta > 0:
+        q, k = rope(q, pos, d.rope_theta), rope(k, pos, d.rope_theta)
+    q, k = q.transpose(1, 2), k.transpose(1, 2)
     kv = torch.cat([k, v.transpose(1, 2)], dim=-1)  # [B, nh, T, 2 dk]
     kv = torch.cat([kv, att_cache], dim=2)  # [new, cache]
     kk, vv = kv[..., :dk], kv[..., dk:]
@@ -170,10 +198,10 @@ def mlp(W, b: int, a: torch.Tensor) -> torch.Tensor:
     return F.linear(F.gelu(F.linear(a, W[p + "fc1.weight"], W[p + "fc1.bias"]), approximate="tanh"), W[p + "fc2.weight"], W[p + "fc2.bias"])
 
 
-def block_chunk(W, d: DiTDims, b: int, h, temb, cnn_cache, att_cache, mask, tr):
+def block_chunk(W, d: DiTDims, b: int, h, temb, cnn_cache, att_cache, mask, tr, pos=None):
     """``_block_chunk`` (``token2wav_batch.py:100-110``)."""
     sh_a, sc_a, g_a, sh_m, sc_m, g_m, sh_c, sc_c, g_c = [m[:, None, :] for m in block_mods(W, b, temb)]
-    o, new_att = attention_chunk(W, d, b, modulate(layer_norm(h, d.eps_block), sh_a, sc_a), att_cache, mask)
+    o, new_att = attention_chunk(W, d, b, modulate(layer_norm(h, d.eps_block), sh_a, sc_a), att_cache, mask, pos)
     h = h + g_a * o
     c, new_cnn = conv_block_chunk(W, d, b, modulate(layer_norm(h, d.eps_block), sh_c, sc_c), cnn_cache, tr)
     h = h + g_c * c
@@ -188,16 +216,16 @@ def pack_inputs(x, mu, spks, cond) -> torch.Tensor:
     return torch.cat([x, mu, spks[:, :, None].expand(-1, -1, T), cond], dim=1).transpose(1, 2)
 
 
-def estimator_chunk(W, d: DiTDims, x, mu, temb, spks, cond, cnn_cache, att_cache, mask, tr):
+def estimator_chunk(W, d: DiTDims, x, mu, temb, spks, cond, cnn_cache, att_cache, mask, tr, pos=None):
     """``_estimator_temb`` (``token2wav_batch.py:787-810``).
 
     x, mu, cond [B, mel, T]; temb [B, H]; spks [B, mel]; cnn_cache [depth, B, 2H, 2]; att_cache [depth, B, nh, L, 2dk];
-    mask [B, T, T + L] bool over keys ``[new, cache]``; tr [B] real frames per row.
+    mask [B, T, T + L] bool over keys ``[new, cache]``; tr [B] real frames per row; pos [B, T] stream positions (rope).
     Returns (dphi [B, mel, T], new cnn [depth, B, 2H, 2], new att [depth, B, nh, T + L, 2dk])."""
     h = F.linear(pack_inputs(x, mu, spks, cond), W["in_proj.weight"], W["in_proj.bias"])
     new_cnn, new_att = [], []
     for b in range(d.depth):
-        h, c, a = block_chunk(W, d, b, h, temb, cnn_cache[b], att_cache[b], mask, tr)
+        h, c, a = block_chunk(W, d, b, h, temb, cnn_cache[b], att_cache[b], mask, tr, pos)
         new_cnn.append(c)
         new_att.append(a)
     sh, sc = [m[:, None, :] for m in final_mods(W, temb)]
@@ -210,10 +238,12 @@ def estimator_chunk(W, d: DiTDims, x, mu, temb, spks, cond, cnn_cache, att_cache
 @dataclass
 class Cache:
     """One request's estimator caches: att [steps, 2 (cond, uncond), depth, nh, L, 2 dk] in the reference order
-    (newest window first), cnn [steps, 2, depth, 2H, 2], and the trim length ``keep`` (prompt mel frames)."""
+    (newest window first), cnn [steps, 2, depth, 2H, 2], the trim length ``keep`` (prompt mel frames), and ``pos``, the
+    stream position of the next window's first frame (frames of kept windows so far; rope only)."""
     att: torch.Tensor
     cnn: torch.Tensor
     keep: int = 0
+    pos: int = 0
 
     @property
     def length(self) -> int:
@@ -274,12 +304,13 @@ def solve(W, d: DiTDims, rand_noise: torch.Tensor, caches: list[Cache], mu: list
         mask = torch.ones(2, T, T + L, dtype=torch.bool)
         mask[:, :, :T] = chunk_mask(T, chunk)
         tr = torch.full((2,), T, dtype=torch.int64)
+        pos = (c.pos + torch.arange(T))[None].expand(2, T)
         new_att, new_cnn = [], []
         for s in range(d.steps):
             temb = t_embed(W, torch.full((2,), ts[s]))
             att = c.att[s].transpose(0, 1)  # [2, depth, ...] -> [depth, 2, ...]
             cnn = c.cnn[s].transpose(0, 1)
-            dphi, nc, na = estimator_chunk(W, d, x.repeat(2, 1, 1), mu_in, temb, spk_in, cond_in, cnn, att, mask, tr)
+            dphi, nc, na = estimator_chunk(W, d, x.repeat(2, 1, 1), mu_in, temb, spk_in, cond_in, cnn, att, mask, tr, pos)
             new_att.append(na.transpose(0, 1))
             new_cnn.append(nc.transpose(0, 1))
             dd, u = dphi.chunk(2, dim=0)
@@ -287,6 +318,7 @@ def solve(W, d: DiTDims, rand_noise: torch.Tensor, caches: list[Cache], mu: list
         if keep[i]:
             c.att = trim(torch.stack(new_att), c.keep)
             c.cnn = torch.stack(new_cnn)
+            c.pos += T
         outs.append(x[0])
     return outs
 
@@ -294,7 +326,7 @@ def solve(W, d: DiTDims, rand_noise: torch.Tensor, caches: list[Cache], mu: list
 def solve_full(W, d: DiTDims, rand_noise, mu: torch.Tensor, spk: torch.Tensor, cond: torch.Tensor, blocks: list[int]) -> torch.Tensor:
     """One request's whole sequence in one solve under the block-causal mask of ``blocks`` (frame counts of
     ``[prompt | w1 | w2 | ..]``): block j's frames see blocks 0..j.  Equals a prompt setup followed by the windows, each
-    with the previous ones as cached keys, as long as no trim happened (no positional encoding, causal convs)."""
+    with the previous ones as cached keys, as long as no trim happened (stream positions for rope, causal convs)."""
     T = mu.shape[1]
     assert sum(blocks) == T
     bid = torch.repeat_interleave(torch.arange(len(blocks)), torch.tensor(blocks))
@@ -306,11 +338,12 @@ def solve_full(W, d: DiTDims, rand_noise, mu: torch.Tensor, spk: torch.Tensor, c
     cond_in = torch.cat([cond[None], torch.zeros_like(cond[None])]).float()
     mask = vis[None].expand(2, T, T).clone()
     tr = torch.full((2,), T, dtype=torch.int64)
+    pos = torch.arange(T)[None].expand(2, T)
     att = torch.zeros(d.depth, 2, d.heads, 0, 2 * d.head_dim)
     cnn = torch.zeros(d.depth, 2, 2 * d.hidden, 2)
     for s in range(d.steps):
         temb = t_embed(W, torch.full((2,), ts[s]))
-        dphi, _, _ = estimator_chunk(W, d, x.repeat(2, 1, 1), mu_in, temb, spk_in, cond_in, cnn, att, mask, tr)
+        dphi, _, _ = estimator_chunk(W, d, x.repeat(2, 1, 1), mu_in, temb, spk_in, cond_in, cnn, att, mask, tr, pos)
         dd, u = dphi.chunk(2, dim=0)
         x = x + dts[s] * ((1.0 + d.cfg_rate) * dd - d.cfg_rate * u)
     return x[0]
@@ -323,4 +356,5 @@ def estimator_forward(W, d: DiTDims, x, mu, t, spks, cond) -> torch.Tensor:
     att = torch.zeros(d.depth, B, d.heads, 0, 2 * d.head_dim)
     mask = torch.ones(B, T, T, dtype=torch.bool)
     tr = torch.full((B,), T, dtype=torch.int64)
-    return estimator_chunk(W, d, x, mu, t_embed(W, t), spks, cond, cnn, att, mask, tr)[0]
+    pos = torch.arange(T)[None].expand(B, T)
+    return estimator_chunk(W, d, x, mu, t_embed(W, t), spks, cond, cnn, att, mask, tr, pos)[0]

@@ -68,8 +68,9 @@ def test_estimator_forward_3000_tokens(dev, full):
 
 
 def _stream_case(W, model, graphs: bool, buckets: bool = False, outs: list | None = None, stats: dict | None = None,
-                 prompts=(70, 40)):
-    d = od.dims_of(W, steps=TINY.steps)
+                 prompts=(70, 40), oracle_rope: float | None = None):
+    rope = model.cfg.rope_theta if oracle_rope is None else oracle_rope
+    d = od.dims_of(W, steps=TINY.steps, rope_theta=rope)
     fd = FastDiT(model, n_slots=4096, max_streams=4, use_graphs=graphs, buckets=buckets)
     g = torch.Generator().manual_seed(1)
     n = len(prompts)
@@ -257,3 +258,66 @@ def test_fp8_streaming_vs_oracle(dev):
         errs.append(rel(got[0].cpu(), ref[0]))
     print("fp8 streaming vs oracle rel-L2 per window", errs)
     assert max(errs) < FP8_TOL
+
+
+ROPE = DiTConfig(hidden=256, depth=2, heads=4, ffn=512, rope_theta=10000.0)
+
+
+@pytest.fixture(scope="module")
+def tiny_rope():
+    """Random weights whose q / k LayerNorm gains are scaled by 8: sharper attention, so that the rotary embedding
+    moves the mel by ~3% (with the plain gains it moves it by 0.4%, inside the tolerance)."""
+    W = init_dit(ROPE, seed=11)
+    for b in range(ROPE.depth):
+        for n in ("q_norm", "k_norm"):
+            W[f"blocks.{b}.attn.{n}.weight"] = W[f"blocks.{b}.attn.{n}.weight"] * 8
+    return W, DiTModel(W, ROPE)
+
+
+def test_rope_streaming(dev, tiny_rope):
+    """The optional rotary embedding (none in the reference) against the oracle's: prompt setups and windows past the
+    trim point, so keys cached at earlier stream positions meet queries at later ones.  Setups and two-request windows
+    (132 to 220 tokens) rotate in the split-K path's q/k kernel, one-request windows (at most 128 tokens) in the
+    small-row GEMM's epilogue.  Every call is also at least 5x further from the oracle without the embedding."""
+    W, model = tiny_rope
+    errs = _stream_case(W, model, graphs=False) + _stream_case(W, model, graphs=False, prompts=(60,))
+    plain = _stream_case(W, model, graphs=False, oracle_rope=0.0) + _stream_case(W, model, graphs=False, prompts=(60,), oracle_rope=0.0)
+    print("rope stream rel-L2 per call", errs, "against the oracle without rope", plain)
+    assert max(errs) < TOL
+    assert all(p > 5 * e for p, e in zip(plain, errs))
+
+
+def test_rope_bucketed_graphs(dev, tiny_rope):
+    """Bucketed graph replays carry the stream positions (their table sits before the variable-length key lists)."""
+    W, model = tiny_rope
+    ea, ga = [], []
+    _stream_case(W, model, graphs=False, outs=ea)
+    errs = _stream_case(W, model, graphs=True, buckets=True, outs=ga)
+    d = max(rel(a, b) for a, b in zip(ga, ea))
+    print("rope bucketed graphs vs eager rel-L2", d, "vs oracle", errs)
+    assert d < 1e-3 and max(errs) < TOL
+
+
+def test_rope_tile_path(dev, tiny_rope):
+    """16 requests x 700 frames (11,200 tokens): the qkv projection on 256 x 256 tiles with its fused q/k LayerNorm,
+    then the separate rotation kernel over q rows and key slots.  Sampled rows against the oracle with and without
+    the embedding."""
+    W, model = tiny_rope
+    fd = FastDiT(model, n_slots=32768, max_streams=16)
+    g = torch.Generator().manual_seed(16)
+    Ts = [700] * 16
+    mus = [torch.randn(80, t, generator=g) for t in Ts]
+    spks = torch.randn(16, 80, generator=g)
+    caches = [fd.new_cache() for _ in Ts]
+    got = fd.solve(caches, [m.cuda() for m in mus], spks.cuda(), None, [False] * 16, chunk=50)
+    idx = (0, 7, 15)
+    res = {}
+    for theta in (ROPE.rope_theta, 0.0):
+        d = od.dims_of(W, steps=ROPE.steps, rope_theta=theta)
+        ref = od.solve(W, d, W["rand_noise"], [od.empty_cache(d) for _ in idx], [mus[i] for i in idx], spks[list(idx)], None,
+                       [False] * len(idx), chunk=50)
+        res[theta] = [rel(got[i].cpu(), r) for i, r in zip(idx, ref)]
+    errs, plain = res[ROPE.rope_theta], res[0.0]
+    print("rope tile-path rel-L2 (rows 0, 7, 15)", errs, "against the oracle without rope", plain)
+    assert max(errs) < TOL
+    assert all(p > 5 * e for p, e in zip(plain, errs))

@@ -18,11 +18,14 @@ def _L(x):
 
 def test_plan_tables_are_consistent():
     rows = _rows([([100, 101, 102], (0, 1), 0), ([], (2, 3), 1), ([200, 201, 202], (4, 5), 0), ([], (6, 7), 1)])
+    for r, pos in zip(rows, (250, 9, 250, 9)):  # stream positions of the rows' next frames (rotary embedding)
+        r.pos = pos
     Ts = [70, 1]
     new = [np.arange(10, 80), np.array([90]), np.arange(300, 370), np.array([390])]
     p = plan_call(rows, Ts, new, [True, False], cnn_scratch=99)
-    tok_row, tok_pos, a_src, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, kv = map(_L, p["parts"])
+    tok_row, tok_pos, a_src, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, tok_abs, kv = map(_L, p["parts"])
     assert p["n_tok"] == 142 and p["half"] == 71 and p["n_rows"] == 4
+    assert tok_abs == [rows[r].pos + t for r, t in zip(tok_row, tok_pos)]
     assert a_src == [i + 2 * r for i, r in enumerate(tok_row)]
     assert tok_pos == [t for T in lens for t in range(T)]
     assert lens == [70, 1, 70, 1] and row_start == [0, 70, 71, 141]
@@ -50,12 +53,14 @@ def test_bucket_table():
 def test_padded_plan_keeps_every_real_row(Ts, keep):
     n = len(Ts)
     rows = _rows([(range(1000 * r, 1000 * r + 7 * r), (2 * r, 2 * r + 1), r % 2) for r in range(2 * n)])
+    for r, row in enumerate(rows):
+        row.pos = 13 * (r % n)
     new = [np.arange(100000 + 1000 * r, 100000 + 1000 * r + Ts[r % n]) for r in range(2 * n)]
     P = [_L(x) for x in plan_call(rows, Ts, new, keep, cnn_scratch=99)["parts"]]
     rb, nb = bucket_of(2 * n, 2 * sum(Ts))
     q = plan_call(rows, Ts, new, keep, cnn_scratch=99, cnn_zero=98, bucket=(rb, nb), kv_scratch=77)
     hr = rb // 2 + 1
-    tok_row, tok_pos, a_src, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, kv = map(_L, q["parts"])
+    tok_row, tok_pos, a_src, new_slot, row_start, lens, kv_off, kv_len, rd, wr, tiles, tok_abs, kv = map(_L, q["parts"])
     assert q["n_rows"] == 2 * hr and q["n_tok"] == nb and q["half"] == nb // 2 and len(tok_row) == nb
     assert q["real_half"] == sum(Ts)
     assert sum(lens[:hr]) == sum(lens[hr:]) == nb // 2
@@ -68,11 +73,13 @@ def test_padded_plan_keeps_every_real_row(Ts, keep):
             if j < n:  # a request row: the same tables as unpadded
                 o = h * n + j
                 assert T == P[5][o] and new_slot[s:s + T] == P[3][P[4][o]:P[4][o] + T]
-                assert kv[kv_off[r]:kv_off[r] + kv_len[r]] == P[11][P[6][o]:P[6][o] + P[7][o]]
+                assert kv[kv_off[r]:kv_off[r] + kv_len[r]] == P[12][P[6][o]:P[6][o] + P[7][o]]
                 assert (rd[r], wr[r]) == (P[8][o], P[9][o])
+                assert tok_abs[s:s + T] == P[11][P[4][o]:P[4][o] + T] == [rows[o].pos + t for t in range(T)]
             else:  # empty rows, then the padding row: scratch key slot, zero conv cache in, scratch conv cache out
                 assert T == (0 if j < hr - 1 else nb // 2 - sum(Ts))
                 assert new_slot[s:s + T] == [77] * T and kv[kv_off[r]:kv_off[r] + kv_len[r]] == [77] * T
+                assert tok_abs[s:s + T] == list(range(T))
                 assert rd[r] == 98 and wr[r] == 99
     assert q["n_tiles"] == len(tiles) // 2 == bucket_tiles(rb, nb)
     live = [(r, q0) for r, q0 in zip(tiles[::2], tiles[1::2]) if q0 < lens[r]]
@@ -102,6 +109,7 @@ def test_row_bookkeeping_follows_the_oracle_trim(keep_len):
         assert row.order == ref
         assert pool.in_use() - 1 == len(row.order)
     assert row.cur == 0  # six kept windows swapped the conv slots six times
+    assert row.pos == 6 * 50  # stream position: frames of the kept windows, trimmed ones included
 
 
 def test_slot_pool_reserved_and_exhaustion():

@@ -153,7 +153,7 @@ def test_euler_cfg_on_a_linear_field(monkeypatch, W):
     d = d_of(W, steps=10, cfg=0.7)
     a, b = 0.8, -0.3
 
-    def field(W_, d_, x, mu, temb, spks, cond, cnn, att, mask, tr):
+    def field(W_, d_, x, mu, temb, spks, cond, cnn, att, mask, tr, pos=None):
         return torch.cat([a * x[:1], b * x[1:]]), cnn[:, :, :, :0], att[:, :, :, :0]
 
     monkeypatch.setattr(od, "estimator_chunk", field)
@@ -169,7 +169,7 @@ def test_noise_is_read_at_the_cache_offset(monkeypatch, W):
     d = d_of(W, steps=1, cfg=0.0)
     seen = []
 
-    def field(W_, d_, x, mu, temb, spks, cond, cnn, att, mask, tr):
+    def field(W_, d_, x, mu, temb, spks, cond, cnn, att, mask, tr, pos=None):
         seen.append(x[0].clone())
         T = x.shape[2]
         return torch.zeros_like(x), cnn, torch.cat([torch.zeros(att.shape[0], att.shape[1], att.shape[2], T, att.shape[4]), att], 3)
@@ -200,3 +200,69 @@ def test_trim_evicts_the_prompt_middle_not_the_newest():
     assert len(order) == P + 100
     assert order[:50] == [f"w3_{i}" for i in range(50)]
     assert order[-100:] == [f"p{i}" for i in range(50, 150)]
+
+
+def test_rope_closed_forms():
+    """The optional rotary embedding (no counterpart in the reference, whose DiT has no positional encoding): the
+    frequency table's endpoints, position 0 is the identity, a unit vector on channel 2i turns into (cos, sin) of
+    pos * theta^(-2i / 64) on channels (2i, 2i + 1) and nowhere else (consecutive pairs, not halves of the head), pair
+    norms are kept, and q.k depends on the difference of the positions only."""
+    f = od.rope_freqs(64, 10000.0)
+    assert f.dtype == torch.float32 and f.shape == (32,)
+    assert float(f[0]) == 1.0 and math.isclose(float(f[31]), 10000.0 ** (-62 / 64), rel_tol=1e-7)
+    assert bool((f[1:] < f[:-1]).all())
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 5, 3, 64, generator=g)
+    assert torch.equal(od.rope(x, torch.zeros(2, 5, dtype=torch.long), 1e4), x)
+    for i in (0, 1, 7, 31):
+        e = torch.zeros(1, 1, 1, 64)
+        e[..., 2 * i] = 1.0
+        y = od.rope(e, torch.tensor([[37]]), 1e4)[0, 0, 0]
+        a = 37 * float(f[i])
+        want = torch.zeros(64)
+        want[2 * i], want[2 * i + 1] = math.cos(a), math.sin(a)
+        torch.testing.assert_close(y, want, rtol=0, atol=1e-6)
+    pos = torch.randint(0, 5000, (2, 5), generator=g)
+    y = od.rope(x, pos, 1e4)
+    torch.testing.assert_close(y.view(2, 5, 3, 32, 2).norm(dim=-1), x.view(2, 5, 3, 32, 2).norm(dim=-1), rtol=1e-5, atol=1e-5)
+    q, k = torch.randn(1, 1, 1, 64, generator=g), torch.randn(1, 1, 1, 64, generator=g)
+
+    def dot(m, n):
+        return float((od.rope(q, torch.tensor([[m]]), 1e4) * od.rope(k, torch.tensor([[n]]), 1e4)).sum())
+
+    assert abs(dot(10, 3) - dot(110, 103)) < 1e-3 and abs(dot(0, 5) - dot(40, 45)) < 1e-3
+    assert abs(dot(10, 3) - dot(10, 4)) > 1e-2
+
+
+def test_rope_streaming_equals_full_sequence(W):
+    """With the rotary embedding on, a prompt setup followed by two kept windows still equals the whole-sequence solve
+    under the block-causal mask: each window's frames take the stream positions after the kept frames before them, and
+    cached keys keep the rotation they were written with.  The embedding changes the result (it is applied)."""
+    d = od.dims_of(W, steps=4, rope_theta=10000.0)
+    g = torch.Generator().manual_seed(3)
+    P, T1, T2 = 12, 6, 9
+    mu = torch.randn(80, P + T1 + T2, generator=g)
+    spk = torch.randn(1, 80, generator=g)
+    pc = torch.randn(80, P, generator=g)
+    c = od.empty_cache(d, keep=1000)
+    outs = [od.solve(W, d, W["rand_noise"], [c], [mu[:, :P]], spk, [pc])[0]]
+    outs.append(od.solve(W, d, W["rand_noise"], [c], [mu[:, P:P + T1]], spk, None)[0])
+    outs.append(od.solve(W, d, W["rand_noise"], [c], [mu[:, P + T1:]], spk, None)[0])
+    assert c.pos == P + T1 + T2
+    cond = torch.cat([pc, torch.zeros(80, T1 + T2)], 1)
+    full = od.solve_full(W, d, W["rand_noise"], mu, spk[0], cond, [P, T1, T2])
+    torch.testing.assert_close(torch.cat(outs, 1), full, rtol=2e-4, atol=2e-4)
+    plain = od.solve_full(W, d_of(W), W["rand_noise"], mu, spk[0], cond, [P, T1, T2])
+    assert float((plain - full).abs().max()) > 1e-3
+
+
+def test_rope_position_survives_the_trim(W):
+    """Positions count kept frames, not cached ones: after a trim the cache is shorter than the stream, the next window
+    still starts at the stream position, and a window that is not kept does not advance it."""
+    d = od.dims_of(W, steps=2, rope_theta=10000.0)
+    g = torch.Generator().manual_seed(5)
+    c = od.empty_cache(d, keep=10)
+    spk = torch.randn(1, 80, generator=g)
+    for T, kp in ((10, True), (60, True), (60, True), (20, False)):
+        od.solve(W, d, W["rand_noise"], [c], [torch.randn(80, T, generator=g)], spk, None, [kp])
+    assert c.pos == 130 and c.length == 10 + 100
