@@ -8,11 +8,14 @@
 //
 // CDNA4 mapping: a workgroup of two waves owns 64 queries of one head; each wave 32 of them.  Keys come in tiles of
 // 64 (two 32-key MFMA halves per barrier), gathered by slot id with 16-byte loads into registers one tile ahead (the
-// slot ids themselves two tiles ahead, so the dependent id -> key load chain is hidden), then stored to LDS: K row-major with the
-// 16-byte chunks XOR-swizzled by key, V transposed (d-major) with its keys permuted so that the probabilities the
-// score MFMA leaves in a lane are exactly the K-slice the P.V MFMA wants from that lane.  Scores are computed
-// transposed, S^T = K . Q^T (v_mfma_f32_32x32x16_bf16, the wave's Q fragment stays in registers), so each lane holds
-// 16 of the 32 keys of its own query and the softmax needs one cross-half exchange; O^T += V^T . P^T.
+// slot ids themselves two tiles ahead, so the dependent id -> key load chain is hidden), then stored to LDS: K and V
+// both row-major (key-major) with the 16-byte chunks XOR-swizzled by key.  Scores are computed transposed,
+// S^T = K . Q^T (v_mfma_f32_32x32x16_bf16, the wave's Q fragment stays in registers), so each lane holds 16 of the 32
+// keys of its own query (two runs of 4 consecutive keys per 8 probabilities) and the softmax needs one cross-half
+// exchange; O^T += V^T . P^T takes its V^T fragments with LDS transpose reads (ds_read_b64_tr_b16: in each group of 16
+// lanes, lane j names a row of four 16-bit values and lane i receives element i % 4 of rows i / 4 + 4 e, e = 0..3), two
+// per fragment, each giving a lane 4 consecutive keys of its own channel d -- exactly the keys whose probabilities
+// the score MFMA left in that lane.
 #include "common.h"
 #include "t2w_internal.h"
 
@@ -22,15 +25,32 @@ namespace {
 
 constexpr float NEG = -1.0e30f;
 
-// key k of a 32-key tile -> its column in the transposed V tile: bits 2 and 3 swapped
-__device__ __forceinline__ int vpos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+
+// V^T fragment of the P.V MFMA from a key-major V tile in LDS (16-byte chunks swizzled by key): lane l gets channel
+// d = d0 + l % 32 and keys kb + 4 (l / 32) + {0..3} (elements 0..3) and kb + 8 + 4 (l / 32) + {0..3} (elements 4..7),
+// the keys whose probabilities the score MFMA leaves in the lanes of that half
+__device__ __forceinline__ bf16x8 vt_frag(const uint4* vtile, int kb, int d0, int lane) {
+  const int g = lane >> 4, j = lane & 15;
+  const int key = kb + 4 * (g >> 1) + (j >> 2);  // the row this lane names: 4 keys x 4 runs of 4 channels per group
+  const int d = d0 + 16 * (g & 1) + 4 * (j & 3);
+  const bf16_t* base = (const bf16_t*)vtile;
+  const int k2 = key + 8;
+  const bf16_t* p1 = base + key * 64 + ((((d >> 3) ^ (key & 7)) << 3) | (d & 7));
+  const bf16_t* p2 = base + k2 * 64 + ((((d >> 3) ^ (k2 & 7)) << 3) | (d & 7));
+  const v4s_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_t*)p1);
+  const v4s_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_t*)p2);
+  const uint4 u = make_uint4((uint32_t)(uint16_t)a.x | ((uint32_t)(uint16_t)a.y << 16), (uint32_t)(uint16_t)a.z | ((uint32_t)(uint16_t)a.w << 16),
+                             (uint32_t)(uint16_t)b.x | ((uint32_t)(uint16_t)b.y << 16), (uint32_t)(uint16_t)b.z | ((uint32_t)(uint16_t)b.w << 16));
+  return as_bf16x8(u);
+}
 
 // KS > 1 (few workgroups, e.g. a streaming chunk): KS groups of two waves share the 64 queries and take every KS-th
 // key tile each; their softmax states (max, sum, output) are merged through LDS at the end.
 template <int KS>
 __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
   __shared__ uint4 ks[KS][2][64 * 8];      // [key][16-byte chunk ^ (key & 7)], 64 keys
-  __shared__ uint4 vt[KS][2][2][64 * 4];   // per 32-key half: [d][16-byte chunk ^ ((d >> 1) & 3)] of permuted keys
+  __shared__ uint4 vt[KS][2][64 * 8];      // [key][16-byte chunk ^ (key & 7)], 64 keys
   // XCD-aware order: consecutive workgroups go to different XCDs, so each XCD takes a contiguous run of (head, tile)
   // pairs; the query tiles of one row and head then share that row's keys and values in one L2
   const int nblk = gridDim.x * gridDim.y, full = (nblk / 8) * 8;
@@ -85,17 +105,6 @@ __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
     rk0##X = kp[0]; rk1##X = kp[1]; rk2##X = kp[2]; rk3##X = kp[3];                     \
     rv0##X = vp[0]; rv1##X = vp[1]; rv2##X = vp[2]; rv3##X = vp[3];                     \
   }
-  const int vp_ = vpos(lk & 31);
-  auto vstore = [](bf16_t* vb, int p, int dbase, uint4 v) {  // 8 consecutive d of one key into the transposed tile
-    const uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
-    const uint32_t ws[4] = {w0, w1, w2, w3};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = dbase + e;
-      const uint32_t wv = ws[e >> 1];
-      vb[d * 32 + (((p >> 3) ^ ((d >> 1) & 3)) << 3) + (p & 7)] = (bf16_t)((e & 1) ? (wv >> 16) : (wv & 0xffff));
-    }
-  };
 #define T2W_LSTORE(s, X)                                         \
   {                                                              \
     uint4* kr = ks[gi][s] + lk * 8;                              \
@@ -103,11 +112,11 @@ __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
     kr[(lc + 1) ^ (lk & 7)] = rk1##X;                           \
     kr[(lc + 2) ^ (lk & 7)] = rk2##X;                           \
     kr[(lc + 3) ^ (lk & 7)] = rk3##X;                           \
-    bf16_t* vb = (bf16_t*)vt[gi][s][lk >> 5];                    \
-    vstore(vb, vp_, (lc + 0) * 8, rv0##X);                      \
-    vstore(vb, vp_, (lc + 1) * 8, rv1##X);                      \
-    vstore(vb, vp_, (lc + 2) * 8, rv2##X);                      \
-    vstore(vb, vp_, (lc + 3) * 8, rv3##X);                      \
+    uint4* vr = vt[gi][s] + lk * 8;                              \
+    vr[(lc + 0) ^ (lk & 7)] = rv0##X;                           \
+    vr[(lc + 1) ^ (lk & 7)] = rv1##X;                           \
+    vr[(lc + 2) ^ (lk & 7)] = rv2##X;                           \
+    vr[(lc + 3) ^ (lk & 7)] = rv3##X;                           \
   }
 
   f32x16 o0, o1;
@@ -207,12 +216,10 @@ __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
         if (sub == 1 && !two) break;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const int chunk = hh * 2 + half;
-          const int d0 = col, d1 = 32 + col;
-          const uint4 v0 = vt[gi][s][sub][d0 * 4 + (chunk ^ ((d0 >> 1) & 3))];
-          const uint4 v1 = vt[gi][s][sub][d1 * 4 + (chunk ^ ((d1 >> 1) & 3))];
-          o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v0), as_bf16x8(pf[sub][hh]), o0, 0, 0, 0);
-          o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(v1), as_bf16x8(pf[sub][hh]), o1, 0, 0, 0);
+          const bf16x8 v0 = vt_frag(vt[gi][s], sub * 32 + hh * 16, 0, lane);
+          const bf16x8 v1 = vt_frag(vt[gi][s], sub * 32 + hh * 16, 32, lane);
+          o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v0, as_bf16x8(pf[sub][hh]), o0, 0, 0, 0);
+          o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v1, as_bf16x8(pf[sub][hh]), o1, 0, 0, 0);
         }
       }
     }
