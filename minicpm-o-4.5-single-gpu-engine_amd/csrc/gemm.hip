@@ -169,7 +169,14 @@ int pick_cfg(const GemmArgs& g) {
   // hardware reciprocal (DiT solve 143.5 -> 142.0 ms against 128x128)
   if (g.M < 1024 || g.N < 256) return 0;
   if (g.w_scale) return 2;
-  return 1;
+  // A 256x256 grid that fills under 70% of its last round of 256 CUs (prompt setups of 1,000-9,000 tokens) loses to the
+  // 128x128 grid when that one's cost is clearly lower.  Measured per round of 256 tiles at K = 1024: 256x256 ~30 us,
+  // 128x128 ~7.5 us plus ~7 us once (e.g. 3,000 rows, N = 1024: 26.5 vs 14.0 us; 8,000 rows: 29.4 vs 22.8 us; 12,800
+  // rows: 33.2 vs 37.3 us, where the 256x256 grid is 78% full)
+  const long t1 = (long)((g.M + 255) / 256) * ((g.N + 255) / 256), t0 = (long)((g.M + 127) / 128) * ((g.N + 127) / 128);
+  const long r1 = (t1 + 255) / 256, r0 = (t0 + 255) / 256;
+  if (10 * t1 >= 7 * 256 * r1) return 1;
+  return 75 * r0 + 70 < 270 * r1 ? 0 : 1;
 }
 
 bool gemm_splits(const GemmArgs& g) {

@@ -51,9 +51,9 @@ def test_estimator_forward_config1(dev, full):
 
 
 def test_estimator_forward_3000_tokens(dev, full):
-    """One estimator forward with 3000 tokens (B=2 rows, T=1500, t=0.3): every block GEMM runs on the 256 x 256 tile
-    GEMM over a partly filled grid (12 row tiles: 48 tiles at N = 1024, 144 for the qkv projection with its fused q/k
-    LayerNorm and key/value scatter)."""
+    """One estimator forward with 3000 tokens (B=2 rows, T=1500, t=0.3): the N = 1024 and 2048 GEMMs run on 128 x 128
+    tiles (a 256 x 256 grid would fill under a fifth of the CUs), the qkv projection with its fused q/k LayerNorm and
+    key/value scatter on 144 tiles of 256 x 256."""
     W, model = full
     fd = FastDiT(model, n_slots=4096, max_streams=2)
     g = torch.Generator().manual_seed(3)
