@@ -3,9 +3,9 @@
 Stages are checked separately so that each bound measures one kernel family: the f0 predictor; the NSF source given the
 oracle's f0 (the frame-rate phase reaches ~1e5 rad over a 400-frame row, so any f0 difference is amplified by sin); the
 decoder + ISTFT given the oracle's source.  End to end, the strict-fp32 bound of the reference
-(``tests/engine/test_token2wav_stream.py:54``: waveform rel-L2 1e-4) holds for the decoder; the whole chain is held to
-the reference's reduced-precision HiFT bound of 1e-2 (``tests/engine/test_hift_tf32.py:227``) because of that phase
-amplification.
+(``tests/engine/test_token2wav_stream.py:54``: waveform rel-L2 1e-4) holds for the decoder; the strict-fp32 chain end
+to end is held to 5e-4 (it measures ~4e-5: its f0 matches the oracle's to 2e-6, too little for the phase to amplify),
+the bf16 decoders to the reference's reduced-precision HiFT bound of 1e-2 (``tests/engine/test_hift_tf32.py:227``).
 """
 
 import pytest
@@ -74,7 +74,10 @@ def test_decoder_given_source(dev, case):
 
 
 def test_forward_noise_end_to_end_with_cache(dev, case):
-    """Equal-length rows through ``forward_noise`` with a 3840-sample source cache (a steady 58-frame window)."""
+    """Equal-length rows through ``forward_noise`` with a 3840-sample source cache (a steady 58-frame window), strict
+    fp32 end to end: f0, source and decoder agree with the oracle closely enough that the phase integration does not
+    amplify anything (measured rel-L2 3.8e-5 speech, 5.0e-5 source), so the bound is 5e-4 rather than the
+    reduced-precision 1e-2 of the bf16 tests."""
     W, h, gm, mels, noise = case
     g = torch.Generator().manual_seed(8)
     mel = torch.randn(3, 80, 58, generator=g) * 2 - 5
@@ -85,7 +88,7 @@ def test_forward_noise_end_to_end_with_cache(dev, case):
     e_sp, e_src = rel(sp.cpu(), rsp), rel(src.cpu(), rsrc)
     print("end-to-end speech rel-L2", e_sp, "source rel-L2", e_src)
     assert torch.equal(src[:, :, :3840].cpu(), cs)
-    assert e_sp < 1e-2 and e_src < 1e-2
+    assert e_sp < 5e-4 and e_src < 5e-4
 
 
 @pytest.mark.parametrize("fusion", ["auto", "on"])
