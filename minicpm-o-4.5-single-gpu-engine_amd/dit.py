@@ -666,3 +666,59 @@ class FastDiT:
         finally:
             self.pool.release(slots)
         return out.view(B, T, mel).permute(0, 2, 1).contiguous()
+
+    @torch.inference_mode()
+    def estimator_chunk(self, x: torch.Tensor, mu: torch.Tensor, t: float, spks: torch.Tensor, cond: torch.Tensor,
+                        cnn_cache: torch.Tensor, att_cache: torch.Tensor, chunk: int = 0):
+        """The estimator on dense caches, as the reference module's ``_estimator`` / ``_estimator_temb`` take them
+        (``engine/runtime/token2wav_batch.py:782-810``): B rows of T new frames, every row's T frames real, with the
+        solve's mask (every cached frame visible; new frames full, or chunk-causal with ``chunk`` > 0).
+
+        x, mu, cond [B, mel, T]; spks [B, mel]; t a scalar; cnn_cache [depth, B, 2H, 2] (conv1's two cached frames,
+        then conv2's, oldest first); att_cache [depth, B, heads, L, 2 * head_dim] (k | v, newest frames first).
+        Returns (dphi [B, mel, T], new cnn_cache [depth, B, 2H, 2], new att_cache [depth, B, heads, T + L,
+        2 * head_dim] with the new frames first), the caches rounded to bf16 as the pools hold them.  The caches go
+        through the step-0 layers of this object's pools (slots and conv rows borrowed for the call)."""
+        cfg, dev = self.cfg, self.device
+        B, mel, T = x.shape
+        D, H, nh, dk = cfg.depth, cfg.hidden, cfg.heads, cfg.head_dim
+        L = int(att_cache.shape[3])
+        if tuple(att_cache.shape) != (D, B, nh, L, 2 * dk) or tuple(cnn_cache.shape) != (D, B, 2 * H, 2):
+            raise ValueError(f"caches of shape {tuple(att_cache.shape)} / {tuple(cnn_cache.shape)} do not fit depth {D}, "
+                             f"{B} rows, {nh} heads, hidden {H}")
+        if len(self.cnn_free) < 2 * B:
+            raise RuntimeError("Token2Wav conv-cache row slots exhausted")
+        rows = torch.cat([x, mu, spks[:, :, None].expand(-1, -1, T), cond], dim=1).to(dev, torch.float32)
+        in_rows = rows.permute(0, 2, 1).reshape(B * T, 4 * mel).contiguous()
+        conv = [self.cnn_free.pop() for _ in range(2 * B)]
+        rd, wr = conv[:B], conv[B:]
+        slots = self.pool.alloc(B * (T + L))
+        try:
+            new = [slots[r * T:(r + 1) * T] for r in range(B)]
+            old = [slots[B * T + r * L:B * T + (r + 1) * L] for r in range(B)]
+            lists = [np.concatenate([new[r], old[r]]) for r in range(B)]
+            if L:
+                ids = torch.as_tensor(np.concatenate(old).astype(np.int64), device=dev)
+                kv = att_cache.to(dev).permute(0, 1, 3, 2, 4).reshape(D, B * L, nh, 2 * dk)  # [depth, B L, heads, 2 dk]
+                self.k_pool[:D].index_copy_(1, ids, kv[..., :dk].reshape(D, B * L, H).to(torch.bfloat16))
+                self.v_pool[:D].index_copy_(1, ids, kv[..., dk:].reshape(D, B * L, H).to(torch.bfloat16))
+            rd_ids = torch.as_tensor(rd, device=dev)
+            # conv_pool[row, step 0, block, conv, frame, :] = cnn_cache[block, row, conv * H : (conv + 1) * H, frame]
+            self.conv_pool[rd_ids, 0] = cnn_cache.to(dev).view(D, B, 2, H, 2).permute(1, 0, 2, 4, 3).to(torch.bfloat16)
+            parts = _layout([T] * B, new, lists, rd, wr)
+            p = {"n_tok": B * T, "n_rows": B, "half": 0, "n_tiles": parts[10].size // 2, "parts": parts}
+            tables = _Upload.new(self._flat(p), dev)
+            out = torch.empty(B * T, mel, device=dev)
+            mods, fin = self.model.tables([float(t)])
+            a = self._args(p, tables, None, None, out, self._workspace(B * T, B), int(chunk), in_rows=in_rows)
+            _lib.check(_lib.lib().t2w_dit_forward(self.model.handle, C.byref(a), 0, mods.data_ptr(), fin.data_ptr(), _lib.stream_handle()),
+                       "dit_forward")
+            all_ids = torch.as_tensor(np.concatenate(lists).astype(np.int64), device=dev)
+            k = self.k_pool[:D].index_select(1, all_ids).view(D, B, T + L, nh, dk)
+            v = self.v_pool[:D].index_select(1, all_ids).view(D, B, T + L, nh, dk)
+            new_att = torch.cat([k, v], dim=-1).permute(0, 1, 3, 2, 4).float().contiguous()
+            new_cnn = self.conv_pool[torch.as_tensor(wr, device=dev), 0].permute(1, 0, 2, 4, 3).reshape(D, B, 2 * H, 2).float()
+        finally:
+            self.pool.release(slots)
+            self.cnn_free += conv
+        return out.view(B, T, mel).permute(0, 2, 1).contiguous(), new_cnn, new_att

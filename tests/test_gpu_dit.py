@@ -321,3 +321,30 @@ def test_rope_tile_path(dev, tiny_rope):
     print("rope tile-path rel-L2 (rows 0, 7, 15)", errs, "against the oracle without rope", plain)
     assert max(errs) < TOL
     assert all(p > 5 * e for p, e in zip(plain, errs))
+
+
+@pytest.mark.parametrize("chunk", [0, 25])
+def test_estimator_chunk_dense_caches(dev, tiny, chunk):
+    """The estimator on dense caches as the reference module passes them (``_estimator_temb``): 2 rows of 50 new frames
+    over 70 cached frames per row, against the oracle's ``estimator_chunk`` with the same caches and mask.  The cached
+    keys come back as the bf16 of what went in, the new keys / values and conv frames as the oracle's to bf16 accuracy."""
+    W, model = tiny
+    d = od.dims_of(W, steps=TINY.steps)
+    fd = FastDiT(model, n_slots=4096, max_streams=2)
+    g = torch.Generator().manual_seed(17)
+    B, T, L, H = 2, 50, 70, TINY.hidden
+    x, mu, cond = (torch.randn(B, 80, T, generator=g) for _ in range(3))
+    spk = torch.randn(B, 80, generator=g)
+    att = torch.randn(d.depth, B, d.heads, L, 2 * d.head_dim, generator=g)
+    cnn = torch.randn(d.depth, B, 2 * H, 2, generator=g)
+    t = 0.4
+    mask = torch.ones(B, T, T + L, dtype=torch.bool)
+    mask[:, :, :T] = od.chunk_mask(T, chunk)
+    ref, ref_cnn, ref_att = od.estimator_chunk(W, d, x, mu, od.t_embed(W, torch.full((B,), t)), spk, cond, cnn, att, mask,
+                                               torch.full((B,), T))
+    got, got_cnn, got_att = fd.estimator_chunk(x.cuda(), mu.cuda(), t, spk.cuda(), cond.cuda(), cnn.cuda(), att.cuda(), chunk=chunk)
+    e, ec, ea = rel(got.cpu(), ref), rel(got_cnn.cpu(), ref_cnn), rel(got_att[:, :, :, :T].cpu(), ref_att[:, :, :, :T])
+    print("dense-cache estimator rel-L2: dphi", e, "new conv cache", ec, "new keys / values", ea)
+    assert e < TOL and ec < 1e-2 and ea < 1e-2
+    assert torch.equal(got_att[:, :, :, T:].cpu(), att.bfloat16().float())
+    assert fd.pool.in_use() == fd.scratch
