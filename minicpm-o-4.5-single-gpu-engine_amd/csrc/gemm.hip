@@ -1,7 +1,7 @@
 // bf16 MFMA GEMM for the DiT linears: C = epilogue(A[M,K] . W[N,K]^T + bias), fp32 accumulation.
 //
 // CDNA4 design.  A workgroup owns a BM x BN output tile; its waves own WTM x WTN sub-tiles made of
-// v_mfma_f32_32x32x16_bf16 blocks.  K advances in stages of 64 (128-byte tile rows).  Every stage is copied straight
+// v_mfma_f32_16x16x32_bf16 blocks (fp8: 32x32x64).  K advances in stages of 64 (128-byte tile rows).  Every stage is copied straight
 // from HBM/L2 into LDS with global_load_lds_dwordx4 (no register staging), 16-byte chunks XOR-swizzled by row so that
 // the fragment reads of 16 consecutive rows cover all 64 LDS banks.  Two LDS stages: the loads of stage k + 2 are issued
 // right after the barrier that retires stage k, and the first fragments of stage k + 1 are read before the last MFMAs
@@ -59,13 +59,13 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   const int m0 = mb * BM, n0 = nb * BN;
   T t(g, m0, n0);
 
-  f32x16 acc[T::TM][T::TN];
+  typename T::acc_t acc[T::TM][T::TN];
 #pragma unroll
   for (int i = 0; i < T::TM; ++i)
 #pragma unroll
     for (int j = 0; j < T::TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < (int)(sizeof(typename T::acc_t) / 4); ++r) acc[i][j][r] = 0.0f;
   typename T::frag_t af[2][T::TM], bf[2][T::TN];
   uint32_t sd0[T::NSC], sd1[T::NSC];  // fp8: activation scale dwords of the stages in buffers 0 and 1
 

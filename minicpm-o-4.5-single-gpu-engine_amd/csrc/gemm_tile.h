@@ -84,15 +84,20 @@ template <bool FP8>
 struct FragT { typedef bf16x8 type; };
 template <>
 struct FragT<true> { typedef i32x8 type; };
+template <int MBE>
+struct AccT { typedef f32x16 type; };
+template <>
+struct AccT<16> { typedef f32x4 type; };
 
-// Writes one wave's accumulators (a WTM x WTN block at rows mw.., columns nw..; acc[i][j] = MFMA block (i, j), lane l
-// holding column nw + j * 32 + q * 8 + (l / 32) * 4 + (0..3) of row mw + i * 32 + l % 32 in registers q * 4 ..) through
+// Writes one wave's accumulators (a WTM x WTN block at rows mw.., columns nw..; acc[i][j] = MFMA block (i, j) of edge
+// MBE: for 32 x 32 blocks lane l holds column nw + j * 32 + q * 8 + (l / 32) * 4 + (0..3) of row mw + i * 32 + l % 32 in
+// registers q * 4 .., for 16 x 16 blocks columns nw + j * 16 + (l / 16) * 4 + (0..3) of row mw + i * 16 + l % 16) through
 // its LDS slab st (32 x WTN fp32, 16-byte chunks XOR-swizzled by row) so that each global access of the epilogue covers
 // whole rows.  bf16 and fp16 outputs go out 16 bytes per lane (8 columns; the fp16 residual's rows of a batch are all
 // loaded before its first store); fp32 outputs 4 columns per lane.  16-byte outputs need ldc % 8 == 0 and a 16-byte
 // aligned C (gemm_bf16 checks).
-template <int EPI, int TM, int TN, int WTM, int WTN>
-__device__ __forceinline__ void tile_store(const GemmArgs& g, const f32x16 (&acc)[TM][TN], float4* st, int mw, int nw, int lane) {
+template <int EPI, int MBE, int TM, int TN, int WTM, int WTN, typename AccT>
+__device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[TM][TN], float4* st, int mw, int nw, int lane) {
   constexpr int CPR = WTN / 4;   // 16-byte chunks per slab row
   constexpr int RPI = 64 / CPR;  // slab rows per read-back instruction
   constexpr int NRB = 32 / RPI;  // read-back instructions per slab
@@ -119,8 +124,8 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const f32x16 (&acc
     }
   }
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    {
+  for (int i = 0; i < WTM / 32; ++i) {  // one 32-row slab at a time
+    if constexpr (MBE == 32) {
       const int r = lane & 31;
 #pragma unroll
       for (int j = 0; j < TN; ++j)
@@ -130,6 +135,16 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const f32x16 (&acc
           st[r * CPR + (c ^ (r & (CPR - 1)))] =
               make_float4(acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
         }
+    } else {
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int r = a * 16 + (lane & 15);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int c = j * 4 + (lane >> 4);
+          st[r * CPR + (c ^ (r & (CPR - 1)))] = make_float4(acc[2 * i + a][j][0], acc[2 * i + a][j][1], acc[2 * i + a][j][2], acc[2 * i + a][j][3]);
+        }
+      }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if constexpr (WIDE && EPI == EPI_QKV) {
@@ -290,14 +305,19 @@ template <int BM, int BN, int WM, int WN, bool TAPS, bool FP8>
 struct Tile {
   static constexpr int NW = WM * WN;
   static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave sub-tile
-  static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA blocks per wave
+  // bf16 runs v_mfma_f32_16x16x32_bf16 blocks (same bytes per FLOP as 32x32x16, measured ~10% faster next to the
+  // stage's global->LDS traffic), fp8 the scaled 32x32x64 blocks
+  static constexpr int MBE = FP8 ? 32 : 16;           // MFMA block edge
+  static constexpr int TM = WTM / MBE, TN = WTN / MBE;  // MFMA blocks per wave
   static constexpr int APW = BM / 8 / NW, BPW = BN / 8 / NW;  // 1 KB (8-row) load blocks per wave and stage
   static constexpr int ES = FP8 ? 1 : 2;              // bytes per element
   static constexpr int BKE = BK * 2 / ES;             // K values per 128-byte stage row
-  static constexpr int NKK = FP8 ? 2 : 4;             // MFMA K steps per stage
+  static constexpr int NKK = 2;                       // MFMA K steps per stage (32 bf16 or 64 fp8 values each)
   static constexpr int NSC = FP8 ? TM : 1;            // scale dwords per lane and stage
   static_assert(APW * NW * 8 == BM && BPW * NW * 8 == BN, "tile rows / waves mismatch");
+  static_assert(WTM % 32 == 0, "the epilogue works in 32-row slabs");
   typedef typename FragT<FP8>::type frag_t;
+  typedef typename AccT<MBE>::type acc_t;
 
   const uint8_t* asrc[APW];
   const uint8_t* bsrc[BPW];
@@ -373,15 +393,16 @@ struct Tile {
         bf[j] = join8(Lb[swz(r, c0)], Lb[swz(r, c0 + 2)]);
       }
     } else {
-      const int chunk = kk * 2 + (lane >> 5);
+      // 16 x 32 operand blocks: lane l holds row l % 16, K values [8 (l / 16), +8) of the step
+      const int chunk = kk * 4 + (lane >> 4);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(La[swz(wm * WTM + i * 32 + (lane & 31), chunk)]);
+      for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(La[swz(wm * WTM + i * 16 + (lane & 15), chunk)]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = as_bf16x8(Lb[swz(wn * WTN + j * 32 + (lane & 31), chunk)]);
+      for (int j = 0; j < TN; ++j) bf[j] = as_bf16x8(Lb[swz(wn * WTN + j * 16 + (lane & 15), chunk)]);
     }
   }
 
-  __device__ __forceinline__ void mma(f32x16 (&acc)[TM][TN], const frag_t (&af)[TM], const frag_t (&bf)[TN],
+  __device__ __forceinline__ void mma(acc_t (&acc)[TM][TN], const frag_t (&af)[TM], const frag_t (&bf)[TN],
                                       const uint32_t (&sd)[NSC], int kk) const {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -392,15 +413,49 @@ struct Tile {
           acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[i][j], 0, 0, 0, 127, 0, sc);
       } else {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
       }
+    }
+  }
+
+  // One 32-K step of 16 x 16 blocks, columns outermost: right after the MFMAs of column j, B fragment j (and, for
+  // j < TM, A fragment j into an) of step kn of buffers (La, Lb) is read, so one register set holds B across steps.
+  // With V the stage's 8 global->LDS loads (already issued in program order) go one per column.
+  template <bool V>
+  __device__ __forceinline__ void step16(acc_t (&acc)[TM][TN], const frag_t (&ac)[TM], frag_t (&an)[TM], frag_t (&bf)[TN],
+                                         const uint4* La, const uint4* Lb, int kn) const {
+    const int chunk = kn * 4 + (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], ac[i], acc[i][j], 0, 0, 0);
+      bf[j] = as_bf16x8(Lb[swz(wn * WTN + j * 16 + (lane & 15), chunk)]);
+      if (j < TM) an[j] = as_bf16x8(La[swz(wm * WTM + j * 16 + (lane & 15), chunk)]);
+    }
+    constexpr int NV = APW + BPW, VPC = (NV + TN - 1) / TN;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
+      if (V && j * VPC < NV) __builtin_amdgcn_sched_group_barrier(0x020, VPC, 0);
+      if (j < TM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
   }
 
   // One K stage from buffers (La, Lb) with scales sd.  Stage kt + 1 must already be in flight into (Na, Nb); after the
   // barrier the loads of stage kt + 2 go into (La, Lb, sd).
-  __device__ __forceinline__ void stage(f32x16 (&acc)[TM][TN], frag_t (&af)[2][TM], frag_t (&bf)[2][TN], uint4* La,
+  __device__ __forceinline__ void stage(acc_t (&acc)[TM][TN], frag_t (&af)[2][TM], frag_t (&bf)[2][TN], uint4* La,
                                         uint4* Lb, uint32_t (&sd)[NSC], const uint4* Na, const uint4* Nb, int kt, int KT) const {
+    if constexpr (MBE == 16) {
+      // bf16: step 0 reads step 1's fragments from (La, Lb); after the barrier step 1 reads the next stage's step 0
+      static_assert(NKK == 2 && TN >= TM && APW + BPW <= TN * 2, "step16 interleave");
+      step16<false>(acc, af[0], af[1], bf[0], La, Lb, 1);
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      __syncthreads();
+      issue(La, Lb, sd, min(kt + 2, KT - 1));
+      step16<true>(acc, af[1], af[0], bf[0], Na, Nb, 0);
+      return;
+    }
     constexpr int RPF = FP8 ? 2 : 1;  // LDS reads per fragment
     constexpr int NV = APW + BPW + (FP8 ? NSC : 0), ND = (TM + TN) * RPF, NM = TM * TN;
 #pragma unroll
@@ -435,8 +490,8 @@ struct Tile {
   }
 
   template <int EPI>
-  __device__ __forceinline__ void store(const f32x16 (&acc)[TM][TN], float4* st, int m0, int n0) const {
-    tile_store<EPI, TM, TN, WTM, WTN>(g, acc, st, m0 + wm * WTM, n0 + wn * WTN, lane);
+  __device__ __forceinline__ void store(const acc_t (&acc)[TM][TN], float4* st, int m0, int n0) const {
+    tile_store<EPI, MBE, TM, TN, WTM, WTN>(g, acc, st, m0 + wm * WTM, n0 + wn * WTN, lane);
   }
 };
 
