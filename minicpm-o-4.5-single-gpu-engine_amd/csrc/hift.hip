@@ -42,6 +42,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvDesc& c, int b, int out_
       switch (c.epi) {
         case EPI_STORE: *yp = v; break;
         case EPI_ELU: *yp = v > 0.f ? v : expm1f(v); break;
+        case EPI_SNAKE: *yp = pre_act(v, PRE_SNAKE, 0.f, c.alpha[co], c.inv[co]); break;
         case EPI_RES: *yp = __fadd_rn(v, c.res[row * c.ldy + co]); break;
         case EPI_ADD_RES: *yp = __fadd_rn(*yp, __fadd_rn(v, c.res[row * c.ldy + co])); break;
         case EPI_RES_MEAN: {
@@ -51,6 +52,87 @@ __device__ __forceinline__ void conv_epilogue(const ConvDesc& c, int b, int out_
           else if (c.sum_mode == 1) *sp = __fadd_rn(*sp, v);
           else *sp = __fdiv_rn(__fadd_rn(*sp, v), (float)c.sum_div);
         } break;
+      }
+    }
+  }
+}
+
+// the tensors the epilogue of four channels reads before it writes: the residual (r) and the output or the running
+// sum it accumulates into (t); loaded ahead so that a batch of rows has all its loads in flight
+__device__ __forceinline__ void conv_epilogue4_loads(const ConvDesc& c, size_t row, int co, float4& r, float4& t) {
+  if (c.epi == EPI_RES || c.epi == EPI_ADD_RES || c.epi == EPI_RES_MEAN) r = *(const float4*)(c.res + row * c.ldy + co);
+  if (c.epi == EPI_ADD_RES) t = *(const float4*)(c.y + row * c.ldy + co);
+  if (c.epi == EPI_RES_MEAN && c.sum_mode != 0) t = *(const float4*)(c.sum + row * c.ldy + co);
+}
+
+// epilogue of four consecutive channels co .. co + 3 of one output row (all inside Cout), with its loads already done
+// (r, t as conv_epilogue4_loads left them)
+// SNK: the caller may pass EPI_SNAKE (the fp32 kernels; kept out of the bf16 kernels, whose registers are full)
+template <bool SNK = false>
+__device__ __forceinline__ void conv_epilogue4_pre(const ConvDesc& c, size_t row, int co, float4 a, float4 r, float4 t) {
+  const float4 bb = *(const float4*)(c.bias + co);
+  float v[4] = {__fadd_rn(a.x, bb.x), __fadd_rn(a.y, bb.y), __fadd_rn(a.z, bb.z), __fadd_rn(a.w, bb.w)};
+  float* yp = c.y + row * c.ldy + co;
+  if (c.epi == EPI_STORE) {
+    *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
+  } else if (c.epi == EPI_ELU) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.f ? v[e] : expm1f(v[e]);
+    *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
+  } else if (SNK && c.epi == EPI_SNAKE) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = pre_act(v[e], PRE_SNAKE, 0.f, c.alpha[co + e], c.inv[co + e]);
+    *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    v[0] = __fadd_rn(v[0], r.x); v[1] = __fadd_rn(v[1], r.y); v[2] = __fadd_rn(v[2], r.z); v[3] = __fadd_rn(v[3], r.w);
+    if (c.epi == EPI_RES) {
+      *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
+    } else if (c.epi == EPI_ADD_RES) {
+      *(float4*)yp = make_float4(__fadd_rn(t.x, v[0]), __fadd_rn(t.y, v[1]), __fadd_rn(t.z, v[2]), __fadd_rn(t.w, v[3]));
+    } else {  // EPI_RES_MEAN
+      float* sp = c.sum + row * c.ldy + co;
+      if (c.sum_mode == 0) {
+        *(float4*)sp = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+        float o[4] = {__fadd_rn(t.x, v[0]), __fadd_rn(t.y, v[1]), __fadd_rn(t.z, v[2]), __fadd_rn(t.w, v[3])};
+        if (c.sum_mode == 2) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = __fdiv_rn(o[e], (float)c.sum_div);
+        }
+        *(float4*)sp = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+}
+
+// conv_epilogue4 with its own loads
+template <bool SNK = false>
+__device__ __forceinline__ void conv_epilogue4(const ConvDesc& c, size_t row, int co, float4 a) {
+  float4 r, t;
+  conv_epilogue4_loads(c, row, co, r, t);
+  conv_epilogue4_pre<SNK>(c, row, co, a, r, t);
+}
+
+// the last n < 4 channels co .. co + n - 1 of a Cout that is not a multiple of 4, element by element
+template <bool SNK = false>
+__device__ __forceinline__ void conv_epilogue_part(const ConvDesc& c, size_t orow, int co0, int n, float4 v) {
+  const float vv[4] = {v.x, v.y, v.z, v.w};
+  for (int e = 0; e < 4 && e < n; ++e) {
+    const int co = co0 + e;
+    float x = __fadd_rn(vv[e], c.bias[co]);
+    float* yp = c.y + orow * c.ldy + co;
+    if (c.epi == EPI_STORE) *yp = x;
+    else if (c.epi == EPI_ELU) *yp = x > 0.f ? x : expm1f(x);
+    else if (SNK && c.epi == EPI_SNAKE) *yp = pre_act(x, PRE_SNAKE, 0.f, c.alpha[co], c.inv[co]);
+    else {
+      x = __fadd_rn(x, c.res[orow * c.ldy + co]);
+      if (c.epi == EPI_RES) *yp = x;
+      else if (c.epi == EPI_ADD_RES) *yp = __fadd_rn(*yp, x);
+      else {
+        float* sp = c.sum + orow * c.ldy + co;
+        if (c.sum_mode == 0) *sp = x;
+        else if (c.sum_mode == 1) *sp = __fadd_rn(*sp, x);
+        else *sp = __fdiv_rn(__fadd_rn(*sp, x), (float)c.sum_div);
       }
     }
   }
@@ -296,6 +378,163 @@ __global__ void __launch_bounds__(256) conv_f32_kernel(ConvDesc c) {
   }
 }
 
+// The same fp32 convolution with its operands copied straight into LDS (global_load_lds_dwordx4, no register staging
+// and no LDS stores), for Cin a multiple of 32 and 16-byte rows.  A stage is one tap and 32 input channels: 128
+// activation rows and 32 WN weight rows of 128 bytes, 16-byte chunks XOR-swizzled by (row / 2) % 8; the lanes of an
+// instruction name the logical chunk that lands in their physical slot.  Rows outside the item (zero padding) and
+// output channels past Cout fetch a 16-byte zero block instead.  A fragment read of 16 bytes gives a lane four K
+// values of its row, which feed four v_mfma_f32_32x32x2f32: lane half h of read q holds K values 4 (2 q + h) .. + 3,
+// so MFMA (q, m) sums the K pair (8 q + m, 8 q + 4 + m) on both operands.  The activation's pre-activation (leaky ReLU
+// or Snake) is applied to the fragment after the read (zero rows stay zero under both).  Two LDS stages, separate
+// objects, the K loop unrolled by two: the loads of stage s + 1 are issued before the MFMAs of stage s.
+__device__ __align__(16) float conv_zero16[4];  // never written: the load source of padding rows
+
+__device__ __forceinline__ int fswz(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr int FD_MAXC = 512;  // Snake: the per-channel parameters are staged in LDS (no global load between the stages)
+
+template <int WN, int PRE>
+__global__ void __launch_bounds__(256, 2) conv_f32_dma_kernel(ConvDesc c) {
+  constexpr int BN = 32 * WN, WM = 4 / WN, WTM = F_BM / WM, TM = WTM / 32;
+  constexpr int RA = F_BM / 8, NB = RA + BN / 8, PW = NB / 4;  // 8-row load blocks: activations, all, per wave
+  static_assert(NB % 4 == 0, "load blocks per wave");
+  __shared__ uint4 sA0[F_BM * 8], sA1[F_BM * 8], sB0[BN * 8], sB1[BN * 8];
+  __shared__ float s_al[PRE == PRE_SNAKE ? FD_MAXC : 1], s_iv[PRE == PRE_SNAKE ? FD_MAXC : 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
+  const int Tin = c.in_len[b], Tout = c.out_len[b];
+  const int oo = c.off_out[ph];
+  const int r_lo = oo >= 0 ? 0 : (-oo + c.s_out - 1) / c.s_out;
+  const int r_hi = Tout - 1 - oo < 0 ? -1 : (Tout - 1 - oo) / c.s_out;
+  const int r0 = r_lo + blockIdx.x * F_BM;
+  if (r0 > r_hi) return;
+  const int co0 = blockIdx.y * BN;
+  const int Cin = c.Cin, Cout = c.Cout, taps = c.taps, ldx = c.ldx, d_in = c.d_in;
+  const int nck = Cin / 32, S = taps * nck;
+  if constexpr (PRE == PRE_SNAKE) {
+    for (int i = tid; i < Cin; i += 256) { s_al[i] = c.alpha[i]; s_iv[i] = c.inv[i]; }
+  }
+  const float* xb = c.x + (size_t)c.in_off[b] * ldx;
+  const float* wph = c.w + (size_t)ph * Cout * taps * Cin;
+  // this lane's rows of its load blocks: activation row base (tap 0) or weight row, and its logical chunk
+  int rbase[PW], lch[PW];
+  bool rok[PW];
+#pragma unroll
+  for (int p = 0; p < PW; ++p) {
+    const int blk = wave + 4 * p, trow = (blk < RA ? blk : blk - RA) * 8 + (lane >> 3);
+    lch[p] = (lane & 7) ^ ((trow >> 1) & 7);
+    if (blk < RA) {
+      const int row = r0 + trow;
+      rok[p] = row <= r_hi;
+      rbase[p] = row * c.s_in + c.off_in[ph];
+    } else {
+      rok[p] = co0 + trow < Cout;
+      rbase[p] = co0 + trow;
+    }
+  }
+  auto issue = [&](uint4* dA, uint4* dB, int s) __attribute__((always_inline)) {
+    const int j = s / nck, ci = (s - j * nck) * 32;
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int blk = wave + 4 * p;
+      const float* src = conv_zero16;
+      uint4* dst;
+      if (blk < RA) {
+        const int in_row = rbase[p] + j * d_in;
+        if (rok[p] && in_row >= 0 && in_row < Tin) src = xb + (size_t)in_row * ldx + ci + lch[p] * 4;
+        dst = dA + blk * 64;
+      } else {
+        if (rok[p]) src = wph + ((size_t)rbase[p] * taps + j) * Cin + ci + lch[p] * 4;
+        dst = dB + (blk - RA) * 64;
+      }
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)dst, 16, 0, 0);
+    }
+  };
+  f32x16 acc[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  const float slope = c.slope;
+  auto compute = [&](const uint4* A, const uint4* B, int s) __attribute__((always_inline)) {
+    const int ci = (s - (s / nck) * nck) * 32;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int ch = 2 * q + (lane >> 5);
+      const float4 wv = *(const float4*)&B[fswz(wn * 32 + (lane & 31), ch)];
+      float4 al = make_float4(0.f, 0.f, 0.f, 0.f), iv = al;
+      if constexpr (PRE == PRE_SNAKE) {
+        al = *(const float4*)(s_al + ci + 4 * ch);
+        iv = *(const float4*)(s_iv + ci + 4 * ch);
+      }
+      float a[TM][4];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const float4 v = *(const float4*)&A[fswz(wm * WTM + i * 32 + (lane & 31), ch)];
+        a[i][0] = v.x; a[i][1] = v.y; a[i][2] = v.z; a[i][3] = v.w;
+        if constexpr (PRE != PRE_NONE) {
+          a[i][0] = pre_act(a[i][0], PRE, slope, al.x, iv.x);
+          a[i][1] = pre_act(a[i][1], PRE, slope, al.y, iv.y);
+          a[i][2] = pre_act(a[i][2], PRE, slope, al.z, iv.z);
+          a[i][3] = pre_act(a[i][3], PRE, slope, al.w, iv.w);
+        }
+      }
+      const float w[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[m], a[i][m], acc[i], 0, 0, 0);
+    }
+  };
+  issue(sA0, sB0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int s = 0; s < S; s += 2) {
+    if (s + 1 < S) issue(sA1, sB1, s + 1);
+    compute(sA0, sB0, s);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (s + 1 < S) {
+      if (s + 2 < S) issue(sA0, sB0, s + 2);
+      compute(sA1, sB1, s + 1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+  }
+  // epilogue through a 4 KB LDS slab per wave (the stage buffers are free after the last barrier): each 32 x 32 block
+  // goes in as the accumulators lie (lane: row lane % 32, channels q 8 + (lane / 32) 4 ..) and comes back as whole row
+  // segments, eight lanes per row of 32 channels, so the output and residual accesses are 16 bytes per lane
+  float4* st = (float4*)sA0 + wave * 256;
+  const int ncols = min(32, Cout - (co0 + wn * 32));
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    {
+      const int t = lane & 31;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c4 = q * 2 + (lane >> 5);
+        st[t * 8 + (c4 ^ (t & 7))] = make_float4(acc[i][q * 4], acc[i][q * 4 + 1], acc[i][q * 4 + 2], acc[i][q * 4 + 3]);
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int c4 = lane & 7;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int row = rr * 8 + (lane >> 3);
+      const int r = r0 + wm * WTM + i * 32 + row;
+      const float4 v = st[row * 8 + (c4 ^ (row & 7))];
+      if (r > r_hi || c4 * 4 >= ncols) continue;
+      const size_t orow = (size_t)c.out_off[b] + (size_t)(r * c.s_out + oo);
+      if (c4 * 4 + 3 < ncols) conv_epilogue4<true>(c, orow, co0 + wn * 32 + c4 * 4, v);
+      else conv_epilogue_part<true>(c, orow, co0 + wn * 32 + c4 * 4, ncols - c4 * 4, v);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+}
+
 // bf16-MFMA convolution (fp32 activations in HBM, bf16 operands, fp32 accumulation) for stride-1 convs and the
 // polyphase transposed convs.  A workgroup owns BM output rows x 64 output channels; its four waves own BM / 4 rows
 // each.  For every 64-channel input chunk the input rows of all taps form one slab of BM + (taps - 1) |d| rows, staged
@@ -314,78 +553,6 @@ __device__ __forceinline__ float pre_fast(float v, int pre, float slope, float a
     return v + inv * (s * s);
   }
   return v;
-}
-
-// the tensors the epilogue of four channels reads before it writes: the residual (r) and the output or the running
-// sum it accumulates into (t); loaded ahead so that a batch of rows has all its loads in flight
-__device__ __forceinline__ void conv_epilogue4_loads(const ConvDesc& c, size_t row, int co, float4& r, float4& t) {
-  if (c.epi == EPI_RES || c.epi == EPI_ADD_RES || c.epi == EPI_RES_MEAN) r = *(const float4*)(c.res + row * c.ldy + co);
-  if (c.epi == EPI_ADD_RES) t = *(const float4*)(c.y + row * c.ldy + co);
-  if (c.epi == EPI_RES_MEAN && c.sum_mode != 0) t = *(const float4*)(c.sum + row * c.ldy + co);
-}
-
-// epilogue of four consecutive channels co .. co + 3 of one output row (all inside Cout), with its loads already done
-// (r, t as conv_epilogue4_loads left them)
-__device__ __forceinline__ void conv_epilogue4_pre(const ConvDesc& c, size_t row, int co, float4 a, float4 r, float4 t) {
-  const float4 bb = *(const float4*)(c.bias + co);
-  float v[4] = {__fadd_rn(a.x, bb.x), __fadd_rn(a.y, bb.y), __fadd_rn(a.z, bb.z), __fadd_rn(a.w, bb.w)};
-  float* yp = c.y + row * c.ldy + co;
-  if (c.epi == EPI_STORE) {
-    *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
-  } else if (c.epi == EPI_ELU) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.f ? v[e] : expm1f(v[e]);
-    *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
-  } else {
-    v[0] = __fadd_rn(v[0], r.x); v[1] = __fadd_rn(v[1], r.y); v[2] = __fadd_rn(v[2], r.z); v[3] = __fadd_rn(v[3], r.w);
-    if (c.epi == EPI_RES) {
-      *(float4*)yp = make_float4(v[0], v[1], v[2], v[3]);
-    } else if (c.epi == EPI_ADD_RES) {
-      *(float4*)yp = make_float4(__fadd_rn(t.x, v[0]), __fadd_rn(t.y, v[1]), __fadd_rn(t.z, v[2]), __fadd_rn(t.w, v[3]));
-    } else {  // EPI_RES_MEAN
-      float* sp = c.sum + row * c.ldy + co;
-      if (c.sum_mode == 0) {
-        *(float4*)sp = make_float4(v[0], v[1], v[2], v[3]);
-      } else {
-        float o[4] = {__fadd_rn(t.x, v[0]), __fadd_rn(t.y, v[1]), __fadd_rn(t.z, v[2]), __fadd_rn(t.w, v[3])};
-        if (c.sum_mode == 2) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = __fdiv_rn(o[e], (float)c.sum_div);
-        }
-        *(float4*)sp = make_float4(o[0], o[1], o[2], o[3]);
-      }
-    }
-  }
-}
-
-// conv_epilogue4 with its own loads
-__device__ __forceinline__ void conv_epilogue4(const ConvDesc& c, size_t row, int co, float4 a) {
-  float4 r, t;
-  conv_epilogue4_loads(c, row, co, r, t);
-  conv_epilogue4_pre(c, row, co, a, r, t);
-}
-
-// the last n < 4 channels co .. co + n - 1 of a Cout that is not a multiple of 4, element by element
-__device__ __forceinline__ void conv_epilogue_part(const ConvDesc& c, size_t orow, int co0, int n, float4 v) {
-  const float vv[4] = {v.x, v.y, v.z, v.w};
-  for (int e = 0; e < 4 && e < n; ++e) {
-    const int co = co0 + e;
-    float x = __fadd_rn(vv[e], c.bias[co]);
-    float* yp = c.y + orow * c.ldy + co;
-    if (c.epi == EPI_STORE) *yp = x;
-    else if (c.epi == EPI_ELU) *yp = x > 0.f ? x : expm1f(x);
-    else {
-      x = __fadd_rn(x, c.res[orow * c.ldy + co]);
-      if (c.epi == EPI_RES) *yp = x;
-      else if (c.epi == EPI_ADD_RES) *yp = __fadd_rn(*yp, x);
-      else {
-        float* sp = c.sum + orow * c.ldy + co;
-        if (c.sum_mode == 0) *sp = x;
-        else if (c.sum_mode == 1) *sp = __fadd_rn(*sp, x);
-        else *sp = __fdiv_rn(__fadd_rn(*sp, x), (float)c.sum_div);
-      }
-    }
-  }
 }
 
 template <int BM>
@@ -1059,8 +1226,8 @@ __global__ void __launch_bounds__(64 * CS_WAVES) conv_f32_split_kernel(ConvDesc 
   const int ncols = min(NB * 32, c.Cout - co0);
   if (ro > r_hi || cn >= ncols) return;
   const size_t orow = (size_t)c.out_off[b] + (size_t)(ro * c.s_out + oo);
-  if (cn + 3 < ncols) conv_epilogue4(c, orow, co0 + cn, sum);
-  else conv_epilogue_part(c, orow, co0 + cn, ncols - cn, sum);
+  if (cn + 3 < ncols) conv_epilogue4<true>(c, orow, co0 + cn, sum);
+  else conv_epilogue_part<true>(c, orow, co0 + cn, ncols - cn, sum);
 }
 
 // f0 = |w . x + b| per frame (one wave per frame row, Linear(C -> 1) then abs)
@@ -1238,6 +1405,17 @@ __global__ void __launch_bounds__(256) istft_kernel(const float* x, const int* f
   }
 }
 
+// y = Snake(x) for a packed [rows, C] buffer, four channels per thread (the same per-element function the convs
+// apply on load, so a conv reading y with no pre-activation sees the values it would have computed)
+__global__ void __launch_bounds__(256) snake_kernel(const float4* x, int C4, long n4, const float* alpha, const float* inv, float4* y) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+    const int c = (int)(i % C4) * 4;
+    const float4 v = x[i];
+    y[i] = make_float4(pre_act(v.x, PRE_SNAKE, 0.f, alpha[c], inv[c]), pre_act(v.y, PRE_SNAKE, 0.f, alpha[c + 1], inv[c + 1]),
+                       pre_act(v.z, PRE_SNAKE, 0.f, alpha[c + 2], inv[c + 2]), pre_act(v.w, PRE_SNAKE, 0.f, alpha[c + 3], inv[c + 3]));
+  }
+}
+
 // rows 1.. of each item's ups output were written one row down; row 0 = input row 1 (ReflectionPad1d((1, 0)))
 __global__ void reflect_kernel(float* x, int C, const int* off, int n_items) {
   const int it = blockIdx.y;
@@ -1250,6 +1428,15 @@ __global__ void reflect_kernel(float* x, int C, const int* off, int n_items) {
 inline unsigned cdiv(long long a, long long b) { return (unsigned)((a + b - 1) / b); }
 
 }  // namespace
+
+hipError_t snake_rows(const float* x, int C, long rows, const float* alpha, const float* inv, float* y, hipStream_t st) {
+  if (rows <= 0) return hipSuccess;
+  if (C % 4 || x == y || ((size_t)x & 15) || ((size_t)y & 15)) return hipErrorInvalidValue;
+  const long n4 = rows * (C / 4);
+  const int grid = (int)std::min<long>((n4 + 255) / 256, 8192);
+  hipLaunchKernelGGL(snake_kernel, dim3(grid), dim3(256), 0, st, (const float4*)x, C / 4, n4, alpha, inv, (float4*)y);
+  return hipGetLastError();
+}
 
 hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
   if (c.n_items <= 0 || max_rows <= 0) return hipSuccess;
@@ -1271,6 +1458,24 @@ hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
   // 64 output channels per workgroup, 32 where the output has no more (conv_post's 18)
   // undilated convs whose Cin is not a multiple of 32 take their K flat
   const bool flat = c.d_in == 1 && c.Cin % F_BK != 0;
+  // the DMA-staged kernel: 32-channel K stages and 16-byte rows (activations and weights)
+  if (c.Cin % 32 == 0 && c.ldx % 4 == 0 && ((size_t)c.x & 15) == 0 && ((size_t)c.w & 15) == 0 &&
+      (c.pre == PRE_NONE || c.pre == PRE_LEAKY || (c.pre == PRE_SNAKE && c.Cin <= FD_MAXC))) {
+    const int wn = c.Cout <= 32 ? 1 : 2;
+    dim3 grid(cdiv(max_rows, F_BM), cdiv(c.Cout, 32 * wn), c.n_items * c.n_phase);
+#define T2W_FD(W, P) hipLaunchKernelGGL((conv_f32_dma_kernel<W, P>), grid, dim3(256), 0, st, c)
+    if (wn == 1) {
+      if (c.pre == PRE_NONE) T2W_FD(1, PRE_NONE);
+      else if (c.pre == PRE_LEAKY) T2W_FD(1, PRE_LEAKY);
+      else T2W_FD(1, PRE_SNAKE);
+    } else {
+      if (c.pre == PRE_NONE) T2W_FD(2, PRE_NONE);
+      else if (c.pre == PRE_LEAKY) T2W_FD(2, PRE_LEAKY);
+      else T2W_FD(2, PRE_SNAKE);
+    }
+#undef T2W_FD
+    return hipGetLastError();
+  }
   if (c.Cout <= 32) {
     dim3 grid(cdiv(max_rows, F_BM), 1, c.n_items * c.n_phase);
     if (flat) hipLaunchKernelGGL((conv_f32_kernel<1, true>), grid, dim3(256), 0, st, c);
@@ -1291,6 +1496,7 @@ size_t conv_bf16_lds(int BM) {
 
 hipError_t conv_bf16(const ConvDesc& c, const bf16_t* wbf, int max_rows, hipStream_t st) {
   if (c.n_items <= 0 || max_rows <= 0) return hipSuccess;
+  if (c.epi == EPI_SNAKE) return hipErrorInvalidValue;  // fp32 convs only
   if (c.n_phase < 1 || c.n_phase > 8 || c.s_in != 1 || c.ldx % 4 || c.ldy % 4) return hipErrorInvalidValue;
   const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
   if (span > HB_MAXSPAN) return hipErrorInvalidValue;
@@ -1359,6 +1565,7 @@ bool resblock_pair_fits(int C, int k, int dil) {
 
 hipError_t resblock_pair_bf16(const ConvDesc& c1, const ConvDesc& c2, int max_rows, hipStream_t st) {
   if (c1.n_items <= 0 || max_rows <= 0) return hipSuccess;
+  if (c2.epi == EPI_SNAKE) return hipErrorInvalidValue;  // fp32 convs only
   const int C = c1.Cin, k = c1.taps;
   const bool same = c1.Cout == C && c2.Cin == C && c2.Cout == C && c2.taps == k && c1.ldx == C && c1.ldy == C && c2.ldx == C &&
                     c2.ldy == C && c1.n_items == c2.n_items && c1.in_off == c2.out_off && c1.in_len == c2.out_len;

@@ -124,10 +124,15 @@ ConvDesc conv_desc(const Ctx& x, const t2w_conv& w, const float* in, int Cin, in
 // fused ResBlock dilations below this many workgroups leave the chip half idle: two convs with smaller tiles instead
 constexpr long kPairMinBlocks = 128;
 
+// whether run() takes c to the bf16 MFMA convolution (else the fp32 one)
+bool on_bf16(const Ctx& x, const ConvDesc& c) {
+  const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
+  return x.bf16 && c.wbf && c.s_in == 1 && span <= 64 && c.ldx % 4 == 0 && c.ldy % 4 == 0;
+}
+
 int run(const Ctx& x, const ConvDesc& c, int out_cls, const char* what) {
   const int mr = x.L.mx[out_cls] / c.s_out + 2;
-  const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
-  if (x.bf16 && c.wbf && c.s_in == 1 && span <= 64 && c.ldx % 4 == 0 && c.ldy % 4 == 0)
+  if (on_bf16(x, c))
     H_CHECK(conv_bf16(c, c.wbf, mr, x.st), what);
   else
     H_CHECK(conv_f32(c, mr, x.st), what);
@@ -138,9 +143,11 @@ int run(const Ctx& x, const ConvDesc& c, int out_cls, const char* what) {
 // goes to `sum` (mean of the stage's ResBlocks, sum_mode 0 / 1 / 2) or, with add_into, is added into add_into.  z and tmp
 // are scratch (z may be `in`, which is then overwritten).  A dilation runs as one fused kernel (conv1's output kept in
 // LDS, written to a scratch buffer other than its input) when the bf16 path fuses and the grid fills the chip, else as
-// two convs through a scratch buffer (the second in place when its input is scratch).
-int resblock(const Ctx& x, const t2w_resblock& rb, int k, const float* in, float* z, float* tmp, int C, int cls, float* sum, int sum_mode,
-             float* add_into) {
+// two convs through a scratch buffer (the second in place when its input is scratch).  Two fp32 convs take their
+// Snakes out of the tap loop (where an element's Snake would be evaluated once per tap): snake1 of the input into
+// `act` (a scratch buffer no other argument names) and snake2 in conv1's epilogue; the values are the same.
+int resblock(const Ctx& x, const t2w_resblock& rb, int k, const float* in, float* z, float* tmp, float* act, int C, int cls, float* sum,
+             int sum_mode, float* add_into) {
   const t2w_hift_dims& d = x.h->d;
   const int mr = x.L.mx[cls] + 2;
   auto other = [&](const float* p) { return p == z ? tmp : z; };  // a scratch buffer that is not p
@@ -170,6 +177,15 @@ int resblock(const Ctx& x, const t2w_resblock& rb, int k, const float* in, float
     if (fused) {
       H_CHECK(resblock_pair_bf16(c1, c2, mr, x.st), "resblock pair");
     } else {
+      if (!on_bf16(x, c1) && !on_bf16(x, c2) && C % 4 == 0) {
+        H_CHECK(snake_rows(cur, C, x.L.tot[cls], c1.alpha, c1.inv, act, x.st), "resblock snake1");
+        c1.x = act;
+        c1.pre = PRE_NONE;
+        c1.epi = EPI_SNAKE;
+        c1.alpha = c2.alpha;
+        c1.inv = c2.inv;
+        c2.pre = PRE_NONE;
+      }
       if (run(x, c1, cls, "resblock conv1")) return 1;
       if (run(x, c2, cls, "resblock conv2")) return 1;
     }
@@ -304,10 +320,11 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
       ConvDesc c = r == 1 ? conv_desc(x, w.src_down[i], B.stft, nsrc, C_S2, B.Z2, cout, cls, 1, 1, 1, 0)
                           : conv_desc(x, w.src_down[i], B.stft, nsrc, C_S2, B.Z2, cout, cls, 2 * r, 1, r, r / 2);
       if (run(x, c, cls, "source down")) return 1;
-      if (resblock(x, w.src_res[i], d.src_kernels[i], B.Z2, B.Z2, B.TMP, cout, cls, nullptr, 0, B.XN)) return 1;
+      // X (the stage input) is dead once the transposed conv has read it: the ResBlocks' Snake scratch
+      if (resblock(x, w.src_res[i], d.src_kernels[i], B.Z2, B.Z2, B.TMP, X, cout, cls, nullptr, 0, B.XN)) return 1;
     }
     for (int j = 0; j < 3; ++j)
-      if (resblock(x, w.res[i * 3 + j], d.res_kernels[j], B.XN, B.Z, B.TMP, cout, cls, Sb, j, nullptr)) return 1;
+      if (resblock(x, w.res[i * 3 + j], d.res_kernels[j], B.XN, B.Z, B.TMP, X, cout, cls, Sb, j, nullptr)) return 1;
     std::swap(X, Sb);  // the mean is the next stage's input
   }
   {

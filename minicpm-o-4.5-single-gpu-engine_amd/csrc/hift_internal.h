@@ -6,7 +6,8 @@
 namespace t2w {
 
 enum PreAct { PRE_NONE = 0, PRE_LEAKY = 1, PRE_SNAKE = 2 };
-enum ConvEpi { EPI_STORE = 0, EPI_ELU = 1, EPI_RES = 2, EPI_ADD_RES = 3, EPI_RES_MEAN = 4 };
+// EPI_SNAKE: y = Snake(conv + bias) with the descriptor's alpha / inv (the next conv's pre-activation, applied once)
+enum ConvEpi { EPI_STORE = 0, EPI_ELU = 1, EPI_RES = 2, EPI_ADD_RES = 3, EPI_RES_MEAN = 4, EPI_SNAKE = 5 };
 
 // y[out_off[b] + r * s_out + off_out[ph], co] = epi(bias[co] + sum_{j, ci} w[ph, co, j, ci] act(x[in_off[b] + r * s_in +
 // j * d_in + off_in[ph], ci])), inputs outside [0, in_len[b]) read as zero.
@@ -45,6 +46,8 @@ hipError_t stft16(const float* s, const int* smp_off, const int* smp_len, const 
 hipError_t istft16(const float* x, const int* fr_off, const int* fr_len, const int* smp_off, int n_items, int max_smp, const float* win,
                    float limit, float* out, hipStream_t st);
 hipError_t reflect_rows(float* x, int C, const int* off, int n_items, hipStream_t st);
+// y = Snake(x) element by element over `rows` packed rows of C channels (C % 4 == 0), y != x
+hipError_t snake_rows(const float* x, int C, long rows, const float* alpha, const float* inv, float* y, hipStream_t st);
 
 int set_error(const char* what, hipError_t e);  // records the message for t2w_last_error(); returns 1
 
