@@ -384,24 +384,23 @@ __global__ void __launch_bounds__(256) conv_f32_kernel(ConvDesc c) {
 // instruction name the logical chunk that lands in their physical slot.  Rows outside the item (zero padding) and
 // output channels past Cout fetch a 16-byte zero block instead.  A fragment read of 16 bytes gives a lane four K
 // values of its row, which feed four v_mfma_f32_32x32x2f32: lane half h of read q holds K values 4 (2 q + h) .. + 3,
-// so MFMA (q, m) sums the K pair (8 q + m, 8 q + 4 + m) on both operands.  The activation's pre-activation (leaky ReLU
-// or Snake) is applied to the fragment after the read (zero rows stay zero under both).  Two LDS stages, separate
-// objects, the K loop unrolled by two: the loads of stage s + 1 are issued before the MFMAs of stage s.
+// so MFMA (q, m) sums the K pair (8 q + m, 8 q + 4 + m) on both operands.  A leaky-ReLU pre-activation is applied to the
+// fragment after the read (zero rows stay zero); Snake convs take conv_f32_kernel (evaluated once per element and stage
+// there, not once per element, tap and wave).  Two LDS stages, separate objects, the K loop unrolled by two: the loads
+// of stage s + 1 are issued before the MFMAs of stage s.
 __device__ __align__(16) float conv_zero16[4];  // never written: the load source of padding rows
 
 __device__ __forceinline__ int fswz(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-constexpr int FD_MAXC = 512;  // Snake: the per-channel parameters are staged in LDS (no global load between the stages)
-
 template <int WN, int PRE>
 __global__ void __launch_bounds__(256, 2) conv_f32_dma_kernel(ConvDesc c) {
   constexpr int BN = 32 * WN, WM = 4 / WN, WTM = F_BM / WM, TM = WTM / 32;
   constexpr int RA = F_BM / 8, NB = RA + BN / 8, PW = NB / 4;  // 8-row load blocks: activations, all, per wave
   static_assert(NB % 4 == 0, "load blocks per wave");
+  static_assert(PRE == PRE_NONE || PRE == PRE_LEAKY, "Snake convs take the register-staged kernel (or Snake out of the conv)");
   __shared__ uint4 sA0[F_BM * 8], sA1[F_BM * 8], sB0[BN * 8], sB1[BN * 8];
-  __shared__ float s_al[PRE == PRE_SNAKE ? FD_MAXC : 1], s_iv[PRE == PRE_SNAKE ? FD_MAXC : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int b = blockIdx.z / c.n_phase, ph = blockIdx.z % c.n_phase;
@@ -414,9 +413,6 @@ __global__ void __launch_bounds__(256, 2) conv_f32_dma_kernel(ConvDesc c) {
   const int co0 = blockIdx.y * BN;
   const int Cin = c.Cin, Cout = c.Cout, taps = c.taps, ldx = c.ldx, d_in = c.d_in;
   const int nck = Cin / 32, S = taps * nck;
-  if constexpr (PRE == PRE_SNAKE) {
-    for (int i = tid; i < Cin; i += 256) { s_al[i] = c.alpha[i]; s_iv[i] = c.inv[i]; }
-  }
   const float* xb = c.x + (size_t)c.in_off[b] * ldx;
   const float* wph = c.w + (size_t)ph * Cout * taps * Cin;
   // this lane's rows of its load blocks: activation row base (tap 0) or weight row, and its logical chunk
@@ -459,27 +455,19 @@ __global__ void __launch_bounds__(256, 2) conv_f32_dma_kernel(ConvDesc c) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
   const float slope = c.slope;
-  auto compute = [&](const uint4* A, const uint4* B, int s) __attribute__((always_inline)) {
-    const int ci = (s - (s / nck) * nck) * 32;
+  auto compute = [&](const uint4* A, const uint4* B) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int ch = 2 * q + (lane >> 5);
       const float4 wv = *(const float4*)&B[fswz(wn * 32 + (lane & 31), ch)];
-      float4 al = make_float4(0.f, 0.f, 0.f, 0.f), iv = al;
-      if constexpr (PRE == PRE_SNAKE) {
-        al = *(const float4*)(s_al + ci + 4 * ch);
-        iv = *(const float4*)(s_iv + ci + 4 * ch);
-      }
       float a[TM][4];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const float4 v = *(const float4*)&A[fswz(wm * WTM + i * 32 + (lane & 31), ch)];
         a[i][0] = v.x; a[i][1] = v.y; a[i][2] = v.z; a[i][3] = v.w;
-        if constexpr (PRE != PRE_NONE) {
-          a[i][0] = pre_act(a[i][0], PRE, slope, al.x, iv.x);
-          a[i][1] = pre_act(a[i][1], PRE, slope, al.y, iv.y);
-          a[i][2] = pre_act(a[i][2], PRE, slope, al.z, iv.z);
-          a[i][3] = pre_act(a[i][3], PRE, slope, al.w, iv.w);
+        if constexpr (PRE == PRE_LEAKY) {
+#pragma unroll
+          for (int m = 0; m < 4; ++m) a[i][m] = pre_act(a[i][m], PRE_LEAKY, slope, 0.f, 0.f);
         }
       }
       const float w[4] = {wv.x, wv.y, wv.z, wv.w};
@@ -494,12 +482,12 @@ __global__ void __launch_bounds__(256, 2) conv_f32_dma_kernel(ConvDesc c) {
   __syncthreads();
   for (int s = 0; s < S; s += 2) {
     if (s + 1 < S) issue(sA1, sB1, s + 1);
-    compute(sA0, sB0, s);
+    compute(sA0, sB0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (s + 1 < S) {
       if (s + 2 < S) issue(sA0, sB0, s + 2);
-      compute(sA1, sB1, s + 1);
+      compute(sA1, sB1);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     }
@@ -1460,18 +1448,16 @@ hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st) {
   const bool flat = c.d_in == 1 && c.Cin % F_BK != 0;
   // the DMA-staged kernel: 32-channel K stages and 16-byte rows (activations and weights)
   if (c.Cin % 32 == 0 && c.ldx % 4 == 0 && ((size_t)c.x & 15) == 0 && ((size_t)c.w & 15) == 0 &&
-      (c.pre == PRE_NONE || c.pre == PRE_LEAKY || (c.pre == PRE_SNAKE && c.Cin <= FD_MAXC))) {
+      (c.pre == PRE_NONE || c.pre == PRE_LEAKY)) {
     const int wn = c.Cout <= 32 ? 1 : 2;
     dim3 grid(cdiv(max_rows, F_BM), cdiv(c.Cout, 32 * wn), c.n_items * c.n_phase);
 #define T2W_FD(W, P) hipLaunchKernelGGL((conv_f32_dma_kernel<W, P>), grid, dim3(256), 0, st, c)
     if (wn == 1) {
       if (c.pre == PRE_NONE) T2W_FD(1, PRE_NONE);
-      else if (c.pre == PRE_LEAKY) T2W_FD(1, PRE_LEAKY);
-      else T2W_FD(1, PRE_SNAKE);
+      else T2W_FD(1, PRE_LEAKY);
     } else {
       if (c.pre == PRE_NONE) T2W_FD(2, PRE_NONE);
-      else if (c.pre == PRE_LEAKY) T2W_FD(2, PRE_LEAKY);
-      else T2W_FD(2, PRE_SNAKE);
+      else T2W_FD(2, PRE_LEAKY);
     }
 #undef T2W_FD
     return hipGetLastError();
