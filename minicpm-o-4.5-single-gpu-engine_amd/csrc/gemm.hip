@@ -100,11 +100,7 @@ template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
 hipError_t launch_tile(const GemmArgs& g, hipStream_t st) {
   const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
   if (g.w_scale) {
-    // fp8 fragments are twice as wide: 64x128 wave tiles would spill, so fp8 runs the 64x64-wave tiles only
-    if constexpr (BM / WM * BN / WN <= 64 * 64)
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, TAPS, true>), dim3(gm * gn), dim3(64 * WM * WN), 0, st, g);
-    else
-      return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, TAPS, true>), dim3(gm * gn), dim3(64 * WM * WN), 0, st, g);
   } else {
     if constexpr (EPI == EPI_GELU_MX8)
       return hipErrorInvalidValue;  // fp8 output only follows fp8 GEMMs
@@ -114,15 +110,28 @@ hipError_t launch_tile(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
-// g without its first r rows (bf16 operands): activation rows (taps: their frame ids), output rows, qkv rows and slots
+// g without its first r rows: activation rows (taps: their frame ids; fp8: codes and their scale rows), output rows
+// (fp8 output: codes and block scales), qkv rows and slots
 template <int EPI>
 GemmArgs rows_from(const GemmArgs& g, int r) {
   GemmArgs h = g;
   h.M = g.M - r;
-  if (g.a_src) h.a_src = g.a_src + r;
-  else h.A = g.A + (size_t)r * g.lda;
-  if (EPI == EPI_F32) h.C = (float*)g.C + (size_t)r * g.ldc;
-  else h.C = (uint16_t*)g.C + (size_t)r * g.ldc;  // bf16 or fp16 rows
+  if (g.a_src) {
+    h.a_src = g.a_src + r;
+  } else if (g.w_scale) {
+    h.A = (const bf16_t*)((const uint8_t*)g.A + (size_t)r * g.lda);
+    h.a_scale = g.a_scale + (size_t)r * g.a_sld;
+  } else {
+    h.A = g.A + (size_t)r * g.lda;
+  }
+  if (EPI == EPI_F32) {
+    h.C = (float*)g.C + (size_t)r * g.ldc;
+  } else if (EPI == EPI_GELU_MX8) {
+    h.C = (uint8_t*)g.C + (size_t)r * g.ldc;
+    h.c_scale = g.c_scale + (size_t)r * g.c_sld;
+  } else {
+    h.C = (uint16_t*)g.C + (size_t)r * g.ldc;  // bf16 or fp16 rows
+  }
   if (EPI == EPI_QKV) {
     h.qk.q_out = g.qk.q_out + (size_t)r * g.qk.H;
     h.qk.slots = g.qk.slots + r;
@@ -139,7 +148,7 @@ hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
   // A 256x256 grid whose last round would leave most of the 256 CUs idle (qkv at 12,800 tokens: 600 tiles = two
   // rounds + 88) runs the rows of its full rounds on 256x256 tiles and the rest on 256x128 tiles, one round of
   // half-size tiles instead of a third round of mostly idle CUs.  The products are the same per output element.
-  if (by_shape && cfg == 1 && !g.w_scale) {
+  if (by_shape && cfg == 1) {
     const long gn = (g.N + 255) / 256, tiles = (long)((g.M + 255) / 256) * gn;
     const long rounds = (tiles + 255) / 256, last = tiles - (rounds - 1) * 256;
     const int rows1 = (int)((rounds - 1) * 256 / gn) * 256;
@@ -163,12 +172,11 @@ hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
 }  // namespace
 
 int pick_cfg(const GemmArgs& g) {
-  // 256x256 tiles (fp8: 256x128) once there are enough rows to fill them.  qkv (N = 3072) took 256x128 while its
+  // 256x256 tiles once there are enough rows to fill them (bf16 and fp8 alike).  qkv (N = 3072) took 256x128 while its
   // epilogue wrote 4 columns per lane (105 us vs 114 at 12800 rows); with 16-byte stores 256x256 is the faster one
   // (DiT solve 132.1 -> 129.6 ms on the same box).  fc1 (N = 2048, GELU) takes 256x256 since its epilogue uses the
   // hardware reciprocal (DiT solve 143.5 -> 142.0 ms against 128x128)
   if (g.M < 1024 || g.N < 256) return 0;
-  if (g.w_scale) return 2;
   // A 256x256 grid that fills under 70% of its last round of 256 CUs (prompt setups of 1,000-9,000 tokens) loses to the
   // 128x128 grid when that one's cost is clearly lower.  Measured per round of 256 tiles at K = 1024: 256x256 ~30 us,
   // 128x128 ~7.5 us plus ~7 us once (e.g. 3,000 rows, N = 1024: 26.5 vs 14.0 us; 8,000 rows: 29.4 vs 22.8 us; 12,800

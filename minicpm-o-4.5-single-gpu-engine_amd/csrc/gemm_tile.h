@@ -442,6 +442,41 @@ struct Tile {
     }
   }
 
+  // fp8, 64 x 128 wave tiles: one 64-K step of 32 x 32 x 64 scaled blocks, columns outermost, with B fragment j (and, for
+  // j < TM, A fragment j into an) of step kn of (La, Lb) read right after column j's MFMAs, as step16 does: one B
+  // register set across steps keeps the wider fp8 fragments within the register budget.  sc: the activation scale
+  // dwords of the step's stage.
+  template <bool V>
+  __device__ __forceinline__ void step8(acc_t (&acc)[TM][TN], const frag_t (&ac)[TM], frag_t (&an)[TM], frag_t (&bf)[TN],
+                                        const uint4* La, const uint4* Lb, int kn, const uint32_t (&sc)[NSC], int kk) const {
+    const int c0 = kn * 4 + (lane >> 5);
+    int e8[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) e8[i] = (int)((sc[i] >> (8 * (kk * 2 + (lane >> 5)))) & 255u);  // E8M0 of the lane's block
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], ac[i], acc[i][j], 0, 0, 0, 127, 0, e8[i]);
+      {
+        const int r = wn * WTN + j * 32 + (lane & 31);
+        bf[j] = join8(Lb[swz(r, c0)], Lb[swz(r, c0 + 2)]);
+      }
+      if (j < TM) {
+        const int r = wm * WTM + j * 32 + (lane & 31);
+        an[j] = join8(La[swz(r, c0)], La[swz(r, c0 + 2)]);
+      }
+    }
+    constexpr int NV = APW + BPW + NSC, VPC = (NV + TN - 1) / TN;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
+      if (V && j * VPC < NV) __builtin_amdgcn_sched_group_barrier(0x020, VPC, 0);
+      if (j < TM) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      else __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+  }
+
   // One K stage from buffers (La, Lb) with scales sd.  Stage kt + 1 must already be in flight into (Na, Nb); after the
   // barrier the loads of stage kt + 2 go into (La, Lb, sd).
   __device__ __forceinline__ void stage(acc_t (&acc)[TM][TN], frag_t (&af)[2][TM], frag_t (&bf)[2][TN], uint4* La,
@@ -454,6 +489,20 @@ struct Tile {
       __syncthreads();
       issue(La, Lb, sd, min(kt + 2, KT - 1));
       step16<true>(acc, af[1], af[0], bf[0], Na, Nb, 0);
+      return;
+    }
+    if constexpr (FP8 && TN > TM) {
+      // step 0 reads step 1's fragments from (La, Lb); after the barrier step 1 (this stage's scales, saved before the
+      // next stage's scale loads overwrite sd) reads the next stage's step 0 from (Na, Nb)
+      static_assert(NKK == 2, "fp8 stage of two 64-K steps");
+      step8<false>(acc, af[0], af[1], bf[0], La, Lb, 1, sd, 0);
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      __syncthreads();
+      uint32_t sl[NSC];
+#pragma unroll
+      for (int i = 0; i < NSC; ++i) sl[i] = sd[i];
+      issue(La, Lb, sd, min(kt + 2, KT - 1));
+      step8<true>(acc, af[1], af[0], bf[0], Na, Nb, 0, sl, 1);
       return;
     }
     constexpr int RPF = FP8 ? 2 : 1;  // LDS reads per fragment
