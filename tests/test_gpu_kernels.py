@@ -348,6 +348,36 @@ def test_gemm_fp8(dev, M, N, K, epi):
         assert rel(out, exact) < 6e-2
 
 
+@pytest.mark.parametrize("N,epi", [(3072, 0), (1024, 2), (2048, 3)])
+def test_gemm_fp8_large_tiles(dev, N, epi):
+    """fp8 at the 12,800-token shapes, where the grid takes 256 x 256 tiles of 64 x 128-wave sub-tiles (and, for
+    N = 3072, the rows of its last partial round on 256 x 128 tiles, whose activation scale rows start past the split):
+    against fp32 matmul of the dequantized operands, as test_gemm_fp8."""
+    L = _lib.lib()
+    M, K = 12800, 1024
+    qa, sa, qw, sw, Ad, Wd, A, W, bias, gate = _fp8_operands(dev, M, N, K, 77 + N + epi)
+    ref = Ad.to(dev) @ Wd.to(dev).t() + bias
+    if epi == 0:
+        out = torch.full((M, N), 7.0, device=dev).bfloat16()
+    elif epi == 2:
+        out = torch.randn(M, N, device=dev).half()
+        h0 = out.float()
+    else:
+        out = torch.zeros(M, N, device=dev)
+    _lib.check(L.t2w_gemm_fp8(qa.data_ptr(), K, None, sa.data_ptr(), K // 32, qw.data_ptr(), sw.data_ptr(), bias.data_ptr(),
+                              gate.data_ptr() if epi == 2 else None, out.data_ptr(), N, M, N, K, epi, _lib.stream_handle()), "gemm_fp8")
+    torch.cuda.synchronize()
+    if epi == 0:
+        assert rel(out.float(), ref) < 6e-3
+    elif epi == 2:
+        assert rel(out.float(), h0 + gate * ref) < 1e-3
+    else:
+        assert rel(out, ref) < 1e-4
+    if N == 3072:  # the rows of the last partial round (the 256 x 128 tail) on their own
+        tail = slice(M - 1536, M)
+        assert rel(out[tail].float(), ref[tail]) < 6e-3
+
+
 def test_gemm_fp8_taps(dev):
     """fp8 taps mode: the block scales of a row come from its three frames."""
     L = _lib.lib()
