@@ -133,6 +133,10 @@ typedef struct {
   int fp8;                  /* 1: the block GEMMs on fp8 MFMA (e4m3 weights, MX fp8 activations; needs fp8 weights) */
   const int* tok_abs;       /* [n_tok] position of the token in its stream (frames of kept windows before it); read
                              * only with globals.rope_freq */
+  int kv_max;               /* 0, or a bound on every row's key-list length (row_kv_len) in this call and in every replay
+                             * of a graph captured from it; bounds up to 512 let the attention hold each row's keys in
+                             * LDS (up to 256: two rows per CU).  A row longer than a stated bound gets NaN attention
+                             * outputs. */
 } t2w_solve_args;
 
 /* includes the fp8 activation buffers once the model has fp8 weights */
@@ -260,10 +264,13 @@ int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const
 /* Block-causal attention of packed rows over paged key slots: q [N, heads * 64]; row r's queries are tokens
  * row_start[r] .. + row_len[r], its keys the slots kv_idx[row_kv_off[r] ..][0 .. row_kv_len[r]) (its new tokens first,
  * then cached keys); tiles [n_tiles, 2] lists (row, first query) of every 64-query tile.  chunk > 0: a new token sees
- * the new tokens of its own and earlier chunks only; cached keys are always visible. */
+ * the new tokens of its own and earlier chunks only; cached keys are always visible.  n_rows: rows of the call;
+ * kv_max: 0, or a bound on every row_kv_len[r] (as t2w_solve_args.kv_max; bounds up to 512 select the row-resident
+ * kernel on calls of 256 or more (row, head) pairs whose rows average three or more 64-query tiles). */
 int t2w_attention(const void* q, const void* k_pool, const void* v_pool, void* out, const int* kv_idx,
                   const int* row_start, const int* row_len, const int* row_kv_off, const int* row_kv_len,
-                  const int* tiles, int n_tiles, int heads, int chunk, float scale, void* stream);
+                  const int* tiles, int n_tiles, int heads, int chunk, float scale, int n_rows, int kv_max,
+                  void* stream);
 
 /* ---------------------------------------------------------------- HiFT vocoder (fp32) */
 

@@ -42,7 +42,7 @@ class SolveArgs(C.Structure):
                [(n, P) for n in ("x0", "stat", "in_rows", "out", "tok_row", "tok_pos", "a_src", "new_slot", "row_start", "row_len",
                                  "row_kv_off", "row_kv_len", "conv_rd", "conv_wr", "kv_idx", "tiles", "k_pool", "v_pool")] + \
                [("pool_layer_stride", C.c_longlong), ("conv_pool", P), ("workspace", P), ("workspace_bytes", C.c_size_t), ("fp8", I),
-                ("tok_abs", P)]
+                ("tok_abs", P), ("kv_max", I)]
 
 
 class DitBlockFp8(C.Structure):
@@ -114,7 +114,7 @@ _SIGS = {
     "t2w_gemm_fp8": (I, [P, I, P, P, I, P, P, P, P, P, I, I, I, I, I, P]),
     "t2w_ln_mod": (I, [P, P, P, F, P, I, I, P]),
     "t2w_qk_norm_scatter": (I, [P, P, P, P, P, F, P, P, P, P, I, I, P]),
-    "t2w_attention": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, F, P]),
+    "t2w_attention": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, F, I, I, P]),
     "t2w_hift_create": (I, [C.POINTER(HiftDims), C.POINTER(HiftWeights), C.POINTER(P)]),
     "t2w_hift_destroy": (None, [P]),
     "t2w_hift_plan_ints": (I, [I]),

@@ -26,6 +26,7 @@ namespace {
 constexpr float NEG = -1.0e30f;
 
 typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // V^T fragment of the P.V MFMA from a key-major V tile in LDS (16-byte chunks swizzled by key): lane l gets channel
 // d = d0 + l % 32 and keys kb + 4 (l / 32) + {0..3} (elements 0..3) and kb + 8 + 4 (l / 32) + {0..3} (elements 4..7),
@@ -310,15 +311,216 @@ __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
   }
 }
 
+// Row-resident form for large calls whose key lists fit in LDS: one workgroup of 8 waves per (row, head) copies the
+// row's whole key and value lists for the head into LDS once (global_load_lds by slot id, the same key-major 16-byte
+// chunk swizzle as the tiles above, and past the list's end up to 63 clamped, finite keys that a last tile overhangs),
+// then its waves take the 32-query blocks, latest (most keys) first, and run each block's key tiles straight from LDS:
+// no gathers, stores or barriers inside the key loop, and the keys and values of a row are read from the pools once
+// per head instead of once per 64-query tile.  The waves take the blocks in a fixed snake order (round r: wave w, or
+// 7 - w on odd rounds), so the costliest blocks spread over the waves.  LDS holds round8(kv_max + 63) keys: with
+// kv_max <= 256 two workgroups share a CU (80 KB each; one copies while the other computes), registers capped at 128
+// per lane for their four waves per SIMD.  Per query the arithmetic is that of attn_kernel, in the same order, so the
+// outputs are the same bits.
+constexpr int ROW_WAVES = 8;
+__host__ __device__ constexpr int row_krows(int kv_max) { return (kv_max + 63 + 7) / 8 * 8; }
+constexpr int ROW_KROWS = row_krows(ATTN_ROW_KMAX);
+
+__global__ void __launch_bounds__(64 * ROW_WAVES) __attribute__((amdgpu_waves_per_eu(4, 4))) attn_row_kernel(AttnArgs a) {
+  extern __shared__ uint4 lds[];  // K rows [KR][8 chunks], then V rows [KR][8 chunks]
+  const int KR = row_krows(a.kv_max);
+  uint4* Ks = lds;
+  uint4* Vs = lds + KR * 8;
+  const int head = blockIdx.x, row = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = a.row_len[row];
+  if (T <= 0) return;
+  const int start = a.row_start[row], kvoff = a.row_kv_off[row], kvlen = a.row_kv_len[row];
+  const int H = a.heads * 64;
+  if (kvlen > a.kv_max) {  // longer than the caller's bound: NaN outputs instead of copies past the LDS lists
+    for (int i = tid; i < T * 64; i += 64 * ROW_WAVES) {
+      const size_t o = (size_t)(start + i / 64) * H + head * 64 + i % 64;
+      if (a.out8) {
+        a.out8[o] = 0x7f;  // e4m3 NaN
+        if (i % 32 == 0) a.out8s[(size_t)(start + i / 64) * (H / 32) + head * 2 + (i % 64) / 32] = 0xff;  // E8M0 NaN
+      } else {
+        a.out[o] = 0x7fc0;  // bf16 NaN
+      }
+    }
+    return;
+  }
+  // keys and values of the row and head into LDS: 8-key blocks, lane l fetching key 8 b + l / 8's chunk (l % 8) ^ key
+  {
+    const int nb8 = row_krows(kvlen) / 8;
+    constexpr int MAXB = ROW_KROWS / 8 / ROW_WAVES;
+    int slot[MAXB];
+#pragma unroll
+    for (int i = 0; i < MAXB; ++i) {
+      const int b8 = wave + ROW_WAVES * i, key = b8 * 8 + (lane >> 3);
+      slot[i] = b8 < nb8 ? a.kv_idx[kvoff + min(key, kvlen - 1)] : 0;
+    }
+    const int ch = ((lane & 7) ^ ((lane >> 3) & 7)) * 8;  // the key's row-local index is b8 * 8 + lane / 8: key & 7 = lane / 8
+#pragma unroll
+    for (int i = 0; i < MAXB; ++i) {
+      const int b8 = wave + ROW_WAVES * i;
+      if (b8 < nb8) {
+        const size_t go = (size_t)slot[i] * H + head * 64 + ch;
+        __builtin_amdgcn_global_load_lds((const void*)(a.k_pool + go), (lds_ptr_t)(Ks + b8 * 64), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(a.v_pool + go), (lds_ptr_t)(Vs + b8 * 64), 16, 0, 0);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+  const int half = lane >> 5, col = lane & 31;
+  const float sl2 = a.scale * 1.4426950408889634f;
+  const int nblk = (T + 31) / 32;
+  for (int rnd = 0; rnd * ROW_WAVES < nblk; ++rnd) {
+    const int bi = rnd * ROW_WAVES + ((rnd & 1) ? ROW_WAVES - 1 - wave : wave);
+    if (bi >= nblk) break;
+    const int q0 = (nblk - 1 - bi) * 32;
+    const int myq = q0 + col, qc = myq < T ? myq : T - 1;
+    const int lim_me = a.chunk > 0 ? min(T, (qc / a.chunk + 1) * a.chunk) : T;
+    const int last = min(q0 + 31, T - 1);
+    const int lim_max = a.chunk > 0 ? min(T, (last / a.chunk + 1) * a.chunk) : T;
+    const int lim_w0 = a.chunk > 0 ? min(T, (q0 / a.chunk + 1) * a.chunk) : T;
+    bf16x8 qf[4];
+    {
+      const bf16_t* qp = a.q + (size_t)(start + qc) * H + head * 64 + half * 8;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) qf[kk] = as_bf16x8(*(const uint4*)(qp + kk * 16));
+    }
+    f32x16 o0, o1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { o0[r] = 0.f; o1[r] = 0.f; }
+    float m = NEG, l = 0.f;
+    const int n1 = (lim_max + 63) / 64, n2 = (kvlen - T + 63) / 64;
+    for (int t = 0; t < n1 + n2; ++t) {
+      const bool cached = t >= n1;
+      const int kb = cached ? T + (t - n1) * 64 : t * 64, ke = cached ? kvlen : lim_max;
+      const int lim = cached ? ke : min(ke, lim_me);
+      const int lim_lo = cached ? ke : min(ke, lim_w0);
+      const bool two = kb + 32 < ke;
+      f32x16 sc[2];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[sub][r] = 0.f;
+        if (sub == 0 || two) {
+          const int kr = kb + sub * 32 + col;
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) {
+            const int chunk = kk * 2 + half;
+            sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(Ks[kr * 8 + (chunk ^ (kr & 7))]), qf[kk], sc[sub], 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const int sb = kb + sub * 32;
+        if (sb + 32 > lim_lo || (sub == 1 && !two)) {
+          const int nvis = lim - (sb + half * 4);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int off = (r >> 2) * 8 + (r & 3);
+            sc[sub][r] = off < nvis ? sc[sub][r] : -__builtin_inff();
+          }
+        }
+      }
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mn = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f((m - mn) * sl2);
+      const float mb = -mn * sl2;
+      float rs = 0.f;
+      uint4 pf[2][2];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          float e[8];
+#pragma unroll
+          for (int x = 0; x < 8; ++x) {
+            e[x] = __builtin_amdgcn_exp2f(fmaf(sc[sub][8 * hh + x], sl2, mb));
+            rs += e[x];
+          }
+          pf[sub][hh] = make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
+        }
+      rs += __shfl_xor(rs, 32, 64);
+      l = l * alpha + rs;
+      m = mn;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) { o0[r] *= alpha; o1[r] *= alpha; }
+      }
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        if (sub == 1 && !two) break;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const bf16x8 v0 = vt_frag(Vs, kb + sub * 32 + hh * 16, 0, lane);
+          const bf16x8 v1 = vt_frag(Vs, kb + sub * 32 + hh * 16, 32, lane);
+          o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v0, as_bf16x8(pf[sub][hh]), o0, 0, 0, 0);
+          o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v1, as_bf16x8(pf[sub][hh]), o1, 0, 0, 0);
+        }
+      }
+    }
+    if (myq >= T) continue;
+    const float inv = 1.0f / l;
+    if (a.out8) {
+      float m0 = 0.f, m1 = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { m0 = fmaxf(m0, fabsf(o0[r])); m1 = fmaxf(m1, fabsf(o1[r])); }
+      m0 = fmaxf(m0, __shfl_xor(m0, 32, 64)) * inv;
+      m1 = fmaxf(m1, __shfl_xor(m1, 32, 64)) * inv;
+      const int e0 = mx_exp(m0), e1 = mx_exp(m1);
+      uint8_t* qp = a.out8 + (size_t)(start + myq) * H + head * 64;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = g * 8 + half * 4;
+        *(uint32_t*)(qp + d) = mx_pack4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv, e0);
+        *(uint32_t*)(qp + 32 + d) = mx_pack4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv, e1);
+      }
+      if (half == 0) {
+        uint8_t* sp = a.out8s + (size_t)(start + myq) * (H / 32) + head * 2;
+        sp[0] = (uint8_t)(e0 + 127);
+        sp[1] = (uint8_t)(e1 + 127);
+      }
+      continue;
+    }
+    bf16_t* op = a.out + (size_t)(start + myq) * H + head * 64;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = g * 8 + half * 4;
+      *(uint2*)(op + d) = make_uint2(pack2(o0[4 * g] * inv, o0[4 * g + 1] * inv), pack2(o0[4 * g + 2] * inv, o0[4 * g + 3] * inv));
+      *(uint2*)(op + 32 + d) = make_uint2(pack2(o1[4 * g] * inv, o1[4 * g + 1] * inv), pack2(o1[4 * g + 2] * inv, o1[4 * g + 3] * inv));
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t attention(const AttnArgs& a, hipStream_t st) {
   if (a.n_tiles <= 0) return hipSuccess;
   // a grid of fewer workgroups than CUs (a streaming chunk) splits each workgroup's key tiles over four wave groups
-  if (a.n_tiles * a.heads < 256)
+  if (a.n_tiles * a.heads < 256) {
     hipLaunchKernelGGL(attn_kernel<4>, dim3(a.n_tiles, a.heads), dim3(512), 0, st, a);
-  else
+  } else if (a.kv_max > 0 && a.kv_max <= ATTN_ROW_KMAX && (long)a.n_rows * a.heads >= 256 && a.n_tiles >= 3 * a.n_rows) {
+    // rows of three or more query tiles on average: with fewer, most of a row workgroup's eight waves would idle
+    // while its whole key list is copied (the tile kernel is faster there)
+    static bool attr = false;
+    if (!attr) {
+      const hipError_t e = hipFuncSetAttribute((const void*)attn_row_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               2 * ROW_KROWS * 8 * (int)sizeof(uint4));
+      if (e != hipSuccess) return e;
+      attr = true;
+    }
+    const size_t lds = 2 * (size_t)row_krows(a.kv_max) * 8 * sizeof(uint4);
+    hipLaunchKernelGGL(attn_row_kernel, dim3(a.heads, a.n_rows), dim3(64 * ROW_WAVES), lds, st, a);
+  } else {
     hipLaunchKernelGGL(attn_kernel<1>, dim3(a.n_tiles, a.heads), dim3(128), 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -256,6 +256,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     at.q = w.q; at.k_pool = kp; at.v_pool = vp; at.out = w.ao; at.kv_idx = a->kv_idx; at.row_start = a->row_start;
     at.row_len = a->row_len; at.row_kv_off = a->row_kv_off; at.row_kv_len = a->row_kv_len; at.tiles = a->tiles;
     at.n_tiles = a->n_tiles; at.heads = d.heads; at.chunk = a->chunk; at.scale = 1.0f / sqrtf((float)d.head_dim);
+    at.n_rows = a->n_rows; at.kv_max = a->kv_max;
     if (f8) { at.out8 = w.o8; at.out8s = w.o8s; }
     T2W_CHECK(attention(at, st), "attention");
     if (f8)
@@ -327,6 +328,7 @@ int check_args(const t2w_dit* m, const t2w_solve_args* a) {
   if (a->fp8 && (m->d.hidden % 128 || m->d.ffn % 128)) return fail("fp8 solve needs hidden and ffn multiples of 128");
   if (a->workspace_bytes < carve(m->d, a->n_tok, a->n_rows, m->fp8_ready(), nullptr, nullptr)) return fail("workspace too small");
   if (a->chunk < 0) return fail("negative chunk");
+  if (a->kv_max < 0) return fail("negative kv_max");
   if (m->g.rope_freq && !a->tok_abs) return fail("rotary embedding needs tok_abs (stream positions)");
   return 0;
 }
@@ -531,11 +533,13 @@ int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const
 
 int t2w_attention(const void* q, const void* k_pool, const void* v_pool, void* out, const int* kv_idx, const int* row_start,
                   const int* row_len, const int* row_kv_off, const int* row_kv_len, const int* tiles, int n_tiles, int heads, int chunk,
-                  float scale, void* stream) {
+                  float scale, int n_rows, int kv_max, void* stream) {
+  if (n_rows < 0 || kv_max < 0) return fail("attention: negative n_rows or kv_max");
   AttnArgs at;
   at.q = (const bf16_t*)q; at.k_pool = (const bf16_t*)k_pool; at.v_pool = (const bf16_t*)v_pool; at.out = (bf16_t*)out;
   at.kv_idx = kv_idx; at.row_start = row_start; at.row_len = row_len; at.row_kv_off = row_kv_off; at.row_kv_len = row_kv_len;
   at.tiles = tiles; at.n_tiles = n_tiles; at.heads = heads; at.chunk = chunk; at.scale = scale;
+  at.n_rows = n_rows; at.kv_max = kv_max;
   T2W_CHECK(attention(at, (hipStream_t)stream), "attention");
   return 0;
 }

@@ -143,7 +143,10 @@ struct AttnArgs {
   float scale;
   uint8_t* out8 = nullptr;   // fp8 mode: MX fp8 codes [tokens, H] (out unused) and block scales [tokens, H / 32]
   uint8_t* out8s = nullptr;
+  int n_rows = 0;            // rows of the call (the row-resident kernel's grid)
+  int kv_max = 0;            // 0, or the caller's bound on every row's key-list length (for every replay of a graph)
 };
+constexpr int ATTN_ROW_KMAX = 512;  // the longest key list the row-resident attention holds in LDS
 hipError_t attention(const AttnArgs& a, hipStream_t st);
 
 hipError_t pack_inputs(const float* x0, const float* stat, bf16_t* a_in, float* x, int half, int mel, hipStream_t st);

@@ -246,6 +246,18 @@ def _layout(lens, new, kv, rd, wr, pos0=None) -> list[np.ndarray]:
             np.asarray(rd, dtype=np.int64), np.asarray(wr, dtype=np.int64), _tile_list(lens), pos0[tok_row] + tok_pos, cat(kv)]
 
 
+ATTN_ROW_KMAX = 512  # key-list length up to which the attention holds a row's keys in LDS (t2w_solve_args.kv_max)
+
+
+def _kv_max(p: dict) -> int:
+    """A call's ``kv_max``: 256 or 512 (the row-resident attention's LDS sizes; lists up to 256 keys let two of its
+    workgroups share a CU) when every row's key list fits, else 0 (no bound).  Graphs are keyed by it, so a replay
+    never breaks the bound its capture stated."""
+    kv = p["parts"][7]
+    top = int(kv.max()) if kv.size else 0
+    return 256 if top <= 256 else ATTN_ROW_KMAX if top <= ATTN_ROW_KMAX else 0
+
+
 def plan_call(rows: list[FastRow], Ts: list[int], new: list[np.ndarray], keep: list[bool], cnn_scratch: int, cnn_zero: int | None = None,
               bucket: tuple[int, int] | None = None, kv_scratch: int | None = None) -> dict:
     """Host plan of one call over ``n`` requests (``engine/runtime/dit_fast.py:223-266``): rows ``[cond 0..n-1 | uncond
@@ -502,7 +514,7 @@ class FastDiT:
         return _lib.SolveArgs(p["n_tok"], p["n_rows"], p["half"], p["n_tiles"], int(chunk), _lib.ptr(x0), _lib.ptr(stat), _lib.ptr(in_rows),
                               out.data_ptr(), tp(0), tp(1), tp(2), tp(3), tp(4), tp(5), tp(6), tp(7), tp(8), tp(9), tp(12), tp(10),
                               self.k_pool.data_ptr(), self.v_pool.data_ptr(), self.n_slots * self.cfg.hidden, self.conv_pool.data_ptr(),
-                              ws.data_ptr(), ws.numel(), int(self.fp8), tp(11))
+                              ws.data_ptr(), ws.numel(), int(self.fp8), tp(11), _kv_max(p))
 
     def _workspace(self, N: int, R: int) -> torch.Tensor:
         need = _lib.lib().t2w_dit_workspace_bytes(self.model.handle, N, R)
@@ -524,7 +536,7 @@ class FastDiT:
             self.counts["eager"] += 1
             return out
         flat = self._flat(p)
-        g = self._bucket_graph(bucket, chunk, flat.size) if bucket is not None else self._exact_graph(p, chunk, flat.size)
+        g = self._bucket_graph(bucket, chunk, flat.size, _kv_max(p)) if bucket is not None else self._exact_graph(p, chunk, flat.size)
         _Upload.into(g["tables"], flat)
         half = p["real_half"]
         g["x0"][:half].copy_(x0)
@@ -577,9 +589,9 @@ class FastDiT:
             self._arena = a
         return a
 
-    def _bucket_graph(self, bucket, chunk: int, n_ints: int) -> dict:
+    def _bucket_graph(self, bucket, chunk: int, n_ints: int, kv_max: int) -> dict:
         arena = self._arena_for(n_ints)
-        key = (bucket, chunk, self.fp8)
+        key = (bucket, chunk, self.fp8, kv_max)
         g = self.graphs.get(key)
         if g is None:
             g = dict(arena, graph=None)
@@ -587,7 +599,7 @@ class FastDiT:
         return g
 
     def _exact_graph(self, p: dict, chunk: int, n_ints: int) -> dict:
-        key = (p["n_tok"], p["n_rows"], p["n_tiles"], chunk, self.fp8)
+        key = (p["n_tok"], p["n_rows"], p["n_tiles"], chunk, self.fp8, _kv_max(p))
         g = self.exact.pop(key, None)
         if g is not None and g["tables"].numel() < n_ints:  # more cached keys than this graph's tables hold
             _lib.lib().t2w_graph_destroy(g["graph"])
@@ -612,7 +624,7 @@ class FastDiT:
             raise RuntimeError("capture needs use_graphs=True")
         p = plan_call([], [], [], [], self.cnn_scratch, self.cnn_zero, (rb, nb), self.kv_scratch)
         flat = self._flat(p)
-        g = self._bucket_graph((rb, nb), chunk, flat.size)
+        g = self._bucket_graph((rb, nb), chunk, flat.size, _kv_max(p))
         if g["graph"] is None:
             _Upload.into(g["tables"], flat)
             g["graph"] = self._capture(p, g, chunk)

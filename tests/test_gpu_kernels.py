@@ -221,7 +221,7 @@ def test_qk_norm_scatter(dev):
         assert torch.equal(vp[slots.long()], qkv.view(N, 3, H)[:, 2])
 
 
-def _attention_case(dev, lens, cached, heads, chunk, seed):
+def _attention_case(dev, lens, cached, heads, chunk, seed, kv_max=0):
     L = _lib.lib()
     g = torch.Generator(device=dev).manual_seed(seed)
     n_slots = 2 * (sum(lens) + sum(cached)) + 64
@@ -246,8 +246,14 @@ def _attention_case(dev, lens, cached, heads, chunk, seed):
     out = torch.zeros(N, H, dtype=torch.bfloat16, device=dev)
     keep = [it(x) for x in (kv, row_start, lens, row_kv_off, row_kv_len, tiles)]  # alive until the kernel ran
     _lib.check(L.t2w_attention(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), out.data_ptr(), *[t.data_ptr() for t in keep], len(tiles) // 2,
-                               heads, chunk, 0.125, _lib.stream_handle()))
+                               heads, chunk, 0.125, len(lens), kv_max, _lib.stream_handle()))
     torch.cuda.synchronize()
+    if kv_max:  # the row-resident kernel does each query's arithmetic in the tile kernel's order: the same bits
+        tile_out = torch.zeros_like(out)
+        _lib.check(L.t2w_attention(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), tile_out.data_ptr(), *[t.data_ptr() for t in keep],
+                                   len(tiles) // 2, heads, chunk, 0.125, len(lens), 0, _lib.stream_handle()))
+        torch.cuda.synchronize()
+        assert torch.equal(out, tile_out)
     worst = 0.0
     for r, (t, c) in enumerate(zip(lens, cached)):
         if t == 0:
@@ -285,6 +291,51 @@ def test_attention_long_rows(dev, chunk):
     cached = [0, 300, 7, 0, 100, 33, 500, 0, 0, 31, 129, 0, 400, 0, 0, 64] * 2
     worst = _attention_case(dev, lens, cached, 16, chunk, 21 + chunk)
     print("long-row attention worst rel-L2", worst)
+
+
+@pytest.mark.parametrize("chunk", [0, 50])
+@pytest.mark.parametrize("kv_max", [256, 512])
+def test_attention_row_resident(dev, chunk, kv_max):
+    """Key lists held in LDS per (row, head): 32 rows of the 16-head grid with new runs of 0..kv_max keys and cached
+    runs that start off the 64-key grid, equal to the tile kernel bit for bit and to fp32.  kv_max 256: two
+    workgroups per CU."""
+    if kv_max == 512:
+        lens = [400, 150, 0, 450, 64, 1, 33, 512, 300, 257, 400, 95, 400, 200, 170, 222] * 2  # 4.1 query tiles per row
+        cached = [0, 300, 7, 62, 100, 33, 479, 0, 0, 31, 112, 0, 112, 312, 0, 64] * 2
+    else:
+        lens = [200, 193, 0, 250, 64, 1, 33, 256, 193, 129, 200, 192, 200, 200, 170, 222] * 2  # 3.1 query tiles per row
+        cached = [0, 63, 7, 6, 100, 33, 223, 0, 0, 31, 56, 0, 56, 0, 0, 34] * 2
+    assert max(t + c for t, c in zip(lens, cached)) == kv_max
+    worst = _attention_case(dev, lens, cached, 16, chunk, 31 + chunk, kv_max=kv_max)
+    print("row-resident attention worst rel-L2", worst)
+
+
+def test_attention_row_bound_broken(dev):
+    """A row longer than the stated bound gets NaN outputs (no reads past the LDS lists); the rows within it are
+    unaffected."""
+    L = _lib.lib()
+    heads, H, lens, cached = 16, 1024, [192] * 16, [0] * 15 + [400]
+    N, n_slots = sum(lens), 3600
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = torch.randn(N, H, device=dev, generator=g).bfloat16()
+    kp = torch.randn(n_slots, H, device=dev, generator=g).bfloat16()
+    vp = torch.randn(n_slots, H, device=dev, generator=g).bfloat16()
+    kv, off, kvl = [], [], []
+    for t, c in zip(lens, cached):
+        off.append(len(kv))
+        kvl.append(t + c)
+        kv += list(range(len(kv), len(kv) + t + c))
+    it = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)  # noqa: E731
+    keep = [it(x) for x in (kv, [192 * r for r in range(16)], lens, off, kvl, [v for r in range(16) for v in (r, 0, r, 64, r, 128)])]
+    outs = []
+    for kv_max in (512, 0):
+        out = torch.zeros(N, H, dtype=torch.bfloat16, device=dev)
+        _lib.check(L.t2w_attention(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), out.data_ptr(), *[t.data_ptr() for t in keep], 48, heads, 0,
+                                   0.125, 16, kv_max, _lib.stream_handle()))
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.isnan(outs[0][15 * 192:]).all() and not torch.isnan(outs[1]).any()
+    assert torch.equal(outs[0][:15 * 192], outs[1][:15 * 192])
 
 
 def test_quant_mx8_matches_oracle(dev):
