@@ -311,6 +311,80 @@ __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
   }
 }
 
+// One 64-key tile [kb, kb + 64) of a key list held in LDS (K and V rows key-major, 16-byte chunks swizzled by key) for
+// the wave's 32 queries: scores S^T = K . Q^T, masks (keys at or past lim invisible; lim_lo the wave's smallest limit),
+// online softmax and O^T += V^T . P^T, in the order and arithmetic of attn_kernel's tile_step
+__device__ __forceinline__ void lds_key_tile(const uint4* Ks, const uint4* Vs, int kb, int ke, int lim, int lim_lo, const bf16x8 (&qf)[4],
+                                             float sl2, int lane, f32x16& o0, f32x16& o1, float& m, float& l) {
+  const int half = lane >> 5, col = lane & 31;
+  const bool two = kb + 32 < ke;
+  f32x16 sc[2];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[sub][r] = 0.f;
+    if (sub == 0 || two) {
+      const int kr = kb + sub * 32 + col;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int chunk = kk * 2 + half;
+        sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(Ks[kr * 8 + (chunk ^ (kr & 7))]), qf[kk], sc[sub], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int sb = kb + sub * 32;
+    if (sb + 32 > lim_lo || (sub == 1 && !two)) {
+      const int nvis = lim - (sb + half * 4);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int off = (r >> 2) * 8 + (r & 3);
+        sc[sub][r] = off < nvis ? sc[sub][r] : -__builtin_inff();
+      }
+    }
+  }
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float mn = fmaxf(m, mx);
+  const float alpha = __builtin_amdgcn_exp2f((m - mn) * sl2);
+  const float mb = -mn * sl2;
+  float rs = 0.f;
+  uint4 pf[2][2];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float e[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        e[x] = __builtin_amdgcn_exp2f(fmaf(sc[sub][8 * hh + x], sl2, mb));
+        rs += e[x];
+      }
+      pf[sub][hh] = make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
+    }
+  rs += __shfl_xor(rs, 32, 64);
+  l = l * alpha + rs;
+  m = mn;
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { o0[r] *= alpha; o1[r] *= alpha; }
+  }
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    if (sub == 1 && !two) break;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const bf16x8 v0 = vt_frag(Vs, kb + sub * 32 + hh * 16, 0, lane);
+      const bf16x8 v1 = vt_frag(Vs, kb + sub * 32 + hh * 16, 32, lane);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v0, as_bf16x8(pf[sub][hh]), o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v1, as_bf16x8(pf[sub][hh]), o1, 0, 0, 0);
+    }
+  }
+}
+
 // Row-resident form for large calls whose key lists fit in LDS: one workgroup of 8 waves per (row, head) copies the
 // row's whole key and value lists for the head into LDS once (global_load_lds by slot id, the same key-major 16-byte
 // chunk swizzle as the tiles above, and past the list's end up to 63 clamped, finite keys that a last tile overhangs),
@@ -325,6 +399,48 @@ constexpr int ROW_WAVES = 8;
 __host__ __device__ constexpr int row_krows(int kv_max) { return (kv_max + 63 + 7) / 8 * 8; }
 constexpr int ROW_KROWS = row_krows(ATTN_ROW_KMAX);
 
+// The key list kv_idx[kvoff ..][0 .. kvlen) of one head into LDS (K and V key-major, 16-byte chunks swizzled by key,
+// rows up to round8(kvlen + 63) with the keys past the end clamped to the last), then waits for it and a barrier.
+// 8-key blocks go to the workgroup's 8 waves in turn; lane l fetches key 8 b + l / 8's chunk (l % 8) ^ key.
+__device__ __forceinline__ void load_key_list(uint4* Ks, uint4* Vs, const AttnArgs& a, int kvoff, int kvlen, int head, int wave,
+                                              int lane) {
+  const int H = a.heads * 64;
+  const int nb8 = row_krows(kvlen) / 8;
+  constexpr int MAXB = ROW_KROWS / 8 / ROW_WAVES;
+  int slot[MAXB];
+#pragma unroll
+  for (int i = 0; i < MAXB; ++i) {
+    const int b8 = wave + ROW_WAVES * i, key = b8 * 8 + (lane >> 3);
+    slot[i] = b8 < nb8 ? a.kv_idx[kvoff + min(key, kvlen - 1)] : 0;
+  }
+  const int ch = ((lane & 7) ^ ((lane >> 3) & 7)) * 8;  // the key's row-local index is b8 * 8 + lane / 8: key & 7 = lane / 8
+#pragma unroll
+  for (int i = 0; i < MAXB; ++i) {
+    const int b8 = wave + ROW_WAVES * i;
+    if (b8 < nb8) {
+      const size_t go = (size_t)slot[i] * H + head * 64 + ch;
+      __builtin_amdgcn_global_load_lds((const void*)(a.k_pool + go), (lds_ptr_t)(Ks + b8 * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(a.v_pool + go), (lds_ptr_t)(Vs + b8 * 64), 16, 0, 0);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+// NaN outputs for queries [q0, q1) of a row whose key list is longer than the caller's bound
+__device__ __forceinline__ void nan_rows(const AttnArgs& a, int start, int q0, int q1, int head, int tid, int nthreads) {
+  const int H = a.heads * 64;
+  for (int i = q0 * 64 + tid; i < q1 * 64; i += nthreads) {
+    const size_t o = (size_t)(start + i / 64) * H + head * 64 + i % 64;
+    if (a.out8) {
+      a.out8[o] = 0x7f;  // e4m3 NaN
+      if (i % 32 == 0) a.out8s[(size_t)(start + i / 64) * (H / 32) + head * 2 + (i % 64) / 32] = 0xff;  // E8M0 NaN
+    } else {
+      a.out[o] = 0x7fc0;  // bf16 NaN
+    }
+  }
+}
+
 __global__ void __launch_bounds__(64 * ROW_WAVES) __attribute__((amdgpu_waves_per_eu(4, 4))) attn_row_kernel(AttnArgs a) {
   extern __shared__ uint4 lds[];  // K rows [KR][8 chunks], then V rows [KR][8 chunks]
   const int KR = row_krows(a.kv_max);
@@ -337,40 +453,10 @@ __global__ void __launch_bounds__(64 * ROW_WAVES) __attribute__((amdgpu_waves_pe
   const int start = a.row_start[row], kvoff = a.row_kv_off[row], kvlen = a.row_kv_len[row];
   const int H = a.heads * 64;
   if (kvlen > a.kv_max) {  // longer than the caller's bound: NaN outputs instead of copies past the LDS lists
-    for (int i = tid; i < T * 64; i += 64 * ROW_WAVES) {
-      const size_t o = (size_t)(start + i / 64) * H + head * 64 + i % 64;
-      if (a.out8) {
-        a.out8[o] = 0x7f;  // e4m3 NaN
-        if (i % 32 == 0) a.out8s[(size_t)(start + i / 64) * (H / 32) + head * 2 + (i % 64) / 32] = 0xff;  // E8M0 NaN
-      } else {
-        a.out[o] = 0x7fc0;  // bf16 NaN
-      }
-    }
+    nan_rows(a, start, 0, T, head, tid, 64 * ROW_WAVES);
     return;
   }
-  // keys and values of the row and head into LDS: 8-key blocks, lane l fetching key 8 b + l / 8's chunk (l % 8) ^ key
-  {
-    const int nb8 = row_krows(kvlen) / 8;
-    constexpr int MAXB = ROW_KROWS / 8 / ROW_WAVES;
-    int slot[MAXB];
-#pragma unroll
-    for (int i = 0; i < MAXB; ++i) {
-      const int b8 = wave + ROW_WAVES * i, key = b8 * 8 + (lane >> 3);
-      slot[i] = b8 < nb8 ? a.kv_idx[kvoff + min(key, kvlen - 1)] : 0;
-    }
-    const int ch = ((lane & 7) ^ ((lane >> 3) & 7)) * 8;  // the key's row-local index is b8 * 8 + lane / 8: key & 7 = lane / 8
-#pragma unroll
-    for (int i = 0; i < MAXB; ++i) {
-      const int b8 = wave + ROW_WAVES * i;
-      if (b8 < nb8) {
-        const size_t go = (size_t)slot[i] * H + head * 64 + ch;
-        __builtin_amdgcn_global_load_lds((const void*)(a.k_pool + go), (lds_ptr_t)(Ks + b8 * 64), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(a.v_pool + go), (lds_ptr_t)(Vs + b8 * 64), 16, 0, 0);
-      }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-  }
+  load_key_list(Ks, Vs, a, kvoff, kvlen, head, wave, lane);
   const int half = lane >> 5, col = lane & 31;
   const float sl2 = a.scale * 1.4426950408889634f;
   const int nblk = (T + 31) / 32;
@@ -399,72 +485,7 @@ __global__ void __launch_bounds__(64 * ROW_WAVES) __attribute__((amdgpu_waves_pe
       const int kb = cached ? T + (t - n1) * 64 : t * 64, ke = cached ? kvlen : lim_max;
       const int lim = cached ? ke : min(ke, lim_me);
       const int lim_lo = cached ? ke : min(ke, lim_w0);
-      const bool two = kb + 32 < ke;
-      f32x16 sc[2];
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[sub][r] = 0.f;
-        if (sub == 0 || two) {
-          const int kr = kb + sub * 32 + col;
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) {
-            const int chunk = kk * 2 + half;
-            sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(Ks[kr * 8 + (chunk ^ (kr & 7))]), qf[kk], sc[sub], 0, 0, 0);
-          }
-        }
-      }
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        const int sb = kb + sub * 32;
-        if (sb + 32 > lim_lo || (sub == 1 && !two)) {
-          const int nvis = lim - (sb + half * 4);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int off = (r >> 2) * 8 + (r & 3);
-            sc[sub][r] = off < nvis ? sc[sub][r] : -__builtin_inff();
-          }
-        }
-      }
-      float mx = -__builtin_inff();
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mn = fmaxf(m, mx);
-      const float alpha = __builtin_amdgcn_exp2f((m - mn) * sl2);
-      const float mb = -mn * sl2;
-      float rs = 0.f;
-      uint4 pf[2][2];
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          float e[8];
-#pragma unroll
-          for (int x = 0; x < 8; ++x) {
-            e[x] = __builtin_amdgcn_exp2f(fmaf(sc[sub][8 * hh + x], sl2, mb));
-            rs += e[x];
-          }
-          pf[sub][hh] = make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
-        }
-      rs += __shfl_xor(rs, 32, 64);
-      l = l * alpha + rs;
-      m = mn;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) { o0[r] *= alpha; o1[r] *= alpha; }
-      }
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        if (sub == 1 && !two) break;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const bf16x8 v0 = vt_frag(Vs, kb + sub * 32 + hh * 16, 0, lane);
-          const bf16x8 v1 = vt_frag(Vs, kb + sub * 32 + hh * 16, 32, lane);
-          o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v0, as_bf16x8(pf[sub][hh]), o0, 0, 0, 0);
-          o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v1, as_bf16x8(pf[sub][hh]), o1, 0, 0, 0);
-        }
-      }
+      lds_key_tile(Ks, Vs, kb, ke, lim, lim_lo, qf, sl2, lane, o0, o1, m, l);
     }
     if (myq >= T) continue;
     const float inv = 1.0f / l;
@@ -499,12 +520,134 @@ __global__ void __launch_bounds__(64 * ROW_WAVES) __attribute__((amdgpu_waves_pe
   }
 }
 
+// Small calls (fewer (tile, head) workgroups than CUs, e.g. a streaming chunk) with a bounded key list: attn_kernel<4>'s
+// grid and key split (four groups of two waves per 64-query tile, group g taking key tiles g, g + 4, ..., merged in
+// group order) with the row's whole key list copied into LDS once instead of gathered tile by tile, so the
+// arithmetic and its order are the same and so are the output bits.
+constexpr int SPLIT_KS = 4;
+constexpr int SPLIT_MERGE_FLOATS = 2 * SPLIT_KS * 34 * 64;  // per (group, wave): o0, o1 (16 x 64 each), m, l (64 each)
+
+__global__ void __launch_bounds__(64 * ROW_WAVES) attn_split_kernel(AttnArgs a) {
+  extern __shared__ uint4 lds[];  // K rows [KR][8], V rows [KR][8]; after the key loop the groups' merge states
+  const int KR = row_krows(a.kv_max);
+  uint4* Ks = lds;
+  uint4* Vs = lds + KR * 8;
+  const int nblk = gridDim.x * gridDim.y, full = (nblk / 8) * 8;
+  int lin = blockIdx.y * gridDim.x + blockIdx.x;
+  if (lin < full) lin = (lin % 8) * (nblk / 8) + lin / 8;
+  const int tile = lin % gridDim.x, head = lin / gridDim.x;
+  const int w8 = threadIdx.x >> 6, gi = threadIdx.x >> 7, lane = threadIdx.x & 63, wave = w8 & 1;
+  const int row = a.tiles[2 * tile];
+  const int q0 = a.tiles[2 * tile + 1];
+  const int T = a.row_len[row];
+  if (q0 >= T) return;
+  const int start = a.row_start[row], kvoff = a.row_kv_off[row], kvlen = a.row_kv_len[row];
+  const int H = a.heads * 64;
+  if (kvlen > a.kv_max) {
+    nan_rows(a, start, q0, min(q0 + 64, T), head, threadIdx.x, 64 * ROW_WAVES);
+    return;
+  }
+  load_key_list(Ks, Vs, a, kvoff, kvlen, head, w8, lane);
+  const int half = lane >> 5, col = lane & 31;
+  const int qpos0 = q0 + wave * 32;
+  const bool active = qpos0 < T;
+  const int myq = qpos0 + col, qc = myq < T ? myq : T - 1;
+  const int lim_me = a.chunk > 0 ? min(T, (qc / a.chunk + 1) * a.chunk) : T;
+  const int tile_last = min(q0 + 63, T - 1);
+  const int lim_max = a.chunk > 0 ? min(T, (tile_last / a.chunk + 1) * a.chunk) : T;
+  const int lim_w0 = a.chunk > 0 ? min(T, (qpos0 / a.chunk + 1) * a.chunk) : T;
+  const float sl2 = a.scale * 1.4426950408889634f;
+  f32x16 o0, o1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) { o0[r] = 0.f; o1[r] = 0.f; }
+  float m = NEG, l = 0.f;
+  if (active) {
+    bf16x8 qf[4];
+    const bf16_t* qp = a.q + (size_t)(start + qc) * H + head * 64 + half * 8;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) qf[kk] = as_bf16x8(*(const uint4*)(qp + kk * 16));
+    const int n1 = (lim_max + 63) / 64, n2 = (kvlen - T + 63) / 64;
+    for (int t = gi; t < n1 + n2; t += SPLIT_KS) {
+      const bool cached = t >= n1;
+      const int kb = cached ? T + (t - n1) * 64 : t * 64, ke = cached ? kvlen : lim_max;
+      const int lim = cached ? ke : min(ke, lim_me);
+      const int lim_lo = cached ? ke : min(ke, lim_w0);
+      lds_key_tile(Ks, Vs, kb, ke, lim, lim_lo, qf, sl2, lane, o0, o1, m, l);
+    }
+  }
+  // merge: the lists are no longer read; groups 1.. leave their states in LDS, group 0 folds them in group order
+  __syncthreads();
+  float* xs = (float*)lds;
+  if (gi > 0) {
+    float* x = xs + (gi * 2 + wave) * (34 * 64);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { x[r * 64 + lane] = o0[r]; x[(16 + r) * 64 + lane] = o1[r]; }
+    x[32 * 64 + lane] = m;
+    x[33 * 64 + lane] = l;
+  }
+  __syncthreads();
+  if (gi > 0 || !active || myq >= T) return;
+#pragma unroll
+  for (int g2 = 1; g2 < SPLIT_KS; ++g2) {
+    const float* y = xs + (g2 * 2 + wave) * (34 * 64);
+    const float mg = y[32 * 64 + lane], lg = y[33 * 64 + lane];
+    const float mn = fmaxf(m, mg);
+    const float fa = __builtin_amdgcn_exp2f((m - mn) * sl2), fb = __builtin_amdgcn_exp2f((mg - mn) * sl2);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      o0[r] = o0[r] * fa + y[r * 64 + lane] * fb;
+      o1[r] = o1[r] * fa + y[(16 + r) * 64 + lane] * fb;
+    }
+    l = l * fa + lg * fb;
+    m = mn;
+  }
+  const float inv = 1.0f / l;
+  if (a.out8) {
+    float m0 = 0.f, m1 = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { m0 = fmaxf(m0, fabsf(o0[r])); m1 = fmaxf(m1, fabsf(o1[r])); }
+    m0 = fmaxf(m0, __shfl_xor(m0, 32, 64)) * inv;
+    m1 = fmaxf(m1, __shfl_xor(m1, 32, 64)) * inv;
+    const int e0 = mx_exp(m0), e1 = mx_exp(m1);
+    uint8_t* qp = a.out8 + (size_t)(start + myq) * H + head * 64;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = g * 8 + half * 4;
+      *(uint32_t*)(qp + d) = mx_pack4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv, e0);
+      *(uint32_t*)(qp + 32 + d) = mx_pack4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv, e1);
+    }
+    if (half == 0) {
+      uint8_t* sp = a.out8s + (size_t)(start + myq) * (H / 32) + head * 2;
+      sp[0] = (uint8_t)(e0 + 127);
+      sp[1] = (uint8_t)(e1 + 127);
+    }
+    return;
+  }
+  bf16_t* op = a.out + (size_t)(start + myq) * H + head * 64;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int d = g * 8 + half * 4;
+    *(uint2*)(op + d) = make_uint2(pack2(o0[4 * g] * inv, o0[4 * g + 1] * inv), pack2(o0[4 * g + 2] * inv, o0[4 * g + 3] * inv));
+    *(uint2*)(op + 32 + d) = make_uint2(pack2(o1[4 * g] * inv, o1[4 * g + 1] * inv), pack2(o1[4 * g + 2] * inv, o1[4 * g + 3] * inv));
+  }
+}
+
 }  // namespace
 
 hipError_t attention(const AttnArgs& a, hipStream_t st) {
   if (a.n_tiles <= 0) return hipSuccess;
   // a grid of fewer workgroups than CUs (a streaming chunk) splits each workgroup's key tiles over four wave groups
-  if (a.n_tiles * a.heads < 256) {
+  if (a.n_tiles * a.heads < 256 && a.kv_max > 0 && a.kv_max <= ATTN_ROW_KMAX) {
+    static bool sattr = false;
+    if (!sattr) {
+      const hipError_t e = hipFuncSetAttribute((const void*)attn_split_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               2 * ROW_KROWS * 8 * (int)sizeof(uint4));
+      if (e != hipSuccess) return e;
+      sattr = true;
+    }
+    const size_t lds = max(2 * (size_t)row_krows(a.kv_max) * 8 * sizeof(uint4), (size_t)SPLIT_MERGE_FLOATS * sizeof(float));
+    hipLaunchKernelGGL(attn_split_kernel, dim3(a.n_tiles, a.heads), dim3(64 * ROW_WAVES), lds, st, a);
+  } else if (a.n_tiles * a.heads < 256) {
     hipLaunchKernelGGL(attn_kernel<4>, dim3(a.n_tiles, a.heads), dim3(512), 0, st, a);
   } else if (a.kv_max > 0 && a.kv_max <= ATTN_ROW_KMAX && (long)a.n_rows * a.heads >= 256 && a.n_tiles >= 3 * a.n_rows) {
     // rows of three or more query tiles on average: with fewer, most of a row workgroup's eight waves would idle
