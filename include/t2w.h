@@ -266,8 +266,7 @@ int t2w_qk_norm_scatter(const void* qkv, const float* qw, const float* qb, const
  * then cached keys); tiles [n_tiles, 2] lists (row, first query) of every 64-query tile.  chunk > 0: a new token sees
  * the new tokens of its own and earlier chunks only; cached keys are always visible.  n_rows: rows of the call;
  * kv_max: 0, or a bound on every row_kv_len[r] (as t2w_solve_args.kv_max; bounds up to 512 select the row-resident
- * kernels: on calls of 256 or more (row, head) pairs whose rows average three or more 64-query tiles, and on calls of
- * fewer than 256 (tile, head) pairs). */
+ * kernel on calls of 256 or more (row, head) pairs whose rows average three or more 64-query tiles). */
 int t2w_attention(const void* q, const void* k_pool, const void* v_pool, void* out, const int* kv_idx,
                   const int* row_start, const int* row_len, const int* row_kv_off, const int* row_kv_len,
                   const int* tiles, int n_tiles, int heads, int chunk, float scale, int n_rows, int kv_max,

@@ -520,134 +520,12 @@ __global__ void __launch_bounds__(64 * ROW_WAVES) __attribute__((amdgpu_waves_pe
   }
 }
 
-// Small calls (fewer (tile, head) workgroups than CUs, e.g. a streaming chunk) with a bounded key list: attn_kernel<4>'s
-// grid and key split (four groups of two waves per 64-query tile, group g taking key tiles g, g + 4, ..., merged in
-// group order) with the row's whole key list copied into LDS once instead of gathered tile by tile, so the
-// arithmetic and its order are the same and so are the output bits.
-constexpr int SPLIT_KS = 4;
-constexpr int SPLIT_MERGE_FLOATS = 2 * SPLIT_KS * 34 * 64;  // per (group, wave): o0, o1 (16 x 64 each), m, l (64 each)
-
-__global__ void __launch_bounds__(64 * ROW_WAVES) attn_split_kernel(AttnArgs a) {
-  extern __shared__ uint4 lds[];  // K rows [KR][8], V rows [KR][8]; after the key loop the groups' merge states
-  const int KR = row_krows(a.kv_max);
-  uint4* Ks = lds;
-  uint4* Vs = lds + KR * 8;
-  const int nblk = gridDim.x * gridDim.y, full = (nblk / 8) * 8;
-  int lin = blockIdx.y * gridDim.x + blockIdx.x;
-  if (lin < full) lin = (lin % 8) * (nblk / 8) + lin / 8;
-  const int tile = lin % gridDim.x, head = lin / gridDim.x;
-  const int w8 = threadIdx.x >> 6, gi = threadIdx.x >> 7, lane = threadIdx.x & 63, wave = w8 & 1;
-  const int row = a.tiles[2 * tile];
-  const int q0 = a.tiles[2 * tile + 1];
-  const int T = a.row_len[row];
-  if (q0 >= T) return;
-  const int start = a.row_start[row], kvoff = a.row_kv_off[row], kvlen = a.row_kv_len[row];
-  const int H = a.heads * 64;
-  if (kvlen > a.kv_max) {
-    nan_rows(a, start, q0, min(q0 + 64, T), head, threadIdx.x, 64 * ROW_WAVES);
-    return;
-  }
-  load_key_list(Ks, Vs, a, kvoff, kvlen, head, w8, lane);
-  const int half = lane >> 5, col = lane & 31;
-  const int qpos0 = q0 + wave * 32;
-  const bool active = qpos0 < T;
-  const int myq = qpos0 + col, qc = myq < T ? myq : T - 1;
-  const int lim_me = a.chunk > 0 ? min(T, (qc / a.chunk + 1) * a.chunk) : T;
-  const int tile_last = min(q0 + 63, T - 1);
-  const int lim_max = a.chunk > 0 ? min(T, (tile_last / a.chunk + 1) * a.chunk) : T;
-  const int lim_w0 = a.chunk > 0 ? min(T, (qpos0 / a.chunk + 1) * a.chunk) : T;
-  const float sl2 = a.scale * 1.4426950408889634f;
-  f32x16 o0, o1;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) { o0[r] = 0.f; o1[r] = 0.f; }
-  float m = NEG, l = 0.f;
-  if (active) {
-    bf16x8 qf[4];
-    const bf16_t* qp = a.q + (size_t)(start + qc) * H + head * 64 + half * 8;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) qf[kk] = as_bf16x8(*(const uint4*)(qp + kk * 16));
-    const int n1 = (lim_max + 63) / 64, n2 = (kvlen - T + 63) / 64;
-    for (int t = gi; t < n1 + n2; t += SPLIT_KS) {
-      const bool cached = t >= n1;
-      const int kb = cached ? T + (t - n1) * 64 : t * 64, ke = cached ? kvlen : lim_max;
-      const int lim = cached ? ke : min(ke, lim_me);
-      const int lim_lo = cached ? ke : min(ke, lim_w0);
-      lds_key_tile(Ks, Vs, kb, ke, lim, lim_lo, qf, sl2, lane, o0, o1, m, l);
-    }
-  }
-  // merge: the lists are no longer read; groups 1.. leave their states in LDS, group 0 folds them in group order
-  __syncthreads();
-  float* xs = (float*)lds;
-  if (gi > 0) {
-    float* x = xs + (gi * 2 + wave) * (34 * 64);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) { x[r * 64 + lane] = o0[r]; x[(16 + r) * 64 + lane] = o1[r]; }
-    x[32 * 64 + lane] = m;
-    x[33 * 64 + lane] = l;
-  }
-  __syncthreads();
-  if (gi > 0 || !active || myq >= T) return;
-#pragma unroll
-  for (int g2 = 1; g2 < SPLIT_KS; ++g2) {
-    const float* y = xs + (g2 * 2 + wave) * (34 * 64);
-    const float mg = y[32 * 64 + lane], lg = y[33 * 64 + lane];
-    const float mn = fmaxf(m, mg);
-    const float fa = __builtin_amdgcn_exp2f((m - mn) * sl2), fb = __builtin_amdgcn_exp2f((mg - mn) * sl2);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      o0[r] = o0[r] * fa + y[r * 64 + lane] * fb;
-      o1[r] = o1[r] * fa + y[(16 + r) * 64 + lane] * fb;
-    }
-    l = l * fa + lg * fb;
-    m = mn;
-  }
-  const float inv = 1.0f / l;
-  if (a.out8) {
-    float m0 = 0.f, m1 = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) { m0 = fmaxf(m0, fabsf(o0[r])); m1 = fmaxf(m1, fabsf(o1[r])); }
-    m0 = fmaxf(m0, __shfl_xor(m0, 32, 64)) * inv;
-    m1 = fmaxf(m1, __shfl_xor(m1, 32, 64)) * inv;
-    const int e0 = mx_exp(m0), e1 = mx_exp(m1);
-    uint8_t* qp = a.out8 + (size_t)(start + myq) * H + head * 64;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = g * 8 + half * 4;
-      *(uint32_t*)(qp + d) = mx_pack4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv, e0);
-      *(uint32_t*)(qp + 32 + d) = mx_pack4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv, e1);
-    }
-    if (half == 0) {
-      uint8_t* sp = a.out8s + (size_t)(start + myq) * (H / 32) + head * 2;
-      sp[0] = (uint8_t)(e0 + 127);
-      sp[1] = (uint8_t)(e1 + 127);
-    }
-    return;
-  }
-  bf16_t* op = a.out + (size_t)(start + myq) * H + head * 64;
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int d = g * 8 + half * 4;
-    *(uint2*)(op + d) = make_uint2(pack2(o0[4 * g] * inv, o0[4 * g + 1] * inv), pack2(o0[4 * g + 2] * inv, o0[4 * g + 3] * inv));
-    *(uint2*)(op + 32 + d) = make_uint2(pack2(o1[4 * g] * inv, o1[4 * g + 1] * inv), pack2(o1[4 * g + 2] * inv, o1[4 * g + 3] * inv));
-  }
-}
-
 }  // namespace
 
 hipError_t attention(const AttnArgs& a, hipStream_t st) {
   if (a.n_tiles <= 0) return hipSuccess;
   // a grid of fewer workgroups than CUs (a streaming chunk) splits each workgroup's key tiles over four wave groups
-  if (a.n_tiles * a.heads < 256 && a.kv_max > 0 && a.kv_max <= ATTN_ROW_KMAX) {
-    static bool sattr = false;
-    if (!sattr) {
-      const hipError_t e = hipFuncSetAttribute((const void*)attn_split_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               2 * ROW_KROWS * 8 * (int)sizeof(uint4));
-      if (e != hipSuccess) return e;
-      sattr = true;
-    }
-    const size_t lds = max(2 * (size_t)row_krows(a.kv_max) * 8 * sizeof(uint4), (size_t)SPLIT_MERGE_FLOATS * sizeof(float));
-    hipLaunchKernelGGL(attn_split_kernel, dim3(a.n_tiles, a.heads), dim3(64 * ROW_WAVES), lds, st, a);
-  } else if (a.n_tiles * a.heads < 256) {
+  if (a.n_tiles * a.heads < 256) {
     hipLaunchKernelGGL(attn_kernel<4>, dim3(a.n_tiles, a.heads), dim3(512), 0, st, a);
   } else if (a.kv_max > 0 && a.kv_max <= ATTN_ROW_KMAX && (long)a.n_rows * a.heads >= 256 && a.n_tiles >= 3 * a.n_rows) {
     // rows of three or more query tiles on average: with fewer, most of a row workgroup's eight waves would idle

@@ -277,18 +277,16 @@ def _attention_case(dev, lens, cached, heads, chunk, seed, kv_max=0):
 
 @pytest.mark.parametrize("chunk", [0, 50])
 @pytest.mark.parametrize("rep", [1, 9])
-@pytest.mark.parametrize("kv_max", [0, 512])
-def test_attention_paged_block_causal(dev, chunk, rep, kv_max):
+def test_attention_paged_block_causal(dev, chunk, rep):
     """Rows of new frames with cached keys in scattered slots; mask: cached keys always visible, new keys by chunk.
-    rep 1: 32 workgroups (the key tiles of each split over four wave groups and merged; with kv_max the key lists are
-    copied into LDS whole, the same bits); rep 9: 288 (one group)."""
-    _attention_case(dev, [50, 1, 0, 130, 64, 65] * rep, [300, 0, 7, 0, 100, 33] * rep, 4, chunk, 9 + chunk, kv_max=kv_max)
+    rep 1: 32 workgroups (the key tiles of each split over four wave groups and merged); rep 9: 288 (one group)."""
+    _attention_case(dev, [50, 1, 0, 130, 64, 65] * rep, [300, 0, 7, 0, 100, 33] * rep, 4, chunk, 9 + chunk)
 
 
 @pytest.mark.parametrize("chunk", [0, 50])
-def test_attention_stream_chunk_split(dev, chunk):
-    """The streaming chunk's call (a CFG pair of 50 new frames over 300 and 470 cached keys, 16 heads) through the
-    split row-resident kernel: equal to the tile kernel bit for bit and to fp32."""
+def test_attention_stream_chunk(dev, chunk):
+    """The streaming chunk's call (a CFG pair of 50 new frames over 300 and 462 cached keys, 16 heads) with the
+    planner's key bound: the bound leaves small calls on the tile kernel (the same bits) and the result matches fp32."""
     _attention_case(dev, [50, 50], [300, 462], 16, chunk, 41 + chunk, kv_max=512)
 
 
