@@ -130,11 +130,13 @@ def _stream_pair(W, Wh, cfg, P, windows, seed, graphs=False):
     return mel_err, got, ref
 
 
-def test_config2_chunk_full_size(dev):
+@pytest.mark.parametrize("graphs", [False, True])
+def test_config2_chunk_full_size(dev, graphs):
     """The streaming chunk of the latency workload at full model size: a 300-frame prompt setup (600 tokens with the CFG
-    pair), then a 50-frame first window and a 50-frame final window through ``decode`` (DiT + HiFT + glue)."""
+    pair), then a 50-frame first window and a 50-frame final window through ``decode`` (DiT + HiFT + glue).  With
+    graphs the DiT solves replay bucket graphs and HiFT its own graphs, as in the latency bench, against the oracle."""
     W, Wh = init_dit(DiTConfig(), seed=1), init_hift(HiFTConfig(), seed=1)
-    mel_err, got, ref = _stream_pair(W, Wh, DiTConfig(), 300, [50, 50], seed=1)
+    mel_err, got, ref = _stream_pair(W, Wh, DiTConfig(), 300, [50, 50], seed=1, graphs=graphs)
     a, b = np.concatenate(got), np.concatenate(ref)
     e = float(np.linalg.norm(a - b) / np.linalg.norm(b))
     print("config-2 window mel rel-L2", mel_err, "audio vs oracle glue on the same mels", e)
