@@ -385,38 +385,38 @@ __device__ __forceinline__ void lds_key_tile(const uint4* Ks, const uint4* Vs, i
   }
 }
 
-// Row-resident form for large calls whose key lists fit in LDS: one workgroup of 8 waves per (row, head) copies the
+// Row-resident form for large calls whose key lists fit in LDS: one workgroup of NWV waves per (row, head) copies the
 // row's whole key and value lists for the head into LDS once (global_load_lds by slot id, the same key-major 16-byte
 // chunk swizzle as the tiles above, and past the list's end up to 63 clamped, finite keys that a last tile overhangs),
 // then its waves take the 32-query blocks, latest (most keys) first, and run each block's key tiles straight from LDS:
 // no gathers, stores or barriers inside the key loop, and the keys and values of a row are read from the pools once
 // per head instead of once per 64-query tile.  The waves take the blocks in a fixed snake order (round r: wave w, or
-// 7 - w on odd rounds), so the costliest blocks spread over the waves.  LDS holds round8(kv_max + 63) keys: with
-// kv_max <= 256 two workgroups share a CU (80 KB each; one copies while the other computes), registers capped at 128
-// per lane for their four waves per SIMD.  Per query the arithmetic is that of attn_kernel, in the same order, so the
-// outputs are the same bits.
-constexpr int ROW_WAVES = 8;
+// NWV - 1 - w on odd rounds), so the costliest blocks spread over the waves.  LDS holds round8(kv_max + 63) keys:
+// with kv_max <= 256 two workgroups of 8 waves share a CU (80 KB each; one copies while the other computes), longer
+// lists take one workgroup of 16 waves per CU (up to 144 KB); either way four waves per SIMD, registers capped at
+// 128 per lane.  Per query the arithmetic is that of attn_kernel, in the same order, so the outputs are the same bits.
 __host__ __device__ constexpr int row_krows(int kv_max) { return (kv_max + 63 + 7) / 8 * 8; }
 constexpr int ROW_KROWS = row_krows(ATTN_ROW_KMAX);
 
 // The key list kv_idx[kvoff ..][0 .. kvlen) of one head into LDS (K and V key-major, 16-byte chunks swizzled by key,
 // rows up to round8(kvlen + 63) with the keys past the end clamped to the last), then waits for it and a barrier.
 // 8-key blocks go to the workgroup's 8 waves in turn; lane l fetches key 8 b + l / 8's chunk (l % 8) ^ key.
+template <int NWV>
 __device__ __forceinline__ void load_key_list(uint4* Ks, uint4* Vs, const AttnArgs& a, int kvoff, int kvlen, int head, int wave,
                                               int lane) {
   const int H = a.heads * 64;
   const int nb8 = row_krows(kvlen) / 8;
-  constexpr int MAXB = ROW_KROWS / 8 / ROW_WAVES;
+  constexpr int MAXB = (ROW_KROWS / 8 + NWV - 1) / NWV;
   int slot[MAXB];
 #pragma unroll
   for (int i = 0; i < MAXB; ++i) {
-    const int b8 = wave + ROW_WAVES * i, key = b8 * 8 + (lane >> 3);
+    const int b8 = wave + NWV * i, key = b8 * 8 + (lane >> 3);
     slot[i] = b8 < nb8 ? a.kv_idx[kvoff + min(key, kvlen - 1)] : 0;
   }
   const int ch = ((lane & 7) ^ ((lane >> 3) & 7)) * 8;  // the key's row-local index is b8 * 8 + lane / 8: key & 7 = lane / 8
 #pragma unroll
   for (int i = 0; i < MAXB; ++i) {
-    const int b8 = wave + ROW_WAVES * i;
+    const int b8 = wave + NWV * i;
     if (b8 < nb8) {
       const size_t go = (size_t)slot[i] * H + head * 64 + ch;
       __builtin_amdgcn_global_load_lds((const void*)(a.k_pool + go), (lds_ptr_t)(Ks + b8 * 64), 16, 0, 0);
@@ -441,7 +441,8 @@ __device__ __forceinline__ void nan_rows(const AttnArgs& a, int start, int q0, i
   }
 }
 
-__global__ void __launch_bounds__(64 * ROW_WAVES) __attribute__((amdgpu_waves_per_eu(4, 4))) attn_row_kernel(AttnArgs a) {
+template <int NWV>
+__global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4, 4))) attn_row_kernel(AttnArgs a) {
   extern __shared__ uint4 lds[];  // K rows [KR][8 chunks], then V rows [KR][8 chunks]
   const int KR = row_krows(a.kv_max);
   uint4* Ks = lds;
@@ -453,15 +454,15 @@ __global__ void __launch_bounds__(64 * ROW_WAVES) __attribute__((amdgpu_waves_pe
   const int start = a.row_start[row], kvoff = a.row_kv_off[row], kvlen = a.row_kv_len[row];
   const int H = a.heads * 64;
   if (kvlen > a.kv_max) {  // longer than the caller's bound: NaN outputs instead of copies past the LDS lists
-    nan_rows(a, start, 0, T, head, tid, 64 * ROW_WAVES);
+    nan_rows(a, start, 0, T, head, tid, 64 * NWV);
     return;
   }
-  load_key_list(Ks, Vs, a, kvoff, kvlen, head, wave, lane);
+  load_key_list<NWV>(Ks, Vs, a, kvoff, kvlen, head, wave, lane);
   const int half = lane >> 5, col = lane & 31;
   const float sl2 = a.scale * 1.4426950408889634f;
   const int nblk = (T + 31) / 32;
-  for (int rnd = 0; rnd * ROW_WAVES < nblk; ++rnd) {
-    const int bi = rnd * ROW_WAVES + ((rnd & 1) ? ROW_WAVES - 1 - wave : wave);
+  for (int rnd = 0; rnd * NWV < nblk; ++rnd) {
+    const int bi = rnd * NWV + ((rnd & 1) ? NWV - 1 - wave : wave);
     if (bi >= nblk) break;
     const int q0 = (nblk - 1 - bi) * 32;
     const int myq = q0 + col, qc = myq < T ? myq : T - 1;
@@ -532,13 +533,19 @@ hipError_t attention(const AttnArgs& a, hipStream_t st) {
     // while its whole key list is copied (the tile kernel is faster there)
     static bool attr = false;
     if (!attr) {
-      const hipError_t e = hipFuncSetAttribute((const void*)attn_row_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               2 * ROW_KROWS * 8 * (int)sizeof(uint4));
+      hipError_t e = hipFuncSetAttribute((const void*)attn_row_kernel<8>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         2 * ROW_KROWS * 8 * (int)sizeof(uint4));
+      if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)attn_row_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                2 * ROW_KROWS * 8 * (int)sizeof(uint4));
       if (e != hipSuccess) return e;
       attr = true;
     }
     const size_t lds = 2 * (size_t)row_krows(a.kv_max) * 8 * sizeof(uint4);
-    hipLaunchKernelGGL(attn_row_kernel, dim3(a.heads, a.n_rows), dim3(64 * ROW_WAVES), lds, st, a);
+    if (a.kv_max <= 256)  // two workgroups of 8 waves per CU
+      hipLaunchKernelGGL(attn_row_kernel<8>, dim3(a.heads, a.n_rows), dim3(64 * 8), lds, st, a);
+    else  // one workgroup of 16 waves per CU
+      hipLaunchKernelGGL(attn_row_kernel<16>, dim3(a.heads, a.n_rows), dim3(64 * 16), lds, st, a);
   } else {
     hipLaunchKernelGGL(attn_kernel<1>, dim3(a.n_tiles, a.heads), dim3(128), 0, st, a);
   }
