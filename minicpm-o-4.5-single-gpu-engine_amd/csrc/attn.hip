@@ -16,6 +16,10 @@
 // lanes, lane j names a row of four 16-bit values and lane i receives element i % 4 of rows i / 4 + 4 e, e = 0..3), two
 // per fragment, each giving a lane 4 consecutive keys of its own channel d -- exactly the keys whose probabilities
 // the score MFMA left in that lane.
+//
+// Large calls whose caller bounds every key list (AttnArgs.kv_max <= 512) take a row-resident form instead: one
+// workgroup per (row, head) copies the whole list into LDS once with global_load_lds and runs every query block of the
+// row from there (attn_row_kernel); the per-query arithmetic and its order are the tile kernel's, so are the bits.
 #include "common.h"
 #include "t2w_internal.h"
 
@@ -529,18 +533,15 @@ hipError_t attention(const AttnArgs& a, hipStream_t st) {
   if (a.n_tiles * a.heads < 256) {
     hipLaunchKernelGGL(attn_kernel<4>, dim3(a.n_tiles, a.heads), dim3(512), 0, st, a);
   } else if (a.kv_max > 0 && a.kv_max <= ATTN_ROW_KMAX && (long)a.n_rows * a.heads >= 256 && a.n_tiles >= 3 * a.n_rows) {
-    // rows of three or more query tiles on average: with fewer, most of a row workgroup's eight waves would idle
-    // while its whole key list is copied (the tile kernel is faster there)
-    static bool attr = false;
-    if (!attr) {
-      hipError_t e = hipFuncSetAttribute((const void*)attn_row_kernel<8>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         2 * ROW_KROWS * 8 * (int)sizeof(uint4));
-      if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void*)attn_row_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                2 * ROW_KROWS * 8 * (int)sizeof(uint4));
-      if (e != hipSuccess) return e;
-      attr = true;
-    }
+    // rows of three or more query tiles on average: with fewer, most of a row workgroup's waves would idle while its
+    // whole key list is copied (the tile kernel is faster there)
+    static const hipError_t attr = [] {  // once per process (thread-safe initialisation): the LDS above 64 KB
+      const int bytes = 2 * ROW_KROWS * 8 * (int)sizeof(uint4);
+      hipError_t e = hipFuncSetAttribute((const void*)attn_row_kernel<8>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+      if (e == hipSuccess) e = hipFuncSetAttribute((const void*)attn_row_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+      return e;
+    }();
+    if (attr != hipSuccess) return attr;
     const size_t lds = 2 * (size_t)row_krows(a.kv_max) * 8 * sizeof(uint4);
     if (a.kv_max <= 256)  // two workgroups of 8 waves per CU
       hipLaunchKernelGGL(attn_row_kernel<8>, dim3(a.heads, a.n_rows), dim3(64 * 8), lds, st, a);

@@ -1503,12 +1503,9 @@ hipError_t conv_bf16(const ConvDesc& c, const bf16_t* wbf, int max_rows, hipStre
   } else if (tiles512 >= 256) {
     constexpr int BM = 512;
     const size_t lds = conv_bf16_lds(BM);
-    static bool attr = false;
-    if (!attr) {
-      hipError_t e = hipFuncSetAttribute((const void*)conv_bf16_kernel<BM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-      attr = true;
-    }
+    static const hipError_t attr =  // once per process (thread-safe initialisation)
+        hipFuncSetAttribute((const void*)conv_bf16_kernel<BM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
     dim3 grid(cdiv(max_rows, BM), cdiv(c.Cout, HB_BN), c.n_items * c.n_phase);
     hipLaunchKernelGGL(conv_bf16_kernel<BM>, grid, dim3(256), lds, st, c, wbf);
   } else {
@@ -1531,12 +1528,9 @@ size_t resblock_pair_lds(int C) {
 template <int C>
 hipError_t launch_pair(const ConvDesc& c1, const ConvDesc& c2, int max_rows, hipStream_t st) {
   const size_t lds = resblock_pair_lds(C);
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)resblock_pair_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  static const hipError_t attr =  // once per process (thread-safe initialisation)
+      hipFuncSetAttribute((const void*)resblock_pair_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) return attr;
   dim3 grid(cdiv(max_rows, resblock_pair_rows(C, c1.taps)), c1.n_items);
   hipLaunchKernelGGL(resblock_pair_kernel<C>, grid, dim3(256), lds, st, c1, c2);
   return hipGetLastError();
