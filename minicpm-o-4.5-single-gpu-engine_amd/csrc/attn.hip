@@ -392,10 +392,9 @@ __device__ __forceinline__ void lds_key_tile(const uint4* Ks, const uint4* Vs, i
 // Row-resident form for large calls whose key lists fit in LDS: one workgroup of NWV waves per (row, head) copies the
 // row's whole key and value lists for the head into LDS once (global_load_lds by slot id, the same key-major 16-byte
 // chunk swizzle as the tiles above, and past the list's end up to 63 clamped, finite keys that a last tile overhangs),
-// then its waves take the 32-query blocks, latest (most keys) first, and run each block's key tiles straight from LDS:
-// no gathers, stores or barriers inside the key loop, and the keys and values of a row are read from the pools once
-// per head instead of once per 64-query tile.  The waves take the blocks in a fixed snake order (round r: wave w, or
-// NWV - 1 - w on odd rounds), so the costliest blocks spread over the waves.  LDS holds round8(kv_max + 63) keys:
+// then each wave takes one 32-query block (T <= kv_max <= 32 NWV) and runs its key tiles straight from LDS: no
+// gathers, stores or barriers inside the key loop, and the keys and values of a row are read from the pools once per
+// head instead of once per 64-query tile.  LDS holds round8(kv_max + 63) keys:
 // with kv_max <= 256 two workgroups of 8 waves share a CU (80 KB each; one copies while the other computes), longer
 // lists take one workgroup of 16 waves per CU (up to 144 KB); either way four waves per SIMD, registers capped at
 // 128 per lane.  Per query the arithmetic is that of attn_kernel, in the same order, so the outputs are the same bits.
@@ -457,17 +456,22 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4
   if (T <= 0) return;
   const int start = a.row_start[row], kvoff = a.row_kv_off[row], kvlen = a.row_kv_len[row];
   const int H = a.heads * 64;
-  if (kvlen > a.kv_max) {  // longer than the caller's bound: NaN outputs instead of copies past the LDS lists
+  if (kvlen > a.kv_max || T > 32 * NWV) {  // longer than the caller's bound: NaN outputs instead of copies past the
+                                          // LDS lists (a row's tokens are part of its list, so T <= kvlen)
     nan_rows(a, start, 0, T, head, tid, 64 * NWV);
     return;
   }
   load_key_list<NWV>(Ks, Vs, a, kvoff, kvlen, head, wave, lane);
   const int half = lane >> 5, col = lane & 31;
   const float sl2 = a.scale * 1.4426950408889634f;
+  // T <= kv_max <= 32 NWV: at most one 32-query block per wave.  Blocks by cost (latest first) go to the waves in a
+  // snake over the SIMDs (wave w runs on SIMD w % 4; round r = w / 4 hands SIMD s the (4 r + s)-th costliest block, or
+  // the (4 r + 3 - s)-th on odd rounds), so each SIMD gets a mix of long and short blocks
   const int nblk = (T + 31) / 32;
-  for (int rnd = 0; rnd * NWV < nblk; ++rnd) {
-    const int bi = rnd * NWV + ((rnd & 1) ? NWV - 1 - wave : wave);
-    if (bi >= nblk) break;
+  {
+    const int r = wave >> 2, sm = wave & 3;
+    const int bi = r * 4 + ((r & 1) ? 3 - sm : sm);
+    if (bi >= nblk) return;
     const int q0 = (nblk - 1 - bi) * 32;
     const int myq = q0 + col, qc = myq < T ? myq : T - 1;
     const int lim_me = a.chunk > 0 ? min(T, (qc / a.chunk + 1) * a.chunk) : T;
@@ -492,7 +496,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4
       const int lim_lo = cached ? ke : min(ke, lim_w0);
       lds_key_tile(Ks, Vs, kb, ke, lim, lim_lo, qf, sl2, lane, o0, o1, m, l);
     }
-    if (myq >= T) continue;
+    if (myq >= T) return;
     const float inv = 1.0f / l;
     if (a.out8) {
       float m0 = 0.f, m1 = 0.f;
@@ -513,7 +517,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4
         sp[0] = (uint8_t)(e0 + 127);
         sp[1] = (uint8_t)(e1 + 127);
       }
-      continue;
+      return;
     }
     bf16_t* op = a.out + (size_t)(start + myq) * H + head * 64;
 #pragma unroll
