@@ -71,6 +71,30 @@ def test_north_star_16x400_chunk50(dev, full):
     assert worst < TOL and same < SAME
 
 
+@pytest.mark.parametrize("Ts", [[400] * 16, [200] * 16], ids=["16x400", "16x200"])
+def test_key_bound_same_solve(dev, full, monkeypatch, Ts):
+    """The planner's key-list bound (512 at 400 frames, 256 at 200: the row-resident attention) leaves the whole packed
+    solve unchanged bit for bit against the same solve without a bound (the tile attention)."""
+    import t2w_amd.dit as dit_mod
+    W, model = full
+    g = torch.Generator().manual_seed(5)
+    mus = [torch.randn(80, t, generator=g).cuda() for t in Ts]
+    spks = torch.randn(len(Ts), 80, generator=g).cuda()
+    outs = {}
+    for bound in (True, False):
+        if not bound:
+            monkeypatch.setattr(dit_mod, "_kv_max", lambda p: 0)
+        fd = FastDiT(model, n_slots=2 * sum(Ts) + 4096, max_streams=len(Ts))
+        caches = [fd.new_cache() for _ in Ts]
+        outs[bound] = torch.cat(fd.solve(caches, mus, spks, None, [False] * len(Ts), chunk=50), dim=1).cpu()
+        for c in caches:
+            fd.release(c)
+    assert dit_mod._kv_max({"parts": [None] * 7 + [np.array([max(Ts)] * 2)]}) == 0  # the patch is in place
+    monkeypatch.undo()
+    assert dit_mod._kv_max({"parts": [None] * 7 + [np.array([max(Ts)] * 2)]}) == (512 if max(Ts) > 256 else 256)
+    assert torch.equal(outs[True], outs[False])
+
+
 def test_ragged_16_streams_150_450(dev, full):
     W, model = full
     Ts = [int(t) for t in np.random.default_rng(2).integers(150, 451, size=16)]

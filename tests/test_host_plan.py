@@ -123,3 +123,14 @@ def test_slot_pool_reserved_and_exhaustion():
     assert pool.in_use() == 1
     b = pool.alloc(7)
     assert sorted(_L(b) + _L(pool.reserved)) == list(range(8))
+
+
+def test_kv_max_classes():
+    """The key-list bound a call states: 256 or 512 when every row's list fits (the row-resident attention's two LDS
+    sizes), 0 beyond 512; it is part of the graph keys, so a replay never exceeds its capture's bound."""
+    import numpy as np
+    from t2w_amd.dit import ATTN_ROW_KMAX, _kv_max
+    part = lambda lens: {"parts": [None] * 7 + [np.array(lens, dtype=np.int64)]}  # noqa: E731
+    assert ATTN_ROW_KMAX == 512
+    assert _kv_max(part([1, 256])) == 256 and _kv_max(part([257, 3])) == 512 and _kv_max(part([512])) == 512
+    assert _kv_max(part([513, 10])) == 0 and _kv_max(part([])) == 256
