@@ -16,6 +16,7 @@ import torch
 
 from . import _lib
 from .config import MEL_CACHE, SOURCE_CACHE, HiFTConfig
+from .weights import fold_weight_norm
 
 
 def chunk_noise_seed(noise_seed: int, chunk: int) -> int:
@@ -30,8 +31,11 @@ REFERENCE_FP32_CONVS = ("conv_pre", "ups.0", "conv_post")
 
 class HiFTModel:
     def __init__(self, W: dict, cfg: HiFTConfig = HiFTConfig(), device: str = "cuda", decode_bf16: bool = False,
-                 use_graphs: bool = False, max_graphs: int = 32, fp32_convs: tuple = (), resblock_fusion: str = "auto"):
-        """``decode_bf16``: the decoder convs on bf16 MFMA (fp32 activations); f0 predictor and source stay fp32.
+                 use_graphs: bool = False, max_graphs: int = 32, fp32_convs: tuple = (), resblock_fusion: str = "auto",
+                 snake_logscale: bool = False):
+        """``W``: plain weights, or a checkpoint's state dict with weight-normalised convolutions (folded here by
+        ``fold_weight_norm``; ``snake_logscale`` when its Snakes store log alphas).
+        ``decode_bf16``: the decoder convs on bf16 MFMA (fp32 activations); f0 predictor and source stay fp32.
         ``resblock_fusion`` (bf16 only): each ResBlock dilation's two convs as one kernel that keeps the first conv's
         output on chip -- "auto" where the call's grid fills the chip, "on" wherever the channel count allows, "off"
         never (two convs through a scratch buffer).
@@ -39,6 +43,7 @@ class HiFTModel:
         ``use_graphs``: calls without overrides replay one captured graph per (row lengths, source-cache length), the
         role of ``HiFTGraphs`` (``engine/runtime/hift_graph.py:22-88``): inputs are copied into the graph's static
         buffers, outputs are returned as copies; at most ``max_graphs`` graphs are kept (least recently used dropped)."""
+        W = fold_weight_norm(W, snake_logscale)
         self.cfg, self.device = cfg, device
         self.decode_bf16 = decode_bf16
         if resblock_fusion not in ("auto", "off", "on"):

@@ -93,6 +93,49 @@ def init_hift(cfg: HiFTConfig = HiFTConfig(), seed: int = 0) -> dict[str, torch.
     return W
 
 
+def fold_weight_norm(sd: dict, snake_logscale: bool = False) -> dict[str, torch.Tensor]:
+    """A HiFT state dict as the kernels take it: weight-normalised convolutions folded to their plain weight and Snake
+    alphas made linear -- what ``make_lean`` does to the module once (``engine/runtime/hift_lean.py:107-134``).
+
+    * ``<m>.parametrizations.weight.original0`` (g) / ``.original1`` (v) (``torch.nn.utils.parametrizations.weight_norm``)
+      and ``<m>.weight_g`` / ``<m>.weight_v`` (the older ``torch.nn.utils.weight_norm``) become ``<m>.weight = g v / |v|``,
+      the norm taken over every axis where g has size 1 -- torch's own ``_weight_norm``, so the weight equals the one
+      ``remove_parametrizations(..., leave_parametrized=True)`` leaves, bit for bit.
+    * ``snake_logscale``: the Snakes were built with ``alpha_logscale`` (a module attribute, not in the state dict), so
+      every ``*.alpha`` becomes ``exp(alpha)``; the kernels then take ``1 / (alpha + 1e-9)`` of that, as the reference.
+    * Every other entry is passed through (as a float32 tensor).  A plain dict folds to itself.
+    """
+    out: dict[str, torch.Tensor] = {}
+    pairs: dict[str, dict[str, torch.Tensor]] = {}
+    for k, v in sd.items():
+        for tag, role in ((".parametrizations.weight.original0", "g"), (".parametrizations.weight.original1", "v"),
+                          (".weight_g", "g"), (".weight_v", "v")):
+            if k.endswith(tag) or k == tag[1:]:
+                pairs.setdefault(k[: -len(tag)] if k.endswith(tag) else "", {})[role] = v
+                break
+        else:
+            out[k] = v.detach().float()
+    for base, gv in pairs.items():
+        if set(gv) != {"g", "v"}:
+            raise ValueError(f"weight norm of {base!r}: both the magnitude and the direction are needed, found {sorted(gv)}")
+        g, v = gv["g"].detach().float(), gv["v"].detach().float()
+        if g.dim() == v.dim() and g.numel() > 1:
+            keep = [d for d in range(v.dim()) if g.shape[d] != 1]
+            if len(keep) != 1 or g.shape[keep[0]] != v.shape[keep[0]]:
+                raise ValueError(f"weight norm of {base!r}: magnitude {tuple(g.shape)} does not fit direction {tuple(v.shape)}")
+            dim = keep[0]
+        else:
+            dim = -1  # one magnitude for the whole tensor
+        name = base + ".weight" if base else "weight"
+        if name in out:
+            raise ValueError(f"{base!r} has both a plain weight and a weight norm")
+        out[name] = torch._weight_norm(v, g.reshape(g.shape if dim >= 0 else ()), dim)
+    if snake_logscale:
+        for k in [k for k in out if k.endswith(".alpha")]:
+            out[k] = torch.exp(out[k])
+    return out
+
+
 def _resblock(ini: _Init, W, p, ch, k, dils):
     for j, _ in enumerate(dils):
         ini.conv(W, f"{p}.convs1.{j}", ch, ch, k)

@@ -380,3 +380,83 @@ def test_encoder_core_order(fw):
     ref = ln(e2, "encoder.after_norm", d.eps_after)
     assert got.shape == ref.shape == (2 * T1, C)
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+
+
+# --- checkpoint folding (product host code; no GPU) -------------------------------------------------------------------
+
+def _weight_normed_checkpoint(W, old_style_every=4):
+    """A stepaudio2-like HiFT state dict for the plain weights ``W``: every conv and transposed conv becomes a torch
+    module under weight norm (``parametrizations.weight_norm``, or for every ``old_style_every``-th one the older
+    ``weight_g`` / ``weight_v`` form) with random magnitudes and directions, Snake alphas stored as logs.  Returns
+    (state dict, the weights torch's own parametrization computes)."""
+    import warnings
+
+    from torch.nn.utils.parametrizations import weight_norm
+
+    g = torch.Generator().manual_seed(9)
+    sd, want = {}, {}
+    n = 0
+    for k, w in W.items():
+        base = k[: -len(".weight")]
+        if k.endswith(".weight") and w.dim() == 3:
+            ci, co = (w.shape[0], w.shape[1]) if base.startswith("ups.") else (w.shape[1], w.shape[0])
+            mod = (torch.nn.ConvTranspose1d if base.startswith("ups.") else torch.nn.Conv1d)(ci, co, w.shape[2])
+            if n % old_style_every == old_style_every - 1:
+                with warnings.catch_warnings():
+                    warnings.simplefilter("ignore")
+                    mod = torch.nn.utils.weight_norm(mod)
+                mod.weight_v.data = torch.randn(mod.weight_v.shape, generator=g)
+                mod.weight_g.data = torch.rand(mod.weight_g.shape, generator=g) + 0.5
+                mod(torch.zeros(1, ci, w.shape[2]))  # the forward pre-hook recomputes the weight from g and v
+            else:
+                mod = weight_norm(mod)
+                pw = mod.parametrizations.weight
+                pw.original1.data = torch.randn(pw.original1.shape, generator=g)
+                pw.original0.data = torch.rand(pw.original0.shape, generator=g) + 0.5
+            n += 1
+            for kk, vv in mod.state_dict().items():
+                if kk != "bias":
+                    sd[f"{base}.{kk}"] = vv.clone()
+            want[k] = mod.weight.detach().clone()
+        elif k.endswith(".alpha"):
+            sd[k] = torch.log(w)
+            want[k] = w
+        else:
+            sd[k] = w
+            want[k] = w
+    return sd, want
+
+
+def test_fold_weight_norm_matches_torch_parametrizations():
+    """Folding a weight-normed HiFT checkpoint gives the weights torch's parametrizations compute (the ones
+    ``remove_parametrizations(leave_parametrized=True)`` keeps, ``hift_lean.py:107-134``), and exp of log-scale
+    alphas; the oracle vocoder built from the folded dict equals the one built from those weights."""
+    from t2w_amd.weights import fold_weight_norm
+
+    W = init_hift(SMALL, seed=4)
+    sd, want = _weight_normed_checkpoint(W)
+    assert any(k.endswith(".parametrizations.weight.original0") for k in sd) and any(k.endswith(".weight_g") for k in sd)
+    got = fold_weight_norm(sd, snake_logscale=True)
+    assert set(got) == set(want)
+    for k in want:
+        if k.endswith(".alpha"):
+            torch.testing.assert_close(got[k], want[k], rtol=1e-6, atol=0)
+        else:
+            assert torch.equal(got[k], want[k]), k
+    mel = t64(RNG.normal(-5, 2, (1, SMALL.mel, 4)))
+    ri, nz = oh.hift_noise(9, [3], 4 * 480)
+    a = oh.forward_noise(oh.HiFT(got, SMALL_DIMS), mel, torch.zeros(1, 1, 0), ri, nz)[0]
+    b = oh.forward_noise(oh.HiFT({k: v.detach() for k, v in want.items()}, SMALL_DIMS), mel, torch.zeros(1, 1, 0), ri, nz)[0]
+    torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
+
+
+def test_fold_weight_norm_plain_dict_unchanged_and_errors():
+    from t2w_amd.weights import fold_weight_norm
+
+    W = init_hift(SMALL, seed=4)
+    f = fold_weight_norm(W)
+    assert set(f) == set(W) and all(torch.equal(f[k], W[k]) for k in W)
+    with pytest.raises(ValueError, match="magnitude and the direction"):
+        fold_weight_norm({"conv_pre.weight_g": torch.ones(3, 1, 1)})
+    with pytest.raises(ValueError, match="does not fit"):
+        fold_weight_norm({"c.weight_g": torch.ones(3, 2, 1), "c.weight_v": torch.ones(3, 2, 5)})
