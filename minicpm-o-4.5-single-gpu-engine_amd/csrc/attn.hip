@@ -50,6 +50,21 @@ __device__ __forceinline__ bf16x8 vt_frag(const uint4* vtile, int kb, int d0, in
   return as_bf16x8(u);
 }
 
+// NaN outputs for queries [q0, q1) of a row whose key list breaks what the kernels assume: longer than the caller's
+// bound, or shorter than the row's own tokens (a row's new frames are the first entries of its list)
+__device__ __forceinline__ void nan_rows(const AttnArgs& a, int start, int q0, int q1, int head, int tid, int nthreads) {
+  const int H = a.heads * 64;
+  for (int i = q0 * 64 + tid; i < q1 * 64; i += nthreads) {
+    const size_t o = (size_t)(start + i / 64) * H + head * 64 + i % 64;
+    if (a.out8) {
+      a.out8[o] = 0x7f;  // e4m3 NaN
+      if (i % 32 == 0) a.out8s[(size_t)(start + i / 64) * (H / 32) + head * 2 + (i % 64) / 32] = 0xff;  // E8M0 NaN
+    } else {
+      a.out[o] = 0x7fc0;  // bf16 NaN
+    }
+  }
+}
+
 // KS > 1 (few workgroups, e.g. a streaming chunk): KS groups of two waves share the 64 queries and take every KS-th
 // key tile each; their softmax states (max, sum, output) are merged through LDS at the end.
 template <int KS>
@@ -68,6 +83,10 @@ __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
   const int T = a.row_len[row];
   if (q0 >= T) return;  // a filler tile past its row's end (padded tile lists): the whole workgroup leaves together
   const int start = a.row_start[row], kvoff = a.row_kv_off[row], kvlen = a.row_kv_len[row];
+  if (kvlen < T) {  // a malformed table: NaN outputs instead of key reads past the row's list (workgroup-uniform exit)
+    nan_rows(a, start, q0, min(q0 + 64, T), head, threadIdx.x, 128 * KS);
+    return;
+  }
   const int H = a.heads * 64;
   const int half = lane >> 5, col = lane & 31;
   const int qpos0 = q0 + wave * 32;
@@ -430,20 +449,6 @@ __device__ __forceinline__ void load_key_list(uint4* Ks, uint4* Vs, const AttnAr
   __syncthreads();
 }
 
-// NaN outputs for queries [q0, q1) of a row whose key list is longer than the caller's bound
-__device__ __forceinline__ void nan_rows(const AttnArgs& a, int start, int q0, int q1, int head, int tid, int nthreads) {
-  const int H = a.heads * 64;
-  for (int i = q0 * 64 + tid; i < q1 * 64; i += nthreads) {
-    const size_t o = (size_t)(start + i / 64) * H + head * 64 + i % 64;
-    if (a.out8) {
-      a.out8[o] = 0x7f;  // e4m3 NaN
-      if (i % 32 == 0) a.out8s[(size_t)(start + i / 64) * (H / 32) + head * 2 + (i % 64) / 32] = 0xff;  // E8M0 NaN
-    } else {
-      a.out[o] = 0x7fc0;  // bf16 NaN
-    }
-  }
-}
-
 template <int NWV>
 __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4, 4))) attn_row_kernel(AttnArgs a) {
   extern __shared__ uint4 lds[];  // K rows [KR][8 chunks], then V rows [KR][8 chunks]
@@ -456,8 +461,8 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4
   if (T <= 0) return;
   const int start = a.row_start[row], kvoff = a.row_kv_off[row], kvlen = a.row_kv_len[row];
   const int H = a.heads * 64;
-  if (kvlen > a.kv_max || T > 32 * NWV) {  // longer than the caller's bound: NaN outputs instead of copies past the
-                                          // LDS lists (a row's tokens are part of its list, so T <= kvlen)
+  if (kvlen > a.kv_max || T > 32 * NWV || kvlen < T) {  // longer than the caller's bound, or shorter than the row's
+                                                       // own tokens: NaN outputs instead of copies past the LDS lists
     nan_rows(a, start, 0, T, head, tid, 64 * NWV);
     return;
   }

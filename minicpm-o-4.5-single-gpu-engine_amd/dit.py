@@ -251,8 +251,15 @@ ATTN_ROW_KMAX = 512  # key-list length up to which the attention holds a row's k
 
 def _kv_max(p: dict) -> int:
     """A call's ``kv_max``: 256 or 512 (the row-resident attention's LDS sizes; lists up to 256 keys let two of its
-    workgroups share a CU) when every row's key list fits, else 0 (no bound).  Graphs are keyed by it, so a replay
-    never breaks the bound its capture stated."""
+    workgroups share a CU) when every row's key list fits, else 0 (no bound).  Exact-shape graphs are keyed by it, so a
+    replay never breaks the bound its capture stated.
+
+    Bucketed calls always state 0: their rows are streaming windows of at most ``MAX_GRAPH_T`` frames or small setup
+    batches, which never meet the row-resident attention's launch condition (at least 16 rows of three or more 64-query
+    tiles on average: a bucket's tiles per row stay below that for every bucket of the table), so the bound would
+    select nothing and would only split one bucket's graph by its rows' cached lengths."""
+    if p.get("bucket") is not None:
+        return 0
     kv = p["parts"][7]
     top = int(kv.max()) if kv.size else 0
     return 256 if top <= 256 else ATTN_ROW_KMAX if top <= ATTN_ROW_KMAX else 0
@@ -309,7 +316,7 @@ def plan_call(rows: list[FastRow], Ts: list[int], new: list[np.ndarray], keep: l
         parts[10] = np.concatenate([parts[10], fill])
         n_tiles = want
     return {"n_tok": int(sum(lens)), "n_rows": R, "half": half + pad, "real_half": half, "n_tiles": n_tiles, "parts": parts,
-            "new": new, "rows": rows}
+            "new": new, "rows": rows, "bucket": bucket}
 
 
 ROW_BUCKETS = (2, 4, 8, 16, 32, 64)  # request rows (both CFG halves) of a graph bucket, padding rows excluded
@@ -346,6 +353,12 @@ def bucket_tiles(rb: int, nb: int) -> int:
     """Attention tiles of a bucket's graph: a half's real rows of T_i tokens take sum ceil(T_i / 64) tiles, at most
     (tokens + 63 rows) / 64, so tokens / 64 + rows per half (the padding row included) covers every call."""
     return 2 * ((nb // 2 + 63) // 64 + rb // 2 + 1)
+
+
+def bucket_graph_key(bucket: tuple[int, int], chunk: int, fp8: bool) -> tuple:
+    """The key of a bucket's graph: the bucket, the chunk mask and the weight format -- nothing that depends on the
+    rows' cached lengths, so a graph captured on a padding-only plan serves every call that pads to its bucket."""
+    return (tuple(bucket), int(chunk), bool(fp8))
 
 
 def all_buckets() -> list[tuple[int, int]]:
@@ -536,7 +549,7 @@ class FastDiT:
             self.counts["eager"] += 1
             return out
         flat = self._flat(p)
-        g = self._bucket_graph(bucket, chunk, flat.size, _kv_max(p)) if bucket is not None else self._exact_graph(p, chunk, flat.size)
+        g = self._bucket_graph(bucket, chunk, flat.size) if bucket is not None else self._exact_graph(p, chunk, flat.size)
         _Upload.into(g["tables"], flat)
         half = p["real_half"]
         g["x0"][:half].copy_(x0)
@@ -589,9 +602,9 @@ class FastDiT:
             self._arena = a
         return a
 
-    def _bucket_graph(self, bucket, chunk: int, n_ints: int, kv_max: int) -> dict:
+    def _bucket_graph(self, bucket, chunk: int, n_ints: int) -> dict:
         arena = self._arena_for(n_ints)
-        key = (bucket, chunk, self.fp8, kv_max)
+        key = bucket_graph_key(bucket, chunk, self.fp8)
         g = self.graphs.get(key)
         if g is None:
             g = dict(arena, graph=None)
@@ -624,7 +637,7 @@ class FastDiT:
             raise RuntimeError("capture needs use_graphs=True")
         p = plan_call([], [], [], [], self.cnn_scratch, self.cnn_zero, (rb, nb), self.kv_scratch)
         flat = self._flat(p)
-        g = self._bucket_graph((rb, nb), chunk, flat.size, _kv_max(p))
+        g = self._bucket_graph((rb, nb), chunk, flat.size)
         if g["graph"] is None:
             _Upload.into(g["tables"], flat)
             g["graph"] = self._capture(p, g, chunk)

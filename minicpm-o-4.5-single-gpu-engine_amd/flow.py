@@ -230,66 +230,61 @@ class FlowEncoder:
         n1, n2 = int(T1.sum()), int(T2.sum())
         n_in, n_gap, n_up = n1 + look * R, n1 + 2 * R, n2 + 2 * s * R
         new1 = self.p1.alloc(n1)
-        try:
+        new2 = wr = None
+        try:  # every slot this call takes goes back if anything before the kernels' launch fails
             new2 = self.p2.alloc(n2)
-        except RuntimeError:
-            self.p1.drop(new1)
-            raise
-        try:
             wr = self.pc.alloc(R)
-        except RuntimeError:
+            cs = lambda n: np.concatenate([[0], np.cumsum(n)[:-1]]).astype(np.int64)  # noqa: E731
+            in0, g0, o1, u0, o2 = cs(T1 + look), cs(T1 + 2), cs(T1), cs(T2 + 2 * s), cs(T2)
+            sid1 = np.repeat(np.arange(R), T1)            # stream of each stack-1 row
+            t_in1 = np.arange(n1) - o1[sid1]              # its frame index
+            sid2 = np.repeat(np.arange(R), T2)
+            f2 = np.arange(n2) - o2[sid2]
+            # conv1 input rows: the window's tokens (a final window: then `look` zero rows); h1 rows for the first T1
+            tok = np.full(n_in, -1, dtype=np.int64)
+            res = np.full(n_in, -1, dtype=np.int64)
+            for r in range(R):
+                tok[in0[r]:in0[r] + toks[r].size] = toks[r]
+                res[in0[r]:in0[r] + T1[r]] = np.arange(o1[r], o1[r] + T1[r])
+            c1_src = np.repeat(in0, T1 + 2)
+            gi = np.arange(n_gap) - np.repeat(g0, T1 + 2)  # position in the stream's gapped block: 0, 1 cache, then frames
+            c1_src = c1_src + np.maximum(gi - 2, 0)
+            c2_src = g0[sid1] + t_in1
+            up_dst = u0[sid1] + 2 * s + s * t_in1
+            up_src = u0[sid2] + f2
+            kv1 = np.concatenate([np.concatenate([st.k1, new1[o1[r]:o1[r] + T1[r]]]) for r, st in enumerate(states)])
+            kv2 = np.concatenate([np.concatenate([st.k2, new2[o2[r]:o2[r] + T2[r]]]) for r, st in enumerate(states)])
+            kv1_off, kv2_off = cs(L1), cs(L2)
+            tiles1 = np.array([(r, q) for r in range(R) for q in range(0, int(T1[r]), 32)], dtype=np.int64).reshape(-1, 2)
+            tiles2 = np.array([(r, q) for r in range(R) for q in range(0, int(T2[r]), 32)], dtype=np.int64).reshape(-1, 2)
+            rd = np.array([st.cnn for st in states], dtype=np.int64)
+            parts = {"tok": tok, "res": res, "c1_src": c1_src, "gofs": g0, "t1": T1, "c2_src": c2_src, "up_dst": up_dst, "uofs": u0,
+                     "o1": o1, "up_src": up_src, "o2": o2, "t2": T2, "cnn_rd": rd, "cnn_wr": wr, "new1": new1, "new2": new2,
+                     "kv1_idx": kv1, "kv1_off": kv1_off, "kv1_len": L1, "tiles1": tiles1.ravel(), "kv2_idx": kv2, "kv2_off": kv2_off,
+                     "kv2_len": L2, "tiles2": tiles2.ravel()}
+            offs, o = {}, 0
+            for k, v in parts.items():
+                offs[k] = o
+                o += max(int(np.asarray(v).size), 1)
+            host = np.zeros(o, dtype=np.int32)
+            for k, v in parts.items():
+                host[offs[k]:offs[k] + np.asarray(v).size] = v
+            meta = _Upload.new(host, self.device)
+            base = meta.data_ptr()
+            ws = self._workspace(n_in, n_gap, n1, n_up, n2)
+            mu = torch.empty(n2, cfg.mel, dtype=torch.float32, device=self.device)
+            args = _lib.FlowArgs(R, n_in, n_gap, n1, n_up, n2, tiles1.shape[0], tiles2.shape[0],
+                                 *[base + 4 * offs[k] for k in parts],
+                                 self.pool1.data_ptr(), self.pool1[0].numel(), self.pool2.data_ptr(), self.pool2[0].numel(),
+                                 self.cnn_pool.data_ptr(), mu.data_ptr(), ws.data_ptr(), ws.numel())
+            _lib.check(_lib.lib().t2w_flow_encode(self.model.handle, C_ref(args), _lib.stream_handle()), "flow encode")
+        except Exception:
             self.p1.drop(new1)
-            self.p2.drop(new2)
+            if new2 is not None:
+                self.p2.drop(new2)
+            if wr is not None:
+                self.pc.drop(wr)
             raise
-        cs = lambda n: np.concatenate([[0], np.cumsum(n)[:-1]]).astype(np.int64)  # noqa: E731
-        in0, g0, o1, u0, o2 = cs(T1 + look), cs(T1 + 2), cs(T1), cs(T2 + 2 * s), cs(T2)
-        sid1 = np.repeat(np.arange(R), T1)            # stream of each stack-1 row
-        t_in1 = np.arange(n1) - o1[sid1]              # its frame index
-        sid2 = np.repeat(np.arange(R), T2)
-        f2 = np.arange(n2) - o2[sid2]
-        # conv1 input rows: the window's tokens (a final window: then `look` zero rows); h1 rows for the first T1
-        tok = np.full(n_in, -1, dtype=np.int64)
-        res = np.full(n_in, -1, dtype=np.int64)
-        for r in range(R):
-            tok[in0[r]:in0[r] + toks[r].size] = toks[r]
-            res[in0[r]:in0[r] + T1[r]] = np.arange(o1[r], o1[r] + T1[r])
-        c1_src = np.repeat(in0, T1 + 2)
-        gi = np.arange(n_gap) - np.repeat(g0, T1 + 2)  # position in the stream's gapped block: 0, 1 cache, then frames
-        c1_src = c1_src + np.maximum(gi - 2, 0)
-        c2_src = g0[sid1] + t_in1
-        up_dst = u0[sid1] + 2 * s + s * t_in1
-        up_src = u0[sid2] + f2
-        kv1 = np.concatenate([np.concatenate([st.k1, new1[o1[r]:o1[r] + T1[r]]]) for r, st in enumerate(states)])
-        kv2 = np.concatenate([np.concatenate([st.k2, new2[o2[r]:o2[r] + T2[r]]]) for r, st in enumerate(states)])
-        kv1_off, kv2_off = cs(L1), cs(L2)
-        tiles1 = np.array([(r, q) for r in range(R) for q in range(0, int(T1[r]), 32)], dtype=np.int64).reshape(-1, 2)
-        tiles2 = np.array([(r, q) for r in range(R) for q in range(0, int(T2[r]), 32)], dtype=np.int64).reshape(-1, 2)
-        rd = np.array([st.cnn for st in states], dtype=np.int64)
-        parts = {"tok": tok, "res": res, "c1_src": c1_src, "gofs": g0, "t1": T1, "c2_src": c2_src, "up_dst": up_dst, "uofs": u0,
-                 "o1": o1, "up_src": up_src, "o2": o2, "t2": T2, "cnn_rd": rd, "cnn_wr": wr, "new1": new1, "new2": new2,
-                 "kv1_idx": kv1, "kv1_off": kv1_off, "kv1_len": L1, "tiles1": tiles1.ravel(), "kv2_idx": kv2, "kv2_off": kv2_off,
-                 "kv2_len": L2, "tiles2": tiles2.ravel()}
-        offs, o = {}, 0
-        for k, v in parts.items():
-            offs[k] = o
-            o += max(int(np.asarray(v).size), 1)
-        host = np.zeros(o, dtype=np.int32)
-        for k, v in parts.items():
-            host[offs[k]:offs[k] + np.asarray(v).size] = v
-        meta = _Upload.new(host, self.device)
-        base = meta.data_ptr()
-        ws = self._workspace(n_in, n_gap, n1, n_up, n2)
-        mu = torch.empty(n2, cfg.mel, dtype=torch.float32, device=self.device)
-        args = _lib.FlowArgs(R, n_in, n_gap, n1, n_up, n2, tiles1.shape[0], tiles2.shape[0],
-                             *[base + 4 * offs[k] for k in parts],
-                             self.pool1.data_ptr(), self.pool1[0].numel(), self.pool2.data_ptr(), self.pool2[0].numel(),
-                             self.cnn_pool.data_ptr(), mu.data_ptr(), ws.data_ptr(), ws.numel())
-        rc = _lib.lib().t2w_flow_encode(self.model.handle, C_ref(args), _lib.stream_handle())
-        if rc != 0:
-            self.p1.drop(new1)
-            self.p2.drop(new2)
-            self.pc.drop(wr)
-            _lib.check(rc, "flow encode")
         # advance the lists: [cache, new]; the first stack as the first half of the trimmed tiled list
         for r, st in enumerate(states):
             c1 = kv1[kv1_off[r]:kv1_off[r] + L1[r]]

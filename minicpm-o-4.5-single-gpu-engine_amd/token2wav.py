@@ -106,30 +106,57 @@ class StreamState:
         return self.hift.noise_seed
 
 
-class PendingAudio:
-    """One decode call's samples on their way to the host (``async_result``): a non-blocking copy of the packed samples
-    into a pinned host buffer on the current stream, and an event after it.  The streams' host-side state is already
-    advanced; ``ready()`` polls the event, ``result()`` waits for it and splits the samples per item."""
+class _PinnedBlocks:
+    """Reusable pinned host blocks for asynchronous results.  Blocks come in power-of-two sizes (at least 64 Ki
+    samples); a block handed back after its copy finished serves the next result of its size class, so a steady
+    decode loop stops allocating pinned memory after its first calls."""
 
-    def __init__(self, flat: torch.Tensor | None, lengths: list[int]):
-        self.lengths = lengths
-        self.host = None
-        if flat is not None and flat.numel():
-            self.host = torch.empty(flat.numel(), dtype=torch.float32, pin_memory=True)
-            self.host.copy_(flat, non_blocking=True)
+    MIN = 1 << 16
+
+    def __init__(self):
+        self.free: dict[int, list[torch.Tensor]] = {}
+
+    def take(self, n: int) -> torch.Tensor:
+        size = max(self.MIN, 1 << max(0, int(n) - 1).bit_length())
+        spare = self.free.get(size)
+        return spare.pop() if spare else torch.empty(size, dtype=torch.float32, pin_memory=True)
+
+    def give(self, block: torch.Tensor) -> None:
+        self.free.setdefault(block.numel(), []).append(block)
+
+
+class PendingAudio:
+    """One decode call's samples on their way to the host (``async_result``; the worker's ``ready`` / ``result``
+    contract, ``token2wav_batch.py:113-136``).  The packed samples are copied into a pinned block of the module's pool
+    on the current stream, with an event behind the copy; the streams' host-side state is already advanced.
+    ``ready()`` polls the event; ``result()`` waits for it once, splits the samples per item and hands the block back
+    to the pool (later calls return the same arrays)."""
+
+    def __init__(self, flat: torch.Tensor | None, lengths: list[int], blocks: _PinnedBlocks):
+        self.lengths = [int(n) for n in lengths]
+        self._blocks = blocks
+        self._block = None
+        self._out: list[np.ndarray] | None = None
+        total = sum(self.lengths)
+        if flat is not None and total:
+            self._block = blocks.take(total)
+            self._block[:total].copy_(flat, non_blocking=True)
         self.event = torch.cuda.Event()
         self.event.record()
 
     def ready(self) -> bool:
-        return self.event.query()
+        return self._out is not None or self.event.query()
 
     def result(self) -> list[np.ndarray]:
-        self.event.synchronize()
-        flat = self.host.numpy() if self.host is not None else np.zeros(0, np.float32)
-        ends = np.cumsum(self.lengths)
-        out = [flat[e - n:e].copy() for n, e in zip(self.lengths, ends)]
-        self.host = None  # the pinned block goes back to torch's host allocator
-        return out
+        if self._out is None:
+            self.event.synchronize()
+            cuts = np.cumsum(self.lengths)[:-1]
+            data = self._block.numpy()[: sum(self.lengths)] if self._block is not None else np.zeros(0, np.float32)
+            self._out = [a.copy() for a in np.split(data, cuts)] if self.lengths else []
+            if self._block is not None:
+                self._blocks.give(self._block)
+                self._block = None
+        return self._out
 
 
 class BatchedToken2Wav:
@@ -146,25 +173,38 @@ class BatchedToken2Wav:
         self.window = torch.from_numpy(np.hamming(2 * SOURCE_CACHE)).to(self.device)  # float64, as the reference's
         self.max_flow_streams = int(max_flow_streams)
         self.fuse_setup_frames = int(fuse_setup_frames)
-        self.profile: dict | None = None  # stage -> [calls, seconds, items] when set (each stage then synchronises)
+        self.profile: dict | None = None  # stage -> [calls, seconds, items] when set (stages timed by events)
         self.trace = None
+        self._open_stages: list[tuple] = []
+        self._blocks = _PinnedBlocks()
 
     def _prof(self, name: str, n: int, fn, *a):
-        """Run one stage; with ``profile`` set, time it between stream synchronisations (``_prof``,
-        ``token2wav_batch.py:311-327``)."""
+        """Run one stage of a call.  With ``profile`` set (a dict: stage -> [calls, seconds, items], the layout the
+        reference's worker reads, ``token2wav_batch.py:197``), the stage is bracketed by two timing events on the
+        current stream and its seconds are the GPU-side span between them: from the moment the stream reaches the
+        stage (its earlier work done) to the stage's last kernel, host launch gaps included.  Nothing synchronises
+        until the call's end, where ``_settle`` reads the events of every stage of the call."""
         if self.profile is None:
             return fn(*a)
-        import time
-
-        torch.cuda.current_stream().synchronize()
-        t = time.perf_counter()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
         r = fn(*a)
-        torch.cuda.current_stream().synchronize()
-        acc = self.profile.setdefault(name, [0, 0.0, 0])
-        acc[0] += 1
-        acc[1] += time.perf_counter() - t
-        acc[2] += n
+        t1.record()
+        self._open_stages.append((name, int(n), t0, t1))
         return r
+
+    def _settle(self) -> None:
+        """Fold the timed stages of the finished call into ``profile``."""
+        if not self._open_stages:
+            return
+        self._open_stages[-1][3].synchronize()
+        for name, n, t0, t1 in self._open_stages:
+            acc = self.profile.setdefault(name, [0, 0.0, 0]) if self.profile is not None else [0, 0.0, 0]
+            acc[0] += 1
+            acc[1] += t0.elapsed_time(t1) * 1e-3
+            acc[2] += n
+        self._open_stages = []
 
     # --- prompts ------------------------------------------------------------------------------------------------------
     def _stage_mu(self, feats: tuple) -> PreSetup:
@@ -186,12 +226,20 @@ class BatchedToken2Wav:
             if 2 * len(t) != int(f[3].shape[1]):
                 raise ValueError(f"prompt of {len(t)} tokens needs a mel of {2 * len(t)} frames, got {int(f[3].shape[1])}")
         states, mu, rows, frames = self.flow.setup(toks)
-        spk = self.flow.model.speaker(torch.cat([f[2].reshape(1, -1).to(self.device, torch.float32) for f in feats_list]))
-        dev = self.device
-        out = []
-        for i, (f, st) in enumerate(zip(feats_list, states)):
-            P = frames[i]
-            out.append(PreSetup(f, self.fast.new_cache(keep=P), mu[rows[i]:rows[i] + P].t(), spk[i:i + 1], f[3][0].to(dev, torch.float32).t(), st))
+        out: list[PreSetup] = []
+        try:
+            spk = self.flow.model.speaker(torch.cat([f[2].reshape(1, -1).to(self.device, torch.float32) for f in feats_list]))
+            dev = self.device
+            for i, f in enumerate(feats_list):
+                P = frames[i]
+                out.append(PreSetup(f, self.fast.new_cache(keep=P), mu[rows[i]:rows[i] + P].t(), spk[i:i + 1],
+                                    f[3][0].to(dev, torch.float32).t(), states[i]))
+        except Exception:  # give back every cache made so far and every encoder state (a pool ran out, say)
+            for p in out:
+                self.release_presetup(p)
+            for st in states[len(out):]:
+                self.flow.release(st)
+            raise
         return out
 
     @torch.inference_mode()
@@ -322,6 +370,7 @@ class BatchedToken2Wav:
             if not self.fuse_setup_frames or frames > self.fuse_setup_frames or len(items) + len(setups) > self.max_flow_streams:
                 raise ValueError(f"fused setups: {len(setups)} prompts of {frames} frames with {len(items)} windows exceed "
                                  f"fuse_setup_frames={self.fuse_setup_frames} / max_flow_streams={self.max_flow_streams}")
+        self._open_stages = []  # stage events of an earlier call that raised are dropped
         pre = self._presetups(setups) if setups else []
         items = self._encode_windows(items)
         rows = [(p.cache, p.mu, p.spk, p.cond, True) for p in pre]
@@ -334,6 +383,7 @@ class BatchedToken2Wav:
                                torch.cat([r[2] for r in part]), conds, [r[4] for r in part])
         prompts = [self._prompt(p) for p in pre]
         out = self._prof("vocode", len(items), self._vocode, items, mels[len(pre):], async_result)
+        self._settle()
         return (out, prompts) if setups else out
 
     def _noise(self, seeds: list[int], n: int):
@@ -383,7 +433,7 @@ class BatchedToken2Wav:
         lengths = [int(p.numel()) for p in pieces]
         flat = torch.cat(pieces).float() if pieces else None
         if async_result:
-            return PendingAudio(flat, lengths)
+            return PendingAudio(flat, lengths, self._blocks)
         host = flat.cpu().numpy() if flat is not None else np.zeros(0, np.float32)
         ends = np.cumsum(lengths)
         return [host[e - n:e] for n, e in zip(lengths, ends)]

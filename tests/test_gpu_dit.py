@@ -177,6 +177,35 @@ def test_solve_streaming_bucketed_graphs(dev, tiny):
     assert d < 1e-3 and max(errs) < TOL
 
 
+def test_captured_buckets_serve_long_caches(dev, tiny):
+    """Graphs captured up front on padding-only plans (``capture``) serve prompt setups and steady windows over caches
+    of 300-450 frames without a capture mid-stream, and match the eager solve."""
+    from t2w_amd.dit import bucket_of
+
+    W, model = tiny
+    fdg = FastDiT(model, n_slots=8192, max_streams=4, use_graphs=True, buckets=True)
+    fde = FastDiT(model, n_slots=8192, max_streams=4)
+    prompts = (300, 380)
+    fdg.capture(*bucket_of(4, 2 * sum(prompts)))
+    fdg.capture(*bucket_of(4, 2 * 100))
+    held = set(fdg.graphs)
+    g = torch.Generator().manual_seed(21)
+    spks = torch.randn(2, 80, generator=g).cuda()
+    cg = [fdg.new_cache(keep=p) for p in prompts]
+    ce = [fde.new_cache(keep=p) for p in prompts]
+    calls = [([torch.randn(80, p, generator=g).cuda() for p in prompts], [torch.randn(80, p, generator=g).cuda() for p in prompts])]
+    calls += [([torch.randn(80, 50, generator=g).cuda() for _ in prompts], None) for _ in range(3)]
+    worst = 0.0
+    for mus, conds in calls:
+        a = fdg.solve(cg, mus, spks, conds, [True, True])
+        b = fde.solve(ce, mus, spks, conds, [True, True])
+        worst = max(worst, max(rel(x.cpu(), y.cpu()) for x, y in zip(a, b)))
+    print("captured buckets vs eager rel-L2", worst, "cached frames", [c.length for c in cg], fdg.counts)
+    assert min(c.length for c in cg) > 256
+    assert set(fdg.graphs) == held and fdg.counts["graph"] == 4
+    assert worst < 1e-3
+
+
 def test_chunk_causal_many_rows(dev, tiny):
     """16 requests x 700 frames (22,400 tokens): the qkv GEMM's 264 tiles of 256 x 256 leave a mostly idle last round,
     so its last 640 rows run on 256 x 128 tiles with the q/k LayerNorm and key scatter of their own rows."""

@@ -458,3 +458,39 @@ def test_gemm_fp8_taps(dev):
                               None, out.data_ptr(), H, N, H, 3 * H, 3, _lib.stream_handle()), "gemm_fp8 taps")
     torch.cuda.synchronize()
     assert rel(out, ref) < 1e-4
+
+
+@pytest.mark.parametrize("kv_max,rows", [(512, 16), (0, 16), (0, 2)])
+def test_attention_list_shorter_than_row(dev, kv_max, rows):
+    """A table whose row states fewer keys than the row's own new frames gets NaN outputs for that row from every
+    attention form (row-resident, tile, and the small-grid tile kernel that splits key tiles over four wave groups);
+    the other rows equal a well-formed call's.  The key table holds every row's full list, so no read could leave it
+    even without the check."""
+    L = _lib.lib()
+    heads, H = 16, 1024
+    T = 192 if rows == 16 else 50
+    lens = [T] * rows
+    N = sum(lens)
+    g = torch.Generator(device=dev).manual_seed(4)
+    q = torch.randn(N, H, device=dev, generator=g).bfloat16()
+    kp = torch.randn(N + 64, H, device=dev, generator=g).bfloat16()
+    vp = torch.randn(N + 64, H, device=dev, generator=g).bfloat16()
+    kv = list(range(N))
+    off = [T * r for r in range(rows)]
+    tiles = [v for r in range(rows) for q0 in range(0, T, 64) for v in (r, q0)]
+    it = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)  # noqa: E731
+    outs = []
+    for short in (False, True):
+        kvl = [T] * rows
+        if short:
+            kvl[rows - 1] = T // 2
+        keep = [it(x) for x in (kv, off, lens, off, kvl, tiles)]
+        out = torch.zeros(N, H, dtype=torch.bfloat16, device=dev)
+        _lib.check(L.t2w_attention(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), out.data_ptr(), *[t.data_ptr() for t in keep], len(tiles) // 2,
+                                   heads, 0, 0.125, rows, kv_max, _lib.stream_handle()))
+        torch.cuda.synchronize()
+        outs.append(out)
+    last = (rows - 1) * T
+    assert not torch.isnan(outs[0]).any()
+    assert torch.isnan(outs[1][last:]).all()
+    assert torch.equal(outs[1][:last], outs[0][:last])

@@ -263,3 +263,32 @@ def test_codec_tokens_end_to_end_mels(dev):
     for st in sts:
         bt.release_stream(st)
     assert fd.pool.in_use() == fd.scratch and enc.in_use() == (0, 0, 0)
+
+
+def test_exhausted_pools_leak_nothing(dev):
+    """Pool exhaustion inside a token-prompt setup (the estimator's conv-cache rows run out after the encoder ran) and
+    inside an encoder call (its conv-cache slots run out after the key slots were taken) raises, and every slot the
+    failed call took is back: the pools read as before the call."""
+    from t2w_amd.config import FlowConfig
+    from t2w_amd.flow import FlowEncoder, FlowModel
+    from t2w_amd.weights import init_flow
+
+    W, Wh, Wf = init_dit(TINY, seed=41), init_hift(HiFTConfig(), seed=42), init_flow(FlowConfig(), seed=43)
+    fd = FastDiT(DiTModel(W, TINY), n_slots=4096, max_streams=1)  # 4 conv rows + 2 reserved: one stream's caches
+    enc = FlowEncoder(FlowModel(Wf, FlowConfig()), n_slots1=1024, n_slots2=2048, n_cnn=3)
+    bt = BatchedToken2Wav(fd, HiFTModel(Wh), flow=enc, noise_device="cpu")
+    g = torch.Generator().manual_seed(8)
+    toks = [torch.randint(0, 6561, (1, n), generator=g) for n in (20, 15)]
+    feats = [(t, torch.tensor([t.shape[1]]), torch.randn(1, 192, generator=g), torch.randn(1, 2 * t.shape[1], 80, generator=g),
+              torch.tensor([2 * t.shape[1]])) for t in toks]
+    before = (enc.in_use(), fd.pool.in_use(), len(fd.cnn_free))
+    with pytest.raises(RuntimeError, match="conv-cache row slots exhausted"):
+        bt.setup_encode(feats)  # the encoder serves both prompts, the second estimator cache does not fit
+    assert (enc.in_use(), fd.pool.in_use(), len(fd.cnn_free)) == before
+    states = [enc.new_state(0) for _ in range(3)]
+    with pytest.raises(RuntimeError):
+        enc.encode(states, [t[0].tolist() for t in toks] + [toks[0][0].tolist()], [False] * 3)  # 3 conv slots, 2 free
+    assert enc.in_use() == before[0]
+    for st in states:
+        enc.release(st)
+    assert enc.in_use() == before[0]

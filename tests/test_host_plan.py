@@ -134,3 +134,38 @@ def test_kv_max_classes():
     assert ATTN_ROW_KMAX == 512
     assert _kv_max(part([1, 256])) == 256 and _kv_max(part([257, 3])) == 512 and _kv_max(part([512])) == 512
     assert _kv_max(part([513, 10])) == 0 and _kv_max(part([])) == 256
+
+
+def test_bucket_graphs_never_take_the_row_resident_attention():
+    """The row-resident attention launches only for calls of at least 256 (row, head) pairs whose rows average three
+    or more 64-query tiles (``attention`` in csrc/attn.hip).  With the model's 16 heads no bucket's padded plan meets
+    both, so bucket plans state no key-list bound (0: the tile kernel, which every bucket call took anyway)."""
+    from t2w_amd.config import DiTConfig
+    from t2w_amd.dit import _kv_max
+
+    heads = DiTConfig().heads
+    for rb, nb in all_buckets():
+        p = plan_call([], [], [], [], cnn_scratch=99, cnn_zero=98, bucket=(rb, nb), kv_scratch=97)
+        assert p["n_rows"] * heads < 256 or p["n_tiles"] < 3 * p["n_rows"], (rb, nb)
+        assert _kv_max(p) == 0
+
+
+def test_steady_window_key_is_the_captured_bucket_key():
+    """A steady streaming call (50 new frames per stream on 300-450 cached frames) pads to a bucket whose graph key is
+    the one ``capture`` / ``capture_all`` create from padding-only plans, whatever the rows' cached lengths."""
+    from t2w_amd.dit import _kv_max, bucket_graph_key
+
+    rng = np.random.default_rng(0)
+    captured = {bucket_graph_key(b, 0, False) for b in all_buckets()}
+    for n in (1, 3, 8, 16, 32):
+        cached = rng.integers(300, 451, n)
+        rows = _rows([(np.arange(10000 * r, 10000 * r + int(cached[r % n])), (2 * r, 2 * r + 1), 0) for r in range(2 * n)])
+        Ts = [50] * n
+        new = [np.arange(500000 + 100 * r, 500000 + 100 * r + 50) for r in range(2 * n)]
+        bucket = bucket_of(2 * n, 2 * sum(Ts))
+        p = plan_call(rows, Ts, new, [True] * n, cnn_scratch=99, cnn_zero=98, bucket=bucket, kv_scratch=97)
+        assert int(p["parts"][7].max()) > 256  # the lists are long: a length-derived bound would have been 512
+        assert _kv_max(p) == 0
+        assert bucket_graph_key(bucket, 0, False) in captured
+        empty = plan_call([], [], [], [], cnn_scratch=99, cnn_zero=98, bucket=bucket, kv_scratch=97)
+        assert _kv_max(empty) == _kv_max(p)
