@@ -74,6 +74,8 @@ def main() -> int:
     ap.add_argument("--latency-only", action="store_true", help="only the per-chunk latency case")
     ap.add_argument("--no-flow", action="store_true", help="skip the flow encoder (codec-token chunk latency, encoder workload)")
     ap.add_argument("--flow-only", action="store_true", help="only the flow encoder workload (16 streams, 28-token windows)")
+    ap.add_argument("--hift-kernels-only", action="store_true",
+                    help="only HiFT's elementwise kernels on the workload's shape (for a rocprofv3 run of just those launches)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant kernel's launches, after three 256 MiB calibration copies (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -88,6 +90,11 @@ def main() -> int:
     if args.roofline_only:
         r = resid_gemm_roofline(cfg, args.streams, args.frames, calibrate=True)
         print(json.dumps({"kernel": r["kernel"], "launch_ms": r["launch_ms"], "tflops": r["achieved"], "calibration_copy_bytes": 2 * (256 << 20)}))
+        return 0
+    if args.hift_kernels_only:
+        from t2w_amd.weights import init_hift
+
+        print(json.dumps(hift_kernel_table(init_hift(HiFTConfig(), seed=3), args.streams, args.frames, args.hift_mode)))
         return 0
     if args.flow_only:
         print(json.dumps(flow_workload(args, flow_encoder())))
@@ -142,8 +149,9 @@ def main() -> int:
     torch.cuda.synchronize()
     dit_dt = (time.perf_counter() - t1) / max(1, args.steps // 2)
 
-    roof = resid_gemm_roofline(cfg, n, T)
+    roof = in_solve_roofline(cfg, fd, caches, mus, spks, args.chunk, resid_gemm_roofline(cfg, n, T))
     roof["traffic"] = pmc_traffic()
+    hk = None if (hift is None or args.no_extra) else hift_kernel_table(Wh, n, T, args.hift_mode)
     gemms = None if args.no_gemms else dit_gemm_table(cfg, n, T)
 
     enc = flow_encoder() if not args.no_flow else None
@@ -184,6 +192,7 @@ def main() -> int:
         "dit_mfma_frac": (gemm_f + attn_f) / dit_dt / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "roofline": roof,
         "dit_gemms": gemms,
+        "hift_kernels": hk,
         "cpu_baseline": cpu,
         **extra,
     }
@@ -246,6 +255,80 @@ def resid_gemm_roofline(cfg, n: int, T: int, calibrate: bool = False) -> dict:
     return {"bound": "mfma", "kernel": "gemm_kernel<256,256,4,2,EPI_RESID_F16,dense> (DiT proj and fc2, alternating)",
             "achieved": ach, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": ach / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
             "launch_ms": ms, "flops_per_launch": flops}
+
+
+def event_bracket_ms(reps: int = 200) -> float:
+    """Median elapsed time of a pair of HIP events recorded back to back right after a small kernel: the part of an
+    event-bracketed launch time that is not the kernel's."""
+    x = torch.zeros(1 << 16, device="cuda")
+    pairs = []
+    for _ in range(reps):
+        x.add_(1.0)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        e1.record()
+        pairs.append((e0, e1))
+    torch.cuda.synchronize()
+    return float(np.median([a.elapsed_time(b) for a, b in pairs]))
+
+
+def in_solve_roofline(cfg, fd, caches, mus, spks, chunk: int, isolated: dict) -> dict:
+    """The dominant kernel's roofline as it runs inside the solve: one eager solve of the workload under the library's
+    launch timer (HIP events around each of its 440 proj / fc2 launches, on the solve's stream); achieved = the mean
+    algorithmic FLOPs per launch (proj and fc2 alternate) / the mean launch time, which is the bracketed time less the
+    time two events recorded back to back take (``event_bracket_ms``: the bracket's own part).  The isolated launches'
+    figures (``resid_gemm_roofline``) are kept under "isolated"."""
+    n = len(mus)
+    _, launches = fd.solve_timed(caches, mus, spks, None, [False] * n, chunk=chunk)
+    ms = [m for k, m, _ in launches if k == "resid_gemm"]
+    if not ms:
+        return isolated
+    N, H, F = 2 * sum(int(m.shape[1]) for m in mus), cfg.hidden, cfg.ffn
+    flops = 2.0 * N * H * (H + F) / 2
+    raw = float(np.mean(ms))
+    bracket = event_bracket_ms()
+    mean = raw - bracket  # the kernel's own time: rocprofv3's durations of the same launches agree with it
+    ach = flops / (mean * 1e-3) / 1e12
+    iso = {k: isolated[k] for k in ("achieved", "frac", "launch_ms")}
+    proj, fc2 = ms[0::2], ms[1::2]
+    return {"bound": "mfma", "kernel": isolated["kernel"], "achieved": ach, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": ach / MFMA_BF16_PEAK_TFLOPS, "traffic": None, "launch_ms": mean, "launches": len(ms),
+            "launch_ms_bracketed": raw, "event_bracket_ms": bracket, "proj_ms": float(np.mean(proj)) - bracket,
+            "fc2_ms": float(np.mean(fc2)) - bracket, "flops_per_launch": flops,
+            "measured": "in-solve: HIP events around every proj / fc2 launch of one eager solve, less the bracket of two "
+                        "back-to-back events",
+            "isolated": iso}
+
+
+def hift_kernel_table(Wh, n: int, T: int, mode: str) -> dict:
+    """HiFT's elementwise kernels on the workload's shape (n rows x T mel frames, no source cache) and the Snake of the
+    strict-fp32 decoder, each launch timed by the library's launch timer (HIP events on the call's stream) after a
+    warm-up call: mean duration, algorithmic HBM bytes per launch (least bytes its operands make it move), GB/s and
+    the fraction of the 8 TB/s HBM peak."""
+    from t2w_amd import _lib
+
+    out = {}
+    for tag in (mode, "fp32"):
+        hm = hift_model(Wh, tag, use_graphs=False)
+        ri, nz = hm.noise([4000 + i for i in range(n)], T * hm.cfg.upsample_scale)
+        mel = torch.randn(n, hm.cfg.mel, T, generator=torch.Generator().manual_seed(8)).cuda() * 2 - 5
+        src = torch.zeros(n, 1, 0, device="cuda")
+        hm.forward_noise(mel, src, ri, nz)
+        with _lib.LaunchTimer(4096) as t:
+            hm.forward_noise(mel, src, ri, nz)
+        agg: dict[str, list] = {}
+        for kind, ms, by in t.launches:
+            agg.setdefault(kind.replace("hift_", ""), []).append((ms, by))
+        for k, v in agg.items():
+            if k in out:
+                continue
+            ms = float(np.mean([a for a, _ in v]))
+            by = float(np.mean([b for _, b in v]))
+            out[k] = {"us": ms * 1e3, "bytes": by, "GB/s": by / ms / 1e6, "frac": by / ms / 1e6 / HBM_PEAK_GBS, "launches": len(v),
+                      "mode": tag}
+        del hm
+    out["shape"] = f"{n} rows x {T} mel frames ({n * T * 480} samples), no source cache"
+    return out
 
 
 def dit_gemm_table(cfg, n: int, T: int) -> dict:
@@ -530,23 +613,29 @@ def cpu_baseline(W, T: int, chunk: int, hift_weights=None) -> dict:
     att = torch.zeros(d.depth, 2, d.heads, 0, 2 * d.head_dim)
     mask = od.chunk_mask(T, chunk)[None].expand(2, T, T)
     tr = torch.full((2,), T, dtype=torch.int64)
+    def median_of(fn, runs: int = 5) -> float:  # one warm-up, then the median of `runs` timed calls
+        fn()
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
     with torch.no_grad():
         temb = od.t_embed(W, torch.full((2,), 0.5))
-        t0 = time.perf_counter()
-        od.estimator_chunk(W, d, x, mu, temb, spk, torch.zeros_like(mu), cnn, att, mask, tr)
-        fwd = time.perf_counter() - t0
+        fwd = median_of(lambda: od.estimator_chunk(W, d, x, mu, temb, spk, torch.zeros_like(mu), cnn, att, mask, tr))
         hift_s = 0.0
         if hift_weights is not None:
             h = oh.HiFT(hift_weights)
             mel = torch.randn(1, 80, T, generator=g) * 2 - 5
             ri, nz = oh.hift_noise(9, [1], T * 480)
-            t0 = time.perf_counter()
-            oh.forward_noise(h, mel, torch.zeros(1, 1, 0), ri, nz)
-            hift_s = time.perf_counter() - t0
+            hift_s = median_of(lambda: oh.forward_noise(h, mel, torch.zeros(1, 1, 0), ri, nz))
     total = 10 * fwd + hift_s
     return {"value": T / total, "unit": "mel frames/s", "cores": cores, "kind": "port",
-            "sample": f"fp32 oracle: 1 estimator forward of a CFG pair (2 x {T} frames, chunk {chunk}) timed and x10 steps, "
-                      f"+ HiFT of one {T}-frame mel ({'timed' if hift_weights is not None else 'not run'}); forward {fwd:.2f} s, HiFT {hift_s:.2f} s"}
+            "sample": f"fp32 oracle: estimator forward of a CFG pair (2 x {T} frames, chunk {chunk}) x 10 steps + HiFT of one "
+                      f"{T}-frame mel ({'timed' if hift_weights is not None else 'not run'}); each the median of 5 runs after one "
+                      f"warm-up: forward {fwd:.2f} s, HiFT {hift_s:.2f} s"}
 
 
 if __name__ == "__main__":

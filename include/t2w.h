@@ -149,6 +149,24 @@ int t2w_dit_solve(const t2w_dit* m, const t2w_solve_args* a, void* stream);
  * tokens) fail with a message.  Every call on a device shares that device's array, so calls that overlap on one
  * device (concurrent streams or threads) race; serialise them.  Nothing in it needs clearing between calls. */
 int t2w_dit_solve_noalloc(const t2w_dit* m, const t2w_solve_args* a, void* stream);
+/* Launch timer, a measurement aid (no counterpart in the reference).  t2w_timer_arm(cap) arms it on the calling
+ * thread; the eager (not capturing) calls that follow bracket each instrumented kernel launch with a pair of HIP events
+ * on its stream, up to cap launches.  t2w_timer_read waits for `stream`, writes the launches' kinds, durations (ms)
+ * and algorithmic HBM bytes (the least its operands make it move) in launch order, up to cap, their count to *n,
+ * and disarms.  Instrumented: the DiT's dense gated-residual tile GEMMs (proj and fc2 of every block, calls of more
+ * than 128 tokens) and HiFT's elementwise kernels. */
+enum {
+  T2W_TIMER_RESID_GEMM = 1,
+  T2W_TIMER_HIFT_PHASE = 2,
+  T2W_TIMER_HIFT_SOURCE = 3,
+  T2W_TIMER_HIFT_STFT = 4,
+  T2W_TIMER_HIFT_ISTFT = 5,
+  T2W_TIMER_HIFT_REFLECT = 6,
+  T2W_TIMER_HIFT_SNAKE = 7,
+  T2W_TIMER_HIFT_F0_HEAD = 8
+};
+int t2w_timer_arm(int cap);
+int t2w_timer_read(void* stream, int* kinds, float* ms, double* bytes, int cap, int* n);
 /* One estimator evaluation at Euler step `step`'s key/value and conv-cache layers with the given tables
  * (mods [depth, 9, H], final_mods [2, H]) on in_rows; writes dphi [n_tok, mel] to a->out. */
 int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const float* mods, const float* final_mods,

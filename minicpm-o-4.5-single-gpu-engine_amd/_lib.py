@@ -105,6 +105,8 @@ _SIGS = {
     "t2w_dit_workspace_bytes": (C.c_size_t, [P, I, I]),
     "t2w_dit_solve": (I, [P, C.POINTER(SolveArgs), P]),
     "t2w_dit_forward": (I, [P, C.POINTER(SolveArgs), I, P, P, P]),
+    "t2w_timer_arm": (I, [I]),
+    "t2w_timer_read": (I, [P, C.POINTER(I), FP, C.POINTER(C.c_double), I, C.POINTER(I)]),
     "t2w_dit_solve_noalloc": (I, [P, C.POINTER(SolveArgs), P]),
     "t2w_gemm_bf16": (I, [P, I, P, P, P, P, P, I, I, I, I, I, P]),
     "t2w_gemm_bf16_tile": (I, [P, I, P, P, P, P, P, I, I, I, I, I, I, P]),
@@ -155,6 +157,31 @@ def lib():
 def check(rc: int, what: str = "") -> None:
     if rc != 0:
         raise RuntimeError(f"t2w {what}: {lib().t2w_last_error().decode()}")
+
+
+TIMER_KINDS = {1: "resid_gemm", 2: "hift_phase", 3: "hift_source", 4: "hift_stft", 5: "hift_istft", 6: "hift_reflect",
+               7: "hift_snake", 8: "hift_f0_head"}  # the T2W_TIMER_* codes of t2w.h
+
+
+class LaunchTimer:
+    """``with LaunchTimer(cap) as t: <eager library calls>`` -> ``t.launches``: (kind name, ms, algorithmic bytes) of
+    every instrumented launch, in launch order (``t2w_timer_arm`` / ``t2w_timer_read``; waits for the current stream)."""
+
+    def __init__(self, cap: int = 8192):
+        self.cap = int(cap)
+        self.launches: list[tuple[str, float, float]] = []
+
+    def __enter__(self):
+        check(lib().t2w_timer_arm(self.cap), "timer_arm")
+        return self
+
+    def __exit__(self, *exc):
+        kinds, ms, by, n = (C.c_int * self.cap)(), (C.c_float * self.cap)(), (C.c_double * self.cap)(), C.c_int()
+        rc = lib().t2w_timer_read(stream_handle(), kinds, ms, by, self.cap, C.byref(n))
+        if exc[0] is None:
+            check(rc, "timer_read")
+        self.launches = [(TIMER_KINDS.get(kinds[i], str(kinds[i])), float(ms[i]), float(by[i])) for i in range(n.value)]
+        return False
 
 
 def exported_symbols() -> list[str]:

@@ -41,7 +41,17 @@ size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 namespace t2w {
 int set_error(const char* what, hipError_t e) { return fail(what, e); }
+LaunchTimer& launch_timer() {
+  thread_local LaunchTimer t;
+  return t;
+}
 }  // namespace t2w
+
+namespace {
+// HBM bytes a gated-residual GEMM of M rows must move at least: A [M, K] bf16, W [N, K] bf16, the fp16 residual
+// read and written, bias and gate
+double resid_bytes(int M, int N, int K) { return 2.0 * M * K + 2.0 * N * K + 4.0 * M * N + 8.0 * N; }
+}  // namespace
 
 // Scratch of t2w_dit_solve_noalloc: the solve's whole workspace (activations, split-K partials) for calls that fit,
 // in device memory the library owns.  Each device holds its own copy from module load until the process ends; host
@@ -265,7 +275,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
       pend = gemm_deferred(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), Sd, w, st, &perr);
       T2W_CHECK(perr, "proj");
     } else {
-      T2W_CHECK(gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F16, st), "proj");
+      T2W_CHECK(timed_launch(T2W_TIMER_RESID_GEMM, resid_bytes(N, H, H), st, [&] { return gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F16, st); }), "proj");
     }
     ConvPlace cp;
     cp.P = w.P; cp.tok_row = a->tok_row; cp.tok_pos = a->tok_pos; cp.row_start = a->row_start; cp.row_len = a->row_len;
@@ -311,7 +321,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
         pend = gemm_deferred(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), Sd, w, st, &perr);
         T2W_CHECK(perr, "fc2");
       } else {
-        T2W_CHECK(gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F16, st), "fc2");
+        T2W_CHECK(timed_launch(T2W_TIMER_RESID_GEMM, resid_bytes(N, H, F), st, [&] { return gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F16, st); }), "fc2");
       }
     }
   }
@@ -453,6 +463,44 @@ int t2w_dit_solve_noalloc(const t2w_dit* m, const t2w_solve_args* a, void* strea
   b.workspace = scr;
   b.workspace_bytes = NOALLOC_SCRATCH_BYTES;
   return t2w_dit_solve(m, &b, stream);
+}
+
+int t2w_timer_arm(int cap) {
+  if (cap <= 0) return fail("timer_arm: capacity must be positive");
+  LaunchTimer& t = launch_timer();
+  for (const TimedLaunch& x : t.v) {
+    (void)hipEventDestroy(x.e0);
+    (void)hipEventDestroy(x.e1);
+  }
+  t.v.clear();
+  t.cap = cap;
+  t.armed = true;
+  return 0;
+}
+
+int t2w_timer_read(void* stream, int* kinds, float* ms, double* bytes, int cap, int* n) {
+  if (!n) return fail("timer_read: null count");
+  *n = 0;
+  LaunchTimer& t = launch_timer();
+  t.armed = false;
+  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  int k = 0;
+  for (const TimedLaunch& x : t.v) {
+    if (e == hipSuccess && k < cap) {
+      float v = 0.f;
+      e = hipEventElapsedTime(&v, x.e0, x.e1);
+      if (kinds) kinds[k] = x.kind;
+      if (ms) ms[k] = v;
+      if (bytes) bytes[k] = x.bytes;
+      ++k;
+    }
+    (void)hipEventDestroy(x.e0);
+    (void)hipEventDestroy(x.e1);
+  }
+  t.v.clear();
+  T2W_CHECK(e, "timer_read");
+  *n = k;
+  return 0;
 }
 
 int t2w_dit_forward(const t2w_dit* m, const t2w_solve_args* a, int step, const float* mods, const float* final_mods, void* stream) {

@@ -10,6 +10,7 @@
 
 #include "../../include/t2w.h"
 #include "hift_internal.h"
+#include "launch_timer.h"
 
 using namespace t2w;
 
@@ -178,7 +179,9 @@ int resblock(const Ctx& x, const t2w_resblock& rb, int k, const float* in, float
       H_CHECK(resblock_pair_bf16(c1, c2, mr, x.st), "resblock pair");
     } else {
       if (!on_bf16(x, c1) && !on_bf16(x, c2) && C % 4 == 0) {
-        H_CHECK(snake_rows(cur, C, x.L.tot[cls], c1.alpha, c1.inv, act, x.st), "resblock snake1");
+        H_CHECK(timed_launch(T2W_TIMER_HIFT_SNAKE, 8.0 * C * x.L.tot[cls], x.st,
+                             [&] { return snake_rows(cur, C, x.L.tot[cls], c1.alpha, c1.inv, act, x.st); }),
+                "resblock snake1");
         c1.x = act;
         c1.pre = PRE_NONE;
         c1.epi = EPI_SNAKE;
@@ -269,7 +272,9 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
       cur = o;
       cin = d.f0_channels;
     }
-    H_CHECK(f0_head(cur, d.f0_channels, w.f0_head_w, w.f0_head_b, B.f0, (int)x.L.tot[C_T], x.st), "f0 head");
+    H_CHECK(timed_launch(T2W_TIMER_HIFT_F0_HEAD, 4.0 * (d.f0_channels + 1) * (x.L.tot[C_T] + 1), x.st,
+                         [&] { return f0_head(cur, d.f0_channels, w.f0_head_w, w.f0_head_b, B.f0, (int)x.L.tot[C_T], x.st); }),
+            "f0 head");
     f0 = B.f0;
   }
   if (f0_out) H_CHECK(hipMemcpyAsync(f0_out, f0, x.L.tot[C_T] * sizeof(float), hipMemcpyDeviceToDevice, x.st), "f0 out");
@@ -278,16 +283,26 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
   const int up = d.up_rates[0] * d.up_rates[1] * d.up_rates[2] * d.hop;
   const float* s = source_override;
   if (!s) {
-    H_CHECK(nsf_phase(f0, x.off(C_T), x.len(C_T), n, harm, (float)d.sr, (float)up, B.phase, x.st), "nsf phase");
-    H_CHECK(nsf_source(B.phase, f0, x.off(C_T), x.len(C_T), x.off(C_SMP), n, x.L.mx[C_T], harm, (float)(1.0 / up), up, d.sine_amp,
-                       d.noise_std, (float)((double)d.sine_amp / 3.0), d.voiced_threshold, noise, w.src_w, w.src_b, cache_source, S,
-                       source, x.st),
+    const double fr = (double)x.L.tot[C_T], smp = (double)x.L.tot[C_SMP], cached = (double)n * S;
+    H_CHECK(timed_launch(T2W_TIMER_HIFT_PHASE, 4.0 * fr * (1 + harm), x.st,
+                         [&] { return nsf_phase(f0, x.off(C_T), x.len(C_T), n, harm, (float)d.sr, (float)up, B.phase, x.st); }),
+            "nsf phase");
+    // noise in and the sample out per generated sample, the cache copied for the first S of a row, f0 and the frame
+    // phases read once
+    H_CHECK(timed_launch(T2W_TIMER_HIFT_SOURCE, (smp - cached) * 4.0 * (harm + 1) + cached * 8.0 + 4.0 * fr * (1 + harm), x.st,
+                         [&] {
+                           return nsf_source(B.phase, f0, x.off(C_T), x.len(C_T), x.off(C_SMP), n, x.L.mx[C_T], harm, (float)(1.0 / up), up,
+                                             d.sine_amp, d.noise_std, (float)((double)d.sine_amp / 3.0), d.voiced_threshold, noise,
+                                             w.src_w, w.src_b, cache_source, S, source, x.st);
+                         }),
             "nsf source");
     s = source;
   } else if (s != source) {
     H_CHECK(hipMemcpyAsync(source, s, x.L.tot[C_SMP] * sizeof(float), hipMemcpyDeviceToDevice, x.st), "source copy");
   }
-  H_CHECK(stft16(s, x.off(C_SMP), x.len(C_SMP), x.off(C_S2), x.len(C_S2), n, x.L.mx[C_S2], w.window, B.stft, x.st), "stft");
+  H_CHECK(timed_launch(T2W_TIMER_HIFT_STFT, 4.0 * x.L.tot[C_SMP] + 4.0 * nsrc * x.L.tot[C_S2], x.st,
+                       [&] { return stft16(s, x.off(C_SMP), x.len(C_SMP), x.off(C_S2), x.len(C_S2), n, x.L.mx[C_S2], w.window, B.stft, x.st); }),
+          "stft");
 
   // decoder
   {
@@ -313,7 +328,9 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
       for (int ph = 0; ph < u; ++ph) { c.off_in[ph] = 0; c.off_out[ph] = ph - p; }
       c.pre = PRE_LEAKY; c.slope = d.lrelu_slope; c.epi = EPI_STORE; c.n_items = n;
       if (run(x, c, i == 2 ? C_S2P : cls, "ups")) return 1;
-      if (i == 2) H_CHECK(reflect_rows(B.XN, cout, x.off(C_S2), n, x.st), "reflection pad");
+      if (i == 2)
+        H_CHECK(timed_launch(T2W_TIMER_HIFT_REFLECT, 8.0 * cout * n, x.st, [&] { return reflect_rows(B.XN, cout, x.off(C_S2), n, x.st); }),
+                "reflection pad");
     }
     {  // source branch: downsampling conv of the source STFT, a ResBlock, added into the stage input
       const int r = i == 0 ? d.up_rates[2] * d.up_rates[1] : (i == 1 ? d.up_rates[2] : 1);
@@ -333,7 +350,8 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
     c.slope = 0.01f;
     if (run(x, c, C_S2, "conv_post")) return 1;
   }
-  H_CHECK(istft16(B.post, x.off(C_S2), x.len(C_S2), x.off(C_SMP), n, x.L.mx[C_SMP], w.window, d.audio_limit, speech, x.st),
+  H_CHECK(timed_launch(T2W_TIMER_HIFT_ISTFT, 4.0 * nsrc * x.L.tot[C_S2] + 4.0 * x.L.tot[C_SMP], x.st,
+                       [&] { return istft16(B.post, x.off(C_S2), x.len(C_S2), x.off(C_SMP), n, x.L.mx[C_SMP], w.window, d.audio_limit, speech, x.st); }),
           "istft");
   return 0;
 }

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "launch_timer.h"
+
 namespace t2w {
 
 typedef uint16_t bf16_t;

@@ -507,13 +507,26 @@ class FastDiT:
         ``keep[i]``: keep the window's keys and conv caches (then trim as the reference does), else leave the caches
         untouched (final flushes).  ``chunk`` > 0: chunk-causal attention among each row's new frames.  Returns each
         stream's mel [mel, T_i] in fp32.  Nothing waits for the GPU."""
+        return self._solve(caches, mu, spks, cond, keep, chunk)
+
+    @torch.inference_mode()
+    def solve_timed(self, caches: list[FastCache], mu: list[torch.Tensor], spks: torch.Tensor, cond: list | None,
+                    keep: list[bool], chunk: int = 0, cap: int = 8192) -> tuple[list[torch.Tensor], list[tuple]]:
+        """``solve`` run eagerly (no graph) under the library's launch timer: (mels, [(kind, ms, bytes)] of every
+        instrumented launch -- the dense gated-residual tile GEMMs, proj and fc2 of every block at calls of more than
+        128 tokens -- timed by HIP events around the launch).  A measurement aid; waits for the GPU."""
+        with _lib.LaunchTimer(cap) as t:
+            out = self._solve(caches, mu, spks, cond, keep, chunk, eager=True)
+        return out, t.launches
+
+    def _solve(self, caches, mu, spks, cond, keep, chunk, eager: bool = False):
         Ts = [int(m.shape[1]) for m in mu]
         x0, stat = self._inputs(caches, mu, spks, cond, Ts)
         rows = [c.rows[0] for c in caches] + [c.rows[1] for c in caches]
         new = [self.pool.alloc(t) for t in Ts + Ts]
-        bucket = bucket_of(2 * len(Ts), 2 * sum(Ts)) if (self.use_graphs and self.buckets) else None
+        bucket = bucket_of(2 * len(Ts), 2 * sum(Ts)) if (self.use_graphs and self.buckets and not eager) else None
         p = plan_call(rows, Ts, new, keep, self.cnn_scratch, self.cnn_zero, bucket, self.kv_scratch)
-        out = self._run(p, x0, stat, chunk, bucket)
+        out = self._run(p, x0, stat, chunk, bucket, eager)
         n = len(caches)
         for i, c in enumerate(caches):
             for h in range(2):
@@ -539,9 +552,9 @@ class FastDiT:
     def _flat(p: dict) -> np.ndarray:
         return np.concatenate([x.astype(np.int32, copy=False) for x in p["parts"]])
 
-    def _run(self, p: dict, x0: torch.Tensor, stat: torch.Tensor, chunk: int, bucket) -> torch.Tensor:
+    def _run(self, p: dict, x0: torch.Tensor, stat: torch.Tensor, chunk: int, bucket, eager: bool = False) -> torch.Tensor:
         L, st = _lib.lib(), _lib.stream_handle()
-        if not self.use_graphs:
+        if not self.use_graphs or eager:
             tables = _Upload.new(self._flat(p), self.device)
             out = torch.empty(p["half"], self.cfg.mel, device=self.device)
             a = self._args(p, tables, x0, stat, out, self._workspace(p["n_tok"], p["n_rows"]), chunk)
