@@ -131,14 +131,26 @@ class HiFTModel:
         except Exception:
             pass
 
-    def noise(self, seeds: list[int], n_samples: int) -> tuple[torch.Tensor, torch.Tensor]:
+    def noise(self, seeds: list[int], n_samples: int, noise_device: str = "cpu") -> tuple[torch.Tensor, torch.Tensor]:
         """Per-row source noise as the reference draws it (``hift_noise``, ``engine/models/token2wav.py:112-121``): row i
-        takes ``rand(1, dim)`` then ``randn(1, dim, n)`` from a generator seeded ``seeds[i]`` (host generator here),
+        takes ``rand(1, dim)`` then ``randn(1, dim, n)`` from a generator seeded ``seeds[i]`` on ``noise_device`` (the
+        reference draws on the vocoder's device; "cpu" gives the host generator's stream, which the parity tests use),
         returned as (rand_ini [B, dim], noise [B, n, dim]) on the device."""
-        gens = [torch.Generator().manual_seed(int(x)) for x in seeds]
-        rand_ini = torch.cat([torch.rand(1, self.dim, generator=g) for g in gens])
-        noise = torch.cat([torch.randn(1, self.dim, n_samples, generator=g) for g in gens]).transpose(1, 2)
+        gens = [torch.Generator(device=noise_device).manual_seed(int(x)) for x in seeds]
+        rand_ini = torch.cat([torch.rand(1, self.dim, generator=g, device=noise_device) for g in gens])
+        noise = torch.cat([torch.randn(1, self.dim, n_samples, generator=g, device=noise_device) for g in gens]).transpose(1, 2)
         return rand_ini.to(self.device), noise.to(self.device)
+
+    @torch.inference_mode()
+    def __call__(self, mel: torch.Tensor, cache_source: torch.Tensor, seeds: list[int], noise_device: str | None = None):
+        """``HiFTGraphs.__call__(mel, cache_source, seeds)`` (``engine/runtime/hift_graph.py:62-88``): the rows' source
+        noise drawn from their chunk seeds (on the vocoder's device, as the reference's ``hift_noise``, unless
+        ``noise_device`` says otherwise), then ``forward_noise`` -- a captured graph per shape with ``use_graphs``.
+        mel [B, 80, T], cache_source [B, 1, S] -> (speech [B, 480 T], source [B, 1, 480 T])."""
+        if len(seeds) != mel.shape[0]:
+            raise ValueError(f"{len(seeds)} seeds for {mel.shape[0]} rows")
+        rand_ini, noise = self.noise(seeds, mel.shape[2] * self.cfg.upsample_scale, noise_device or str(mel.device))
+        return self.forward_noise(mel, cache_source, rand_ini, noise)
 
     def _workspace(self, frames: list[int]) -> torch.Tensor:
         fr = (C.c_int * len(frames))(*frames)

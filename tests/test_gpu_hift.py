@@ -184,3 +184,28 @@ def test_hift_graphs_equal_eager():
         torch.cuda.synchronize()
         assert torch.equal(sp_e, sp_g) and torch.equal(src_e, src_g), (rep, lens)
     assert graphed.counts["graph"] == 5 and len(graphed.graphs) == 2
+
+
+def test_call_with_seeds(dev, case):
+    """``HiFTModel(mel, cache_source, seeds)`` (the ``HiFTGraphs.__call__`` contract): noise drawn from each row's seed
+    -- on the host generator it is the oracle's ``hift_noise`` draw (speech within the strict bound of the oracle fed the
+    same seeds), on the device it is what the reference's device generators give (equal to ``forward_noise`` on that
+    draw, bit for bit); a graph replay of the same call gives the same bits."""
+    W, h, gm, mels, noise = case
+    mel = torch.cat([m[:, :, :50] for m in mels[:3]])
+    cs = torch.randn(3, 1, 480, generator=torch.Generator().manual_seed(9)) * 0.1
+    seeds = [11, 12, 13]
+    sp, src = gm(mel.cuda(), cs.cuda(), seeds, noise_device="cpu")
+    ri, nz = oh.hift_noise(9, seeds, 50 * 480)
+    rsp, rsrc = oh.forward_noise(h, mel, cs, ri, nz)
+    e = rel(sp.cpu(), rsp)
+    print("seeded call vs oracle rel-L2", e)
+    assert e < 5e-4 and torch.equal(src.cpu()[:, :, :480], cs)
+    a = gm(mel.cuda(), cs.cuda(), seeds)
+    gens = [torch.Generator(device="cuda").manual_seed(s) for s in seeds]
+    ri_d = torch.cat([torch.rand(1, 9, generator=g, device="cuda") for g in gens])
+    nz_d = torch.cat([torch.randn(1, 9, 50 * 480, generator=g, device="cuda") for g in gens]).transpose(1, 2)
+    b = gm.forward_noise(mel.cuda(), cs.cuda(), ri_d, nz_d)
+    assert torch.equal(a[0], b[0])
+    gg = HiFTModel(W, HiFTConfig(), use_graphs=True)
+    assert torch.equal(gg(mel.cuda(), cs.cuda(), seeds)[0], a[0]) and gg.counts["graph"] == 1
