@@ -165,6 +165,8 @@ def main() -> int:
         extra.update(extra_workloads(args, cfg, fd, spks, hift, Wh))
     if enc is not None:
         extra["flow_encoder"] = flow_workload(args, enc)
+    if not args.no_extra:
+        extra["co_scheduling"] = cu_share_workload(args, model, fd, caches, mus, spks, Wh)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -455,6 +457,52 @@ def chunk_latency(model, Wh, args, enc=None) -> dict:
                          "device-to-host copy; the no_encoder figures pass 50-frame mu windows; stage times are means of "
                          "profiled calls")
     return out
+
+
+def cu_share_workload(args, model, fd, caches, mus, spks, Wh) -> dict:
+    """The module on a CU-masked stream (co-scheduling with other work of the same process, without MPS): the
+    16 x 400 solve (its graph replayed on the masked stream) and the per-chunk latency of the DiT + HiFT decode path
+    (50-frame windows on a 300-frame prompt, graphs), at shares of the device's CUs evenly spread over its XCDs."""
+    from t2w_amd.cosched import CUStream, device_cus
+    from t2w_amd.dit import FastDiT
+    from t2w_amd.token2wav import BatchedToken2Wav, prompt_features
+
+    total = device_cus()
+    n = len(mus)
+    fl = FastDiT(model, n_slots=8192, max_streams=4, use_graphs=True)
+    bt = BatchedToken2Wav(fl, hift_model(Wh, args.hift_mode)) if Wh is not None else None
+    g = torch.Generator().manual_seed(13)
+    mel = model.cfg.mel
+    mk = lambda *s: torch.randn(*s, generator=g).cuda()  # noqa: E731
+    res = {}
+    for share in (total, 3 * total // 4, total // 2, total // 4):
+        cs = CUStream(share)
+        with cs:
+            fd.solve(caches, mus, spks, None, [False] * n, chunk=args.chunk)
+            cs.stream.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(3):
+                fd.solve(caches, mus, spks, None, [False] * n, chunk=args.chunk)
+            cs.stream.synchronize()
+            solve_ms = (time.perf_counter() - t0) / 3 * 1e3
+            p50 = None
+            if bt is not None:
+                st = bt.new_stream(bt.setup(prompt_features(mk(mel, 300), mk(mel), mk(mel, 300))), noise_seed=5, adopt=True)
+                ts = []
+                for i in range(13):
+                    w = mk(mel, 50)
+                    cs.stream.synchronize()
+                    a = time.perf_counter()
+                    bt.decode([(st, w, False)])
+                    if i >= 3:
+                        ts.append(time.perf_counter() - a)
+                bt.release_stream(st)
+                p50 = float(np.median(ts) * 1e3)
+        cs.close()
+        res[str(share)] = {"solve_16x400_ms": solve_ms, "p50_chunk_no_encoder_ms": p50}
+    return {"device_cus": total, "by_cus": res,
+            "case": "CU-masked stream (t2w_stream_create_cu_mask), CUs evenly spread over the XCDs; solve: the 16 x 400 "
+                    "workload's graph; chunk: BatchedToken2Wav.decode of 50-frame mu windows, 300-frame prompt"}
 
 
 def flow_workload(args, enc) -> dict:

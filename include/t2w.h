@@ -340,6 +340,20 @@ int t2w_hift_forward(const t2w_hift* h, int n_items, const int* frames, const in
  * conv's output on chip where the call's grid fills the chip (else as two convs), 2 always as two convs, 3 as one kernel
  * wherever the channel count allows (64, 128 or 256).  The modes give the same result up to the order of fp32 sums. */
 
+/* ---------------------------------------------------------------- co-scheduling on one GPU (CU-masked streams)
+ * The reference runs Token2Wav in a worker process of its own beside the Thinker/Talker and shares the GPU through CUDA
+ * MPS (engine/runtime/t2w_worker.py:858-924, scripts/serve_engine.sh:1-45).  Here the module can run in the engine's
+ * own process on a stream of its own, optionally restricted to a set of CUs, so the two share the GPU without a
+ * separate process: t2w_stream_create_cu_mask makes a stream of the current device whose kernels (graph replays
+ * included) run only on the CUs whose bits are set in mask[0 .. n_words) (bit i of word w = CU 32 w + i), at the
+ * default priority.  Each word must hold one run of at least 8 consecutive bits, or none: the runtime fails to create
+ * queues whose masks interleave single CUs or leave a group fewer than 8, and such masks are refused here.
+ * t2w_device_cus gives the current device's CU count.  Release the stream with
+ * t2w_stream_destroy (after its work is done). */
+int t2w_device_cus(int* n);
+int t2w_stream_create_cu_mask(const uint32_t* mask, int n_words, void** out);
+int t2w_stream_destroy(void* stream);
+
 /* ---------------------------------------------------------------- graphs (hipGraph capture of a stream) */
 
 typedef struct t2w_graph t2w_graph;

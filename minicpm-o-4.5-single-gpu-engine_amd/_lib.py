@@ -130,6 +130,9 @@ _SIGS = {
     "t2w_flow_workspace_bytes": (C.c_size_t, [P, I, I, I, I, I]),
     "t2w_flow_encode": (I, [P, C.POINTER(FlowArgs), P]),
     "t2w_flow_speaker": (I, [P, P, P, I, P]),
+    "t2w_device_cus": (I, [C.POINTER(I)]),
+    "t2w_stream_create_cu_mask": (I, [C.POINTER(C.c_uint32), I, C.POINTER(P)]),
+    "t2w_stream_destroy": (I, [P]),
     "t2w_graph_begin": (I, [P]),
     "t2w_graph_end": (I, [P, C.POINTER(P)]),
     "t2w_graph_launch": (I, [P, P]),

@@ -597,6 +597,42 @@ struct t2w_graph {
   hipGraphExec_t exec;
 };
 
+int t2w_device_cus(int* n) {
+  if (!n) return fail("device_cus: null output");
+  int dev = 0;
+  T2W_CHECK(hipGetDevice(&dev), "hipGetDevice");
+  T2W_CHECK(hipDeviceGetAttribute(n, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
+  return 0;
+}
+
+int t2w_stream_create_cu_mask(const uint32_t* mask, int n_words, void** out) {
+  if (!mask || !out || n_words <= 0) return fail("stream_create_cu_mask: null mask or output");
+  int cus = 0;
+  if (t2w_device_cus(&cus)) return 1;
+  int set = 0;
+  for (int w = 0; w < n_words; ++w) {
+    for (int b = 0; b < 32; ++b)
+      if ((mask[w] >> b) & 1u) set += 32 * w + b < cus ? 1 : 0;
+    // each 32-CU word one run of at least 8 consecutive CUs, or none: the runtime's queue creation fails on masks
+    // that interleave single CUs or give a group fewer than 8 (measured: 2 and 4 fail, 8 and more pass), and the
+    // failure then sticks to the process's later calls
+    const uint32_t low = mask[w] ? (mask[w] >> __builtin_ctz(mask[w])) : 0u;
+    if ((low & (low + 1u)) || (low && __builtin_popcount(low) < 8))
+      return fail("stream_create_cu_mask: each 32-bit word of the mask must be one run of at least 8 consecutive CUs, or empty");
+  }
+  if (set == 0) return fail("stream_create_cu_mask: the mask names none of the device's CUs");
+  hipStream_t s = nullptr;
+  T2W_CHECK(hipExtStreamCreateWithCUMask(&s, (uint32_t)n_words, mask), "hipExtStreamCreateWithCUMask");
+  *out = (void*)s;
+  return 0;
+}
+
+int t2w_stream_destroy(void* stream) {
+  if (!stream) return 0;
+  T2W_CHECK(hipStreamDestroy((hipStream_t)stream), "stream destroy");
+  return 0;
+}
+
 int t2w_graph_begin(void* stream) {
   T2W_CHECK(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal), "begin capture");
   return 0;

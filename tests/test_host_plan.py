@@ -169,3 +169,28 @@ def test_steady_window_key_is_the_captured_bucket_key():
         assert bucket_graph_key(bucket, 0, False) in captured
         empty = plan_call([], [], [], [], cnn_scratch=99, cnn_zero=98, bucket=bucket, kv_scratch=97)
         assert _kv_max(empty) == _kv_max(p)
+
+
+def test_cu_mask_spread():
+    """The co-scheduling mask gives 32-CU groups equal shares as runs from each group's first CU, at least 8 CUs in
+    every group it uses (the runtime refuses masks that interleave single CUs or give a group fewer)."""
+    from t2w_amd.cosched import spread_mask
+
+    ones = lambda m: [bin(x).count("1") for x in m]  # noqa: E731
+    assert spread_mask(64, total=256) == [0xFF] * 8
+    assert spread_mask(256, total=256) == [0xFFFFFFFF] * 8
+    assert spread_mask(128, total=256) == [0xFFFF] * 8
+    assert spread_mask(32, total=256) == [0xFF] * 4 + [0] * 4
+    assert spread_mask(8, total=256) == [0xFF] + [0] * 7
+    m = spread_mask(100, total=256)
+    assert ones(m) == [13] * 4 + [12] * 4 and all(x & (x + 1) == 0 for x in m)
+    assert ones(spread_mask(20, total=256)) == [10, 10] + [0] * 6
+    m = spread_mask(70, total=72)  # a short last group
+    assert sum(ones(m)) == 70 and all(k == 0 or k >= 8 for k in ones(m))
+    for n in range(8, 257):
+        m = spread_mask(n, total=256)
+        assert sum(ones(m)) == n and all(k == 0 or k >= 8 for k in ones(m)) and all(x & (x + 1) == 0 for x in m)
+    with pytest.raises(ValueError):
+        spread_mask(4, total=256)
+    with pytest.raises(ValueError):
+        spread_mask(300, total=256)
