@@ -393,12 +393,14 @@ def pmc_traffic() -> float | None:
 
 
 def flow_encoder(seed: int = 5):
-    """The flow encoder (CosyVoice2-style conformer, width 512) with random-init weights and pools for the workloads."""
+    """The flow encoder (CosyVoice2-style conformer, width 512) with random-init weights and pools for the workloads;
+    window calls replay captured graphs."""
     from t2w_amd.config import FlowConfig
     from t2w_amd.flow import FlowEncoder, FlowModel
     from t2w_amd.weights import init_flow
 
-    return FlowEncoder(FlowModel(init_flow(FlowConfig(), seed), FlowConfig()), n_slots1=16384, n_slots2=32768, n_cnn=1024)
+    return FlowEncoder(FlowModel(init_flow(FlowConfig(), seed), FlowConfig()), n_slots1=16384, n_slots2=32768, n_cnn=1024,
+                       use_graphs=True)
 
 
 def _latency(bt, st, wins, reps: int) -> tuple[float, dict]:

@@ -159,9 +159,19 @@ class FlowModel:
 
 class FlowEncoder:
     """Stream caches of the flow encoder and its packed call.  ``n_slots1`` / ``n_slots2``: frames per first / second
-    stack pool (each stream's lists hold about keep / 2 + 75 and keep + 150 of them); ``n_cnn``: conv-cache slots."""
+    stack pool (each stream's lists hold about keep / 2 + 75 and keep + 150 of them); ``n_cnn``: conv-cache slots.
 
-    def __init__(self, model: FlowModel, n_slots1: int = 32768, n_slots2: int = 65536, n_cnn: int = 4096):
+    ``use_graphs``: window calls replay a captured hipGraph of the whole encoder call (the role of ``EncoderGraphs``,
+    ``engine/runtime/dit_graph.py:210-352``), one per call shape -- the row count and the packed row totals, which fix
+    every launch of the call; the rows' tables go to the graph's own device arena before each replay (the key lists at
+    a fixed capacity of ``rmax`` keys per row, so their lengths do not enter the shape), and ``mu`` is copied out of the
+    graph's output buffer.  Prompt setups run eagerly.  At most ``max_graphs`` shapes are kept (least recently used
+    dropped)."""
+
+    VAR_TABLES = ("kv1_idx", "kv2_idx")  # tables whose length is not fixed by the call's shape
+
+    def __init__(self, model: FlowModel, n_slots1: int = 32768, n_slots2: int = 65536, n_cnn: int = 4096, use_graphs: bool = False,
+                 max_graphs: int = 16):
         cfg, dev = model.cfg, model.device
         self.model, self.cfg, self.device = model, cfg, dev
         C = cfg.dim
@@ -172,6 +182,16 @@ class FlowEncoder:
         self.pc = RefPool(n_cnn, reserved=1)  # slot 0 stays zero: the empty cache
         self.zero_cnn = int(self.pc.reserved[0])
         self._ws = None
+        self.use_graphs, self.max_graphs = use_graphs, max_graphs
+        self.graphs: dict[tuple, dict] = {}
+        self.counts = {"graph": 0, "eager": 0}
+        self._cap = None
+
+    def __del__(self):
+        try:
+            self.drop_graphs()
+        except Exception:
+            pass
 
     # --- states -------------------------------------------------------------------------------------------------------
     def new_state(self, keep: int) -> FlowState:
@@ -205,11 +225,76 @@ class FlowEncoder:
             self._ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=self.device)
         return self._ws
 
+    # --- graphs -----------------------------------------------------------------------------------------------------
+    def _graph_layout(self, parts: dict, R: int) -> tuple[dict, int]:
+        """Offsets of the call's tables in a graph arena: the tables whose sizes the call shape fixes, in order, then the
+        two key lists at ``R * rmax`` entries each."""
+        offs, o = {}, 0
+        for k, v in parts.items():
+            if k not in self.VAR_TABLES:
+                offs[k] = o
+                o += max(int(np.asarray(v).size), 1)
+        for k in self.VAR_TABLES:
+            offs[k] = o
+            o += R * self.cfg.rmax
+        return offs, o
+
+    def _flow_args(self, shape: tuple, base: int, offs: dict, keys, ws: torch.Tensor, mu: torch.Tensor) -> "_lib.FlowArgs":
+        return _lib.FlowArgs(*shape, *[base + 4 * offs[k] for k in keys], self.pool1.data_ptr(), self.pool1[0].numel(),
+                             self.pool2.data_ptr(), self.pool2[0].numel(), self.cnn_pool.data_ptr(), mu.data_ptr(), ws.data_ptr(),
+                             ws.numel())
+
+    def _graph_call(self, shape: tuple, parts: dict) -> torch.Tensor:
+        """Replay (capturing on first use) the graph of a call of this ``shape`` = (R, n_in, n_gap, n1, n_up, n2,
+        tiles1, tiles2) with the call's tables; returns a copy of its mu [n2, mel]."""
+        L = _lib.lib()
+        R, n2 = shape[0], shape[5]
+        g = self.graphs.pop(shape, None)
+        if g is None:
+            while len(self.graphs) >= self.max_graphs:
+                L.t2w_graph_destroy(self.graphs.pop(next(iter(self.graphs)))["graph"])
+            offs, size = self._graph_layout(parts, R)
+            need = int(L.t2w_flow_workspace_bytes(self.model.handle, *shape[1:6]))
+            g = {"offs": offs, "arena": torch.zeros(size, dtype=torch.int32, device=self.device),
+                 "ws": torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=self.device),
+                 "mu": torch.empty(n2, self.cfg.mel, dtype=torch.float32, device=self.device), "graph": None}
+        host = np.zeros(g["arena"].numel(), dtype=np.int32)
+        for k, v in parts.items():
+            v = np.asarray(v)
+            host[g["offs"][k]:g["offs"][k] + v.size] = v
+        _Upload.into(g["arena"], host)
+        if g["graph"] is None:
+            if self._cap is None:
+                self._cap = torch.cuda.Stream()
+            self._cap.wait_stream(torch.cuda.current_stream())
+            cst = self._cap.cuda_stream
+            args = self._flow_args(shape, g["arena"].data_ptr(), g["offs"], parts, g["ws"], g["mu"])
+            _lib.check(L.t2w_graph_begin(cst), "graph_begin")
+            rc = L.t2w_flow_encode(self.model.handle, C_ref(args), cst)
+            h = _lib.P()
+            rc2 = L.t2w_graph_end(cst, C_ref(h))
+            _lib.check(rc, "flow encode (capture)")
+            _lib.check(rc2, "graph_end")
+            torch.cuda.current_stream().wait_stream(self._cap)
+            g["graph"] = h
+        self.graphs[shape] = g  # most recently used last
+        _lib.check(L.t2w_graph_launch(g["graph"], _lib.stream_handle()), "graph_launch")
+        self.counts["graph"] += 1
+        return g["mu"].clone()
+
+    def drop_graphs(self) -> None:
+        for g in self.graphs.values():
+            if g["graph"] is not None:
+                _lib.lib().t2w_graph_destroy(g["graph"])
+        self.graphs = {}
+
     @torch.inference_mode()
-    def encode(self, states: list[FlowState], windows: list, lasts: list[bool]) -> tuple[torch.Tensor, list[int], list[int]]:
+    def encode(self, states: list[FlowState], windows: list, lasts: list[bool], graph: bool | None = None
+               ) -> tuple[torch.Tensor, list[int], list[int]]:
         """One call over every stream's window (token lists; a non-final window carries ``look`` lookahead tokens at its
         end).  Returns (mu [sum T2, mel] fp32 on the device, each stream's first row, each stream's T2) and advances the
-        states (a final window's state is released)."""
+        states (a final window's state is released).  ``graph``: replay a captured graph of the call's shape (default
+        ``use_graphs``)."""
         cfg = self.cfg
         look, s, C = cfg.look, cfg.stride, cfg.dim
         R = len(states)
@@ -262,22 +347,23 @@ class FlowEncoder:
                      "o1": o1, "up_src": up_src, "o2": o2, "t2": T2, "cnn_rd": rd, "cnn_wr": wr, "new1": new1, "new2": new2,
                      "kv1_idx": kv1, "kv1_off": kv1_off, "kv1_len": L1, "tiles1": tiles1.ravel(), "kv2_idx": kv2, "kv2_off": kv2_off,
                      "kv2_len": L2, "tiles2": tiles2.ravel()}
-            offs, o = {}, 0
-            for k, v in parts.items():
-                offs[k] = o
-                o += max(int(np.asarray(v).size), 1)
-            host = np.zeros(o, dtype=np.int32)
-            for k, v in parts.items():
-                host[offs[k]:offs[k] + np.asarray(v).size] = v
-            meta = _Upload.new(host, self.device)
-            base = meta.data_ptr()
-            ws = self._workspace(n_in, n_gap, n1, n_up, n2)
-            mu = torch.empty(n2, cfg.mel, dtype=torch.float32, device=self.device)
-            args = _lib.FlowArgs(R, n_in, n_gap, n1, n_up, n2, tiles1.shape[0], tiles2.shape[0],
-                                 *[base + 4 * offs[k] for k in parts],
-                                 self.pool1.data_ptr(), self.pool1[0].numel(), self.pool2.data_ptr(), self.pool2[0].numel(),
-                                 self.cnn_pool.data_ptr(), mu.data_ptr(), ws.data_ptr(), ws.numel())
-            _lib.check(_lib.lib().t2w_flow_encode(self.model.handle, C_ref(args), _lib.stream_handle()), "flow encode")
+            shape = (R, n_in, n_gap, n1, n_up, n2, tiles1.shape[0], tiles2.shape[0])
+            if self.use_graphs if graph is None else graph:
+                mu = self._graph_call(shape, parts)
+            else:
+                offs, o = {}, 0
+                for k, v in parts.items():
+                    offs[k] = o
+                    o += max(int(np.asarray(v).size), 1)
+                host = np.zeros(o, dtype=np.int32)
+                for k, v in parts.items():
+                    host[offs[k]:offs[k] + np.asarray(v).size] = v
+                meta = _Upload.new(host, self.device)
+                ws = self._workspace(n_in, n_gap, n1, n_up, n2)
+                mu = torch.empty(n2, cfg.mel, dtype=torch.float32, device=self.device)
+                args = self._flow_args(shape, meta.data_ptr(), offs, parts, ws, mu)
+                _lib.check(_lib.lib().t2w_flow_encode(self.model.handle, C_ref(args), _lib.stream_handle()), "flow encode")
+                self.counts["eager"] += 1
         except Exception:
             self.p1.drop(new1)
             if new2 is not None:
@@ -319,7 +405,7 @@ class FlowEncoder:
         states = [self.new_state(cfg.stride * t.size) for t in toks]
         windows = [np.concatenate([t, np.full(cfg.look, SILENCE_TOKEN, dtype=np.int64)]) for t in toks]
         try:
-            mu, rows, frames = self.encode(states, windows, [False] * len(states))
+            mu, rows, frames = self.encode(states, windows, [False] * len(states), graph=False)
         except Exception:
             for st in states:
                 self.release(st)

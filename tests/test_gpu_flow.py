@@ -117,3 +117,33 @@ def test_window_errors(flow):
     with pytest.raises(ValueError):
         enc.encode([st], [[d.vocab] * 5], [True])
     assert enc.in_use() == (0, 0, 0)
+
+
+def test_window_graphs_equal_eager(dev):
+    """Window calls replayed from captured graphs (one per call shape; the key lists' lengths are not part of it)
+    equal the eager calls bit for bit, through steady, ramped and final windows past the trim; prompt setups stay
+    eager."""
+    W = init_flow(FlowConfig(), seed=11)
+    model = FlowModel(W, FlowConfig(), device=dev)
+    encs = [FlowEncoder(model, n_slots1=4096, n_slots2=8192, n_cnn=64, use_graphs=gr) for gr in (False, True)]
+    g = torch.Generator().manual_seed(4)
+    tok = lambda n: torch.randint(0, 6561, (n,), generator=g).tolist()  # noqa: E731
+    prompts = [tok(40), tok(23)]
+    sts = [e.setup(prompts)[0] for e in encs]
+    plan = [([28, 28], [False, False])] * 6 + [([13, 28], [False, False]), ([28, 9], [False, True])]
+    for sizes, lasts in plan:
+        wins = [tok(n) for n in sizes]
+        live = [i for i in range(2) if sts[0][i] is not None]
+        outs = [e.encode([st[i] for i in live], [wins[i] for i in live], [lasts[i] for i in live])[0] for e, st in zip(encs, sts)]
+        assert torch.equal(outs[0], outs[1])
+        for st in sts:
+            for i in live:
+                if lasts[i]:
+                    st[i] = None
+    assert encs[1].counts["graph"] == len(plan) and encs[1].counts["eager"] == 1  # the setup
+    assert len(encs[1].graphs) < len(plan)  # steady windows share one graph
+    for e, st in zip(encs, sts):
+        for x in st:
+            if x is not None:
+                e.release(x)
+    assert all(e.in_use() == (0, 0, 0) for e in encs)
