@@ -161,6 +161,8 @@ def main() -> int:
     if not args.no_fp8:
         extra["fp8"] = fp8_workload(args, cfg, model, mus, spks, hift, hsrc if hift is not None else None,
                                     hnoise if hift is not None else None, step)
+        extra["fp8_weights"] = fp8_workload(args, cfg, model, mus, spks, hift, hsrc if hift is not None else None,
+                                            hnoise if hift is not None else None, step, mode="weights")
     if not args.no_extra:
         extra.update(extra_workloads(args, cfg, fd, spks, hift, Wh))
     if enc is not None:
@@ -550,14 +552,15 @@ def flow_workload(args, enc) -> dict:
             "case": "16 windows of 28 codec tokens in one encoder call, caches after 4 windows (trimmed)"}
 
 
-def fp8_workload(args, cfg, model, mus, spks, hift, hsrc, hnoise, bf16_step) -> dict:
-    """The same 16 x 400 workload with the block GEMMs on fp8 MFMA (e4m3 weights with per-output-channel scales, MX
-    fp8 activations); error of its mels against the bf16 solve's on identical inputs and weights."""
+def fp8_workload(args, cfg, model, mus, spks, hift, hsrc, hnoise, bf16_step, mode="mx") -> dict:
+    """The same 16 x 400 workload with fp8 block GEMMs; error of its mels against the bf16 solve's on identical inputs
+    and weights.  mode "mx": fp8 MFMA (e4m3 weights with per-output-channel scales, MX fp8 activations); "weights":
+    the same e4m3 weights dequantized to bf16 before each GEMM, bf16 activations and MFMA (config 5 as written)."""
     from t2w_amd.dit import FastDiT
 
     n = len(mus)
     T = int(mus[0].shape[1])
-    f8 = FastDiT(model, n_slots=max(8192, 2 * n * T + 4096), max_streams=n + 2, use_graphs=True, fp8=True)
+    f8 = FastDiT(model, n_slots=max(8192, 2 * n * T + 4096), max_streams=n + 2, use_graphs=True, fp8=True if mode == "mx" else mode)
     caches = [f8.new_cache() for _ in range(n)]
 
     def step():
@@ -586,8 +589,10 @@ def fp8_workload(args, cfg, model, mus, spks, hift, hsrc, hnoise, bf16_step) -> 
     del f8
     return {"mel_frames_per_s": n * T / dt, "ms_per_step": dt * 1e3, "dit_solve_ms": dit_dt * 1e3,
             "mel_rel_l2_vs_bf16": float(d.norm() / r.norm()), "mel_max_abs_vs_bf16": float(d.abs().max()),
-            "config": f"{n} streams x {T} frames, CFG B={2 * n}, chunk {args.chunk}, block GEMMs fp8 e4m3 / MX fp8, "
-                      "in_proj / final linear / attention bf16" + ("" if hift is None else " + HiFT")}
+            "config": f"{n} streams x {T} frames, CFG B={2 * n}, chunk {args.chunk}, block GEMMs "
+                      + ("fp8 e4m3 / MX fp8 on fp8 MFMA" if mode == "mx" else "e4m3 weights (per-channel scales) dequantized "
+                         "to bf16, bf16 activations and MFMA")
+                      + ", in_proj / final linear / attention bf16" + ("" if hift is None else " + HiFT")}
 
 
 def extra_workloads(args, cfg, fd, spks, hift, Wh) -> dict:

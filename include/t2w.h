@@ -130,7 +130,9 @@ typedef struct {
   void* conv_pool;          /* [row slots, steps, depth, 2, 2, H] bf16 */
   void* workspace;
   size_t workspace_bytes;
-  int fp8;                  /* 1: the block GEMMs on fp8 MFMA (e4m3 weights, MX fp8 activations; needs fp8 weights) */
+  int fp8;                  /* 0: bf16 block GEMMs; 1: fp8 MFMA (e4m3 weights, MX fp8 activations); 2: e4m3 weights
+                             * with per-output-channel scales dequantized to bf16 before each block GEMM, bf16
+                             * activations and MFMA (1 and 2 need fp8 weights) */
   const int* tok_abs;       /* [n_tok] position of the token in its stream (frames of kept windows before it); read
                              * only with globals.rope_freq */
   int kv_max;               /* 0, or a bound on every row's key-list length (row_kv_len) in this call and in every replay

@@ -106,6 +106,7 @@ struct Work {  // carve of the caller's workspace for n tokens, R rows
   // fp8 mode: MX fp8 activations (codes, block scales) of the qkv / fc1 inputs, the attention output, the conv frame
   // buffer and the fc1 output
   uint8_t *a8, *a8s, *o8, *o8s, *P8, *P8s, *b8, *b8s;
+  bf16_t* wdq;  // fp8 weight-only mode: the current GEMM's weights dequantized to bf16
 };
 
 // calls of up to this many tokens get a split-K partial area of SPLITK_BYTES
@@ -130,7 +131,10 @@ size_t carve(const t2w_dit_dims& d, int N, int R, bool fp8, char* base, Work* w)
   t.part_bytes = N <= SPLITK_MAX_TOK ? SPLITK_BYTES : 0;
   t.part = t.part_bytes ? (float*)take(t.part_bytes) : nullptr;
   t.a8 = t.a8s = t.o8 = t.o8s = t.P8 = t.P8s = t.b8 = t.b8s = nullptr;
+  t.wdq = nullptr;
   if (fp8) {
+    const size_t wmax = std::max((size_t)3 * H * H, (size_t)H * d.ffn);
+    t.wdq = (bf16_t*)take(wmax * 2);
     const size_t F = (size_t)d.ffn, NP = (size_t)N + 2 * R;
     t.a8 = (uint8_t*)take((size_t)N * H); t.a8s = (uint8_t*)take((size_t)N * H / 32);
     t.o8 = (uint8_t*)take((size_t)N * H); t.o8s = (uint8_t*)take((size_t)N * H / 32);
@@ -223,7 +227,15 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
   const int N = a->n_tok, R = a->n_rows, H = d.hidden, F = d.ffn, M = d.mel, D = d.depth;
   T2W_CHECK(gemm_bf16(gemm_args(w.a_in, 4 * M, nullptr, m->g.in_w, m->g.in_b, nullptr, w.h, H, N, H, 4 * M, &w), EPI_F16, st), "in_proj");
   const long long cstride = (long long)d.steps * D * 4 * H;
-  const bool f8 = a->fp8 != 0;
+  const bool f8 = a->fp8 == 1;  // fp8 MFMA, MX fp8 activations
+  const bool w8 = a->fp8 == 2;  // e4m3 weights dequantized per GEMM, bf16 activations and MFMA
+  hipError_t derr = hipSuccess;
+  // the block GEMM's bf16 weights: its own, or (w8) its e4m3 weights dequantized into w.wdq just before it
+  auto wt = [&](const void* bf, const void* q8, const float* s8, int N, int K) -> const void* {
+    if (!w8) return bf;
+    if (derr == hipSuccess) derr = dequant_w8((const uint8_t*)q8, s8, N, K, w.wdq, st);
+    return w.wdq;
+  };
   // Calls of few tokens: the gated-residual GEMMs and conv1 split K over several workgroups per tile and the row
   // kernel that reads their result next finishes their epilogue (pend: the result it has to finish).
   const int Sd = f8 ? 0 : defer_splits(d, N, w, false), St = f8 ? 0 : defer_splits(d, N, w, true);
@@ -232,7 +244,7 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
   hipError_t perr = hipSuccess;
   for (int b = 0; b < D; ++b) {
     const t2w_dit_block& k = m->blocks[b];
-    const t2w_dit_block_fp8* k8 = f8 ? &m->blocks8[b] : nullptr;
+    const t2w_dit_block_fp8* k8 = (f8 || w8) ? &m->blocks8[b] : nullptr;
     const float* md = mods + (size_t)b * 9 * H;
     const float *sh_a = md, *sc_a = md + H, *g_a = md + 2 * H, *sh_m = md + 3 * H, *sc_m = md + 4 * H, *g_m = md + 5 * H;
     const float *sh_c = md + 6 * H, *sc_c = md + 7 * H, *g_c = md + 8 * H;
@@ -246,7 +258,9 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     } else {
       T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st, pend), "ln_mod msa");
       pend = Pend();
-      gq = gemm_args(w.abuf, H, nullptr, k.qkv_w, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H, &w);
+      gq = gemm_args(w.abuf, H, nullptr, wt(k.qkv_w, k8 ? k8->qkv_w8 : nullptr, k8 ? k8->qkv_ws : nullptr, 3 * H, H), k.qkv_b, nullptr,
+                     w.big, 3 * H, N, 3 * H, H, &w);
+      T2W_CHECK(derr, "dequant qkv");
     }
     gq.qk = QkvOut{w.q, kp, vp, a->new_slot, k.qn_w, k.qn_b, k.kn_w, k.kn_b, d.eps_qk, H, m->g.rope_freq, a->tok_abs};
     const bool small_qkv = gemm_small_fits(gq, EPI_QKV);
@@ -272,10 +286,14 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     if (f8)
       T2W_CHECK(gemm_bf16(gemm8(w.o8, H, nullptr, w.o8s, k8->proj_w8, k8->proj_ws, k.proj_b, g_a, w.h, H, N, H, H), EPI_RESID_F16, st), "proj");
     else if (S) {
-      pend = gemm_deferred(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), Sd, w, st, &perr);
+      const void* pw = wt(k.proj_w, k8 ? k8->proj_w8 : nullptr, k8 ? k8->proj_ws : nullptr, H, H);
+      T2W_CHECK(derr, "dequant proj");
+      pend = gemm_deferred(gemm_args(w.ao, H, nullptr, pw, k.proj_b, g_a, w.h, H, N, H, H, &w), Sd, w, st, &perr);
       T2W_CHECK(perr, "proj");
     } else {
-      T2W_CHECK(timed_launch(T2W_TIMER_RESID_GEMM, resid_bytes(N, H, H), st, [&] { return gemm_bf16(gemm_args(w.ao, H, nullptr, k.proj_w, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F16, st); }), "proj");
+      const void* pw = wt(k.proj_w, k8 ? k8->proj_w8 : nullptr, k8 ? k8->proj_ws : nullptr, H, H);
+      T2W_CHECK(derr, "dequant proj");
+      T2W_CHECK(timed_launch(T2W_TIMER_RESID_GEMM, resid_bytes(N, H, H), st, [&] { return gemm_bf16(gemm_args(w.ao, H, nullptr, pw, k.proj_b, g_a, w.h, H, N, H, H, &w), EPI_RESID_F16, st); }), "proj");
     }
     ConvPlace cp;
     cp.P = w.P; cp.tok_row = a->tok_row; cp.tok_pos = a->tok_pos; cp.row_start = a->row_start; cp.row_len = a->row_len;
@@ -288,11 +306,15 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     pend = Pend();
     if (f8) {
       T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c1_w8, k8->c1_ws, k.c1_b, nullptr, w.ao, H, N, H, 3 * H), EPI_BF16, st), "conv1");
-    } else if (S) {
-      pend = gemm_deferred(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), St, w, st, &perr);
-      T2W_CHECK(perr, "conv1");
     } else {
-      T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c1_w, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), EPI_BF16, st), "conv1");
+      const void* cw = wt(k.c1_w, k8 ? k8->c1_w8 : nullptr, k8 ? k8->c1_ws : nullptr, H, 3 * H);
+      T2W_CHECK(derr, "dequant conv1");
+      if (S) {
+        pend = gemm_deferred(gemm_args(w.P, H, a->a_src, cw, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), St, w, st, &perr);
+        T2W_CHECK(perr, "conv1");
+      } else {
+        T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, cw, k.c1_b, nullptr, w.ao, H, N, H, 3 * H, &w), EPI_BF16, st), "conv1");
+      }
     }
     cp.cache_base = cbase + 2 * H;
     cp.cache_out_base = cbase + 2 * H;
@@ -300,11 +322,15 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     pend = Pend();
     if (f8) {
       T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c2_w8, k8->c2_ws, k.c2_b, g_c, w.h, H, N, H, 3 * H), EPI_RESID_F16, st), "conv2");
-    } else if (S) {
-      pend = gemm_deferred(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), St, w, st, &perr);
-      T2W_CHECK(perr, "conv2");
     } else {
-      T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, k.c2_w, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), EPI_RESID_F16, st), "conv2");
+      const void* cw = wt(k.c2_w, k8 ? k8->c2_w8 : nullptr, k8 ? k8->c2_ws : nullptr, H, 3 * H);
+      T2W_CHECK(derr, "dequant conv2");
+      if (S) {
+        pend = gemm_deferred(gemm_args(w.P, H, a->a_src, cw, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), St, w, st, &perr);
+        T2W_CHECK(perr, "conv2");
+      } else {
+        T2W_CHECK(gemm_bf16(gemm_args(w.P, H, a->a_src, cw, k.c2_b, g_c, w.h, H, N, H, 3 * H, &w), EPI_RESID_F16, st), "conv2");
+      }
     }
     if (f8) {
       T2W_CHECK(ln_mod_mx8(w.h, sh_m, sc_m, d.eps_block, w.a8, w.a8s, N, H, st), "ln_mod mlp");
@@ -316,12 +342,16 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     } else {
       T2W_CHECK(ln_mod(w.h, sh_m, sc_m, d.eps_block, w.abuf, N, H, st, pend), "ln_mod mlp");
       pend = Pend();
-      T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, k.fc1_w, k.fc1_b, nullptr, w.big, F, N, F, H, &w), EPI_GELU_BF16, st), "fc1");
+      const void* f1w = wt(k.fc1_w, k8 ? k8->fc1_w8 : nullptr, k8 ? k8->fc1_ws : nullptr, F, H);
+      T2W_CHECK(derr, "dequant fc1");
+      T2W_CHECK(gemm_bf16(gemm_args(w.abuf, H, nullptr, f1w, k.fc1_b, nullptr, w.big, F, N, F, H, &w), EPI_GELU_BF16, st), "fc1");
+      const void* f2w = wt(k.fc2_w, k8 ? k8->fc2_w8 : nullptr, k8 ? k8->fc2_ws : nullptr, H, F);
+      T2W_CHECK(derr, "dequant fc2");
       if (S) {
-        pend = gemm_deferred(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), Sd, w, st, &perr);
+        pend = gemm_deferred(gemm_args(w.big, F, nullptr, f2w, k.fc2_b, g_m, w.h, H, N, H, F, &w), Sd, w, st, &perr);
         T2W_CHECK(perr, "fc2");
       } else {
-        T2W_CHECK(timed_launch(T2W_TIMER_RESID_GEMM, resid_bytes(N, H, F), st, [&] { return gemm_bf16(gemm_args(w.big, F, nullptr, k.fc2_w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F16, st); }), "fc2");
+        T2W_CHECK(timed_launch(T2W_TIMER_RESID_GEMM, resid_bytes(N, H, F), st, [&] { return gemm_bf16(gemm_args(w.big, F, nullptr, f2w, k.fc2_b, g_m, w.h, H, N, H, F, &w), EPI_RESID_F16, st); }), "fc2");
       }
     }
   }
@@ -334,8 +364,9 @@ int check_args(const t2w_dit* m, const t2w_solve_args* a) {
   if (check_model(m)) return 1;
   if (!a) return fail("null args");
   if (a->n_tok <= 0 || a->n_rows <= 0) return fail("empty call");
+  if (a->fp8 < 0 || a->fp8 > 2) return fail("fp8 must be 0 (bf16), 1 (fp8 MFMA) or 2 (e4m3 weights, bf16 MFMA)");
   if (a->fp8 && !m->fp8_ready()) return fail("fp8 solve needs fp8 weights for every block");
-  if (a->fp8 && (m->d.hidden % 128 || m->d.ffn % 128)) return fail("fp8 solve needs hidden and ffn multiples of 128");
+  if (a->fp8 == 1 && (m->d.hidden % 128 || m->d.ffn % 128)) return fail("fp8 solve needs hidden and ffn multiples of 128");
   if (a->workspace_bytes < carve(m->d, a->n_tok, a->n_rows, m->fp8_ready(), nullptr, nullptr)) return fail("workspace too small");
   if (a->chunk < 0) return fail("negative chunk");
   if (a->kv_max < 0) return fail("negative kv_max");

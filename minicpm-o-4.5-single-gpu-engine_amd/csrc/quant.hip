@@ -30,7 +30,34 @@ __global__ void __launch_bounds__(256) quant_mx8_kernel(const bf16_t* x, int ldx
   if ((k & 31) == 0) s[(size_t)m * (K / 32) + k / 32] = (uint8_t)(se + 127);
 }
 
+// out[n, k] = bf16(e4m3(w8[n, k]) * ws[n]): the fp32 product rounded once to bf16; eight codes per thread
+__global__ void __launch_bounds__(256) dequant_w8_kernel(const uint8_t* w8, const float* ws, int N, int K, bf16_t* out) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  const int per_row = K / 8;
+  if (t >= (long)N * per_row) return;
+  const int n = (int)(t / per_row), k = (int)(t - (long)n * per_row) * 8;
+  const uint2 c = *(const uint2*)(w8 + (size_t)n * K + k);
+  const float sc = ws[n];
+  uint32_t o[4];
+  const uint32_t w[2] = {c.x, c.y};
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[j], false);  // bytes 0, 1
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[j], true);   // bytes 2, 3
+    o[2 * j] = pack2(lo[0] * sc, lo[1] * sc);
+    o[2 * j + 1] = pack2(hi[0] * sc, hi[1] * sc);
+  }
+  *(uint4*)(out + (size_t)n * K + k) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 }  // namespace
+
+hipError_t dequant_w8(const uint8_t* w8, const float* ws, int N, int K, bf16_t* out, hipStream_t st) {
+  if (N <= 0 || K % 8) return N <= 0 ? hipSuccess : hipErrorInvalidValue;
+  const long threads = (long)N * (K / 8);
+  hipLaunchKernelGGL(dequant_w8_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, w8, ws, N, K, out);
+  return hipGetLastError();
+}
 
 hipError_t quant_mx8(const bf16_t* x, int ldx, int M, int K, uint8_t* q, int ldq, uint8_t* s, hipStream_t st) {
   if (M <= 0) return hipSuccess;

@@ -93,6 +93,8 @@ SplitPlan splitk_plan(int M, int N, int K, size_t ws_bytes);
 // MX fp8 quantization: x [M, K] bf16 (rows ldx apart) -> q [M, K] e4m3 (rows ldq apart), s [M, K / 32] E8M0; K % 32 == 0
 hipError_t quant_mx8(const bf16_t* x, int ldx, int M, int K, uint8_t* q, int ldq, uint8_t* s, hipStream_t st);
 hipError_t gemm_splitk(const GemmArgs& g, int epi, const SplitPlan& p, float* part, hipStream_t st);
+// e4m3 weights with per-output-channel scales to bf16: out [N, K] = bf16(e4m3(w8) * ws[n]); K % 8 == 0
+hipError_t dequant_w8(const uint8_t* w8, const float* ws, int N, int K, bf16_t* out, hipStream_t st);
 
 // Per-token row kernels of the DiT block (H = hidden, one wave per token); h is the fp16 residual stream [N, H].
 // With pd.part set they first finish a pending gated residual (h updated in place) or, for ln_mish_conv, take the

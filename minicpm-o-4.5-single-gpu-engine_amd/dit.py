@@ -355,10 +355,11 @@ def bucket_tiles(rb: int, nb: int) -> int:
     return 2 * ((nb // 2 + 63) // 64 + rb // 2 + 1)
 
 
-def bucket_graph_key(bucket: tuple[int, int], chunk: int, fp8: bool) -> tuple:
-    """The key of a bucket's graph: the bucket, the chunk mask and the weight format -- nothing that depends on the
-    rows' cached lengths, so a graph captured on a padding-only plan serves every call that pads to its bucket."""
-    return (tuple(bucket), int(chunk), bool(fp8))
+def bucket_graph_key(bucket: tuple[int, int], chunk: int, fp8: int) -> tuple:
+    """The key of a bucket's graph: the bucket, the chunk mask and the GEMM format (0 bf16, 1 fp8 MFMA, 2 e4m3
+    weights) -- nothing that depends on the rows' cached lengths, so a graph captured on a padding-only plan serves
+    every call that pads to its bucket."""
+    return (tuple(bucket), int(chunk), int(fp8))
 
 
 def all_buckets() -> list[tuple[int, int]]:
@@ -408,17 +409,23 @@ class FastDiT:
     ``engine/runtime/dit_fast.py``: ``new_cache / release / clone / solve / capture / capture_all``, attributes ``pool``,
     ``scratch``, ``cnn_free``, ``counts``, ``use_graphs``)."""
 
-    def __init__(self, model: DiTModel, n_slots: int = 32768, max_streams: int = 96, use_graphs: bool = False, fp8: bool = False,
+    FP8_MODES = {False: 0, None: 0, "bf16": 0, True: 1, "mx": 1, "weights": 2}
+
+    def __init__(self, model: DiTModel, n_slots: int = 32768, max_streams: int = 96, use_graphs: bool = False, fp8: bool | str = False,
                  buckets: bool = True, max_exact_graphs: int = 8):
-        """``n_slots`` cached frames per pool (one CFG row's frame each).  ``fp8``: the block GEMMs on fp8 MFMA (the model
-        needs fp8 weights).  ``use_graphs``: every call replays a captured hipGraph of its whole 10-step solve; with
+        """``n_slots`` cached frames per pool (one CFG row's frame each).  ``fp8``: True / "mx": the block GEMMs on fp8
+        MFMA (e4m3 weights, MX fp8 activations); "weights": e4m3 weights with per-output-channel scales, dequantized to
+        bf16 just before each block GEMM, bf16 activations and MFMA (both need a model built with fp8 weights).  ``use_graphs``: every call replays a captured hipGraph of its whole 10-step solve; with
         ``buckets`` a call that fits a (rows, tokens) bucket is padded to it, so one graph serves all its calls
         (``capture_all`` makes them all up front); other calls take a graph of their exact shape (the last
         ``max_exact_graphs`` are kept)."""
-        if fp8 and not model.fp8:
+        if fp8 not in self.FP8_MODES:
+            raise ValueError(f"fp8 must be False, True / 'mx' or 'weights', not {fp8!r}")
+        mode = self.FP8_MODES[fp8]
+        if mode and not model.fp8:
             raise ValueError("fp8 solves need a DiTModel built with fp8=True")
         cfg = model.cfg
-        self.model, self.cfg, self.device, self.fp8 = model, cfg, model.device, fp8
+        self.model, self.cfg, self.device, self.fp8 = model, cfg, model.device, mode
         self.use_graphs, self.buckets, self.max_exact_graphs = use_graphs, buckets, max_exact_graphs
         S, D, H = cfg.steps, cfg.depth, cfg.hidden
         self.pool = SlotPool(n_slots, reserved=1)

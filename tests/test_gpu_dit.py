@@ -377,3 +377,44 @@ def test_estimator_chunk_dense_caches(dev, tiny, chunk):
     assert e < TOL and ec < 1e-2 and ea < 1e-2
     assert torch.equal(got_att[:, :, :, T:].cpu(), att.bfloat16().float())
     assert fd.pool.in_use() == fd.scratch
+
+
+def _dequantized_weights(W, model8, cfg):
+    """The plain weights W with every block GEMM weight replaced by its e4m3 codes times their per-channel scale (fp32),
+    in W's own layouts: a bf16 model of these holds exactly what the weight-only fp8 solve computes with."""
+    H = cfg.hidden
+    Wd = dict(W)
+    for b, blk8 in enumerate(model8.blocks8):
+        deq = {k: blk8[k + "_w8"].cpu().view(torch.float8_e4m3fn).float() * blk8[k + "_ws"].cpu()[:, None]
+               for k in ("qkv", "proj", "c1", "c2", "fc1", "fc2")}
+        p, a = f"blocks.{b}.", f"blocks.{b}.attn."
+        Wd[a + "to_q.weight"], Wd[a + "to_k.weight"], Wd[a + "to_v.weight"] = deq["qkv"].split(H)
+        Wd[a + "proj.weight"] = deq["proj"]
+        Wd[p + "conv.block.1.weight"] = deq["c1"].reshape(H, 3, H).permute(0, 2, 1).contiguous()
+        Wd[p + "conv.block.6.weight"] = deq["c2"].reshape(H, 3, H).permute(0, 2, 1).contiguous()
+        Wd[p + "mlp.fc1.weight"], Wd[p + "mlp.fc2.weight"] = deq["fc1"], deq["fc2"]
+    return Wd
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_fp8_weights_mode_is_bf16_on_dequantized_weights(dev, graphs):
+    """fp8="weights" (e4m3 weights with per-output-channel scales, bf16 activations and MFMA): a streaming solve (setups,
+    windows at 100 tokens with their deferred GEMMs, a 1,400-token call on tile GEMMs) equals, bit for bit, the bf16
+    solve of a model whose weights are the dequantized ones -- the dequantization is bf16(e4m3 x scale), nothing more."""
+    W = init_dit(TINY, seed=13)
+    model8 = DiTModel(W, TINY, fp8=True)
+    modeld = DiTModel(_dequantized_weights(W, model8, TINY), TINY)
+    g = torch.Generator().manual_seed(3)
+    spk = torch.randn(2, 80, generator=g).cuda()
+    calls = [([torch.randn(80, 60, generator=g).cuda() for _ in range(2)], True),
+             ([torch.randn(80, 50, generator=g).cuda() for _ in range(2)], False),
+             ([torch.randn(80, 700, generator=g).cuda() for _ in range(2)], False)]
+    outs = []
+    for model, mode in ((model8, "weights"), (modeld, False)):
+        fd = FastDiT(model, n_slots=8192, max_streams=2, use_graphs=graphs, fp8=mode)
+        caches = [fd.new_cache(keep=60) for _ in range(2)]
+        res = []
+        for mus, cond in calls:
+            res.append(torch.cat(fd.solve(caches, mus, spk, [m * 0.5 for m in mus] if cond else None, [True, True]), 1).cpu())
+        outs.append(torch.cat(res, 1))
+    assert torch.equal(outs[0], outs[1])

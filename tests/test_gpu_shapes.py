@@ -127,20 +127,23 @@ def test_ragged_16_streams_150_450(dev, full):
     assert worst < TOL and same < SAME
 
 
-def test_fp8_16x400_vs_bf16(dev, full):
+@pytest.mark.parametrize("mode", [True, "weights"], ids=["mx", "weights"])
+def test_fp8_16x400_vs_bf16(dev, full, mode):
+    """fp8 block GEMMs at 16 x 400 against the bf16 solve: "mx" (fp8 MFMA, MX fp8 activations) and "weights" (e4m3
+    weights with per-output-channel scales, bf16 activations and MFMA: BASELINE config 5 as written)."""
     W, model = full
     g = torch.Generator().manual_seed(4)
     mus = [torch.randn(80, 400, generator=g).cuda() for _ in range(16)]
     spks = torch.randn(16, 80, generator=g).cuda()
     outs = []
-    for fp8 in (False, True):
+    for fp8 in (False, mode):
         fd = FastDiT(model, n_slots=16 * 800 + 4096, max_streams=16, fp8=fp8)
         caches = [fd.new_cache() for _ in range(16)]
         outs.append([o.cpu() for o in fd.solve(caches, mus, spks, None, [False] * 16, chunk=50)])
         for c in caches:
             fd.release(c)
     e = max(rel(a, b) for a, b in zip(outs[1], outs[0]))
-    print("fp8 vs bf16 mel rel-L2 (16 x 400)", e)
+    print(f"fp8 ({mode}) vs bf16 mel rel-L2 (16 x 400)", e)
     assert e < FP8_TOL
 
 

@@ -156,7 +156,7 @@ def test_steady_window_key_is_the_captured_bucket_key():
     from t2w_amd.dit import _kv_max, bucket_graph_key
 
     rng = np.random.default_rng(0)
-    captured = {bucket_graph_key(b, 0, False) for b in all_buckets()}
+    captured = {bucket_graph_key(b, 0, 0) for b in all_buckets()}
     for n in (1, 3, 8, 16, 32):
         cached = rng.integers(300, 451, n)
         rows = _rows([(np.arange(10000 * r, 10000 * r + int(cached[r % n])), (2 * r, 2 * r + 1), 0) for r in range(2 * n)])
@@ -166,7 +166,7 @@ def test_steady_window_key_is_the_captured_bucket_key():
         p = plan_call(rows, Ts, new, [True] * n, cnn_scratch=99, cnn_zero=98, bucket=bucket, kv_scratch=97)
         assert int(p["parts"][7].max()) > 256  # the lists are long: a length-derived bound would have been 512
         assert _kv_max(p) == 0
-        assert bucket_graph_key(bucket, 0, False) in captured
+        assert bucket_graph_key(bucket, 0, 0) in captured
         empty = plan_call([], [], [], [], cnn_scratch=99, cnn_zero=98, bucket=bucket, kv_scratch=97)
         assert _kv_max(empty) == _kv_max(p)
 
