@@ -231,6 +231,19 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
   const bool w8 = a->fp8 == 2;  // e4m3 weights dequantized per GEMM, bf16 activations and MFMA
   hipError_t derr = hipSuccess;
   // the block GEMM's bf16 weights: its own, or (w8) its e4m3 weights dequantized into w.wdq just before it
+  // calls of more than 1024 tokens: the row kernel before each block GEMM also reads that GEMM's weights (and the one
+  // after it, where no row kernel comes between), so they are cached when the GEMM starts (w8: its dequantization
+  // already leaves them there)
+  const bool pf_on = N > 1024 && !w8;
+  auto pf_of = [&](const void* a0, size_t b0, const void* a1 = nullptr, size_t b1 = 0) {
+    Prefetch pf;
+    if (pf_on) {
+      pf.p[0] = a0; pf.bytes[0] = b0;
+      pf.p[1] = a1; pf.bytes[1] = b1;
+    }
+    return pf;
+  };
+  const size_t eb = f8 ? 1 : 2;  // bytes per weight
   auto wt = [&](const void* bf, const void* q8, const float* s8, int N, int K) -> const void* {
     if (!w8) return bf;
     if (derr == hipSuccess) derr = dequant_w8((const uint8_t*)q8, s8, N, K, w.wdq, st);
@@ -253,10 +266,12 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     bf16_t* vp = (bf16_t*)a->v_pool + layer;
     GemmArgs gq;
     if (f8) {
-      T2W_CHECK(ln_mod_mx8(w.h, sh_a, sc_a, d.eps_block, w.a8, w.a8s, N, H, st), "ln_mod msa");
+      T2W_CHECK(ln_mod_mx8(w.h, sh_a, sc_a, d.eps_block, w.a8, w.a8s, N, H, st,
+                           pf_of(k8->qkv_w8, eb * 3 * H * H, k8->proj_w8, eb * H * H)), "ln_mod msa");
       gq = gemm8(w.a8, H, nullptr, w.a8s, k8->qkv_w8, k8->qkv_ws, k.qkv_b, nullptr, w.big, 3 * H, N, 3 * H, H);
     } else {
-      T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st, pend), "ln_mod msa");
+      T2W_CHECK(ln_mod(w.h, sh_a, sc_a, d.eps_block, w.abuf, N, H, st, pend, pf_of(k.qkv_w, eb * 3 * H * H, k.proj_w, eb * H * H)),
+                "ln_mod msa");
       pend = Pend();
       gq = gemm_args(w.abuf, H, nullptr, wt(k.qkv_w, k8 ? k8->qkv_w8 : nullptr, k8 ? k8->qkv_ws : nullptr, 3 * H, H), k.qkv_b, nullptr,
                      w.big, 3 * H, N, 3 * H, H, &w);
@@ -302,7 +317,8 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     bf16_t* cbase = (bf16_t*)a->conv_pool + ((size_t)(step * D + b) * 2) * 2 * H;
     cp.cache_base = cbase;
     cp.cache_out_base = cbase;
-    T2W_CHECK(ln_mod_conv(w.h, sh_c, sc_c, d.eps_block, cp, H, st, pend), "ln_mod_conv");
+    T2W_CHECK(ln_mod_conv(w.h, sh_c, sc_c, d.eps_block, cp, H, st, pend, pf_of(f8 ? k8->c1_w8 : k.c1_w, eb * 3 * H * H)),
+              "ln_mod_conv");
     pend = Pend();
     if (f8) {
       T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c1_w8, k8->c1_ws, k.c1_b, nullptr, w.ao, H, N, H, 3 * H), EPI_BF16, st), "conv1");
@@ -318,7 +334,8 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
     }
     cp.cache_base = cbase + 2 * H;
     cp.cache_out_base = cbase + 2 * H;
-    T2W_CHECK(ln_mish_conv(w.ao, k.cln_w, k.cln_b, d.eps_conv, cp, H, st, pend), "ln_mish_conv");
+    T2W_CHECK(ln_mish_conv(w.ao, k.cln_w, k.cln_b, d.eps_conv, cp, H, st, pend, pf_of(f8 ? k8->c2_w8 : k.c2_w, eb * 3 * H * H)),
+              "ln_mish_conv");
     pend = Pend();
     if (f8) {
       T2W_CHECK(gemm_bf16(gemm8(w.P8, H, a->a_src, w.P8s, k8->c2_w8, k8->c2_ws, k.c2_b, g_c, w.h, H, N, H, 3 * H), EPI_RESID_F16, st), "conv2");
@@ -333,14 +350,16 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
       }
     }
     if (f8) {
-      T2W_CHECK(ln_mod_mx8(w.h, sh_m, sc_m, d.eps_block, w.a8, w.a8s, N, H, st), "ln_mod mlp");
+      T2W_CHECK(ln_mod_mx8(w.h, sh_m, sc_m, d.eps_block, w.a8, w.a8s, N, H, st,
+                           pf_of(k8->fc1_w8, eb * F * H, k8->fc2_w8, eb * H * F)), "ln_mod mlp");
       GemmArgs g1 = gemm8(w.a8, H, nullptr, w.a8s, k8->fc1_w8, k8->fc1_ws, k.fc1_b, nullptr, w.b8, F, N, F, H);
       g1.c_scale = w.b8s;
       g1.c_sld = F / 32;
       T2W_CHECK(gemm_bf16(g1, EPI_GELU_MX8, st), "fc1");
       T2W_CHECK(gemm_bf16(gemm8(w.b8, F, nullptr, w.b8s, k8->fc2_w8, k8->fc2_ws, k.fc2_b, g_m, w.h, H, N, H, F), EPI_RESID_F16, st), "fc2");
     } else {
-      T2W_CHECK(ln_mod(w.h, sh_m, sc_m, d.eps_block, w.abuf, N, H, st, pend), "ln_mod mlp");
+      T2W_CHECK(ln_mod(w.h, sh_m, sc_m, d.eps_block, w.abuf, N, H, st, pend, pf_of(k.fc1_w, eb * F * H, k.fc2_w, eb * H * F)),
+                "ln_mod mlp");
       pend = Pend();
       const void* f1w = wt(k.fc1_w, k8 ? k8->fc1_w8 : nullptr, k8 ? k8->fc1_ws : nullptr, F, H);
       T2W_CHECK(derr, "dequant fc1");

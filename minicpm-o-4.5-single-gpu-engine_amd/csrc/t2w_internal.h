@@ -99,11 +99,18 @@ hipError_t dequant_w8(const uint8_t* w8, const float* ws, int N, int K, bf16_t* 
 // Per-token row kernels of the DiT block (H = hidden, one wave per token); h is the fp16 residual stream [N, H].
 // With pd.part set they first finish a pending gated residual (h updated in place) or, for ln_mish_conv, take the
 // pending GEMM's bf16-rounded value as their input row instead of y.
+// Byte ranges (device memory) that a row kernel without a pending GEMM also reads, in workgroups of its own after its
+// rows, so that the weights of the GEMMs that follow are in the device's caches (the 256 MB memory-side cache) when
+// they start; the values are discarded.  Up to two ranges, 16-byte aligned.
+struct Prefetch {
+  const void* p[2] = {nullptr, nullptr};
+  size_t bytes[2] = {0, 0};
+};
 hipError_t ln_mod(f16_t* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H,
-                  hipStream_t st, const Pend& pd = Pend());
+                  hipStream_t st, const Pend& pd = Pend(), const Prefetch& pf = Prefetch());
 // ln_mod with MX fp8 output: codes q [N, H], block scales qs [N, H / 32]
 hipError_t ln_mod_mx8(const f16_t* h, const float* shift, const float* scale1, float eps, uint8_t* q, uint8_t* qs, int N,
-                      int H, hipStream_t st);
+                      int H, hipStream_t st, const Prefetch& pf = Prefetch());
 
 struct ConvPlace {   // where the normed frames of a causal conv go (the padded frame buffer and the conv caches)
   bf16_t* P;          // [N + 2 R, H]: per row r its two cached frames, then its T_r frames
@@ -122,9 +129,9 @@ struct ConvPlace {   // where the normed frames of a causal conv go (the padded 
 };
 
 hipError_t ln_mod_conv(f16_t* h, const float* shift, const float* scale1, float eps, const ConvPlace& cp, int H,
-                       hipStream_t st, const Pend& pd = Pend());
+                       hipStream_t st, const Pend& pd = Pend(), const Prefetch& pf = Prefetch());
 hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float eps, const ConvPlace& cp, int H,
-                        hipStream_t st, const Pend& pd = Pend());
+                        hipStream_t st, const Pend& pd = Pend(), const Prefetch& pf = Prefetch());
 // rotary embedding of the q rows [N, H] and of the keys at slots[n] after the tile GEMM's q / k epilogue: channel pair
 // (2i, 2i + 1) of each head turned by pos[n] * rfreq[i] (bf16 in and out)
 hipError_t rope_qk(bf16_t* q, bf16_t* k_pool, const int* slots, const int* pos, const float* rfreq, int N, int H, hipStream_t st);
