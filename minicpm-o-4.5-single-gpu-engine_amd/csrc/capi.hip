@@ -6,6 +6,7 @@
 #include <initializer_list>
 #include <mutex>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -233,8 +234,9 @@ int run_estimator(const t2w_dit* m, const t2w_solve_args* a, const Work& w, int 
   // the block GEMM's bf16 weights: its own, or (w8) its e4m3 weights dequantized into w.wdq just before it
   // calls of more than 1024 tokens: the row kernel before each block GEMM also reads that GEMM's weights (and the one
   // after it, where no row kernel comes between), so they are cached when the GEMM starts (w8: its dequantization
-  // already leaves them there)
-  const bool pf_on = N > 1024 && !w8;
+  // already leaves them there).  Streaming chunks do not: their row kernels are short, and reading the weights there
+  // puts the reads on the critical path (chunk DiT 14.8 -> 19.1 ms measured)
+  const bool pf_on = !w8 && N > 1024;
   auto pf_of = [&](const void* a0, size_t b0, const void* a1 = nullptr, size_t b1 = 0) {
     Prefetch pf;
     if (pf_on) {

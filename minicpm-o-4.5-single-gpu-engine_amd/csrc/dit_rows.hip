@@ -187,14 +187,15 @@ __device__ __forceinline__ void row_store_mx8(const float (&v)[VPL], uint8_t* qr
   }
 }
 
-// Workgroup `b` of a row kernel's prefetch workgroups: reads its 4 x blockDim 16-byte units of the two ranges (taken
-// as one sequence) and discards them (an empty asm keeps the loads)
+// Workgroup `b` of a row kernel's prefetch workgroups: reads its PF_UNITS 16-byte units of the two ranges (taken as
+// one sequence; PF_UNITS / blockDim per thread) and discards them (an empty asm keeps the loads)
+constexpr int PF_UNITS = 1024;
 __device__ __forceinline__ void prefetch_part(const Prefetch& pf, unsigned b) {
   const long n0 = (long)(pf.bytes[0] / 16), n1 = (long)(pf.bytes[1] / 16);
-  long i = (long)b * blockDim.x * 4 + threadIdx.x;
+  long i = (long)b * PF_UNITS + threadIdx.x;
   uint32_t acc = 0;
-#pragma unroll
-  for (int u = 0; u < 4; ++u, i += blockDim.x) {
+  const int per = PF_UNITS / blockDim.x;
+  for (int u = 0; u < per; ++u, i += blockDim.x) {
     if (i < n0) {
       const uint4 v = ((const uint4*)pf.p[0])[i];
       acc ^= v.x ^ v.y ^ v.z ^ v.w;
@@ -232,7 +233,7 @@ __global__ void __launch_bounds__(256) ln_mod_kernel(f16_t* h, const float* shif
                                                      bf16_t* out, uint8_t* q, uint8_t* qs, int N, int H, Pend pd, Prefetch pf,
                                                      unsigned row_blocks) {
   constexpr int G = VPL >= 8 ? 8 : 4;  // fp16 rows: 16 bytes per lane and instruction
-  if (!PEND && blockIdx.x >= row_blocks) {  // the prefetch workgroups, after every row's
+  if (blockIdx.x >= row_blocks) {  // the prefetch workgroups, after every row's
     prefetch_part(pf, blockIdx.x - row_blocks);
     return;
   }
@@ -300,7 +301,7 @@ template <int VPL, bool PEND>
 __global__ void __launch_bounds__(256) ln_mod_conv_kernel(f16_t* h, const float* shift, const float* scale1, float eps,
                                                           ConvPlace cp, int H, Pend pd, Prefetch pf, unsigned row_blocks) {
   constexpr int G = VPL >= 8 ? 8 : 4;
-  if (!PEND && blockIdx.x >= row_blocks) {
+  if (blockIdx.x >= row_blocks) {
     prefetch_part(pf, blockIdx.x - row_blocks);
     return;
   }
@@ -326,7 +327,7 @@ __global__ void __launch_bounds__(256) ln_mod_conv_kernel(f16_t* h, const float*
 template <int VPL, bool PEND>
 __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, const float* lw, const float* lb, float eps,
                                                            ConvPlace cp, int H, Pend pd, Prefetch pf, unsigned row_blocks) {
-  if (!PEND && blockIdx.x >= row_blocks) {
+  if (blockIdx.x >= row_blocks) {
     prefetch_part(pf, blockIdx.x - row_blocks);
     return;
   }
@@ -535,11 +536,11 @@ inline int row_waves(long long rows) { return rows <= 1024 ? 1 : 4; }
     default: return hipErrorInvalidValue;  \
   }
 
-// workgroups of 64 w threads that read a prefetch's ranges 4 x 16 bytes per thread (none without ranges)
-inline unsigned prefetch_blocks(const Prefetch& pf, int w) {
-  if ((pf.bytes[0] && ((size_t)pf.p[0] & 15)) || (pf.bytes[1] && ((size_t)pf.p[1] & 15))) return 0;  // unaligned: skipped
+// workgroups that read a prefetch's ranges, PF_UNITS 16-byte units each (none without ranges or when unaligned)
+inline unsigned prefetch_blocks(const Prefetch& pf) {
+  if ((pf.bytes[0] && ((size_t)pf.p[0] & 15)) || (pf.bytes[1] && ((size_t)pf.p[1] & 15))) return 0;
   const size_t units = pf.bytes[0] / 16 + pf.bytes[1] / 16;
-  return (unsigned)((units + 256 * w - 1) / (256 * w));
+  return (unsigned)((units + PF_UNITS - 1) / PF_UNITS);
 }
 
 hipError_t ln_mod(f16_t* h, const float* shift, const float* scale1, float eps, bf16_t* out, int N, int H, hipStream_t st,
@@ -549,9 +550,9 @@ hipError_t ln_mod(f16_t* h, const float* shift, const float* scale1, float eps, 
   const int w = row_waves(N);
   const unsigned rb = blocks_for(N, w);
   if (pd.part) {
-    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, true>), dim3(rb), dim3(64 * w), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H, pd, Prefetch(), rb));
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, true>), dim3(rb + prefetch_blocks(pf)), dim3(64 * w), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H, pd, pf, rb));
   } else {
-    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, false>), dim3(rb + prefetch_blocks(pf, w)), dim3(64 * w), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H, pd, pf, rb));
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, false>), dim3(rb + prefetch_blocks(pf)), dim3(64 * w), 0, st, h, shift, scale1, eps, out, nullptr, nullptr, N, H, pd, pf, rb));
   }
   return hipGetLastError();
 }
@@ -562,7 +563,7 @@ hipError_t ln_mod_mx8(const f16_t* h, const float* shift, const float* scale1, f
   // nothing pending: h is only read
   const int w = row_waves(N);
   const unsigned rb = blocks_for(N, w);
-  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, false>), dim3(rb + prefetch_blocks(pf, w)), dim3(64 * w), 0, st, const_cast<f16_t*>(h), shift, scale1, eps, nullptr, q, qs, N, H, Pend(), pf, rb));
+  T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_kernel<V, false>), dim3(rb + prefetch_blocks(pf)), dim3(64 * w), 0, st, const_cast<f16_t*>(h), shift, scale1, eps, nullptr, q, qs, N, H, Pend(), pf, rb));
   return hipGetLastError();
 }
 
@@ -573,9 +574,9 @@ hipError_t ln_mod_conv(f16_t* h, const float* shift, const float* scale1, float 
   const int w = row_waves(cp.N + cp.R);
   const unsigned rb = blocks_for(cp.N + cp.R, w);
   if (pd.part) {
-    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_conv_kernel<V, true>), dim3(rb), dim3(64 * w), 0, st, h, shift, scale1, eps, cp, H, pd, Prefetch(), rb));
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_conv_kernel<V, true>), dim3(rb + prefetch_blocks(pf)), dim3(64 * w), 0, st, h, shift, scale1, eps, cp, H, pd, pf, rb));
   } else {
-    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_conv_kernel<V, false>), dim3(rb + prefetch_blocks(pf, w)), dim3(64 * w), 0, st, h, shift, scale1, eps, cp, H, pd, pf, rb));
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mod_conv_kernel<V, false>), dim3(rb + prefetch_blocks(pf)), dim3(64 * w), 0, st, h, shift, scale1, eps, cp, H, pd, pf, rb));
   }
   return hipGetLastError();
 }
@@ -587,9 +588,9 @@ hipError_t ln_mish_conv(const bf16_t* y, const float* w, const float* b, float e
   const int wv = row_waves(cp.N + cp.R);
   const unsigned rb = blocks_for(cp.N + cp.R, wv);
   if (pd.part) {
-    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mish_conv_kernel<V, true>), dim3(rb), dim3(64 * wv), 0, st, y, w, b, eps, cp, H, pd, Prefetch(), rb));
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mish_conv_kernel<V, true>), dim3(rb + prefetch_blocks(pf)), dim3(64 * wv), 0, st, y, w, b, eps, cp, H, pd, pf, rb));
   } else {
-    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mish_conv_kernel<V, false>), dim3(rb + prefetch_blocks(pf, wv)), dim3(64 * wv), 0, st, y, w, b, eps, cp, H, pd, pf, rb));
+    T2W_VPL_DISPATCH(H, hipLaunchKernelGGL((ln_mish_conv_kernel<V, false>), dim3(rb + prefetch_blocks(pf)), dim3(64 * wv), 0, st, y, w, b, eps, cp, H, pd, pf, rb));
   }
   return hipGetLastError();
 }
