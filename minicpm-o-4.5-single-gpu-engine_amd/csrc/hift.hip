@@ -819,11 +819,10 @@ __global__ void __launch_bounds__(256, 2) resblock_pair_kernel(ConvDesc c1, Conv
         hl[hswz(sr, sch)] = o;
       }
     }
+    // taps in pairs with the two weight sets in fixed roles: the loads of tap j + 1 (into wb) and j + 2 (into wa) are
+    // issued before the MFMAs of taps j and j + 1
     bf16x8 wa[4][2], wb[4][2];
-    load_w(w1, 0, c0, wa);
-    __syncthreads();
-    for (int j = 0; j < k; ++j) {
-      if (j + 1 < k) load_w(w1, j + 1, c0, wb);
+    auto tap1 = [&](const bf16x8 (&w)[4][2], int j) __attribute__((always_inline)) {
       const int shift = j * dil;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
@@ -832,16 +831,20 @@ __global__ void __launch_bounds__(256, 2) resblock_pair_kernel(ConvDesc c1, Conv
 #pragma unroll
         for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(hl[hswz(ws + i * 32 + (lane & 31) + shift, chunk)]);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          if (i >= live1) break;
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[kk][jj], af[i], acc[i][jj], 0, 0, 0);
-        }
+          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w[kk][jj], af[i], acc[i][jj], 0, 0, 0);
       }
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) wa[kk][jj] = wb[kk][jj];
+    };
+    load_w(w1, 0, c0, wa);
+    __syncthreads();
+    for (int j = 0; j < k; j += 2) {
+      if (j + 1 < k) load_w(w1, j + 1, c0, wb);
+      tap1(wa, j);
+      if (j + 1 < k) {
+        if (j + 2 < k) load_w(w1, j + 2, c0, wa);
+        tap1(wb, j + 1);
+      }
     }
   }
 
@@ -887,11 +890,7 @@ __global__ void __launch_bounds__(256, 2) resblock_pair_kernel(ConvDesc c1, Conv
   // next step's weights loaded while this step's MFMAs run
   {
     bf16x8 wa[4][2], wb[4][2];
-    load_w(w2, 0, 0, wa);
-    const int steps = (C / 64) * k;
-    for (int sidx = 0, c0 = 0, j = 0; sidx < steps; ++sidx) {
-      const int nj = j + 1 == k ? 0 : j + 1, nc0 = j + 1 == k ? c0 + 64 : c0;
-      if (sidx + 1 < steps) load_w(w2, nj, nc0, wb);
+    auto tap2 = [&](const bf16x8 (&w)[4][2], int j, int c0) __attribute__((always_inline)) {
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const int chunk = (c0 >> 3) + kk * 2 + (lane >> 5);
@@ -902,18 +901,31 @@ __global__ void __launch_bounds__(256, 2) resblock_pair_kernel(ConvDesc c1, Conv
           af[i] = as_bf16x8(hl[s * CH + (chunk ^ (s & MSK))]);
         }
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          if (i >= live2) break;
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[kk][jj], af[i], acc[i][jj], 0, 0, 0);
-        }
+          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w[kk][jj], af[i], acc[i][jj], 0, 0, 0);
       }
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) wa[kk][jj] = wb[kk][jj];
-      j = nj;
-      c0 = nc0;
+    };
+    // the (chunk, tap) step after (j, c0)
+    auto next = [&](int& j, int& c0) __attribute__((always_inline)) {
+      if (j + 1 == k) { j = 0; c0 += 64; } else { ++j; }
+    };
+    load_w(w2, 0, 0, wa);
+    const int steps = (C / 64) * k;
+    int j = 0, c0 = 0;
+    for (int sidx = 0; sidx < steps; sidx += 2) {  // steps in pairs, weight sets in fixed roles as in conv1
+      int j1 = j, c1 = c0;
+      next(j1, c1);
+      if (sidx + 1 < steps) load_w(w2, j1, c1, wb);
+      tap2(wa, j, c0);
+      if (sidx + 1 < steps) {
+        int j2 = j1, c2 = c1;
+        next(j2, c2);
+        if (sidx + 2 < steps) load_w(w2, j2, c2, wa);
+        tap2(wb, j1, c1);
+        j = j2;
+        c0 = c2;
+      }
     }
   }
 
