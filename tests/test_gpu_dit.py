@@ -418,3 +418,26 @@ def test_fp8_weights_mode_is_bf16_on_dequantized_weights(dev, graphs):
             res.append(torch.cat(fd.solve(caches, mus, spk, [m * 0.5 for m in mus] if cond else None, [True, True]), 1).cpu())
         outs.append(torch.cat(res, 1))
     assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_fp8_weights_mode_large_call(dev, graphs):
+    """fp8="weights" on a call of 8,400 CFG tokens (2 streams x 2,100 frames, chunk 50), where every block GEMM is a tile
+    GEMM of 256-row tiles: still bit for bit the bf16 solve of the dequantized weights, and within bf16 solve error of
+    the fp32 oracle on those weights."""
+    W = init_dit(TINY, seed=17)
+    model8 = DiTModel(W, TINY, fp8=True)
+    Wd = _dequantized_weights(W, model8, TINY)
+    modeld = DiTModel(Wd, TINY)
+    g = torch.Generator().manual_seed(5)
+    spk = torch.randn(2, 80, generator=g)
+    mus = [torch.randn(80, 2100, generator=g) for _ in range(2)]
+    outs = []
+    for model, mode in ((model8, "weights"), (modeld, False)):
+        fd = FastDiT(model, n_slots=16384, max_streams=2, use_graphs=graphs, fp8=mode)
+        caches = [fd.new_cache() for _ in range(2)]
+        outs.append(torch.cat(fd.solve(caches, [m.cuda() for m in mus], spk.cuda(), None, [False, False], chunk=50), 1).cpu())
+    assert torch.equal(outs[0], outs[1])
+    d = od.dims_of(Wd, steps=TINY.steps)
+    ref = od.solve(Wd, d, Wd["rand_noise"], [od.empty_cache(d) for _ in range(2)], mus, spk, None, [False, False], chunk=50)
+    assert rel(outs[0], torch.cat(ref, 1)) < TOL
