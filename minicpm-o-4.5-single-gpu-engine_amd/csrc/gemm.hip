@@ -197,6 +197,10 @@ bool gemm_splits(const GemmArgs& g) {
 
 hipError_t gemm_bf16(const GemmArgs& g, int epi, hipStream_t st, int cfg) {
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
+  // the tile kernels address both operands by 32-bit byte offsets (taps mode: frame rows up to M + 65536)
+  const size_t es = g.w_scale ? 1 : 2;
+  if ((size_t)(g.M + 65536) * g.lda * es >= ((size_t)1 << 32) || (size_t)g.N * g.ldb * es >= ((size_t)1 << 32))
+    return hipErrorInvalidValue;
   if (cfg < 0 && gemm_small_fits(g, epi)) return gemm_small(g, epi, st);
   // the tile epilogues store bf16 rows 16 bytes per lane
   const bool bf16_out = epi == EPI_BF16 || epi == EPI_GELU_BF16 || epi == EPI_RESID_F16 || epi == EPI_F16;  // 16-bit rows

@@ -319,8 +319,10 @@ struct Tile {
   typedef typename FragT<FP8>::type frag_t;
   typedef typename AccT<MBE>::type acc_t;
 
-  const uint8_t* asrc[APW];
-  const uint8_t* bsrc[BPW];
+  // byte offsets of this lane's load rows from g.A / g.B (32-bit: gemm_bf16 keeps both operands under 4 GB), so the
+  // loads take the operand base from scalar registers
+  uint32_t asrc[APW];
+  uint32_t bsrc[BPW];
   const uint8_t* sbase[NSC];  // fp8: this lane's activation rows' scale rows
   const GemmArgs& g;
   int lane, wave, wm, wn;
@@ -333,19 +335,17 @@ struct Tile {
     wn = wave % WN;
     // this lane's 16 bytes of each of its wave's load blocks: tile row blk * 8 + lane / 8, logical chunk (lane % 8) ^ key
     const int lrow = lane >> 3;
-    const uint8_t* A = (const uint8_t*)g.A;
-    const uint8_t* B = (const uint8_t*)g.B;
 #pragma unroll
     for (int p = 0; p < APW; ++p) {
       const int trow = (wave + p * NW) * 8 + lrow;
       const int m = min(m0 + trow, g.M - 1);  // rows past M load row M - 1; their results are never stored
       const int ch = (lane & 7) ^ swz_key(trow);
-      asrc[p] = A + (size_t)(TAPS ? g.a_src[m] : m) * g.lda * ES + ch * 16;
+      asrc[p] = (uint32_t)(TAPS ? g.a_src[m] : m) * (uint32_t)(g.lda * ES) + ch * 16;
     }
 #pragma unroll
     for (int p = 0; p < BPW; ++p) {
       const int trow = (wave + p * NW) * 8 + lrow;
-      bsrc[p] = B + (size_t)min(n0 + trow, g.N - 1) * g.ldb * ES + ((lane & 7) ^ swz_key(trow)) * 16;
+      bsrc[p] = (uint32_t)min(n0 + trow, g.N - 1) * (uint32_t)(g.ldb * ES) + ((lane & 7) ^ swz_key(trow)) * 16;
     }
     if (FP8) {
 #pragma unroll
@@ -367,12 +367,14 @@ struct Tile {
       srow = tap;
       sblk = (k0 - tap * g.tapC) / 32;
     }
+    const uint8_t* A = (const uint8_t*)g.A;
+    const uint8_t* B = (const uint8_t*)g.B;
 #pragma unroll
     for (int p = 0; p < APW; ++p)
-      __builtin_amdgcn_global_load_lds((const void*)(asrc[p] + aoff), (lds_ptr_t)(la + (wave + p * NW) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(A + (asrc[p] + (uint32_t)aoff)), (lds_ptr_t)(la + (wave + p * NW) * 64), 16, 0, 0);
 #pragma unroll
     for (int p = 0; p < BPW; ++p)
-      __builtin_amdgcn_global_load_lds((const void*)(bsrc[p] + (size_t)k0 * ES), (lds_ptr_t)(lb + (wave + p * NW) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(B + (bsrc[p] + (uint32_t)(k0 * ES))), (lds_ptr_t)(lb + (wave + p * NW) * 64), 16, 0, 0);
     if (FP8) {
 #pragma unroll
       for (int i = 0; i < NSC; ++i) sd[i] = *(const uint32_t*)(sbase[i] + (size_t)srow * g.a_sld + sblk);
