@@ -59,6 +59,18 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// sum over the wave, the same value in every lane, with no LDS round trip: each 16-lane DPP row sums itself
+// (row16_sum), then the four row sums are added in row order from scalar reads of lanes 0, 16, 32 and 48
+__device__ __forceinline__ float wave_sum_rows(float v) {
+  v = row16_sum(v);
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return ((r0 + r1) + r2) + r3;
+}
+
 // Rotary position embedding (RoFormer, consecutive channel pairs): y[0..NV) holds whole pairs of one head, pair e / 2
 // turning by the angle pos * freq[e / 2] (the fp32 product, then an accurate sine and cosine of it)
 template <int NV>

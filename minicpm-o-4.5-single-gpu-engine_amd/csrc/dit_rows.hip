@@ -207,20 +207,21 @@ __device__ __forceinline__ void prefetch_part(const Prefetch& pf, unsigned b) {
   asm volatile("" ::"v"(acc));
 }
 
-// LayerNorm statistics over a row spread across the wave: v -> (v - mean) * rstd
+// LayerNorm statistics over a row spread across the wave: v -> (v - mean) * rstd (the two sums through DPP rows and
+// lane reads: no LDS round trips on the row's latency chain)
 template <int VPL>
 __device__ __forceinline__ void normalize(float (&v)[VPL], int H, float eps) {
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) s += v[i];
-  const float mean = wave_sum(s) / (float)H;
+  const float mean = wave_sum_rows(s) / (float)H;
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     v[i] -= mean;
     q += v[i] * v[i];
   }
-  const float rstd = rsqrtf(wave_sum(q) / (float)H + eps);
+  const float rstd = rsqrtf(wave_sum_rows(q) / (float)H + eps);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) v[i] *= rstd;
 }
@@ -241,11 +242,12 @@ __global__ void __launch_bounds__(256) ln_mod_kernel(f16_t* h, const float* shif
   const int n = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (n >= N) return;
   float v[VPL], sc[VPL], sh[VPL];
+  // the modulation (the same for every row, cache hits) is loaded with the row, not after its statistics
+  row_load_f32<VPL, G>(scale1, lane, sc);
+  row_load_f32<VPL, G>(shift, lane, sh);
   row_load_f16<VPL, G>(h + (size_t)n * H, lane, v);
   if (PEND) pend_resid<VPL, G>(pd, h + (size_t)n * H, n, lane, v);
   normalize<VPL>(v, H, eps);
-  row_load_f32<VPL, G>(scale1, lane, sc);
-  row_load_f32<VPL, G>(shift, lane, sh);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) v[i] = v[i] * sc[i] + sh[i];
   if (q) {
@@ -261,13 +263,27 @@ __global__ void __launch_bounds__(256) ln_mod_kernel(f16_t* h, const float* shif
 // cache frame t - T + 2 when t >= T - 2.  Row programs copy the two cached frames in front of the row's frames and,
 // for rows of fewer than two tokens, produce the new cache from the old one (the reference's _conv_place and
 // _conv_row_cache, engine/runtime/dit_kernels.py:217-248).
+// where token n's frame goes: its row r, position t, the row's length T and cache slot wr (loaded before the token's
+// row, so that this chain of index loads is not on the path after its statistics)
+struct TokPlace {
+  int r, t, T, wr;
+};
+__device__ __forceinline__ TokPlace tok_place(const ConvPlace& cp, int n) {
+  TokPlace p;
+  p.r = cp.tok_row[n];
+  p.t = cp.tok_pos[n];
+  p.T = cp.row_len[p.r];
+  p.wr = cp.wr[p.r];
+  return p;
+}
+
 template <int VPL, int G>
-__device__ __forceinline__ void place_token(const ConvPlace& cp, int n, int H, int lane, const float (&v)[VPL], const uint32_t (&o)[VPL / 2]) {
-  const int r = cp.tok_row[n], t = cp.tok_pos[n], T = cp.row_len[r];
-  const size_t f = (size_t)(n + 2 * r + 2);
+__device__ __forceinline__ void place_token(const ConvPlace& cp, const TokPlace& tp, int n, int H, int lane, const float (&v)[VPL],
+                                            const uint32_t (&o)[VPL / 2]) {
+  const size_t f = (size_t)(n + 2 * tp.r + 2);
   if (cp.P8) row_store_mx8<VPL, G>(v, cp.P8 + f * H, cp.P8s + f * (H / 32), lane);
   else row_store_bf<VPL, G>(cp.P + f * H, lane, o);
-  if (t >= T - 2) row_store_bf<VPL, G>(cp.cache_out_base + (size_t)cp.wr[r] * cp.cache_stride + (size_t)(t - T + 2) * H, lane, o);
+  if (tp.t >= tp.T - 2) row_store_bf<VPL, G>(cp.cache_out_base + (size_t)tp.wr * cp.cache_stride + (size_t)(tp.t - tp.T + 2) * H, lane, o);
 }
 
 // both cached frames are loaded before the first store (the frame buffer and the caches are distinct memory)
@@ -309,16 +325,17 @@ __global__ void __launch_bounds__(256) ln_mod_conv_kernel(f16_t* h, const float*
   const int w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (w < cp.N) {
     float v[VPL], sc[VPL], sh[VPL];
+    const TokPlace tp = tok_place(cp, w);
+    row_load_f32<VPL, G>(scale1, lane, sc);
+    row_load_f32<VPL, G>(shift, lane, sh);
     row_load_f16<VPL, G>(h + (size_t)w * H, lane, v);
     if (PEND) pend_resid<VPL, G>(pd, h + (size_t)w * H, w, lane, v);
     normalize<VPL>(v, H, eps);
-    row_load_f32<VPL, G>(scale1, lane, sc);
-    row_load_f32<VPL, G>(shift, lane, sh);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) v[i] = v[i] * sc[i] + sh[i];
     uint32_t o[VPL / 2];
     pack_bf<VPL>(v, o);
-    place_token<VPL, G>(cp, w, H, lane, v, o);
+    place_token<VPL, G>(cp, tp, w, H, lane, v, o);
   } else if (w < cp.N + cp.R) {
     place_row<VPL, G>(cp, w - cp.N, H, lane);
   }
@@ -336,6 +353,9 @@ __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, cons
   if (w < cp.N) {
     constexpr int G = VPL >= 8 ? 8 : 4;  // the row comes in as bf16
     float v[VPL], a[VPL], b[VPL];
+    const TokPlace tp = tok_place(cp, w);
+    row_load_f32<VPL, G>(lw, lane, a);
+    row_load_f32<VPL, G>(lb, lane, b);
     if (PEND) {  // the pending conv GEMM's value, rounded to bf16 as its own epilogue would
       pend_value<VPL, G>(pd, w, lane, v);
 #pragma unroll
@@ -346,13 +366,11 @@ __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, cons
       words_to_f32<VPL>(wv, v);
     }
     normalize<VPL>(v, H, eps);
-    row_load_f32<VPL, G>(lw, lane, a);
-    row_load_f32<VPL, G>(lb, lane, b);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) v[i] = mish(v[i] * a[i] + b[i]);
     uint32_t o[VPL / 2];
     pack_bf<VPL>(v, o);
-    place_token<VPL, G>(cp, w, H, lane, v, o);
+    place_token<VPL, G>(cp, tp, w, H, lane, v, o);
   } else if (w < cp.N + cp.R) {
     place_row<VPL, VPL >= 8 ? 8 : 4>(cp, w - cp.N, H, lane);
   }
