@@ -208,7 +208,7 @@ __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
       float mx = -__builtin_inff();
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = fmaxf(mx, xor32(mx));
       // m starts at a finite -1e30: keys all invisible so far give exp2(-inf) = 0 and leave m, l and o alone
       const float mn = fmaxf(m, mx);
       const float alpha = __builtin_amdgcn_exp2f((m - mn) * sl2);
@@ -228,7 +228,7 @@ __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
           }
           pf[sub][hh] = make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
         }
-      rs += __shfl_xor(rs, 32, 64);
+      rs += xor32(rs);
       l = l * alpha + rs;
       m = mn;
       if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // the running max moved for some query of the wave
@@ -370,7 +370,7 @@ __device__ __forceinline__ void lds_key_tile(const uint4* Ks, const uint4* Vs, i
   float mx = -__builtin_inff();
 #pragma unroll
   for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = fmaxf(mx, xor32(mx));
   const float mn = fmaxf(m, mx);
   const float alpha = __builtin_amdgcn_exp2f((m - mn) * sl2);
   const float mb = -mn * sl2;
@@ -388,7 +388,7 @@ __device__ __forceinline__ void lds_key_tile(const uint4* Ks, const uint4* Vs, i
       }
       pf[sub][hh] = make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
     }
-  rs += __shfl_xor(rs, 32, 64);
+  rs += xor32(rs);
   l = l * alpha + rs;
   m = mn;
   if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {

@@ -59,6 +59,15 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// x of lane l ^ 32 (the other half of the wave) through v_permlane32_swap, a VALU op (no LDS round trip): the swap of
+// x with itself leaves lanes 32..63 of the first result holding lanes 0..31 and lanes 0..31 of the second holding
+// lanes 32..63
+__device__ __forceinline__ float xor32(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 // sum over the wave, the same value in every lane, with no LDS round trip: each 16-lane DPP row sums itself
 // (row16_sum), then the four row sums are added in row order from scalar reads of lanes 0, 16, 32 and 48
 __device__ __forceinline__ float wave_sum_rows(float v) {
