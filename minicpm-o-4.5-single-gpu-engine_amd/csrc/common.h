@@ -59,6 +59,16 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// sum over an aligned group of 8 lanes, every lane gets it: DPP swaps within quads (lane ^ 1, lane ^ 2), then the
+// half-row mirror pairs the two quads; the same sums as a butterfly over lane ^ 1, ^ 2, ^ 4 (after the first two
+// steps a quad's lanes agree), with no LDS round trip
+__device__ __forceinline__ float sum8(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)); // row_half_mirror
+  return v;
+}
+
 // x of lane l ^ 32 (the other half of the wave) through v_permlane32_swap, a VALU op (no LDS round trip): the swap of
 // x with itself leaves lanes 32..63 of the first result holding lanes 0..31 and lanes 0..31 of the second holding
 // lanes 32..63

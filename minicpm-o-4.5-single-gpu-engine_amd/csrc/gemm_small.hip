@@ -40,6 +40,16 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
   const int kb = z * KT / S, KS = (z + 1) * KT / S - kb;  // this workgroup's K split
   const int nw = blockDim.x >> 6;
   const int s0 = kb + w * KS / nw, s1 = kb + (w + 1) * KS / nw;  // this wave's steps (possibly none)
+  // the epilogue's bias (and gate) of the four columns a thread of the first four waves finishes, loaded before the K
+  // steps so that they are in registers when the block has been summed
+  float4 eb = make_float4(0.f, 0.f, 0.f, 0.f), eg = eb;
+  if (EPI != EPI_PART && tid < 256) {
+    const int en = n0 + (tid >> 6) * 8 + ((tid & 63) >> 5) * 4;
+    if (en + 3 < g.N) {
+      eb = *(const float4*)(g.bias + en);
+      if (EPI == EPI_RESID_F16) eg = *(const float4*)(g.gate + en);
+    }
+  }
   // Load instruction kk of a step covers rows kk * 8 + lane / 8, eight lanes per row (its 64 K values, one 128-byte
   // line): whole lines per instruction run at about 1.4x the CU's rate for 32-byte pieces of 32 rows.  The wave's slab
   // turns them into MFMA fragments (lane (c, h) takes bytes h * 64 + kk * 16 of row c), 16-byte chunks XOR-swizzled by
@@ -129,7 +139,7 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
       *(float4*)(part + (size_t)mo * g.ldc + n) = a;
       return;
     }
-    const float4 b = *(const float4*)(g.bias + n);
+    const float4 b = eb;
     float o[4] = {v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
     const size_t off = (size_t)mo * g.ldc + n;
     if (EPI == EPI_GELU_BF16) {
@@ -143,7 +153,7 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_kernel(GemmArgs g) {
     if (EPI == EPI_BF16 || EPI == EPI_GELU_BF16) {
       *(uint2*)((bf16_t*)g.C + off) = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
     } else if (EPI == EPI_RESID_F16) {
-      const float4 gt = *(const float4*)(g.gate + n);
+      const float4 gt = eg;
       uint2* hp = (uint2*)((f16_t*)g.C + off);
       const uint2 hv = *hp;
       *hp = make_uint2(pack2h(lo2h(hv.x) + gt.x * o[0], hi2h(hv.x) + gt.y * o[1]), pack2h(lo2h(hv.y) + gt.z * o[2], hi2h(hv.y) + gt.w * o[3]));
@@ -261,6 +271,21 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_qkv_kernel(GemmArgs 
   const int n0 = blockIdx.x * 64, m0 = blockIdx.y * 32;
   const int KS = g.K / 64;
   const int s0 = w * KS / GS_WAVES, s1 = (w + 1) * KS / GS_WAVES;  // at most one step
+  // the epilogue's operands (threads of the first eight waves: token row er, columns ec4 .. ec4 + 3 of the head) are
+  // loaded before the K step, so that they are in registers when the block has been summed
+  const QkvOut& o = g.qk;
+  const int er = tid >> 4, ec4 = (tid & 15) * 4;  // 16 consecutive lanes (a DPP row) per token row
+  const int part = n0 / o.H;                       // q, k or v
+  float4 eb = make_float4(0.f, 0.f, 0.f, 0.f), elw = eb, elb = eb;
+  int eslot = 0;
+  if (tid < 512) {
+    eb = *(const float4*)(g.bias + n0 + ec4);
+    if (part < 2) {
+      elw = *(const float4*)((part ? o.kw : o.qw) + ec4);
+      elb = *(const float4*)((part ? o.kb : o.qb) + ec4);
+    }
+    if (part > 0 && m0 + er < g.M) eslot = o.slots[m0 + er];
+  }
   const int lr = lane >> 3, lc = lane & 7;  // whole-line loads and the slab's swizzle, as in gemm_small_kernel
   f32x16 acc[2];
 #pragma unroll
@@ -316,19 +341,18 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_qkv_kernel(GemmArgs 
   }
   __syncthreads();
   if (tid >= 512) return;
-  const QkvOut& o = g.qk;
-  const int r = tid >> 4, c4 = (tid & 15) * 4;  // 16 consecutive lanes (a DPP row) per token row
+  const int r = er, c4 = ec4;
   const float4 a = *(const float4*)&rowm[r][c4];
-  const float4 b = *(const float4*)(g.bias + n0 + c4);
+  const float4 b = eb;
   float y[4] = {bf2f(f2bf(a.x + b.x)), bf2f(f2bf(a.y + b.y)), bf2f(f2bf(a.z + b.z)), bf2f(f2bf(a.w + b.w))};
-  const int part = n0 / o.H, hc = n0 - part * o.H + c4;  // q, k or v; column within the part
+  const int hc = n0 - part * o.H + c4;  // column within the part
   if (part < 2) {
     const float mean = row16_sum(y[0] + y[1] + y[2] + y[3]) * (1.0f / 64.0f);
     float var = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) { y[e] -= mean; var += y[e] * y[e]; }
     const float rstd = rsqrtf(row16_sum(var) * (1.0f / 64.0f) + o.eps);
-    const float4 lw = *(const float4*)((part ? o.kw : o.qw) + c4), lb = *(const float4*)((part ? o.kb : o.qb) + c4);
+    const float4 lw = elw, lb = elb;
     y[0] = y[0] * rstd * lw.x + lb.x;
     y[1] = y[1] * rstd * lw.y + lb.y;
     y[2] = y[2] * rstd * lw.z + lb.z;
@@ -337,7 +361,7 @@ __global__ void __launch_bounds__(64 * GS_WAVES) gemm_small_qkv_kernel(GemmArgs 
   }
   const int mo = m0 + r;
   if (mo >= g.M) return;
-  bf16_t* dst = part == 0 ? o.q_out + (size_t)mo * o.H : (part == 1 ? o.k_pool : o.v_pool) + (size_t)o.slots[mo] * o.H;
+  bf16_t* dst = part == 0 ? o.q_out + (size_t)mo * o.H : (part == 1 ? o.k_pool : o.v_pool) + (size_t)eslot * o.H;
   *(uint2*)(dst + hc) = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
 }
 

@@ -17,9 +17,13 @@ constexpr int BK = 64;  // K values per stage (128 bytes of bf16 per tile row)
 __device__ __forceinline__ int swz_key(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ swz_key(row)); }
 
-// Output columns n .. n + 3 of one lane: bias (and gate) loaded once, before any output row is touched.
-template <int EPI>
+// Output columns n .. n + 3 of one lane: bias (and gate) loaded once, before any output row is touched.  SC: the fp8
+// tiles, whose weights carry per-channel scales; elsewhere the scale is the constant 1 and its multiply folds away --
+// except for fp16 outputs, where acc * scale + bias and the fp16 conversion stay one mixed-precision FMA with a single
+// rounding (a plain fp32 add would round twice)
+template <int EPI, bool SC0>
 struct Cols {
+  static constexpr bool SC = SC0 || EPI == EPI_F16;
   float4 bias, gate, wsc;
   int n;
   bool full;  // all four columns inside N
@@ -30,7 +34,7 @@ struct Cols {
     if (full) {
       bias = *(const float4*)(g.bias + n);
       if (EPI == EPI_RESID_F16) gate = *(const float4*)(g.gate + n);
-      if (g.w_scale) wsc = *(const float4*)(g.w_scale + n);
+      if (SC && g.w_scale) wsc = *(const float4*)(g.w_scale + n);
     }
   }
   // finished output of accumulator values a for full columns (h: the residual row's current values)
@@ -59,7 +63,7 @@ struct Cols {
   __device__ __forceinline__ void put_partial(const GemmArgs& g, int m, float4 a) const {
     const float v[4] = {a.x, a.y, a.z, a.w};
     for (int e = 0; e < 4 && n + e < g.N; ++e) {
-      const float x = v[e] * (g.w_scale ? g.w_scale[n + e] : 1.0f) + g.bias[n + e];
+      const float x = v[e] * (SC && g.w_scale ? g.w_scale[n + e] : 1.0f) + g.bias[n + e];
       const size_t o = (size_t)m * g.ldc + n + e;
       if (EPI == EPI_BF16) ((bf16_t*)g.C)[o] = f2bf(act_apply(x, act));
       else if (EPI == EPI_GELU_BF16) ((bf16_t*)g.C)[o] = f2bf(gelu_tanh(x));
@@ -106,8 +110,9 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
                         WTN % 8 == 0;
   constexpr int CW = WTN / 8, RW = 64 / CW;  // wide: lanes per slab row, slab rows per instruction
   const int cc = WIDE ? (lane % CW) * 2 : lane % CPR;
-  const Cols<EPI> cols(g, nw + cc * 4);
-  const Cols<EPI> cols2(g, nw + cc * 4 + 4);  // wide: the lane's second four columns
+  constexpr bool SC = MBE == 32;  // the fp8 tiles (32 x 32 blocks) are the scaled ones
+  const Cols<EPI, SC> cols(g, nw + cc * 4);
+  const Cols<EPI, SC> cols2(g, nw + cc * 4 + 4);  // wide: the lane's second four columns
   // EPI_QKV: this lane's part (q, k, v), column and head offset, and the LayerNorm affine of its four columns
   int qpart = 0, qcol = 0;
   float4 qlw = make_float4(0.f, 0.f, 0.f, 0.f), qlb = qlw, qlw2 = qlw, qlb2 = qlw;  // wide: 8 columns
@@ -176,16 +181,12 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
           float sm = 0.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) sm += y[e];
-          sm += __shfl_xor(sm, 1, 64);
-          sm += __shfl_xor(sm, 2, 64);
-          sm += __shfl_xor(sm, 4, 64);
+          sm = sum8(sm);
           const float mean = sm * (1.0f / 64.0f);
           float q = 0.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) { y[e] -= mean; q += y[e] * y[e]; }
-          q += __shfl_xor(q, 1, 64);
-          q += __shfl_xor(q, 2, 64);
-          q += __shfl_xor(q, 4, 64);
+          q = sum8(q);
           const float rstd = rsqrtf(q * (1.0f / 64.0f) + o.eps);
           const float lw[8] = {qlw.x, qlw.y, qlw.z, qlw.w, qlw2.x, qlw2.y, qlw2.z, qlw2.w};
           const float lb[8] = {qlb.x, qlb.y, qlb.z, qlb.w, qlb2.x, qlb2.y, qlb2.z, qlb2.w};
