@@ -308,8 +308,8 @@ __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
     float m0 = 0.f, m1 = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) { m0 = fmaxf(m0, fabsf(o0[r])); m1 = fmaxf(m1, fabsf(o1[r])); }
-    m0 = fmaxf(m0, __shfl_xor(m0, 32, 64)) * inv;
-    m1 = fmaxf(m1, __shfl_xor(m1, 32, 64)) * inv;
+    m0 = fmaxf(m0, xor32(m0)) * inv;
+    m1 = fmaxf(m1, xor32(m1)) * inv;
     const int e0 = mx_exp(m0), e1 = mx_exp(m1);
     uint8_t* qp = a.out8 + (size_t)(start + myq) * H + head * 64;
 #pragma unroll
@@ -507,8 +507,8 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4
       float m0 = 0.f, m1 = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) { m0 = fmaxf(m0, fabsf(o0[r])); m1 = fmaxf(m1, fabsf(o1[r])); }
-      m0 = fmaxf(m0, __shfl_xor(m0, 32, 64)) * inv;
-      m1 = fmaxf(m1, __shfl_xor(m1, 32, 64)) * inv;
+      m0 = fmaxf(m0, xor32(m0)) * inv;
+      m1 = fmaxf(m1, xor32(m1)) * inv;
       const int e0 = mx_exp(m0), e1 = mx_exp(m1);
       uint8_t* qp = a.out8 + (size_t)(start + myq) * H + head * 64;
 #pragma unroll

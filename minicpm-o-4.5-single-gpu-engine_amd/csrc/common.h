@@ -69,6 +69,31 @@ __device__ __forceinline__ float sum8(float v) {
   return v;
 }
 
+// the same over aligned groups of 4 lanes (the butterfly's lane ^ 1, ^ 2 steps exactly) and the maximum over groups
+// of 4 or 8 (any pairing gives the same maximum)
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  return v;
+}
+__device__ __forceinline__ float quad_max(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+  return v;
+}
+__device__ __forceinline__ float max8(float v) {
+  v = quad_max(v);
+  return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+}
+// sum over aligned groups of L = 4, 8 or 16 lanes, the butterfly's sums over lane ^ 1 .. ^ (L / 2)
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(L == 4 || L == 8 || L == 16, "DPP groups");
+  if constexpr (L == 4) return quad_sum(v);
+  else if constexpr (L == 8) return sum8(v);
+  else return row16_sum(v);
+}
+
 // x of lane l ^ 32 (the other half of the wave) through v_permlane32_swap, a VALU op (no LDS round trip): the swap of
 // x with itself leaves lanes 32..63 of the first result holding lanes 0..31 and lanes 0..31 of the second holding
 // lanes 32..63

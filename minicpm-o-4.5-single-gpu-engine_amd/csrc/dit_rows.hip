@@ -176,8 +176,7 @@ __device__ __forceinline__ void row_store_mx8(const float (&v)[VPL], uint8_t* qr
     float a = 0.f;
 #pragma unroll
     for (int j = 0; j < G; ++j) a = fmaxf(a, fabsf(x[j]));
-#pragma unroll
-    for (int o = 1; o < 32 / G; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    a = 32 / G == 4 ? quad_max(a) : max8(a);  // the block's 32 / G lanes (DPP, no LDS)
     const int se = mx_exp(a);
     const int c = row_col<G>(k, lane);
     const uint32_t w0 = mx_pack4(x[0], x[1], x[2], x[3], se);
@@ -399,8 +398,7 @@ __global__ void __launch_bounds__(256) qk_norm_kernel(const bf16_t* qkv, const f
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) s += v[i];
-#pragma unroll
-    for (int o = 1; o < LPH; o <<= 1) s += __shfl_xor(s, o, 64);
+    s = group_sum<LPH>(s);
     const float mean = s * (1.0f / 64.0f);
     float q = 0.f;
 #pragma unroll
@@ -408,8 +406,7 @@ __global__ void __launch_bounds__(256) qk_norm_kernel(const bf16_t* qkv, const f
       v[i] -= mean;
       q += v[i] * v[i];
     }
-#pragma unroll
-    for (int o = 1; o < LPH; o <<= 1) q += __shfl_xor(q, o, 64);
+    q = group_sum<LPH>(q);
     const float rstd = rsqrtf(q * (1.0f / 64.0f) + eps);
     const float* w = which ? kw : qw;
     const float* b = which ? kb : qb;

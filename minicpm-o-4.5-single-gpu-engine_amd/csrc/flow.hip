@@ -280,7 +280,7 @@ __global__ void __launch_bounds__(64) flow_rel_attn_kernel(RelAttnArgs a) {
       sv[r] = x;
       mx = fmaxf(mx, x);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(mx, xor32(mx));
     const float mn = fmaxf(m, mx), corr = __builtin_amdgcn_exp2f(m - mn);
     float ls = 0.f;
 #pragma unroll
@@ -288,7 +288,7 @@ __global__ void __launch_bounds__(64) flow_rel_attn_kernel(RelAttnArgs a) {
       sv[r] = __builtin_amdgcn_exp2f(sv[r] - mn);
       ls += sv[r];
     }
-    ls += __shfl_xor(ls, 32, 64);
+    ls += xor32(ls);
     l = l * corr + ls;
     m = mn;
 #pragma unroll

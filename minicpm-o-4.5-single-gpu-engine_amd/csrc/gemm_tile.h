@@ -282,9 +282,7 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
             // the 8 lanes holding this row's 32 consecutive columns share one block scale (N % 32 == 0)
             const float4 o = cols.apply(v[x], h[x]);
             float a = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
-            a = fmaxf(a, __shfl_xor(a, 1, 64));
-            a = fmaxf(a, __shfl_xor(a, 2, 64));
-            a = fmaxf(a, __shfl_xor(a, 4, 64));
+            a = max8(a);
             const int se = mx_exp(a);
             if (m[x] < g.M && cols.full) {
               *(uint32_t*)((uint8_t*)g.C + (size_t)m[x] * g.ldc + cols.n) = mx_pack4(o.x, o.y, o.z, o.w, se);

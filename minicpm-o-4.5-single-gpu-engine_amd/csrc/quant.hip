@@ -23,8 +23,7 @@ __global__ void __launch_bounds__(256) quant_mx8_kernel(const bf16_t* x, int ldx
   float a = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[j]));
-  a = fmaxf(a, __shfl_xor(a, 1, 64));
-  a = fmaxf(a, __shfl_xor(a, 2, 64));
+  a = quad_max(a);  // the block's four lanes (DPP)
   const int se = mx_exp(a);
   *(uint2*)(q + (size_t)m * ldq + k) = make_uint2(mx_pack4(v[0], v[1], v[2], v[3], se), mx_pack4(v[4], v[5], v[6], v[7], se));
   if ((k & 31) == 0) s[(size_t)m * (K / 32) + k / 32] = (uint8_t)(se + 127);
