@@ -567,7 +567,10 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
   const int span = (c.taps - 1) * (c.d_in < 0 ? -c.d_in : c.d_in);
   const int srows = BM + span;
   const int cin_pad = (c.Cin + 63) & ~63;
-  const bf16_t* wph = wbf + ((size_t)ph * ((c.Cout + 63) & ~63) + co0) * c.taps * cin_pad;
+  // this tile's weights in fragment order: 1 KB blocks (32 output channels, one tap, 16 input channels) in the order
+  // (output block, tap, input block), the tile's first block at the row-major offset of its first weight
+  const bf16_t* wph = (const bf16_t*)c.wfr + ((size_t)ph * ((c.Cout + 63) & ~63) + co0) * c.taps * cin_pad;
+  const int nib = cin_pad / 16;
   // wave-uniform count of this wave's 32-row blocks that hold output rows
   const int live = min(TM, max(0, (r_hi - (r0 + wave * WTM)) / 32 + 1));
 
@@ -579,13 +582,14 @@ __global__ void __launch_bounds__(256, 2) conv_bf16_kernel(ConvDesc c, const bf1
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // this lane's weight fragments of tap j: channel rows co0 + jj * 32 + lane % 32, K chunk kk * 2 + lane / 32
+  // this lane's weight fragments of tap j: channel rows co0 + jj * 32 + lane % 32, K chunk kk * 2 + lane / 32 (one
+  // contiguous kilobyte per (kk, jj) for the wave)
   auto load_w = [&](int j, int c0, bf16x8 (&w)[4][2]) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj)
-        w[kk][jj] = as_bf16x8(*(const uint4*)(wph + ((size_t)(jj * 32 + (lane & 31)) * c.taps + j) * cin_pad + c0 + kk * 16 + (lane >> 5) * 8));
+        w[kk][jj] = as_bf16x8(*(const uint4*)(wph + ((size_t)((jj * c.taps + j) * nib + (c0 >> 4) + kk) * 512 + lane * 8)));
   };
   const int sch = tid & 7;  // this thread's 8-channel chunk of the slab rows
   for (int c0 = 0; c0 < c.Cin; c0 += 64) {
@@ -757,8 +761,8 @@ __global__ void __launch_bounds__(256, 2) resblock_pair_kernel(ConvDesc c1, Conv
   const int u0 = t0 - h2 * dil;  // item time of conv1 slab row 0
   const int srows = BM1 + (k - 1) * dil;
   const float* xb = c1.x + (size_t)c1.in_off[b] * C;
-  const bf16_t* w1 = (const bf16_t*)c1.wbf + (size_t)wn * 64 * k * C;
-  const bf16_t* w2 = (const bf16_t*)c2.wbf + (size_t)wn * 64 * k * C;
+  const bf16_t* w1 = (const bf16_t*)c1.wfr + (size_t)wn * 64 * k * C;  // fragment order, this wave's 64 output channels
+  const bf16_t* w2 = (const bf16_t*)c2.wfr + (size_t)wn * 64 * k * C;
   const float* a1 = c1.alpha;
   const float* iv1 = c1.inv;
   const int ws = wm * WTM;  // this wave's first tile row
@@ -777,12 +781,13 @@ __global__ void __launch_bounds__(256, 2) resblock_pair_kernel(ConvDesc c1, Conv
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   // this lane's fragments of tap j, input channels c0 .. c0 + 63: channel rows jj * 32 + lane % 32 of the wave's 64
+  // (one contiguous kilobyte per (kk, jj) for the wave)
   auto load_w = [&](const bf16_t* w, int j, int c0, bf16x8 (&f)[4][2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj)
-        f[kk][jj] = as_bf16x8(*(const uint4*)(w + ((size_t)(jj * 32 + (lane & 31)) * k + j) * C + c0 + kk * 16 + (lane >> 5) * 8));
+        f[kk][jj] = as_bf16x8(*(const uint4*)(w + ((size_t)((jj * k + j) * (C / 16) + (c0 >> 4) + kk)) * 512 + lane * 8));
   };
 
   // conv1 over the BM1 rows, one 64-channel input chunk at a time
@@ -1512,6 +1517,8 @@ hipError_t conv_bf16(const ConvDesc& c, const bf16_t* wbf, int max_rows, hipStre
       dim3 grid(cdiv(max_rows, 32), cdiv(c.Cout, 64), c.n_items * c.n_phase);
       hipLaunchKernelGGL(conv_bf16_split_kernel<2>, grid, dim3(64 * CS_WAVES), 0, st, c, wbf);
     }
+  } else if (!c.wfr) {
+    return hipErrorInvalidValue;  // the slab tiles read the fragment-ordered copy
   } else if (tiles512 >= 256) {
     constexpr int BM = 512;
     const size_t lds = conv_bf16_lds(BM);
@@ -1526,6 +1533,30 @@ hipError_t conv_bf16(const ConvDesc& c, const bf16_t* wbf, int max_rows, hipStre
     dim3 grid(cdiv(max_rows, BM), cdiv(c.Cout, HB_BN), c.n_items * c.n_phase);
     hipLaunchKernelGGL(conv_bf16_kernel<BM>, grid, dim3(256), lds, st, c, wbf);
   }
+  return hipGetLastError();
+}
+
+namespace {
+// one thread per 16-byte unit of the fragment-ordered copy (layout in hift_internal.h)
+__global__ void weight_fragments_kernel(const uint4* __restrict__ w, uint4* __restrict__ f, int taps, int nib, long n16) {
+  const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+  if (i >= n16) return;
+  const int lane = (int)(i & 63);
+  long blk = i >> 6;  // ((row block) * taps + j) * nib + ib
+  const int ib = (int)(blk % nib);
+  blk /= nib;
+  const int j = (int)(blk % taps);
+  const long row = (blk / taps) * 32 + (lane & 31);  // ph * (Cout padded) + output channel
+  f[i] = w[((row * taps + j) * nib * 16 + ib * 16 + (lane >> 5) * 8) >> 3];
+}
+}  // namespace
+
+hipError_t conv_weight_fragments(const uint16_t* wbf, uint16_t* out, int n_phase, int Cout, int taps, int Cin, hipStream_t st) {
+  if (!wbf || !out || n_phase < 1 || Cout < 1 || taps < 1 || Cin < 1) return hipErrorInvalidValue;
+  const long co_pad = (Cout + 63) & ~63, ci_pad = (Cin + 63) & ~63;
+  const long n16 = (long)n_phase * co_pad * taps * ci_pad / 8;
+  hipLaunchKernelGGL(weight_fragments_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, st, (const uint4*)wbf, (uint4*)out, taps,
+                     (int)(ci_pad / 16), n16);
   return hipGetLastError();
 }
 
@@ -1566,7 +1597,7 @@ hipError_t resblock_pair_bf16(const ConvDesc& c1, const ConvDesc& c2, int max_ro
                     c1.off_out[0] == 0 && c2.off_out[0] == 0;
   const bool acts = c1.pre == PRE_SNAKE && c2.pre == PRE_SNAKE && c1.epi == EPI_STORE && c2.res == c1.x &&
                     (c2.epi == EPI_RES || c2.epi == EPI_ADD_RES || c2.epi == EPI_RES_MEAN);
-  if (!same || !geom || !acts || !resblock_pair_fits(C, k, c1.d_in) || !c1.wbf || !c2.wbf) return hipErrorInvalidValue;
+  if (!same || !geom || !acts || !resblock_pair_fits(C, k, c1.d_in) || !c1.wfr || !c2.wfr) return hipErrorInvalidValue;
   if (c2.y == c1.x || (c2.epi == EPI_RES_MEAN && c2.sum == c1.x)) return hipErrorInvalidValue;  // halo rows of x are read by other workgroups
   if (C == 64) return launch_pair<64>(c1, c2, max_rows, st);
   if (C == 128) return launch_pair<128>(c1, c2, max_rows, st);

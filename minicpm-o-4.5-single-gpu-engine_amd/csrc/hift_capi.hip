@@ -37,6 +37,13 @@ struct t2w_hift {
   t2w_hift_dims d;
   t2w_hift_weights w;
   int chans[4];
+  // each bf16 conv's weights in MFMA fragment order (made by t2w_hift_create, freed by t2w_hift_destroy), by wbf
+  std::vector<std::pair<const void*, uint16_t*>> frag;
+  const uint16_t* frag_of(const void* wbf) const {
+    for (const auto& f : frag)
+      if (f.first == wbf) return f.second;
+    return nullptr;
+  }
 };
 
 namespace {
@@ -116,7 +123,7 @@ ConvDesc conv_desc(const Ctx& x, const t2w_conv& w, const float* in, int Cin, in
   ConvDesc c{};
   c.x = in; c.ldx = Cin; c.in_off = x.off(in_cls); c.in_len = x.len(in_cls);
   c.y = out; c.ldy = Cout; c.out_off = x.off(out_cls); c.out_len = x.len(out_cls);
-  c.w = w.w; c.wbf = (const uint16_t*)w.wbf; c.bias = w.b; c.Cin = Cin; c.Cout = Cout; c.taps = k;
+  c.w = w.w; c.wbf = (const uint16_t*)w.wbf; c.wfr = x.h->frag_of(w.wbf); c.bias = w.b; c.Cin = Cin; c.Cout = Cout; c.taps = k;
   c.s_in = s; c.d_in = dil; c.s_out = 1; c.n_phase = 1; c.off_in[0] = -p; c.off_out[0] = 0;
   c.pre = PRE_NONE; c.epi = EPI_STORE; c.n_items = x.n;
   return c;
@@ -213,11 +220,47 @@ int t2w_hift_create(const t2w_hift_dims* dims, const t2w_hift_weights* w, t2w_hi
   h->w = *w;
   h->chans[0] = d.base;
   for (int i = 0; i < 3; ++i) h->chans[i + 1] = d.base >> (i + 1);
+  // fragment-ordered copies of the bf16 weights, one per distinct wbf, in the shapes the forward gives each conv
+  auto add = [&](const t2w_conv& cv, int n_phase, int Cout, int taps, int Cin) -> hipError_t {
+    if (!cv.wbf || h->frag_of(cv.wbf)) return hipSuccess;
+    uint16_t* p = nullptr;
+    const size_t bytes = (size_t)n_phase * ((Cout + 63) & ~63) * taps * ((Cin + 63) & ~63) * sizeof(uint16_t);
+    hipError_t e = hipMalloc((void**)&p, bytes);
+    if (e != hipSuccess) return e;
+    h->frag.push_back({cv.wbf, p});
+    return conv_weight_fragments((const uint16_t*)cv.wbf, p, n_phase, Cout, taps, Cin, nullptr);
+  };
+  const int nsrc = d.n_fft + 2;
+  hipError_t e = add(w->conv_pre, 1, d.base, 7, d.mel);
+  for (int i = 0; i < 3 && e == hipSuccess; ++i) {
+    const int u = d.up_rates[i], cout = h->chans[i + 1];
+    e = add(w->ups[i], u, cout, (d.up_kernels[i] + u - 1) / u, h->chans[i]);
+    const int r = i == 0 ? d.up_rates[2] * d.up_rates[1] : (i == 1 ? d.up_rates[2] : 1);
+    if (e == hipSuccess) e = add(w->src_down[i], 1, cout, r == 1 ? 1 : 2 * r, nsrc);
+    for (int j = 0; j < 3 && e == hipSuccess; ++j) {
+      e = add(w->src_res[i].c1[j], 1, cout, d.src_kernels[i], cout);
+      if (e == hipSuccess) e = add(w->src_res[i].c2[j], 1, cout, d.src_kernels[i], cout);
+      for (int q = 0; q < 3 && e == hipSuccess; ++q) {
+        e = add(w->res[i * 3 + q].c1[j], 1, cout, d.res_kernels[q], cout);
+        if (e == hipSuccess) e = add(w->res[i * 3 + q].c2[j], 1, cout, d.res_kernels[q], cout);
+      }
+    }
+  }
+  if (e == hipSuccess) e = add(w->conv_post, 1, nsrc, 7, h->chans[3]);
+  if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+  if (e != hipSuccess) {
+    t2w_hift_destroy(h);
+    return t2w::set_error("hift_create: bf16 weight copies", e);
+  }
   *out = h;
   return 0;
 }
 
-void t2w_hift_destroy(t2w_hift* h) { delete h; }
+void t2w_hift_destroy(t2w_hift* h) {
+  if (!h) return;
+  for (auto& f : h->frag) (void)hipFree(f.second);
+  delete h;
+}
 
 int t2w_hift_plan_ints(int n_items) { return 2 * N_CLS * n_items; }
 
@@ -323,7 +366,7 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
       c.y = B.XN; c.ldy = cout;
       c.out_off = x.off(i == 2 ? C_S2P : cls);
       c.out_len = x.len(i == 2 ? C_S2P : cls);
-      c.w = w.ups[i].w; c.wbf = (const uint16_t*)w.ups[i].wbf; c.bias = w.ups[i].b; c.Cin = cin; c.Cout = cout; c.taps = (k + u - 1) / u;
+      c.w = w.ups[i].w; c.wbf = (const uint16_t*)w.ups[i].wbf; c.wfr = h->frag_of(w.ups[i].wbf); c.bias = w.ups[i].b; c.Cin = cin; c.Cout = cout; c.taps = (k + u - 1) / u;
       c.s_in = 1; c.d_in = -1; c.s_out = u; c.n_phase = u;
       for (int ph = 0; ph < u; ++ph) { c.off_in[ph] = 0; c.off_out[ph] = ph - p; }
       c.pre = PRE_LEAKY; c.slope = d.lrelu_slope; c.epi = EPI_STORE; c.n_items = n;

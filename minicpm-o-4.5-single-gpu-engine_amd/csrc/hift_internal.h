@@ -18,6 +18,7 @@ struct ConvDesc {
   const int* out_off; const int* out_len;
   const float* w; const float* bias;  // w [n_phase, Cout, taps, Cin]
   const uint16_t* wbf;                // bf16 weights for conv_bf16 (or null)
+  const uint16_t* wfr;                // the same weights in MFMA fragment order (conv_weight_fragments); the tile kernels read these
   int Cin, Cout, taps;
   int s_in, d_in, s_out;
   int n_phase;
@@ -28,8 +29,13 @@ struct ConvDesc {
 };
 
 hipError_t conv_f32(const ConvDesc& c, int max_rows, hipStream_t st);
-// stride-1 / polyphase convs on bf16 MFMA; wbf: bf16 weights [n_phase, Cout padded to 64, taps, Cin padded to 64]
+// stride-1 / polyphase convs on bf16 MFMA; wbf: bf16 weights [n_phase, Cout padded to 64, taps, Cin padded to 64], and
+// c.wfr the same weights in fragment order (the slab-tile kernels need it)
 hipError_t conv_bf16(const ConvDesc& c, const uint16_t* wbf, int max_rows, hipStream_t st);
+// wbf [n_phase, Cout padded to 64, taps, Cin padded to 64] -> out (same size) in MFMA fragment order: for phase ph, output
+// block cb of 32 channels, tap j and input block ib of 16 channels, one 1 KB block whose lane l holds the 8 weights of
+// output channel cb * 32 + l % 32, input channels ib * 16 + (l / 32) * 8 .. + 7 (the A operand of a 32x32x16 MFMA)
+hipError_t conv_weight_fragments(const uint16_t* wbf, uint16_t* out, int n_phase, int Cout, int taps, int Cin, hipStream_t st);
 // One ResBlock dilation (conv c1 with Snake, conv c2 with Snake and the residual c1.x) in one kernel on bf16 MFMA,
 // conv1's output kept in LDS.  c2 writes y (EPI_RES / EPI_ADD_RES) or the running mean (EPI_RES_MEAN); y must not be x.
 bool resblock_pair_fits(int C, int k, int dil);
