@@ -221,7 +221,7 @@ def _timed(launch, reps: int = 20, warm: int = 3) -> float:
 
 
 def resid_gemm_roofline(cfg, n: int, T: int, calibrate: bool = False) -> dict:
-    """The dominant kernel of the DiT solve by total time: the gated fp16-residual GEMM instantiation (256 x 256
+    """The dominant kernel of the DiT solve by total time: the gated fp16-residual GEMM instantiation (208 x 256
     tiles, dense A) that runs the attention output projection (K = H) and fc2 (K = F) of every block.  Its launches
     are timed as the solve issues them, proj and fc2 alternating at the workload's 2 n T tokens, 20 launches with HIP
     events on their own stream; achieved = the mean algorithmic FLOPs per launch / the mean launch time.  calibrate:
@@ -256,7 +256,7 @@ def resid_gemm_roofline(cfg, n: int, T: int, calibrate: bool = False) -> dict:
     ms = _timed(launch, reps=20, warm=4)
     flops = 2.0 * N * H * (H + F) / 2
     ach = flops / (ms * 1e-3) / 1e12
-    return {"bound": "mfma", "kernel": "gemm_kernel<256,256,4,2,EPI_RESID_F16,dense> (DiT proj and fc2, alternating)",
+    return {"bound": "mfma", "kernel": "gemm_kernel<208,256,2,4,EPI_RESID_F16,dense> (DiT proj and fc2, alternating)",
             "achieved": ach, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": ach / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
             "launch_ms": ms, "flops_per_launch": flops}
 

@@ -259,7 +259,7 @@ int t2w_flow_speaker(const t2w_flow* m, const float* spk, float* out, int R, voi
 int t2w_gemm_bf16(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                   void* C, int ldc, int M, int N, int K, int epi, void* stream);
 /* t2w_gemm_bf16 with an explicit tile configuration (-1: chosen by shape; 0: 128x128 of 4 waves, 1: 256x256 of
- * 8 waves, 2: 256x128 of 8 waves) for tile sweeps.
+ * 8 waves, 2: 256x128 of 8 waves, 3: 208x256 of 8 waves) for tile sweeps.
  * K % 64 == 0, lda % 8 == 0 (taps mode: lda % 64 == 0). */
 int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, const float* bias, const float* gate,
                        void* C, int ldc, int M, int N, int K, int epi, int tile, void* stream);

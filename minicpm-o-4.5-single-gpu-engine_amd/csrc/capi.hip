@@ -578,7 +578,7 @@ int t2w_gemm_bf16_tile(const void* A, int lda, const int* a_src, const void* W, 
   if (lda % 8) return fail("lda must be a multiple of 8 (16-byte rows)");
   if (epi < 0 || (epi > 3 && epi != EPI_F16)) return fail("bad epilogue");
   if (a_src && (K % lda || lda % 64)) return fail("taps mode: K must be a multiple of lda, lda of 64");
-  if (tile > 2) return fail("bad tile configuration");
+  if (tile > 3) return fail("bad tile configuration");
   T2W_CHECK(gemm_bf16(gemm_args(A, lda, a_src, W, bias, gate, C, ldc, M, N, K), epi, (hipStream_t)stream, tile), "gemm");
   return 0;
 }

@@ -37,26 +37,9 @@ int pick_cfg(const GemmArgs& g);
 
 namespace {
 
-template <int BM, int BN, int WM, int WN, int EPI, bool TAPS, bool FP8>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
-  using T = Tile<BM, BN, WM, WN, TAPS, FP8>;
-  __shared__ uint4 sA0[BM * 8], sA1[BM * 8], sB0[BN * 8], sB1[BN * 8];
-
-  // XCD-aware order: consecutive workgroups go to different XCDs, so the tiles of one XCD are a contiguous run (they
-  // share A rows and W columns in that XCD's L2)
-  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
-  const int nblk = gm * gn, full = (nblk / 8) * 8;
-  int b = blockIdx.x;
-  if (b < full) b = (b % 8) * (nblk / 8) + b / 8;
-  // wide grids (more than 8 column tiles, e.g. qkv) walk groups of 4 row tiles column by column, so that the tiles
-  // one XCD runs at a time share 4 A row blocks and 8 W column blocks instead of all W columns of one row block
-  int mb = b / gn, nb = b % gn;
-  if (gn > 8) {
-    const int grp = b / (4 * gn), rows = min(4, gm - grp * 4), r = b - grp * 4 * gn;
-    mb = grp * 4 + r % rows;
-    nb = r / rows;
-  }
-  const int m0 = mb * BM, n0 = nb * BN;
+// The K loop and epilogue of one tile for the waves of tile type T (stage buffers named at compile time once inlined).
+template <typename T, int EPI, int BM, int BN>
+__device__ __forceinline__ void tile_body(const GemmArgs& g, uint4* sA0, uint4* sA1, uint4* sB0, uint4* sB1, int m0, int n0) {
   T t(g, m0, n0);
 
   typename T::acc_t acc[T::TM][T::TN];
@@ -96,11 +79,46 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   t.template store<EPI>(acc, st, m0, n0);
 }
 
+template <int BM, int BN, int WM, int WN, int EPI, bool TAPS, bool FP8>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
+  __shared__ uint4 sA0[BM * 8], sA1[BM * 8], sB0[BN * 8], sB1[BN * 8];
+
+  // XCD-aware order: consecutive workgroups go to different XCDs, so the tiles of one XCD are a contiguous run (they
+  // share A rows and W columns in that XCD's L2)
+  const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
+  const int nblk = gm * gn, full = (nblk / 8) * 8;
+  int b = blockIdx.x;
+  if (b < full) b = (b % 8) * (nblk / 8) + b / 8;
+  // wide grids (more than 8 column tiles, e.g. qkv) walk groups of 4 row tiles column by column, so that the tiles
+  // one XCD runs at a time share 4 A row blocks and 8 W column blocks instead of all W columns of one row block
+  int mb = b / gn, nb = b % gn;
+  if (gn > 8) {
+    const int grp = b / (4 * gn), rows = min(4, gm - grp * 4), r = b - grp * 4 * gn;
+    mb = grp * 4 + r % rows;
+    nb = r / rows;
+  }
+  const int m0 = mb * BM, n0 = nb * BN;
+  if constexpr (BM == 208) {
+    // 13 row blocks of 16: the first wave row owns 7 (rows 0..111), the second 6 (rows 112..207); waves w and w + 4
+    // share a SIMD, so every SIMD runs 13 row blocks x 4 column blocks.  Both wave types pass the same barriers.
+    static_assert(WM == 2 && WN == 4 && BN == 256 && !FP8, "208-row tiles: 2 x 4 waves, bf16");
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < WN)
+      tile_body<Tile<BM, BN, WM, WN, TAPS, FP8, 7, 0>, EPI, BM, BN>(g, sA0, sA1, sB0, sB1, m0, n0);
+    else
+      tile_body<Tile<BM, BN, WM, WN, TAPS, FP8, 6, 112>, EPI, BM, BN>(g, sA0, sA1, sB0, sB1, m0, n0);
+  } else {
+    tile_body<Tile<BM, BN, WM, WN, TAPS, FP8>, EPI, BM, BN>(g, sA0, sA1, sB0, sB1, m0, n0);
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int EPI, bool TAPS>
 hipError_t launch_tile(const GemmArgs& g, hipStream_t st) {
   const int gm = (g.M + BM - 1) / BM, gn = (g.N + BN - 1) / BN;
   if (g.w_scale) {
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, TAPS, true>), dim3(gm * gn), dim3(64 * WM * WN), 0, st, g);
+    if constexpr (BM == 208)
+      return hipErrorInvalidValue;  // bf16 only
+    else
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, TAPS, true>), dim3(gm * gn), dim3(64 * WM * WN), 0, st, g);
   } else {
     if constexpr (EPI == EPI_GELU_MX8)
       return hipErrorInvalidValue;  // fp8 output only follows fp8 GEMMs
@@ -140,13 +158,14 @@ GemmArgs rows_from(const GemmArgs& g, int r) {
   return h;
 }
 
-// tile configurations: 0 = 128x128 (4 waves of 64x64), 1 = 256x256 (8 waves of 64x128), 2 = 256x128 (8 waves of 64x64)
+// tile configurations: 0 = 128x128 (4 waves of 64x64), 1 = 256x256 (8 waves of 64x128), 2 = 256x128 (8 waves of 64x64),
+// 3 = 208x256 (bf16; 8 waves of 112x64 and 96x64)
 template <int EPI, bool TAPS>
 hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
   const bool by_shape = cfg < 0;
   if (cfg < 0) cfg = pick_cfg(g);
-  // A 256x256 grid whose last round would leave most of the 256 CUs idle (qkv at 12,800 tokens: 600 tiles = two
-  // rounds + 88) runs the rows of its full rounds on 256x256 tiles and the rest on 256x128 tiles, one round of
+  // A 256x256 grid whose last round would leave most of the 256 CUs idle (the fp8 qkv at 12,800 tokens: 600 tiles =
+  // two rounds + 88) runs the rows of its full rounds on 256x256 tiles and the rest on 256x128 tiles, one round of
   // half-size tiles instead of a third round of mostly idle CUs.  The products are the same per output element.
   if (by_shape && cfg == 1) {
     const long gn = (g.N + 255) / 256, tiles = (long)((g.M + 255) / 256) * gn;
@@ -165,6 +184,7 @@ hipError_t launch_epi(const GemmArgs& g, int cfg, hipStream_t st) {
     case 0: return launch_tile<128, 128, 2, 2, EPI, TAPS>(g, st);
     case 1: return launch_tile<256, 256, 4, 2, EPI, TAPS>(g, st);
     case 2: return launch_tile<256, 128, 4, 2, EPI, TAPS>(g, st);
+    case 3: return launch_tile<208, 256, 2, 4, EPI, TAPS>(g, st);
   }
   return hipErrorInvalidValue;
 }
@@ -183,14 +203,20 @@ int pick_cfg(const GemmArgs& g) {
   // rows: 33.2 vs 37.3 us, where the 256x256 grid is 78% full)
   const long t1 = (long)((g.M + 255) / 256) * ((g.N + 255) / 256), t0 = (long)((g.M + 127) / 128) * ((g.N + 127) / 128);
   const long r1 = (t1 + 255) / 256, r0 = (t0 + 255) / 256;
-  if (10 * t1 >= 7 * 256 * r1) return 1;
-  return 75 * r0 + 70 < 270 * r1 ? 0 : 1;
+  if (10 * t1 < 7 * 256 * r1 && 75 * r0 + 70 < 270 * r1) return 0;
+  // 256x256 wins over 128x128.  The 208x256 tile holds 13/16 of the rows (and MFMA work per SIMD) of a 256x256 one:
+  // where its grid needs no more rounds of 256 CUs, every round is shorter.  Measured at 12,800 tokens (us per launch,
+  // 256x256 -> 208x256): N = 1024, K = 1024 37.2 -> 35.2 (248 tiles in one round instead of 200 on 200 CUs); taps
+  // K = 3072 77.7 -> 72.1; N = 2048 63.8 -> 59.0; N = 3072 89.4 -> 84.5 (three rounds either way; the split into
+  // 256x256 and 256x128 tiles in launch_epi: 87.0).  bf16 only (fp8 blocks are 32 rows).
+  const long t3 = (long)((g.M + 207) / 208) * ((g.N + 255) / 256), r3 = (t3 + 255) / 256;
+  return !g.w_scale && r3 <= r1 ? 3 : 1;
 }
 
 bool gemm_splits(const GemmArgs& g) {
   if (!g.ws || g.w_scale || g.M <= 0) return false;
   // a grid of fewer than 128 tiles leaves most of the 256 CUs idle: split K instead
-  const int c = pick_cfg(g), bm = c == 0 ? 128 : 256, bn = c == 1 ? 256 : 128;
+  const int c = pick_cfg(g), bm = c == 0 ? 128 : (c == 3 ? 208 : 256), bn = c == 1 || c == 3 ? 256 : 128;
   const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
   return tiles < 128 && splitk_plan(g.M, g.N, g.K, g.ws_bytes).splits > 1;
 }

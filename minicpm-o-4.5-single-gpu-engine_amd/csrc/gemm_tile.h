@@ -129,7 +129,8 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
     }
   }
 #pragma unroll
-  for (int i = 0; i < WTM / 32; ++i) {  // one 32-row slab at a time
+  for (int i = 0; i < (WTM + 31) / 32; ++i) {  // one 32-row slab at a time (bf16: the last may hold 16 rows)
+    const int nrow = (i + 1) * 32 <= WTM ? 32 : 16;  // rows of this slab (a constant once unrolled)
     if constexpr (MBE == 32) {
       const int r = lane & 31;
 #pragma unroll
@@ -143,6 +144,7 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
     } else {
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
+        if (2 * i + a >= TM) break;
         const int r = a * 16 + (lane & 15);
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
@@ -162,6 +164,7 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
       int slot[NB];
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
+        if (b * RW >= nrow) break;
         const int row = b * RW + lane / CW;
         const int m = mw + i * 32 + row;
         a0[b] = st[row * CPR + (cc ^ (row & (CPR - 1)))];
@@ -170,6 +173,7 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
+        if (b * RW >= nrow) break;
         const int m = mw + i * 32 + b * RW + lane / CW;
         float y[8] = {a0[b].x * cols.wsc.x + cols.bias.x, a0[b].y * cols.wsc.y + cols.bias.y,
                       a0[b].z * cols.wsc.z + cols.bias.z, a0[b].w * cols.wsc.w + cols.bias.w,
@@ -204,6 +208,7 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
       if constexpr (EPI == EPI_RESID_F16) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
+          if (b * RW >= nrow) break;
           const int m = mw + i * 32 + b * RW + lane / CW;
           hv[b] = make_uint4(0u, 0u, 0u, 0u);
           if (m < g.M && cols2.full) hv[b] = *(const uint4*)((const f16_t*)g.C + (size_t)m * g.ldc + cols.n);
@@ -211,6 +216,7 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
+        if (b * RW >= nrow) break;
         const int row = b * RW + lane / CW;
         const int m = mw + i * 32 + row;
         const float4 v0 = st[row * CPR + (cc ^ (row & (CPR - 1)))];
@@ -239,10 +245,12 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
     } else {
 #pragma unroll
       for (int b = 0; b < NRB; b += RB) {
+        if (b * RPI >= nrow) break;
         float4 v[RB], h[RB];
         int m[RB], slot[RB];
 #pragma unroll
         for (int x = 0; x < RB; ++x) {
+          if ((b + x) * RPI >= nrow) break;
           const int row = (b + x) * RPI + lane / CPR;
           m[x] = mw + i * 32 + row;
           v[x] = st[row * CPR + (cc ^ (row & (CPR - 1)))];
@@ -256,6 +264,7 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
         }
 #pragma unroll
         for (int x = 0; x < RB; ++x) {
+          if ((b + x) * RPI >= nrow) break;
           if constexpr (EPI == EPI_QKV) {
             // the 16 lanes (one DPP row) holding this row's 64 columns of one head: heads are 64-aligned in the tile
             const QkvOut& o = g.qk;
@@ -300,21 +309,26 @@ __device__ __forceinline__ void tile_store(const GemmArgs& g, const AccT (&acc)[
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool TAPS, bool FP8>
+// TMX > 0: an uneven row split (bf16 only): this wave type owns TMX 16-row blocks from tile row ROW0 (the kernel
+// instantiates one Tile per wave row and picks by wave), e.g. a 208-row tile as 112 + 96 rows
+template <int BM, int BN, int WM, int WN, bool TAPS, bool FP8, int TMX = 0, int ROW0 = 0>
 struct Tile {
   static constexpr int NW = WM * WN;
-  static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave sub-tile
   // bf16 runs v_mfma_f32_16x16x32_bf16 blocks (same bytes per FLOP as 32x32x16, measured ~10% faster next to the
   // stage's global->LDS traffic), fp8 the scaled 32x32x64 blocks
   static constexpr int MBE = FP8 ? 32 : 16;           // MFMA block edge
+  static constexpr int WTM = TMX ? TMX * MBE : BM / WM, WTN = BN / WN;  // wave sub-tile
   static constexpr int TM = WTM / MBE, TN = WTN / MBE;  // MFMA blocks per wave
-  static constexpr int APW = BM / 8 / NW, BPW = BN / 8 / NW;  // 1 KB (8-row) load blocks per wave and stage
+  // 1 KB (8-row) load blocks per stage, and per wave (the last A round may cover only the first waves)
+  static constexpr int NAB = BM / 8, APW = (NAB + NW - 1) / NW, BPW = BN / 8 / NW;
+  static constexpr bool AREM = NAB % NW != 0;
   static constexpr int ES = FP8 ? 1 : 2;              // bytes per element
   static constexpr int BKE = BK * 2 / ES;             // K values per 128-byte stage row
   static constexpr int NKK = 2;                       // MFMA K steps per stage (32 bf16 or 64 fp8 values each)
   static constexpr int NSC = FP8 ? TM : 1;            // scale dwords per lane and stage
-  static_assert(APW * NW * 8 == BM && BPW * NW * 8 == BN, "tile rows / waves mismatch");
-  static_assert(WTM % 32 == 0, "the epilogue works in 32-row slabs");
+  static_assert(NAB * 8 == BM && BPW * NW * 8 == BN, "tile rows / waves mismatch");
+  static_assert(WTM % 32 == 0 || (!FP8 && WTM % 16 == 0), "the epilogue works in 32-row slabs (bf16: a last 16-row one)");
+  static_assert(TMX == 0 || !FP8, "uneven row splits are bf16 only");
   typedef typename FragT<FP8>::type frag_t;
   typedef typename AccT<MBE>::type acc_t;
 
@@ -325,6 +339,7 @@ struct Tile {
   const uint8_t* sbase[NSC];  // fp8: this lane's activation rows' scale rows
   const GemmArgs& g;
   int lane, wave, wm, wn;
+  int mrow;  // this wave's first tile row
 
   __device__ __forceinline__ Tile(const GemmArgs& g_, int m0, int n0) : g(g_) {
     const int tid = threadIdx.x;
@@ -332,6 +347,7 @@ struct Tile {
     wave = tid >> 6;
     wm = wave / WN;
     wn = wave % WN;
+    mrow = TMX ? ROW0 : wm * WTM;
     // this lane's 16 bytes of each of its wave's load blocks: tile row blk * 8 + lane / 8, logical chunk (lane % 8) ^ key
     const int lrow = lane >> 3;
 #pragma unroll
@@ -349,7 +365,7 @@ struct Tile {
     if (FP8) {
 #pragma unroll
       for (int i = 0; i < NSC; ++i) {
-        const int m = min(m0 + wm * WTM + i * 32 + (lane & 31), g.M - 1);
+        const int m = min(m0 + mrow + i * 32 + (lane & 31), g.M - 1);
         sbase[i] = g.a_scale + (size_t)(TAPS ? g.a_src[m] : m) * g.a_sld;
       }
     }
@@ -368,8 +384,11 @@ struct Tile {
     }
     const uint8_t* A = (const uint8_t*)g.A;
     const uint8_t* B = (const uint8_t*)g.B;
+    constexpr int APF = AREM ? APW - 1 : APW;  // A rounds every wave loads
+    if (AREM && wave + APF * NW < NAB)  // first, so the unconditional loads stay in the block of the MFMAs they interleave with
+      __builtin_amdgcn_global_load_lds((const void*)(A + (asrc[APF] + (uint32_t)aoff)), (lds_ptr_t)(la + (wave + APF * NW) * 64), 16, 0, 0);
 #pragma unroll
-    for (int p = 0; p < APW; ++p)
+    for (int p = 0; p < APF; ++p)
       __builtin_amdgcn_global_load_lds((const void*)(A + (asrc[p] + (uint32_t)aoff)), (lds_ptr_t)(la + (wave + p * NW) * 64), 16, 0, 0);
 #pragma unroll
     for (int p = 0; p < BPW; ++p)
@@ -385,7 +404,7 @@ struct Tile {
       const int c0 = kk * 4 + (lane >> 5);  // 16-byte pieces of the two 32-value blocks of this K step
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const int r = wm * WTM + i * 32 + (lane & 31);
+        const int r = mrow + i * 32 + (lane & 31);
         af[i] = join8(La[swz(r, c0)], La[swz(r, c0 + 2)]);
       }
 #pragma unroll
@@ -397,7 +416,7 @@ struct Tile {
       // 16 x 32 operand blocks: lane l holds row l % 16, K values [8 (l / 16), +8) of the step
       const int chunk = kk * 4 + (lane >> 4);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(La[swz(wm * WTM + i * 16 + (lane & 15), chunk)]);
+      for (int i = 0; i < TM; ++i) af[i] = as_bf16x8(La[swz(mrow + i * 16 + (lane & 15), chunk)]);
 #pragma unroll
       for (int j = 0; j < TN; ++j) bf[j] = as_bf16x8(Lb[swz(wn * WTN + j * 16 + (lane & 15), chunk)]);
     }
@@ -431,15 +450,36 @@ struct Tile {
 #pragma unroll
       for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], ac[i], acc[i][j], 0, 0, 0);
       bf[j] = as_bf16x8(Lb[swz(wn * WTN + j * 16 + (lane & 15), chunk)]);
-      if (j < TM) an[j] = as_bf16x8(La[swz(wm * WTM + j * 16 + (lane & 15), chunk)]);
+      if (j < TM) an[j] = as_bf16x8(La[swz(mrow + j * 16 + (lane & 15), chunk)]);
     }
-    constexpr int NV = APW + BPW, VPC = (NV + TN - 1) / TN;
+    constexpr int NV = APW - (AREM ? 1 : 0) + BPW, VPC = (NV + TN - 1) / TN;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
       if (V && j * VPC < NV) __builtin_amdgcn_sched_group_barrier(0x020, VPC, 0);
       if (j < TM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  }
+
+  // The same with rows outermost, for wave tiles taller than wide (TM > TN): right after the MFMAs of row i, A fragment
+  // i (and, for i < TN, B fragment i into bn) of step kn is read, so one register set holds A across steps.
+  template <bool V>
+  __device__ __forceinline__ void step16r(acc_t (&acc)[TM][TN], const frag_t (&bc)[TN], frag_t (&bn)[TN], frag_t (&af)[TM],
+                                          const uint4* La, const uint4* Lb, int kn) const {
+    const int chunk = kn * 4 + (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bc[j], af[i], acc[i][j], 0, 0, 0);
+      af[i] = as_bf16x8(La[swz(mrow + i * 16 + (lane & 15), chunk)]);
+      if (i < TN) bn[i] = as_bf16x8(Lb[swz(wn * WTN + i * 16 + (lane & 15), chunk)]);
+    }
+    constexpr int NV = APW - (AREM ? 1 : 0) + BPW, VPR = (NV + TM - 1) / TM;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, TN, 0);
+      if (V && i * VPR < NV) __builtin_amdgcn_sched_group_barrier(0x020, VPR, 0);
     }
   }
 
@@ -464,7 +504,7 @@ struct Tile {
         bf[j] = join8(Lb[swz(r, c0)], Lb[swz(r, c0 + 2)]);
       }
       if (j < TM) {
-        const int r = wm * WTM + j * 32 + (lane & 31);
+        const int r = mrow + j * 32 + (lane & 31);
         an[j] = join8(La[swz(r, c0)], La[swz(r, c0 + 2)]);
       }
     }
@@ -482,7 +522,17 @@ struct Tile {
   // barrier the loads of stage kt + 2 go into (La, Lb, sd).
   __device__ __forceinline__ void stage(acc_t (&acc)[TM][TN], frag_t (&af)[2][TM], frag_t (&bf)[2][TN], uint4* La,
                                         uint4* Lb, uint32_t (&sd)[NSC], const uint4* Na, const uint4* Nb, int kt, int KT) const {
-    if constexpr (MBE == 16) {
+    if constexpr (MBE == 16 && TM > TN) {
+      // rows outermost: B double buffered, A single
+      static_assert(NKK == 2, "step16r interleave");
+      step16r<false>(acc, bf[0], bf[1], af[0], La, Lb, 1);
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      __syncthreads();
+      issue(La, Lb, sd, min(kt + 2, KT - 1));
+      step16r<true>(acc, bf[1], bf[0], af[0], Na, Nb, 0);
+      return;
+    }
+    if constexpr (MBE == 16 && TM <= TN) {
       // bf16: step 0 reads step 1's fragments from (La, Lb); after the barrier step 1 reads the next stage's step 0
       static_assert(NKK == 2 && TN >= TM && APW + BPW <= TN * 2, "step16 interleave");
       step16<false>(acc, af[0], af[1], bf[0], La, Lb, 1);
@@ -541,7 +591,7 @@ struct Tile {
 
   template <int EPI>
   __device__ __forceinline__ void store(const acc_t (&acc)[TM][TN], float4* st, int m0, int n0) const {
-    tile_store<EPI, MBE, TM, TN, WTM, WTN>(g, acc, st, m0 + wm * WTM, n0 + wn * WTN, lane);
+    tile_store<EPI, MBE, TM, TN, WTM, WTN>(g, acc, st, m0 + mrow, n0 + wn * WTN, lane);
   }
 };
 

@@ -934,38 +934,59 @@ __global__ void __launch_bounds__(256, 2) resblock_pair_kernel(ConvDesc c1, Conv
     }
   }
 
-  // epilogue as in conv_bf16_kernel: bias, residual (the input rows), and the output / running-mean update
-  __syncthreads();  // every wave is done with the conv2 slab
-  float4* st = (float4*)hl + wave * (32 * 16);
+  // epilogue as in conv_bf16_kernel: bias, residual (the input rows), and the output / running-mean update.  Each
+  // block's residual rows are loaded one block ahead (block 0's before the barrier), so their latency overlaps the
+  // previous block's stores instead of being paid once per block.
   const int co0 = wn * 64;
   const int r_end = min(r0 + BO, T);
+  const int c4 = lane & 15;
+  const size_t row0 = (size_t)c2.out_off[b];
+  const float* resb = c2.res + row0 * C;
+  auto res_loads = [&](int i, float4 (&rv)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int r = r0 + ws + i * 32 + rr * 4 + (lane >> 4);
+      rv[rr] = r < r_end ? *(const float4*)(resb + (uint32_t)(r * C + co0 + c4 * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  float4 rn[8];
+  if (live2 > 0) res_loads(0, rn);
+  __syncthreads();  // every wave is done with the conv2 slab
+  float4* st = (float4*)hl + wave * (32 * 16);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     if (i >= live2) break;
+    float4 rr4[8];
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) rr4[rr] = rn[rr];
     const int t = lane & 31;
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int c4 = jj * 8 + q * 2 + (lane >> 5);
-        st[t * 16 + (c4 ^ (t & 15))] = make_float4(acc[i][jj][q * 4], acc[i][jj][q * 4 + 1], acc[i][jj][q * 4 + 2], acc[i][jj][q * 4 + 3]);
+        const int cc = jj * 8 + q * 2 + (lane >> 5);
+        st[t * 16 + (cc ^ (t & 15))] = make_float4(acc[i][jj][q * 4], acc[i][jj][q * 4 + 1], acc[i][jj][q * 4 + 2], acc[i][jj][q * 4 + 3]);
       }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const int c4 = lane & 15;
-    float4 vv4[8], rr4[8], tt4[8];
+    float4 vv4[8], tt4[8];
 #pragma unroll
     for (int rr = 0; rr < 8; ++rr) {
       const int row = rr * 4 + (lane >> 4);
       const int r = r0 + ws + i * 32 + row;
       vv4[rr] = st[row * 16 + (c4 ^ (row & 15))];
-      rr4[rr] = tt4[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (r < r_end) conv_epilogue4_loads(c2, (size_t)c2.out_off[b] + (size_t)r, co0 + c4 * 4, rr4[rr], tt4[rr]);
+      tt4[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (r < r_end) {
+        const size_t o = (row0 + r) * C + co0 + c4 * 4;
+        if (c2.epi == EPI_ADD_RES) tt4[rr] = *(const float4*)(c2.y + o);
+        else if (c2.epi == EPI_RES_MEAN && c2.sum_mode != 0) tt4[rr] = *(const float4*)(c2.sum + o);
+      }
     }
+    if (i + 1 < live2) res_loads(i + 1, rn);
 #pragma unroll
     for (int rr = 0; rr < 8; ++rr) {
       const int row = rr * 4 + (lane >> 4);
       const int r = r0 + ws + i * 32 + row;
-      if (r < r_end) conv_epilogue4_pre(c2, (size_t)c2.out_off[b] + (size_t)r, co0 + c4 * 4, vv4[rr], rr4[rr], tt4[rr]);
+      if (r < r_end) conv_epilogue4_pre(c2, row0 + (size_t)r, co0 + c4 * 4, vv4[rr], rr4[rr], tt4[rr]);
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }

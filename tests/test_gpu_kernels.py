@@ -78,11 +78,11 @@ def test_gemm_row_split_taps(dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(1100, 640, 1024), (2048, 3072, 1024), (1300, 1024, 3072), (300, 256, 128)])
-@pytest.mark.parametrize("tile", [0, 1, 2])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 def test_gemm_tiles(dev, M, N, K, tile, epi):
-    """Explicit tile configurations (0: four waves of 64 x 64; 1: eight waves of 64 x 128; 2: eight waves of 64 x 64)
-    with ragged rows and columns against fp32."""
+    """Explicit tile configurations (0: four waves of 64 x 64; 1: eight waves of 64 x 128; 2: eight waves of 64 x 64;
+    3: 208-row tiles of eight waves of 112 x 64 and 96 x 64) with ragged rows and columns against fp32."""
     L = _lib.lib()
     g = torch.Generator(device=dev).manual_seed(M + N * 3 + K * 5 + epi)
     A = torch.randn(M, K, device=dev, generator=g).bfloat16()
@@ -103,6 +103,32 @@ def test_gemm_tiles(dev, M, N, K, tile, epi):
                                     out.data_ptr(), N, M, N, K, epi, tile, _lib.stream_handle()), "gemm tile")
     torch.cuda.synchronize()
     assert rel(out.float(), ref) < {0: 6e-3, 1: 6e-3, 2: 1e-3, 3: 1e-5}[epi]
+
+
+@pytest.mark.parametrize("M,N", [(12800, 1024), (2979, 2048), (416, 256)])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_gemm_208_rows_equal_256(dev, M, N, epi):
+    """The 208-row tile and the 256 x 256 tile sum every output in the same K order and apply the same epilogue: equal
+    bits, dense and taps mode (12,800 rows: the DiT's proj / conv / fc shapes at 16 streams x 400 frames)."""
+    L = _lib.lib()
+    g = torch.Generator(device=dev).manual_seed(M + N + epi)
+    H = 1024
+    P = torch.randn(M + 2, H, device=dev, generator=g).bfloat16()
+    W = (torch.randn(N, 3 * H, device=dev, generator=g) / (3 * H) ** 0.5).bfloat16()
+    bias = torch.randn(N, device=dev, generator=g)
+    gate = torch.randn(N, device=dev, generator=g)
+    a_src = torch.arange(M, dtype=torch.int32, device=dev)
+    h0 = torch.randn(M, N, device=dev, generator=g).half()
+    for taps in (False, True):
+        outs = []
+        for tile in (1, 3):
+            out = h0.clone() if epi == 2 else (torch.zeros(M, N, device=dev) if epi == 3 else torch.full((M, N), 7.0, device=dev).bfloat16())
+            _lib.check(L.t2w_gemm_bf16_tile(P.data_ptr(), H, a_src.data_ptr() if taps else None, W.data_ptr(), bias.data_ptr(),
+                                            gate.data_ptr() if epi == 2 else None, out.data_ptr(), N, M, N, 3 * H if taps else H, epi,
+                                            tile, _lib.stream_handle()), "gemm tile")
+            outs.append(out)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]), (taps, epi)
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (37, 3072, 1024), (100, 1024, 2048), (100, 80, 1024), (300, 2048, 1024), (600, 1024, 320)])
@@ -157,7 +183,7 @@ def test_gemm_splitk_taps(dev):
 
 
 @pytest.mark.parametrize("lens,tile", [([5, 0, 1, 2, 3, 40, 0, 17, 1, 56], -1), ([400] * 3, -1), ([400] * 3, 1), ([400] * 3, 2),
-                                       ([5, 0, 300, 2, 3, 400, 0, 17, 1, 560], 0)])
+                                       ([400] * 3, 3), ([5, 0, 300, 2, 3, 400, 0, 17, 1, 560], 0)])
 def test_gemm_conv_taps(dev, lens, tile):
     """Taps mode: row m reads three consecutive frames starting at a_src[m] of the padded frame buffer; equals a
     kernel-3 conv over [2 cached frames | row frames] (F.conv1d, fp32).  tile: as chosen by shape (-1) or explicit."""
