@@ -968,25 +968,25 @@ __global__ void __launch_bounds__(256, 2) resblock_pair_kernel(ConvDesc c1, Conv
         st[t * 16 + (cc ^ (t & 15))] = make_float4(acc[i][jj][q * 4], acc[i][jj][q * 4 + 1], acc[i][jj][q * 4 + 2], acc[i][jj][q * 4 + 3]);
       }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    float4 vv4[8], tt4[8];
+    float4 vv4[8];
 #pragma unroll
     for (int rr = 0; rr < 8; ++rr) {
       const int row = rr * 4 + (lane >> 4);
-      const int r = r0 + ws + i * 32 + row;
       vv4[rr] = st[row * 16 + (c4 ^ (row & 15))];
-      tt4[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (r < r_end) {
-        const size_t o = (row0 + r) * C + co0 + c4 * 4;
-        if (c2.epi == EPI_ADD_RES) tt4[rr] = *(const float4*)(c2.y + o);
-        else if (c2.epi == EPI_RES_MEAN && c2.sum_mode != 0) tt4[rr] = *(const float4*)(c2.sum + o);
-      }
     }
     if (i + 1 < live2) res_loads(i + 1, rn);
+    // the running sum / accumulated output (the stage's last dilation only) per row, next to its store
 #pragma unroll
     for (int rr = 0; rr < 8; ++rr) {
       const int row = rr * 4 + (lane >> 4);
       const int r = r0 + ws + i * 32 + row;
-      if (r < r_end) conv_epilogue4_pre(c2, row0 + (size_t)r, co0 + c4 * 4, vv4[rr], rr4[rr], tt4[rr]);
+      if (r < r_end) {
+        const uint32_t o = (uint32_t)(r * C + co0 + c4 * 4);
+        float4 t4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c2.epi == EPI_ADD_RES) t4 = *(const float4*)(c2.y + row0 * C + o);
+        else if (c2.epi == EPI_RES_MEAN && c2.sum_mode != 0) t4 = *(const float4*)(c2.sum + row0 * C + o);
+        conv_epilogue4_pre(c2, row0 + (size_t)r, co0 + c4 * 4, vv4[rr], rr4[rr], t4);
+      }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
