@@ -319,14 +319,16 @@ struct Tile {
   static constexpr int MBE = FP8 ? 32 : 16;           // MFMA block edge
   static constexpr int WTM = TMX ? TMX * MBE : BM / WM, WTN = BN / WN;  // wave sub-tile
   static constexpr int TM = WTM / MBE, TN = WTN / MBE;  // MFMA blocks per wave
-  // 1 KB (8-row) load blocks per stage, and per wave (the last A round may cover only the first waves)
-  static constexpr int NAB = BM / 8, APW = (NAB + NW - 1) / NW, BPW = BN / 8 / NW;
-  static constexpr bool AREM = NAB % NW != 0;
+  // 1 KB (8-row) load blocks per stage and wave; A rows past the last whole round (BM = 208: 16 rows) go two per wave
+  // as one 4-byte-per-lane load (every wave issues the same loads, so no branch splits the interleaved stage)
+  static constexpr int APW = BM / 8 / NW, BPW = BN / 8 / NW;
+  static constexpr int AREMR = BM - APW * NW * 8;  // A rows of the remainder
+  static constexpr bool AREM = AREMR != 0;
   static constexpr int ES = FP8 ? 1 : 2;              // bytes per element
   static constexpr int BKE = BK * 2 / ES;             // K values per 128-byte stage row
   static constexpr int NKK = 2;                       // MFMA K steps per stage (32 bf16 or 64 fp8 values each)
   static constexpr int NSC = FP8 ? TM : 1;            // scale dwords per lane and stage
-  static_assert(NAB * 8 == BM && BPW * NW * 8 == BN, "tile rows / waves mismatch");
+  static_assert((AREMR == 0 || AREMR == 2 * NW) && BPW * NW * 8 == BN, "tile rows / waves mismatch");
   static_assert(WTM % 32 == 0 || (!FP8 && WTM % 16 == 0), "the epilogue works in 32-row slabs (bf16: a last 16-row one)");
   static_assert(TMX == 0 || !FP8, "uneven row splits are bf16 only");
   typedef typename FragT<FP8>::type frag_t;
@@ -336,6 +338,7 @@ struct Tile {
   // loads take the operand base from scalar registers
   uint32_t asrc[APW];
   uint32_t bsrc[BPW];
+  uint32_t arem;  // the remainder rows: this lane's 4 bytes
   const uint8_t* sbase[NSC];  // fp8: this lane's activation rows' scale rows
   const GemmArgs& g;
   int lane, wave, wm, wn;
@@ -356,6 +359,14 @@ struct Tile {
       const int m = min(m0 + trow, g.M - 1);  // rows past M load row M - 1; their results are never stored
       const int ch = (lane & 7) ^ swz_key(trow);
       asrc[p] = (uint32_t)(TAPS ? g.a_src[m] : m) * (uint32_t)(g.lda * ES) + ch * 16;
+    }
+    if constexpr (AREM) {
+      // wave w loads rows APW NW 8 + 2 w and + 1: lane l the 4 bytes at LDS chunk position (l % 32) / 4 of row
+      // + l / 32, i.e. logical chunk position ^ key
+      const int trow = APW * NW * 8 + 2 * wave + (lane >> 5);
+      const int m = min(m0 + trow, g.M - 1);
+      const int ch = ((lane & 31) >> 2) ^ swz_key(trow);
+      arem = (uint32_t)(TAPS ? g.a_src[m] : m) * (uint32_t)(g.lda * ES) + ch * 16 + (lane & 3) * 4;
     }
 #pragma unroll
     for (int p = 0; p < BPW; ++p) {
@@ -384,11 +395,10 @@ struct Tile {
     }
     const uint8_t* A = (const uint8_t*)g.A;
     const uint8_t* B = (const uint8_t*)g.B;
-    constexpr int APF = AREM ? APW - 1 : APW;  // A rounds every wave loads
-    if (AREM && wave + APF * NW < NAB)  // first, so the unconditional loads stay in the block of the MFMAs they interleave with
-      __builtin_amdgcn_global_load_lds((const void*)(A + (asrc[APF] + (uint32_t)aoff)), (lds_ptr_t)(la + (wave + APF * NW) * 64), 16, 0, 0);
+    if constexpr (AREM)
+      __builtin_amdgcn_global_load_lds((const void*)(A + (arem + (uint32_t)aoff)), (lds_ptr_t)(la + (APW * NW * 8 + 2 * wave) * 8), 4, 0, 0);
 #pragma unroll
-    for (int p = 0; p < APF; ++p)
+    for (int p = 0; p < APW; ++p)
       __builtin_amdgcn_global_load_lds((const void*)(A + (asrc[p] + (uint32_t)aoff)), (lds_ptr_t)(la + (wave + p * NW) * 64), 16, 0, 0);
 #pragma unroll
     for (int p = 0; p < BPW; ++p)
@@ -438,9 +448,10 @@ struct Tile {
     }
   }
 
-  // One 32-K step of 16 x 16 blocks, columns outermost: right after the MFMAs of column j, B fragment j (and, for
-  // j < TM, A fragment j into an) of step kn of buffers (La, Lb) is read, so one register set holds B across steps.
-  // With V the stage's 8 global->LDS loads (already issued in program order) go one per column.
+  // One 32-K step of 16 x 16 blocks, columns outermost: right after the MFMAs of column j, B fragment j (and A
+  // fragment j into an for j < TM, or with more row than column blocks A fragments [j TM / TN, (j + 1) TM / TN)) of
+  // step kn of buffers (La, Lb) is read, so one register set holds B across steps.  With V the stage's global->LDS
+  // loads (already issued in program order) are spread over the columns.
   template <bool V>
   __device__ __forceinline__ void step16(acc_t (&acc)[TM][TN], const frag_t (&ac)[TM], frag_t (&an)[TM], frag_t (&bf)[TN],
                                          const uint4* La, const uint4* Lb, int kn) const {
@@ -450,38 +461,26 @@ struct Tile {
 #pragma unroll
       for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], ac[i], acc[i][j], 0, 0, 0);
       bf[j] = as_bf16x8(Lb[swz(wn * WTN + j * 16 + (lane & 15), chunk)]);
-      if (j < TM) an[j] = as_bf16x8(La[swz(mrow + j * 16 + (lane & 15), chunk)]);
+      // A fragments of the next step: fragment j after column j (TM <= TN), else fragments [j TM / TN, (j + 1) TM / TN)
+      if constexpr (TM <= TN) {
+        if (j < TM) an[j] = as_bf16x8(La[swz(mrow + j * 16 + (lane & 15), chunk)]);
+      } else {
+#pragma unroll
+        for (int i = j * TM / TN; i < (j + 1) * TM / TN; ++i) an[i] = as_bf16x8(La[swz(mrow + i * 16 + (lane & 15), chunk)]);
+      }
     }
-    constexpr int NV = APW - (AREM ? 1 : 0) + BPW, VPC = (NV + TN - 1) / TN;
+    constexpr int NV = APW + (AREM ? 1 : 0) + BPW, VPC = (NV + TN - 1) / TN;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
       if (V && j * VPC < NV) __builtin_amdgcn_sched_group_barrier(0x020, VPC, 0);
-      if (j < TM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      if (nA(j) >= 2) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+      else if (nA(j) == 1) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
   }
-
-  // The same with rows outermost, for wave tiles taller than wide (TM > TN): right after the MFMAs of row i, A fragment
-  // i (and, for i < TN, B fragment i into bn) of step kn is read, so one register set holds A across steps.
-  template <bool V>
-  __device__ __forceinline__ void step16r(acc_t (&acc)[TM][TN], const frag_t (&bc)[TN], frag_t (&bn)[TN], frag_t (&af)[TM],
-                                          const uint4* La, const uint4* Lb, int kn) const {
-    const int chunk = kn * 4 + (lane >> 4);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bc[j], af[i], acc[i][j], 0, 0, 0);
-      af[i] = as_bf16x8(La[swz(mrow + i * 16 + (lane & 15), chunk)]);
-      if (i < TN) bn[i] = as_bf16x8(Lb[swz(wn * WTN + i * 16 + (lane & 15), chunk)]);
-    }
-    constexpr int NV = APW - (AREM ? 1 : 0) + BPW, VPR = (NV + TM - 1) / TM;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, TN, 0);
-      if (V && i * VPR < NV) __builtin_amdgcn_sched_group_barrier(0x020, VPR, 0);
-    }
-  }
+  // A fragments read after column j's MFMAs
+  static constexpr int nA(int j) { return TM <= TN ? (j < TM ? 1 : 0) : (j + 1) * TM / TN - j * TM / TN; }
 
   // fp8, 64 x 128 wave tiles: one 64-K step of 32 x 32 x 64 scaled blocks, columns outermost, with B fragment j (and, for
   // j < TM, A fragment j into an) of step kn of (La, Lb) read right after column j's MFMAs, as step16 does: one B
@@ -522,19 +521,9 @@ struct Tile {
   // barrier the loads of stage kt + 2 go into (La, Lb, sd).
   __device__ __forceinline__ void stage(acc_t (&acc)[TM][TN], frag_t (&af)[2][TM], frag_t (&bf)[2][TN], uint4* La,
                                         uint4* Lb, uint32_t (&sd)[NSC], const uint4* Na, const uint4* Nb, int kt, int KT) const {
-    if constexpr (MBE == 16 && TM > TN) {
-      // rows outermost: B double buffered, A single
-      static_assert(NKK == 2, "step16r interleave");
-      step16r<false>(acc, bf[0], bf[1], af[0], La, Lb, 1);
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-      __syncthreads();
-      issue(La, Lb, sd, min(kt + 2, KT - 1));
-      step16r<true>(acc, bf[1], bf[0], af[0], Na, Nb, 0);
-      return;
-    }
-    if constexpr (MBE == 16 && TM <= TN) {
+    if constexpr (MBE == 16) {
       // bf16: step 0 reads step 1's fragments from (La, Lb); after the barrier step 1 reads the next stage's step 0
-      static_assert(NKK == 2 && TN >= TM && APW + BPW <= TN * 2, "step16 interleave");
+      static_assert(NKK == 2 && APW + BPW <= TN * 2, "step16 interleave");
       step16<false>(acc, af[0], af[1], bf[0], La, Lb, 1);
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       __syncthreads();
