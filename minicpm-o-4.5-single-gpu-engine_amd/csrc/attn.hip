@@ -50,6 +50,23 @@ __device__ __forceinline__ bf16x8 vt_frag(const uint4* vtile, int kb, int d0, in
   return as_bf16x8(u);
 }
 
+// The maximum of the 32 scores a lane holds for its query in a 64-key tile (MFMA results or -inf, never NaN), in 16
+// v_max3_f32: through fmaxf each MFMA result is first canonicalised by a v_max_f32 of its own (56 instructions in all)
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ float tile_score_max(const f32x16 (&sc)[2]) {
+  float m0 = max3_raw(sc[0][0], sc[0][1], sc[0][2]), m1 = max3_raw(sc[1][0], sc[1][1], sc[1][2]);
+#pragma unroll
+  for (int r = 3; r < 15; r += 2) {
+    m0 = max3_raw(m0, sc[0][r], sc[0][r + 1]);
+    m1 = max3_raw(m1, sc[1][r], sc[1][r + 1]);
+  }
+  return max3_raw(max3_raw(m0, sc[0][15], sc[1][15]), m1, m1);
+}
+
 // NaN outputs for queries [q0, q1) of a row whose key list breaks what the kernels assume: longer than the caller's
 // bound, or shorter than the row's own tokens (a row's new frames are the first entries of its list)
 __device__ __forceinline__ void nan_rows(const AttnArgs& a, int start, int q0, int q1, int head, int tid, int nthreads) {
@@ -205,9 +222,7 @@ __global__ void __launch_bounds__(128 * KS, 2) attn_kernel(AttnArgs a) {
           }
         }
       }
-      float mx = -__builtin_inff();
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+      float mx = tile_score_max(sc);
       mx = fmaxf(mx, xor32(mx));
       // m starts at a finite -1e30: keys all invisible so far give exp2(-inf) = 0 and leave m, l and o alone
       const float mn = fmaxf(m, mx);
@@ -367,9 +382,7 @@ __device__ __forceinline__ void lds_key_tile(const uint4* Ks, const uint4* Vs, i
       }
     }
   }
-  float mx = -__builtin_inff();
-#pragma unroll
-  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+  float mx = tile_score_max(sc);
   mx = fmaxf(mx, xor32(mx));
   const float mn = fmaxf(m, mx);
   const float alpha = __builtin_amdgcn_exp2f((m - mn) * sl2);
