@@ -106,10 +106,11 @@ def test_gemm_tiles(dev, M, N, K, tile, epi):
 
 
 @pytest.mark.parametrize("M,N", [(12800, 1024), (2979, 2048), (416, 256)])
-@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 7])
 def test_gemm_208_rows_equal_256(dev, M, N, epi):
     """The 208-row tile and the 256 x 256 tile sum every output in the same K order and apply the same epilogue: equal
-    bits, dense and taps mode (12,800 rows: the DiT's proj / conv / fc shapes at 16 streams x 400 frames)."""
+    bits, dense and taps mode, every epilogue of the tile entry (7: fp16 out, the DiT's in_proj) (12,800 rows: the
+    DiT's proj / conv / fc shapes at 16 streams x 400 frames)."""
     L = _lib.lib()
     g = torch.Generator(device=dev).manual_seed(M + N + epi)
     H = 1024
@@ -119,10 +120,17 @@ def test_gemm_208_rows_equal_256(dev, M, N, epi):
     gate = torch.randn(N, device=dev, generator=g)
     a_src = torch.arange(M, dtype=torch.int32, device=dev)
     h0 = torch.randn(M, N, device=dev, generator=g).half()
-    for taps in (False, True):
+    for taps in (False,) if epi == 7 else (False, True):  # the fp16 epilogue has no taps form
         outs = []
         for tile in (1, 3):
-            out = h0.clone() if epi == 2 else (torch.zeros(M, N, device=dev) if epi == 3 else torch.full((M, N), 7.0, device=dev).bfloat16())
+            if epi == 2:
+                out = h0.clone()
+            elif epi == 3:
+                out = torch.zeros(M, N, device=dev)
+            elif epi == 7:  # fp16 out
+                out = torch.full((M, N), 7.0, device=dev).half()
+            else:
+                out = torch.full((M, N), 7.0, device=dev).bfloat16()
             _lib.check(L.t2w_gemm_bf16_tile(P.data_ptr(), H, a_src.data_ptr() if taps else None, W.data_ptr(), bias.data_ptr(),
                                             gate.data_ptr() if epi == 2 else None, out.data_ptr(), N, M, N, 3 * H if taps else H, epi,
                                             tile, _lib.stream_handle()), "gemm tile")
