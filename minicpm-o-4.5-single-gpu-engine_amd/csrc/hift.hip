@@ -1340,7 +1340,7 @@ __global__ void source_kernel(const float* phase, const float* f0, const int* fr
 }
 
 // STFT of the source (n_fft 16, hop 4, centred, reflect padding, periodic Hann window): frame f of item i ->
-// [re_0..re_8 | im_0..im_8]
+// [re_0..re_8 | im_0..im_8 | 14 zeros] (STFT_LD floats, written as 16-byte stores)
 __global__ void stft_kernel(const float* s, const int* smp_off, const int* smp_len, const int* fr_off, const int* fr_len,
                             const float* win, float* out) {
   const int it = blockIdx.y;
@@ -1357,7 +1357,7 @@ __global__ void stft_kernel(const float* s, const int* smp_off, const int* smp_l
     if (p >= n) p = 2 * (n - 1) - p;
     v[k] = __fmul_rn(x[p], win[k]);
   }
-  float* o = out + (size_t)(fr_off[it] + f) * 18;
+  float o[STFT_LD];
 #pragma unroll
   for (int b = 0; b < 9; ++b) {
     float re = 0.f, im = 0.f;
@@ -1369,6 +1369,11 @@ __global__ void stft_kernel(const float* s, const int* smp_off, const int* smp_l
     o[b] = re;
     o[9 + b] = im;
   }
+#pragma unroll
+  for (int b = 18; b < STFT_LD; ++b) o[b] = 0.f;
+  float4* dst = (float4*)(out + (size_t)(fr_off[it] + f) * STFT_LD);
+#pragma unroll
+  for (int q = 0; q < STFT_LD / 4; ++q) dst[q] = make_float4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
 }
 
 // ISTFT (``istft_overlap_add``): mag = min(exp(x_re), 100), phase = sin(x_im), spectrum mag (cos phase, sin phase);

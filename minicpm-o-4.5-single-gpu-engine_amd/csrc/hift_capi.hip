@@ -44,6 +44,9 @@ struct t2w_hift {
       if (f.first == wbf) return f.second;
     return nullptr;
   }
+  // the source downsampling convs' fp32 weights with their 18 input channels padded to STFT_LD ([Cout][taps][32], made
+  // by t2w_hift_create), read with the padded STFT rows
+  float* src_w32[3] = {nullptr, nullptr, nullptr};
 };
 
 namespace {
@@ -93,7 +96,7 @@ size_t carve(const t2w_hift* h, const Lens& L, char* base, Bufs* b) {
   t.f0b = take((size_t)L.tot[C_T] * d.f0_channels);
   t.f0 = take(L.tot[C_T]);
   t.phase = take((size_t)L.tot[C_T] * (d.harmonics + 1));
-  t.stft = take((size_t)L.tot[C_S2] * (d.n_fft + 2));
+  t.stft = take((size_t)L.tot[C_S2] * STFT_LD);
   t.X = take(big);
   t.XN = take(big);
   t.Z = take(big);
@@ -247,6 +250,19 @@ int t2w_hift_create(const t2w_hift_dims* dims, const t2w_hift_weights* w, t2w_hi
     }
   }
   if (e == hipSuccess) e = add(w->conv_post, 1, nsrc, 7, h->chans[3]);
+  for (int i = 0; i < 3 && e == hipSuccess; ++i) {  // the source downsampling weights, input channels padded with zeros
+    const int r = i == 0 ? d.up_rates[2] * d.up_rates[1] : (i == 1 ? d.up_rates[2] : 1), taps = r == 1 ? 1 : 2 * r;
+    const size_t rows = (size_t)h->chans[i + 1] * taps;
+    if (!w->src_down[i].w) {
+      e = hipErrorInvalidValue;
+      break;
+    }
+    e = hipMalloc((void**)&h->src_w32[i], rows * STFT_LD * sizeof(float));
+    if (e == hipSuccess) e = hipMemsetAsync(h->src_w32[i], 0, rows * STFT_LD * sizeof(float), nullptr);
+    if (e == hipSuccess)
+      e = hipMemcpy2DAsync(h->src_w32[i], STFT_LD * sizeof(float), w->src_down[i].w, nsrc * sizeof(float), nsrc * sizeof(float), rows,
+                           hipMemcpyDeviceToDevice, nullptr);
+  }
   if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
   if (e != hipSuccess) {
     t2w_hift_destroy(h);
@@ -259,6 +275,8 @@ int t2w_hift_create(const t2w_hift_dims* dims, const t2w_hift_weights* w, t2w_hi
 void t2w_hift_destroy(t2w_hift* h) {
   if (!h) return;
   for (auto& f : h->frag) (void)hipFree(f.second);
+  for (float* p : h->src_w32)
+    if (p) (void)hipFree(p);
   delete h;
 }
 
@@ -343,7 +361,7 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
   } else if (s != source) {
     H_CHECK(hipMemcpyAsync(source, s, x.L.tot[C_SMP] * sizeof(float), hipMemcpyDeviceToDevice, x.st), "source copy");
   }
-  H_CHECK(timed_launch(T2W_TIMER_HIFT_STFT, 4.0 * x.L.tot[C_SMP] + 4.0 * nsrc * x.L.tot[C_S2], x.st,
+  H_CHECK(timed_launch(T2W_TIMER_HIFT_STFT, 4.0 * x.L.tot[C_SMP] + 4.0 * STFT_LD * x.L.tot[C_S2], x.st,
                        [&] { return stft16(s, x.off(C_SMP), x.len(C_SMP), x.off(C_S2), x.len(C_S2), n, x.L.mx[C_S2], w.window, B.stft, x.st); }),
           "stft");
 
@@ -377,8 +395,9 @@ int t2w_hift_forward(const t2w_hift* h, int n, const int* frames, const int* pla
     }
     {  // source branch: downsampling conv of the source STFT, a ResBlock, added into the stage input
       const int r = i == 0 ? d.up_rates[2] * d.up_rates[1] : (i == 1 ? d.up_rates[2] : 1);
-      ConvDesc c = r == 1 ? conv_desc(x, w.src_down[i], B.stft, nsrc, C_S2, B.Z2, cout, cls, 1, 1, 1, 0)
-                          : conv_desc(x, w.src_down[i], B.stft, nsrc, C_S2, B.Z2, cout, cls, 2 * r, 1, r, r / 2);
+      ConvDesc c = r == 1 ? conv_desc(x, w.src_down[i], B.stft, STFT_LD, C_S2, B.Z2, cout, cls, 1, 1, 1, 0)
+                          : conv_desc(x, w.src_down[i], B.stft, STFT_LD, C_S2, B.Z2, cout, cls, 2 * r, 1, r, r / 2);
+      c.w = x.h->src_w32[i];  // padded like the STFT rows
       if (run(x, c, cls, "source down")) return 1;
       // X (the stage input) is dead once the transposed conv has read it: the ResBlocks' Snake scratch
       if (resblock(x, w.src_res[i], d.src_kernels[i], B.Z2, B.Z2, B.TMP, X, cout, cls, nullptr, 0, B.XN)) return 1;

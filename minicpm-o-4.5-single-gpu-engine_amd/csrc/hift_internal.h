@@ -47,6 +47,9 @@ hipError_t nsf_phase(const float* f0, const int* fr_off, const int* fr_len, int 
 hipError_t nsf_source(const float* phase, const float* f0, const int* fr_off, const int* fr_len, const int* smp_off, int n_items,
                       int max_frames, int harm, float inv_scale, int up, float amp, float noise_std, float unvoiced_amp, float thr,
                       const float* noise, const float* lw, const float* lb, const float* cache, int S, float* out, hipStream_t st);
+// STFT frames are rows of STFT_LD floats: the 9 real parts, the 9 imaginary parts, then zeros, so that the source
+// downsampling convs read 16-byte-aligned rows of 32 channels (their weights padded alike) on the DMA-staged kernel
+constexpr int STFT_LD = 32;
 hipError_t stft16(const float* s, const int* smp_off, const int* smp_len, const int* fr_off, const int* fr_len, int n_items, int max_fr,
                   const float* win, float* out, hipStream_t st);
 hipError_t istft16(const float* x, const int* fr_off, const int* fr_len, const int* smp_off, int n_items, int max_smp, const float* win,
