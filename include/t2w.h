@@ -324,7 +324,9 @@ typedef struct {
 /* The handle keeps the weight pointers (the caller keeps the weights alive) and, for every conv with a bf16 copy, makes a
  * device copy of it in the MFMA operand order its kernels read (the same size; freed by t2w_hift_destroy); the copies
  * are made on the null stream and are complete when create returns.  The bf16 weights are read only there: writes to
- * them after create are not seen by the bf16 convs (create a new handle); the fp32 weights are read at every call. */
+ * them after create are not seen by the bf16 convs (create a new handle).  So are the fp32 weights of the three source
+ * downsampling convs (src_down[i].w, required), copied with their 18 input channels padded to 32; the other fp32
+ * weights are read at every call. */
 int t2w_hift_create(const t2w_hift_dims* dims, const t2w_hift_weights* w, t2w_hift** out);
 void t2w_hift_destroy(t2w_hift* h);
 /* Plan of a call over n_items rows with frames[i] mel frames (host array): ints for t2w_hift_plan to fill, which the
