@@ -233,12 +233,16 @@ __global__ void __launch_bounds__(256) ln_mod_kernel(f16_t* h, const float* shif
                                                      bf16_t* out, uint8_t* q, uint8_t* qs, int N, int H, Pend pd, Prefetch pf,
                                                      unsigned row_blocks) {
   constexpr int G = VPL >= 8 ? 8 : 4;  // fp16 rows: 16 bytes per lane and instruction
-  if (blockIdx.x >= row_blocks) {  // the prefetch workgroups, after every row's
-    prefetch_part(pf, blockIdx.x - row_blocks);
+  // the prefetch workgroups come first, so the weight reads start with the rows' instead of trailing them (16 x 400
+  // solve 98.5 -> 98.0 ms, same bits); the row blocks follow
+  const unsigned pfb = gridDim.x - row_blocks;
+  if (blockIdx.x < pfb) {
+    prefetch_part(pf, blockIdx.x);
     return;
   }
+  const unsigned rblk = blockIdx.x - pfb;
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int n = rblk * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (n >= N) return;
   float v[VPL], sc[VPL], sh[VPL];
   // the modulation (the same for every row, cache hits) is loaded with the row, not after its statistics
@@ -316,12 +320,14 @@ template <int VPL, bool PEND>
 __global__ void __launch_bounds__(256) ln_mod_conv_kernel(f16_t* h, const float* shift, const float* scale1, float eps,
                                                           ConvPlace cp, int H, Pend pd, Prefetch pf, unsigned row_blocks) {
   constexpr int G = VPL >= 8 ? 8 : 4;
-  if (blockIdx.x >= row_blocks) {
-    prefetch_part(pf, blockIdx.x - row_blocks);
+  const unsigned pfb = gridDim.x - row_blocks;
+  if (blockIdx.x < pfb) {
+    prefetch_part(pf, blockIdx.x);
     return;
   }
+  const unsigned rblk = blockIdx.x - pfb;
   const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int w = rblk * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (w < cp.N) {
     float v[VPL], sc[VPL], sh[VPL];
     const TokPlace tp = tok_place(cp, w);
@@ -343,12 +349,14 @@ __global__ void __launch_bounds__(256) ln_mod_conv_kernel(f16_t* h, const float*
 template <int VPL, bool PEND>
 __global__ void __launch_bounds__(256) ln_mish_conv_kernel(const bf16_t* y, const float* lw, const float* lb, float eps,
                                                            ConvPlace cp, int H, Pend pd, Prefetch pf, unsigned row_blocks) {
-  if (blockIdx.x >= row_blocks) {
-    prefetch_part(pf, blockIdx.x - row_blocks);
+  const unsigned pfb = gridDim.x - row_blocks;
+  if (blockIdx.x < pfb) {
+    prefetch_part(pf, blockIdx.x);
     return;
   }
+  const unsigned rblk = blockIdx.x - pfb;
   const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int w = rblk * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (w < cp.N) {
     constexpr int G = VPL >= 8 ? 8 : 4;  // the row comes in as bf16
     float v[VPL], a[VPL], b[VPL];
